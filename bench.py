@@ -1,0 +1,321 @@
+"""Benchmark of the MI355X quantized-matmul hot path.
+
+Default workload (one JSON line on stdout): BASELINE config 3, the W4A16
+lm_head -- M=1, K=1024, V=248094 -- as one fused GEMV + argmax launch per
+step, with 8 distinct weight copies (1.06 GB) rotated so no step hits the
+256 MB MALL.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
+(132,484,244 B per step, inputs resident in HBM).  `--workload` selects the
+other BASELINE configs (gemv1, mlp, lm_head, prefill, w8a8).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload lm_head]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "W4A16 M=1 GEMV HBM GB/s (% peak) + µs/call; prefill GEMM TFLOPS (% MFMA)"
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+INT8_MFMA_PEAK_TOPS = 5000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def load_pkg():
+    sys.path.insert(0, str(ROOT))
+    import __graft_entry__ as ge
+    return ge.load_package()
+
+
+def f16_normal(rng, shape, std):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16).view(np.uint16)
+
+
+def to_dev_f16(a_u16):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16)).cuda().view(torch.float16)
+
+
+def timed_launches(launch, n_sets, steps, warmup):
+    """Runs `launch(i)` for warmup + steps iterations on the current stream.
+    Returns (total_ms over the timed steps, per-launch kernel ms list)."""
+    import torch
+    for i in range(warmup):
+        launch(i % n_sets)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        ev[i][0].record()
+        launch((warmup + i) % n_sets)
+        ev[i][1].record()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1), [a.elapsed_time(b) for a, b in ev]
+
+
+def traffic_from_profiles(workload: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), committed in profiles/traffic.json."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(workload, {}).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+# --------------------------------------------------------------------------- #
+# CPU baseline: the oracle's restatement of the reference CPU path            #
+# --------------------------------------------------------------------------- #
+def cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes, budget_s=12.0):
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import load_oracle       # cpu_baseline leg only: the oracle is timed, not shipped
+    o = load_oracle()
+    w8 = o.unpack_awq(qweight, qzeros)
+    cores = min(16, os.cpu_count() or 1)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 20):
+        t = time.perf_counter()
+        logits = o.w4a16_matmul(x, w8, scales, nthreads=cores)[0, :V]
+        tok = int(np.argmax(logits))  # first maximum, as the reference's scan
+        times.append(time.perf_counter() - t)
+    med = float(np.median(times))
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full lm_head K=1024 V={V}: oracle fp32 group formula over unpacked int8 (q-z) "
+                      f"+ argmax, {len(times)} calls, median {med * 1e3:.1f} ms/call",
+            "us_per_call": round(med * 1e6, 1), "token": tok}
+
+
+def cpu_baseline_generic(fn, nbytes_or_flops, unit, sample, budget_s=10.0):
+    cores = min(16, os.cpu_count() or 1)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 20):
+        t = time.perf_counter()
+        fn(cores)
+        times.append(time.perf_counter() - t)
+    med = float(np.median(times))
+    scale = 1e9 if unit == "GB/s" else 1e12
+    return {"value": round(nbytes_or_flops / med / scale, 4), "unit": unit, "cores": cores, "kind": "port",
+            "sample": f"{sample}, {len(times)} calls, median {med * 1e3:.2f} ms/call", "us_per_call": round(med * 1e6, 1)}
+
+
+# --------------------------------------------------------------------------- #
+# workloads                                                                    #
+# --------------------------------------------------------------------------- #
+def w4a16_bytes(K, N):
+    G = K // 128
+    return K * N // 2 + G * N * 2 + G * N // 2
+
+
+def wl_lm_head(pkg, args):
+    import torch
+    K, V, NW = 1024, 248094, 248096
+    copies = args.copies or 8
+    rng = np.random.default_rng(1)
+    t = time.perf_counter()
+    w = f16_normal(rng, (K, NW), 0.02)
+    x = f16_normal(rng, (1, K), 1.0)
+    qweight, qzeros, scales = pkg.quantize_int4(w)
+    del w
+    qw, sc, zr = pkg.pack_awq(qweight, qzeros, scales)
+    log(f"[lm_head] synthetic weights quantised + packed in {time.perf_counter() - t:.1f} s")
+    base = pkg.W4A16QuantizedWeight.from_packed(qw, sc, zr, K, NW, 0)
+    heads = [pkg.LmHeadW4A16(base, V)]
+    for _ in range(copies - 1):
+        wc = pkg.W4A16QuantizedWeight(base.qweight.clone(), base.scales.clone(), base.zeros.clone(), K, NW, 0)
+        heads.append(pkg.LmHeadW4A16(wc, V))
+    xd = to_dev_f16(x)
+    logits = torch.empty(V, dtype=torch.float16, device="cuda")
+    nbytes = K * V // 2 + (K // 128) * V * 2 + (K // 128) * V // 2 + 2 * V + 2 * K
+    total_ms, kms = timed_launches(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
+    token = int(heads[0].token.item())
+    res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
+               config={"workload": "w4a16_lm_head_gemv_argmax", "M": 1, "K": K, "V": V,
+                       "weight_copies_rotated": copies, "rotated_bytes": copies * (qw.nbytes + sc.nbytes + zr.nbytes),
+                       "algorithmic_bytes_per_step": nbytes, "token": token},
+               dtype="w4a16 (f16 x int4, f32 accumulate)", kernel="w4a16_gemv_kernel<argmax>")
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes)
+    return res
+
+
+def wl_gemv1(pkg, args):
+    import torch
+    K = N = 1024
+    sets = args.copies or 1024          # 1024 x 0.55 MB = 562 MB rotated
+    rng = np.random.default_rng(1)
+    w = f16_normal(rng, (K, N), 0.02)
+    x = f16_normal(rng, (1, K), 1.0)
+    qweight, qzeros, scales = pkg.quantize_int4(w)
+    base = pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales)
+    ws = [base] + [pkg.W4A16QuantizedWeight(base.qweight.clone(), base.scales.clone(), base.zeros.clone(), K, N, 0)
+                   for _ in range(sets - 1)]
+    xd = to_dev_f16(x)
+    out = torch.empty((1, N), dtype=torch.float16, device="cuda")
+    nbytes = w4a16_bytes(K, N) + 2 * K + 2 * N
+    total_ms, kms = timed_launches(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps, args.warmup)
+    res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
+               config={"workload": "w4a16_gemv_1024x1024", "M": 1, "K": K, "N": N, "weight_sets_rotated": sets},
+               dtype="w4a16 (f16 x int4, f32 accumulate)", kernel="w4a16_gemv_kernel")
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "tests"))
+        from helpers import load_oracle
+        o = load_oracle()
+        w8 = o.unpack_awq(qweight, qzeros)
+        res["cpu_baseline"] = cpu_baseline_generic(lambda c: o.w4a16_matmul(x, w8, scales, nthreads=1), nbytes, "GB/s",
+                                                   "K=N=1024 GEMV, oracle fp32 group formula, 1 thread", 5.0)
+        res["cpu_baseline"]["cores"] = 1
+    return res
+
+
+def wl_mlp(pkg, args):
+    """Config 2: gate/up 1024->3584, silu*mul, down 3584->1024, 24 layer sets x 4 copies."""
+    import torch
+    H, I = 1024, 3584
+    nsets, reps = 24, args.copies or 4
+    layers = []
+    for s in range(nsets):
+        rng = np.random.default_rng(100 + s)
+        mats = []
+        for (K, N) in ((H, I), (H, I), (I, H)):
+            qweight, qzeros, scales = pkg.quantize_int4(f16_normal(rng, (K, N), 0.02))
+            mats.append(pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales))
+        layers.append(mats)
+    sets = list(layers)
+    for _ in range(reps - 1):
+        sets += [[pkg.W4A16QuantizedWeight(m.qweight.clone(), m.scales.clone(), m.zeros.clone(), m.K, m.N, 0)
+                  for m in L] for L in layers]
+    x = to_dev_f16(f16_normal(np.random.default_rng(1), (1, H), 1.0))
+    g = torch.empty((1, I), dtype=torch.float16, device="cuda")
+    u = torch.empty_like(g)
+    a = torch.empty_like(g)
+    y = torch.empty((1, H), dtype=torch.float16, device="cuda")
+
+    def block(i):
+        L = sets[i]
+        pkg.matmul_w4a16(x, L[0], g)
+        pkg.matmul_w4a16(x, L[1], u)
+        pkg.silu_mul(g, u, a)
+        pkg.matmul_w4a16(a, L[2], y)
+
+    nbytes = 2 * w4a16_bytes(H, I) + w4a16_bytes(I, H) + 2 * H * 2 + 2 * I * 2 * 3 + 2 * H
+    total_ms, kms = timed_launches(block, len(sets), args.steps, args.warmup)
+    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
+                config={"workload": "w4a16_mlp_block_decode", "M": 1, "hidden": H, "intermediate": I,
+                        "weight_sets_rotated": len(sets)},
+                dtype="w4a16 (f16 x int4, f32 accumulate)", kernel="mlp block (4 launches)")
+
+
+def wl_prefill(pkg, args):
+    import torch
+    M, K, N = args.M or 2048, args.K or 1024, args.N or 3584
+    rng = np.random.default_rng(1)
+    qweight, qzeros, scales = pkg.quantize_int4(f16_normal(rng, (K, N), 0.02))
+    w = pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales)
+    x = to_dev_f16(f16_normal(rng, (M, K), 1.0))
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    flops = 2.0 * M * K * N
+    total_ms, kms = timed_launches(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps, args.warmup)
+    return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TFLOP/s", bound="mfma",
+                config={"workload": "w4a16_prefill_gemm", "M": M, "K": K, "N": N},
+                dtype="w4a16 (f16 MFMA, f32 accumulate)", kernel="w4a16_gemm_kernel")
+
+
+def wl_w8a8(pkg, args):
+    import torch
+    M, K, N = args.M or 1024, args.K or 1024, args.N or 3584
+    rng = np.random.default_rng(1)
+    wq = pkg.quantize_dense_weight_w8a8(to_dev_f16(f16_normal(rng, (K, N), 0.02)))
+    xq, xs, _ = pkg.w8a8_quantize(to_dev_f16(f16_normal(rng, (M, K), 1.0)))
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    flops = 2.0 * M * K * N
+    total_ms, kms = timed_launches(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps, args.warmup)
+    return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TOP/s", bound="mfma",
+                config={"workload": "w8a8_gemm_fused", "M": M, "K": K, "N": N},
+                dtype="int8 (i32 accumulate, fused f16 epilogue)", kernel="w8a8_gemm_kernel<kn,f16>")
+
+
+WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp, "prefill": wl_prefill, "w8a8": wl_w8a8}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="lm_head", choices=sorted(WORKLOADS))
+    ap.add_argument("--copies", type=int, default=0, help="distinct weight sets rotated (0: workload default)")
+    ap.add_argument("--M", type=int, default=0)
+    ap.add_argument("--K", type=int, default=0)
+    ap.add_argument("--N", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: every box in this build has a single MI355X and the hot path "
+              "has no multi-GPU leg (see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (the HIP kernels have no CPU fallback)", file=sys.stderr)
+        sys.exit(3)
+    pkg = load_pkg()
+    r = WORKLOADS[args.workload](pkg, args)
+    steps = args.steps
+    ms_per_step = r["total_ms"] / steps
+    kms = np.array(r["kernel_ms"])
+    kmean = float(kms.mean())
+    scale = 1e9 if r["unit"] == "GB/s" else 1e12
+    value = r["bytes"] / (ms_per_step / 1e3) / scale
+    achieved = r["bytes"] / (kmean / 1e3) / scale
+    peak = HBM_PEAK_GBS if r["bound"] == "hbm" else (INT8_MFMA_PEAK_TOPS if r["unit"] == "TOP/s" else FP16_MFMA_PEAK_TFLOPS)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": r["unit"],
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_call": round(ms_per_step * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": r["dtype"],
+        "data": "synthetic (seeded N(0,1) fp16 activations, N(0,0.02) fp16 weights quantised in-build)",
+        "config": r["config"],
+        "roofline": {
+            "bound": r["bound"],
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": "GB/s" if r["bound"] == "hbm" else ("TOP/s" if r["unit"] == "TOP/s" else "TFLOP/s"),
+            "frac": round(achieved / peak, 4),
+            "traffic": traffic_from_profiles(r["config"]["workload"]),
+            "kernel": r["kernel"],
+            "kernel_us_mean": round(kmean * 1e3, 3),
+            "kernel_us_median": round(float(np.median(kms)) * 1e3, 3),
+        },
+        "cpu_baseline": r.get("cpu_baseline"),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

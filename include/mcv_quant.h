@@ -1,0 +1,223 @@
+/*
+ * mcv_quant.h -- C-ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * This is the boundary below the C++ operator surface (namespace minicpmv, see
+ * minicpm-v-4.6-orangepi_amd/cpp/include/minicpmv/).  In the reference that
+ * boundary is the aclnn two-phase ABI generated from each custom operator's
+ * OpDef, e.g. aclnnMatmulW4a16CustomGetWorkspaceSize + aclnnMatmulW4a16Custom
+ * (src/csrc/lib/ops.cpp:1087-1094, OpDef src/csrc/custom_ops/op_host/
+ * matmul_w4a16_custom.cpp:47-75).  Here each operator is one plain function.
+ *
+ * Conventions
+ *   - Only plain pointers, sizes and enums cross the boundary.  Pointers named
+ *     *_dev are device (HBM) pointers; *_host are host pointers.  fp16 data is
+ *     passed as raw IEEE binary16 bits (uint16_t / void*).
+ *   - Device entry points are stream-ordered and asynchronous on `stream`
+ *     (a hipStream_t; NULL means the legacy default stream).  They never
+ *     allocate or free caller memory and never synchronise, except where noted.
+ *   - Every entry point returns MCV_OK (0) or an MCV_ERR_* code; the message of
+ *     the last failure on the calling thread is returned by mcv_last_error().
+ *   - Shapes are validated on the host before any launch; a bad shape is an
+ *     error return, never a kernel launch.
+ *
+ * W4A16 weight layout on the device ("slab-64", MCV_W4_LAYOUT_SLAB64)
+ *   A K x N int4 weight (K % 128 == 0, any N >= 1) is cut into slabs of 64
+ *   output columns (Npad = 64 * ceil(N / 64); padding columns are zero) and
+ *   chunks of 32 k.  One chunk of one slab is 1 KiB: 64 lanes x 16 bytes,
+ *   lane l holding column 64*slab + l, so a wave's 128-bit loads are one
+ *   contiguous 1 KiB line.  Byte offset of (slab, chunk c, lane l) =
+ *   ((slab * (K/32) + c) * 64 + l) * 16; within those 16 bytes word w
+ *   (little-endian uint32) holds k = 32c + 8w + order[s] in nibble s
+ *   (bits 4s..4s+3), order = {0,2,4,6,1,3,5,7}.
+ *   Scales: fp16 [K/128][Npad] (zero for padding columns).
+ *   Zeros: uint32 [K/128][Npad/8], nibble s of word j holding column 8j + s.
+ *   Effective zero = nibble + zero_bias (0 for AWQ/synthetic, 1 for GPTQ v1).
+ *   Dequantised value w[k][n] = (q - (z + zero_bias)) * s[k/128][n].
+ */
+#ifndef MCV_QUANT_H
+#define MCV_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mcv_stream_t; /* hipStream_t */
+
+enum mcv_status {
+    MCV_OK = 0,
+    MCV_ERR_INVALID_ARG = 1, /* null pointer, bad enum, bad size */
+    MCV_ERR_SHAPE = 2,       /* shape constraint violated */
+    MCV_ERR_HIP = 3,         /* HIP runtime error (launch, device query) */
+    MCV_ERR_UNSUPPORTED = 4, /* input format the library cannot represent */
+    MCV_ERR_NO_DEVICE = 5    /* no usable gfx950 device / kernels not loadable */
+};
+
+enum mcv_dtype { MCV_F32 = 0, MCV_F16 = 1 };
+enum mcv_w8_layout { MCV_W8_KN = 0 /* [K][N], the reference's layout */, MCV_W8_NK = 1 /* [N][K] */ };
+
+#define MCV_W4_GROUP 128
+#define MCV_W4_LAYOUT_SLAB64 1
+
+/* Message of the last failed call on this thread ("" if none).  Replaces the
+ * std::runtime_error text of check_acl (src/csrc/include/minicpmv/acl_context.h:11-15). */
+const char* mcv_last_error(void);
+/* Library version string. */
+const char* mcv_version(void);
+
+/* ---------------------------------------------------------------- sizes -- */
+/* Byte sizes of the slab-64 packed tensors for a K x N weight (0 on bad shape). */
+int64_t mcv_w4a16_packed_weight_bytes(int64_t K, int64_t N);
+int64_t mcv_w4a16_packed_scale_bytes(int64_t K, int64_t N);
+int64_t mcv_w4a16_packed_zero_bytes(int64_t K, int64_t N);
+
+/* ---------------------------------------------------- host-side packers -- */
+/* Replaces unpack_awq_weight + pack_w4a16_weight
+ * (src/csrc/lib/quantized_weight.cpp:122-160, 48-73): AutoAWQ gemm tensors
+ * (qweight int32 [K][N/8], qzeros int32 [K/128][N/8], scales fp16 [K/128][N])
+ * to slab-64.  Nibbles are re-laid, never widened to int8.  zero_bias = 0.
+ * Output buffers are host memory of the mcv_w4a16_packed_*_bytes sizes. */
+int mcv_w4a16_pack_awq(const int32_t* qweight_host, const int32_t* qzeros_host,
+                       const uint16_t* scales_host, int64_t K, int64_t N,
+                       void* qw_host, uint16_t* scales_out_host, uint32_t* zeros_out_host);
+
+/* Replaces unpack_gptq_weight + pack_w4a16_weight
+ * (src/csrc/lib/quantized_weight.cpp:75-120, 48-73): GPTQ v1 tensors (qweight
+ * int32 [K/8][N], qzeros int32 [G][N/8], g_idx int32 [K] or NULL, scales fp16
+ * [G][N]) to slab-64 with zero_bias = 1 (GPTQ stores zero - 1, :112).  g_idx
+ * must be k/128 for every k (no act-order): MCV_ERR_UNSUPPORTED otherwise. */
+int mcv_w4a16_pack_gptq(const int32_t* qweight_host, const int32_t* qzeros_host,
+                        const int32_t* g_idx_host, const uint16_t* scales_host,
+                        int64_t K, int64_t N, int64_t groups,
+                        void* qw_host, uint16_t* scales_out_host, uint32_t* zeros_out_host);
+
+/* Build-defined synthetic int4 quantiser (the reference has none; it only
+ * unpacks AutoAWQ/GPTQ checkpoints).  Per (group g, column n) over the 128
+ * fp16 values w of the group: s = fp16_rne(max(max(w) - min(w), 1e-5) / 15),
+ * z = clamp(rne(-min(w) / s), 0, 15), q = clamp(rne(w / s) + z, 0, 15).
+ * Output is AutoAWQ gemm packing (qweight int32 [K][N/8], qzeros int32
+ * [K/128][N/8], scales fp16 [K/128][N]), readable by the reference's
+ * unpack_awq_weight (src/csrc/lib/quantized_weight.cpp:122-160) and by
+ * mcv_w4a16_pack_awq.  w_kn_host is fp16 [K][N], K % 128 == 0, N % 8 == 0.
+ * Runs on up to `nthreads` host threads (<= 0: all hardware threads). */
+int mcv_w4a16_quantize_host(const uint16_t* w_kn_host, int64_t K, int64_t N, int32_t* qweight_host,
+                            int32_t* qzeros_host, uint16_t* scales_host, int nthreads);
+
+/* Inverse of the packers, for round trips and inspection: writes the nibble q
+ * ([K][N] uint8, may be NULL), the effective zero z + zero_bias ([K/128][N]
+ * uint8, may be NULL) and the unpadded scales ([K/128][N] fp16, may be NULL). */
+int mcv_w4a16_unpack_host(const void* qw_host, const uint16_t* scales_host,
+                          const uint32_t* zeros_host, int zero_bias, int64_t K, int64_t N,
+                          uint8_t* q_kn_host, uint8_t* zeff_gn_host, uint16_t* scales_gn_host);
+
+/* ------------------------------------------------------ W4A16 on device -- */
+/* out[M][N] fp16 = x[M][K] fp16 . dequant(W) with fp32 accumulation.
+ * Replaces matmul_w4a16 / aclnnMatmulW4a16Custom (src/csrc/lib/ops.cpp:1030-1095,
+ * kernel src/csrc/custom_ops/op_kernel/matmul_w4a16_custom.cpp:157-168), which
+ * accepts M = 1 only; any M >= 1 is accepted here.  Small M runs the streaming
+ * GEMV kernel, larger M the LDS-dequant + fp16 MFMA GEMM kernel. */
+int mcv_w4a16_gemm(const void* x_dev, int64_t M, int64_t K, int64_t N,
+                   const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                   int zero_bias, void* out_dev, mcv_stream_t stream);
+
+/* The two kernels behind mcv_w4a16_gemm, callable directly (same contract). */
+int mcv_w4a16_gemv(const void* x_dev, int64_t M, int64_t K, int64_t N,
+                   const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                   int zero_bias, void* out_dev, mcv_stream_t stream);
+int mcv_w4a16_gemm_mfma(const void* x_dev, int64_t M, int64_t K, int64_t N,
+                        const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                        int zero_bias, void* out_dev, mcv_stream_t stream);
+
+/* Materialise dequantised weights: w_f16_kn [K][N] = fp16 RNE((q - z) * s)
+ * and/or w8_kn [K][N] = q - z (int8), either may be NULL.  The int8 form is
+ * the reference's unpacked w_int8 (src/csrc/lib/quantized_weight.cpp:155). */
+int mcv_w4a16_dequant(const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                      int zero_bias, int64_t K, int64_t N,
+                      void* w_f16_kn_dev, int8_t* w8_kn_dev, mcv_stream_t stream);
+
+/* The reference's own W4A16 device format: int8 (q - z) tile-packed by
+ * pack_w4a16_weight (src/csrc/lib/quantized_weight.cpp:41-73) into
+ * [(K/128)*8*tilesPerBlock*128][tile_len], fp16 scales [K/128][N], M = 1.
+ * Same validation as src/csrc/lib/ops.cpp:1037-1079. */
+int mcv_w4a16_gemv_tiled_i8(const void* x_dev, int64_t K, int64_t N, int64_t tile_len,
+                            int64_t packed_rows, const int8_t* w_dev, const void* scales_dev,
+                            void* out_dev, mcv_stream_t stream);
+
+/* Workspace for mcv_w4a16_lm_head_argmax: device memory of this many bytes,
+ * zero-filled once before its first use.  Each call leaves it zero-filled
+ * again; calls that share one workspace must not overlap. */
+int64_t mcv_lm_head_workspace_bytes(void);
+
+/* Greedy lm_head over a W4A16 weight: logits[v] = x . W[:, v] (fp16 RNE of the
+ * fp32 sum) for v < V, and token = the first index of the maximum logit, with
+ * fp16 subnormals compared as zero and NaN never winning (language_model.cpp:
+ * 444-479).  x is [1][K]; the weight is K x N as packed (N >= V; columns from
+ * V on are ignored, like the reference's clipped chunk tails, :472).
+ * logits_dev may be NULL.  token_dev receives an int64 on the device.
+ * Replaces the 16 chunk matmuls + 16 D2H copies + host scan of lm_head_greedy
+ * (src/csrc/lib/language_model.cpp:412-482) with one kernel. */
+int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
+                             const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                             int zero_bias, void* logits_dev, int64_t* token_dev,
+                             void* workspace_dev, mcv_stream_t stream);
+
+/* ------------------------------------------------------- W8A8 on device -- */
+/* Per-row symmetric int8 activation quantisation: scale = max|x| / 127
+ * (floor 1e-8), q = trunc(clamp(x * (1/scale), -128, 127) +- 0.5).
+ * Replaces w8a8_quantize (src/csrc/lib/ops.cpp:1135-1171, kernel
+ * op_kernel/w8a8_quantize_custom.cpp:18-47), which accepts M = 1 only.
+ * x_scale_f32_dev [M] receives the fp32 scale; x_scale_f16_dev [M] (may be
+ * NULL) its fp16 RNE encoding, the reference's stored form. */
+int mcv_w8a8_quantize_act(const void* x_dev, int64_t M, int64_t K, int8_t* xq_dev,
+                          float* x_scale_f32_dev, void* x_scale_f16_dev, mcv_stream_t stream);
+
+/* acc[M][N] int32 = xq[M][K] . W exactly.  W is int8 in layout w_layout.
+ * Replaces matmul_w8a8_i32 (src/csrc/lib/ops.cpp:1097-1133, kernel
+ * op_kernel/matmul_w8a8_i32_custom.cpp:15-48), which accepts M = 1 only. */
+int mcv_w8a8_gemm_i32(const int8_t* xq_dev, int64_t M, int64_t K, int64_t N,
+                      const int8_t* w_dev, int w_layout, int32_t* acc_dev, mcv_stream_t stream);
+
+/* Dequant epilogue: out = fp16 RNE(((float)acc * w_scale[n]) * x_scale[m]).
+ * Scales are fp32 or fp16 (mcv_dtype).  Replaces w8a8_dequant
+ * (src/csrc/lib/ops.cpp:1173-1210, op_kernel/w8a8_dequant_custom.cpp:33-69). */
+int mcv_w8a8_dequant(const int32_t* acc_dev, const void* x_scale_dev, int x_scale_dtype,
+                     const void* w_scale_dev, int w_scale_dtype, int64_t M, int64_t N,
+                     void* out_dev, mcv_stream_t stream);
+
+/* Fused int8 GEMM + dequant epilogue: the int32 accumulator never leaves the
+ * chip.  Bit-identical to mcv_w8a8_gemm_i32 followed by mcv_w8a8_dequant.
+ * Replaces the matmul_w8a8_i32 + w8a8_dequant pair of
+ * matmul_decode_w8a8_prequant (src/csrc/lib/decoder_layer.cpp:216-224). */
+int mcv_w8a8_gemm_f16(const int8_t* xq_dev, const void* x_scale_dev, int x_scale_dtype,
+                      int64_t M, int64_t K, int64_t N, const int8_t* w_dev, int w_layout,
+                      const void* w_scale_dev, int w_scale_dtype, void* out_dev,
+                      mcv_stream_t stream);
+
+/* Host-side per-output-channel weight quantiser: replaces
+ * quantize_dense_weight_w8a8 (src/csrc/lib/quantized_weight.cpp:231-268) minus
+ * its device round trip.  w_kn_host fp16 [K][N]; q_host int8 in out_layout;
+ * scale_f32_host [N]; scale_f16_host [N] (truncating encode, :253), may be NULL. */
+int mcv_w8a8_quantize_weight_host(const uint16_t* w_kn_host, int64_t K, int64_t N,
+                                  int8_t* q_host, int out_layout, float* scale_f32_host,
+                                  uint16_t* scale_f16_host);
+
+/* ------------------------------------------------------------ elementwise -- */
+/* out = fp16 RNE(silu(g) * u) in fp32, n elements.  Replaces silu_mul
+ * (src/csrc/lib/ops.cpp:437-456, op_kernel/silu_mul_custom.cpp:38-89). */
+int mcv_silu_mul(const void* gate_dev, const void* up_dev, void* out_dev, int64_t n,
+                 mcv_stream_t stream);
+
+/* Per-row argmax of fp16 [M][N] into int64 [M], first maximum wins, fp16
+ * subnormals compare as zero, NaN never wins.  Replaces argmax_last_dim
+ * (src/csrc/lib/ops.cpp:324-355) with the tie rule of lm_head_greedy
+ * (src/csrc/lib/language_model.cpp:473-479). */
+int mcv_argmax_f16(const void* x_dev, int64_t M, int64_t N, int64_t* idx_dev,
+                   mcv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MCV_QUANT_H */

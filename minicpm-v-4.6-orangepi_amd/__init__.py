@@ -1,0 +1,441 @@
+"""MI355X (gfx950) quantized-matmul hot path of the MiniCPM-V 4.6 engine.
+
+Python host mirror of the reference's C++ operator surface
+(src/csrc/include/minicpmv/ops.h:95-126, quantized_weight.h:11-28) over the
+C-ABI in include/mcv_quant.h.  torch supplies device memory and streams only;
+every operator runs a hand-written HIP kernel from lib/libmcv_quant.so and
+fails loudly (McvError) when that library is missing or the device is not a
+gfx950.  There is no CPU fallback.
+
+The directory name is not a Python identifier; load it with ``load()`` from
+``__graft_entry__`` or ``importlib`` (see tests/conftest.py).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "lib" / "libmcv_quant.so"
+GROUP = 128
+SLAB = 64
+
+MCV_F32, MCV_F16 = 0, 1
+W8_KN, W8_NK = 0, 1
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_vp = ctypes.c_void_p
+
+
+class McvError(RuntimeError):
+    """Raised when a C-ABI call returns a non-zero status."""
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+# name -> (restype, argtypes) for every entry point of include/mcv_quant.h
+_SIGS = {
+    "mcv_last_error": (ctypes.c_char_p, []),
+    "mcv_version": (ctypes.c_char_p, []),
+    "mcv_w4a16_packed_weight_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "mcv_w4a16_packed_scale_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "mcv_w4a16_packed_zero_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "mcv_w4a16_pack_awq": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "mcv_w4a16_pack_gptq": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "mcv_w4a16_quantize_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int]),
+    "mcv_w4a16_unpack_host": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "mcv_w4a16_gemm": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
+    "mcv_w4a16_gemv": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
+    "mcv_w4a16_gemm_mfma": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
+    "mcv_w4a16_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
+    "mcv_lm_head_workspace_bytes": (_c_i64, []),
+    "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
+    "mcv_w8a8_quantize_act": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
+    "mcv_w8a8_gemm_i32": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
+    "mcv_w8a8_dequant": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),
+    "mcv_w8a8_gemm_f16": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _vp, _vp]),
+    "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
+    "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
+    "mcv_argmax_f16": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded C-ABI library; raises McvError if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise McvError(f"HIP library not built: {LIB_PATH} is missing (run __graft_entry__.build())")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = handle
+    return _LIB
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise McvError(f"{what} failed (status {rc}): {lib().mcv_last_error().decode()}")
+
+
+def _np_ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "host arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+# --------------------------------------------------------------------------- #
+# host-side packing / quantisation (numpy in, numpy out)                       #
+# --------------------------------------------------------------------------- #
+def packed_sizes(K: int, N: int) -> tuple[int, int, int]:
+    L = lib()
+    return (L.mcv_w4a16_packed_weight_bytes(K, N), L.mcv_w4a16_packed_scale_bytes(K, N),
+            L.mcv_w4a16_packed_zero_bytes(K, N))
+
+
+def _alloc_packed(K: int, N: int):
+    wb, sb, zb = packed_sizes(K, N)
+    if wb == 0:
+        raise McvError(f"bad W4A16 shape K={K} N={N} (K must be a positive multiple of 128)")
+    return np.empty(wb, np.uint8), np.empty(sb // 2, np.uint16), np.empty(zb // 4, np.uint32)
+
+
+def pack_awq(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray):
+    """AutoAWQ gemm tensors -> slab-64 (qw bytes, scales [G][Npad] u16, zeros [G][Npad/8] u32)."""
+    qweight = np.ascontiguousarray(qweight, np.int32)
+    qzeros = np.ascontiguousarray(qzeros, np.int32)
+    scales = np.ascontiguousarray(scales).view(np.uint16)
+    K, N = qweight.shape[0], qweight.shape[1] * 8
+    qw, sc, zr = _alloc_packed(K, N)
+    _check(lib().mcv_w4a16_pack_awq(_np_ptr(qweight), _np_ptr(qzeros), _np_ptr(scales), K, N, _np_ptr(qw),
+                                    _np_ptr(sc), _np_ptr(zr)), "mcv_w4a16_pack_awq")
+    return qw, sc, zr
+
+
+def pack_gptq(qweight: np.ndarray, qzeros: np.ndarray, g_idx: Optional[np.ndarray], scales: np.ndarray):
+    """GPTQ v1 tensors -> slab-64 (zero_bias 1)."""
+    qweight = np.ascontiguousarray(qweight, np.int32)
+    qzeros = np.ascontiguousarray(qzeros, np.int32)
+    scales = np.ascontiguousarray(scales).view(np.uint16)
+    K, N = qweight.shape[0] * 8, qweight.shape[1]
+    groups = scales.shape[0]
+    gp = 0
+    if g_idx is not None:
+        g_idx = np.ascontiguousarray(g_idx, np.int32)
+        gp = _np_ptr(g_idx)
+    qw, sc, zr = _alloc_packed(K, N)
+    _check(lib().mcv_w4a16_pack_gptq(_np_ptr(qweight), _np_ptr(qzeros), gp, _np_ptr(scales), K, N, groups,
+                                     _np_ptr(qw), _np_ptr(sc), _np_ptr(zr)), "mcv_w4a16_pack_gptq")
+    return qw, sc, zr
+
+
+def unpack(qw: np.ndarray, scales: np.ndarray, zeros: np.ndarray, zero_bias: int, K: int, N: int):
+    """slab-64 -> (q [K][N] u8, effective zero [G][N] u8, scales [G][N] u16)."""
+    q = np.empty((K, N), np.uint8)
+    z = np.empty((K // GROUP, N), np.uint8)
+    s = np.empty((K // GROUP, N), np.uint16)
+    _check(lib().mcv_w4a16_unpack_host(_np_ptr(np.ascontiguousarray(qw)), _np_ptr(np.ascontiguousarray(scales)),
+                                       _np_ptr(np.ascontiguousarray(zeros)), zero_bias, K, N, _np_ptr(q), _np_ptr(z),
+                                       _np_ptr(s)), "mcv_w4a16_unpack_host")
+    return q, z, s
+
+
+def quantize_int4(w_kn_f16: np.ndarray, nthreads: int = 0):
+    """Build-defined synthetic int4 quantiser -> AutoAWQ (qweight, qzeros, scales u16)."""
+    w = np.ascontiguousarray(w_kn_f16).view(np.uint16)
+    K, N = w.shape
+    qweight = np.empty((K, N // 8), np.int32)
+    qzeros = np.empty((K // GROUP, N // 8), np.int32)
+    scales = np.empty((K // GROUP, N), np.uint16)
+    _check(lib().mcv_w4a16_quantize_host(_np_ptr(w), K, N, _np_ptr(qweight), _np_ptr(qzeros), _np_ptr(scales),
+                                         nthreads), "mcv_w4a16_quantize_host")
+    return qweight, qzeros, scales
+
+
+def quantize_w8a8_weight_host(w_kn_f16: np.ndarray, layout: int = W8_KN):
+    """Per-channel int8 weight quantiser (quantized_weight.cpp:231-268) -> (q, scale f32 [N], scale f16 bits [N])."""
+    w = np.ascontiguousarray(w_kn_f16).view(np.uint16)
+    K, N = w.shape
+    q = np.empty((K, N) if layout == W8_KN else (N, K), np.int8)
+    s32 = np.empty(N, np.float32)
+    s16 = np.empty(N, np.uint16)
+    _check(lib().mcv_w8a8_quantize_weight_host(_np_ptr(w), K, N, _np_ptr(q), layout, _np_ptr(s32), _np_ptr(s16)),
+           "mcv_w8a8_quantize_weight_host")
+    return q, s32, s16
+
+
+# --------------------------------------------------------------------------- #
+# device side (torch tensors as memory)                                        #
+# --------------------------------------------------------------------------- #
+def _torch():
+    import torch
+    return torch
+
+
+def _stream(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _dev(t) -> int:
+    return int(t.data_ptr())
+
+
+@dataclass
+class W4A16QuantizedWeight:
+    """Device W4A16 weight in the slab-64 layout.
+
+    Mirrors W4A16QuantizedWeight (src/csrc/include/minicpmv/quantized_weight.h:11-17)
+    with the zero-points kept on the device (`zeros`, `zero_bias`) instead of
+    being folded into an int8 (q - z) tensor.
+    """
+
+    qweight: "object"   # torch.uint8 [packed bytes]
+    scales: "object"    # torch.int16 [G][Npad] (fp16 bits)
+    zeros: "object"     # torch.int32 [G][Npad/8]
+    K: int
+    N: int
+    zero_bias: int = 0
+    group_size: int = GROUP
+
+    @classmethod
+    def from_packed(cls, qw, sc, zr, K, N, zero_bias=0, device="cuda"):
+        torch = _torch()
+        return cls(torch.from_numpy(qw).to(device), torch.from_numpy(sc.view(np.int16)).to(device),
+                   torch.from_numpy(zr.view(np.int32)).to(device), K, N, zero_bias)
+
+    @classmethod
+    def from_awq(cls, qweight, qzeros, scales, device="cuda"):
+        qweight = np.asarray(qweight)
+        K, N = qweight.shape[0], qweight.shape[1] * 8
+        return cls.from_packed(*pack_awq(qweight, qzeros, scales), K, N, 0, device)
+
+    @classmethod
+    def from_gptq(cls, qweight, qzeros, g_idx, scales, device="cuda"):
+        qweight = np.asarray(qweight)
+        K, N = qweight.shape[0] * 8, qweight.shape[1]
+        return cls.from_packed(*pack_gptq(qweight, qzeros, g_idx, scales), K, N, 1, device)
+
+    def ptrs(self):
+        return _dev(self.qweight), _dev(self.scales), _dev(self.zeros)
+
+
+def load_w4a16_quantized_weight(tensors: dict, base: str, device="cuda") -> W4A16QuantizedWeight:
+    """Mirror of load_w4a16_quantized_weight (quantized_weight.cpp:212-228): GPTQ when
+    `base.g_idx` exists, AutoAWQ otherwise.  `tensors` maps names to numpy arrays
+    (e.g. from safetensors.numpy.load_file)."""
+    qweight, qzeros, scales = tensors[base + ".qweight"], tensors[base + ".qzeros"], tensors[base + ".scales"]
+    if base + ".g_idx" in tensors:
+        return W4A16QuantizedWeight.from_gptq(qweight, qzeros, tensors[base + ".g_idx"], scales, device)
+    return W4A16QuantizedWeight.from_awq(qweight, qzeros, scales, device)
+
+
+def has_w4a16_quantized_weight(tensors: dict, base: str) -> bool:
+    """quantized_weight.cpp:206-210."""
+    return all(base + s in tensors for s in (".qweight", ".qzeros", ".scales"))
+
+
+def _w4_call(fn_name: str, x, w: W4A16QuantizedWeight, out, stream):
+    torch = _torch()
+    if x.dtype != torch.float16 or x.dim() != 2 or x.shape[1] != w.K or not x.is_contiguous():
+        raise McvError(f"{fn_name}: x must be contiguous fp16 [M, {w.K}]")
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, w.N), dtype=torch.float16, device=x.device)
+    if out.dtype != torch.float16 or tuple(out.shape) != (M, w.N) or not out.is_contiguous():
+        raise McvError(f"{fn_name}: out must be contiguous fp16 [{M}, {w.N}]")
+    q, s, z = w.ptrs()
+    _check(getattr(lib(), fn_name)(_dev(x), M, w.K, w.N, q, s, z, w.zero_bias, _dev(out), _stream(stream)), fn_name)
+    return out
+
+
+def matmul_w4a16(x, w: W4A16QuantizedWeight, out=None, stream=None):
+    """out[M, N] = x[M, K] . dequant(w), any M (ops.h:104-108 generalised)."""
+    return _w4_call("mcv_w4a16_gemm", x, w, out, stream)
+
+
+def matmul_w4a16_gemv(x, w, out=None, stream=None):
+    return _w4_call("mcv_w4a16_gemv", x, w, out, stream)
+
+
+def matmul_w4a16_mfma(x, w, out=None, stream=None):
+    return _w4_call("mcv_w4a16_gemm_mfma", x, w, out, stream)
+
+
+def w4a16_dequant(w: W4A16QuantizedWeight, f16=True, i8=False, stream=None):
+    torch = _torch()
+    wf = torch.empty((w.K, w.N), dtype=torch.float16, device=w.qweight.device) if f16 else None
+    w8 = torch.empty((w.K, w.N), dtype=torch.int8, device=w.qweight.device) if i8 else None
+    q, s, z = w.ptrs()
+    _check(lib().mcv_w4a16_dequant(q, s, z, w.zero_bias, w.K, w.N, _dev(wf) if wf is not None else 0,
+                                   _dev(w8) if w8 is not None else 0, _stream(stream)), "mcv_w4a16_dequant")
+    return wf, w8
+
+
+def matmul_w4a16_tiled(x, w_int8, scales, out, stream=None):
+    """The reference's 4-argument matmul_w4a16 (ops.cpp:1030-1095): int8 (q - z)
+    tile-packed by pack_w4a16_weight, fp16 scales [K/128, N], M = 1."""
+    torch = _torch()
+    if x.dtype != torch.float16 or x.dim() != 2 or x.shape[0] != 1:
+        raise McvError("matmul_w4a16 x must be [1, K]")
+    if w_int8.dtype != torch.int8 or w_int8.dim() != 2:
+        raise McvError("matmul_w4a16 w must be [packed_rows, tile_len]")
+    K, N = x.shape[1], scales.shape[1]
+    if tuple(scales.shape) != (K // GROUP, N) or tuple(out.shape) != (1, N):
+        raise McvError("matmul_w4a16 scales must be [K/128, N] and out [1, N]")
+    _check(lib().mcv_w4a16_gemv_tiled_i8(_dev(x), K, N, w_int8.shape[1], w_int8.shape[0], _dev(w_int8), _dev(scales),
+                                         _dev(out), _stream(stream)), "matmul_w4a16")
+    return out
+
+
+class LmHeadW4A16:
+    """Greedy lm_head over a W4A16 weight [K, >= vocab] with the argmax fused
+    into the GEMV (replaces lm_head_greedy's 16 chunk matmuls + host scan,
+    src/csrc/lib/language_model.cpp:412-482).  Owns its zero-filled workspace."""
+
+    def __init__(self, w: W4A16QuantizedWeight, vocab: int):
+        torch = _torch()
+        if vocab > w.N:
+            raise McvError(f"vocab {vocab} exceeds weight width {w.N}")
+        self.w, self.vocab = w, vocab
+        nbytes = lib().mcv_lm_head_workspace_bytes()
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=w.qweight.device)
+        self.token = torch.zeros(1, dtype=torch.int64, device=w.qweight.device)
+
+    def launch(self, x, logits=None, stream=None):
+        """Stream-ordered: fills self.token (and logits if given); no sync."""
+        torch = _torch()
+        if x.dtype != torch.float16 or x.numel() != self.w.K or not x.is_contiguous():
+            raise McvError(f"lm_head x must be contiguous fp16 [1, {self.w.K}]")
+        if logits is not None and (logits.dtype != torch.float16 or logits.numel() != self.vocab):
+            raise McvError(f"lm_head logits must be fp16 [{self.vocab}]")
+        q, s, z = self.w.ptrs()
+        _check(lib().mcv_w4a16_lm_head_argmax(_dev(x), self.w.K, self.w.N, self.vocab, q, s, z, self.w.zero_bias,
+                                              _dev(logits) if logits is not None else 0, _dev(self.token),
+                                              _dev(self.workspace), _stream(stream)), "mcv_w4a16_lm_head_argmax")
+        return self.token
+
+    def __call__(self, x, logits=None) -> int:
+        self.launch(x, logits)
+        return int(self.token.item())
+
+
+# ----------------------------------------------------------------- W8A8 ----- #
+@dataclass
+class W8A8QuantizedWeight:
+    """Mirrors W8A8QuantizedWeight (quantized_weight.h:19-24) plus the fp32 scale."""
+
+    w_int8: "object"       # torch.int8, [K, N] (W8_KN) or [N, K] (W8_NK)
+    w_scale: "object"      # torch.float16 [N] (truncating encode, the reference's stored form)
+    w_scale_f32: "object"  # torch.float32 [N]
+    K: int
+    N: int
+    layout: int = W8_KN
+
+
+def quantize_dense_weight_w8a8(weight_kn, layout: int = W8_KN) -> W8A8QuantizedWeight:
+    """quantized_weight.cpp:231-268 without the device round trip: fp16 [K, N] -> int8 + scales."""
+    torch = _torch()
+    w_np = weight_kn.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16) \
+        if hasattr(weight_kn, "detach") else np.asarray(weight_kn).view(np.uint16)
+    K, N = w_np.shape
+    q, s32, s16 = quantize_w8a8_weight_host(w_np, layout)
+    dev = weight_kn.device if hasattr(weight_kn, "device") and weight_kn.device.type == "cuda" else "cuda"
+    return W8A8QuantizedWeight(torch.from_numpy(q).to(dev), torch.from_numpy(s16.view(np.int16)).to(dev).view(torch.float16),
+                               torch.from_numpy(s32).to(dev), K, N, layout)
+
+
+def w8a8_quantize(x, x_int8=None, x_scale=None, x_scale_f16=None, stream=None):
+    """Per-row activation quant (ops.cpp:1135-1171 generalised to M rows).
+    Returns (x_int8 [M, K], x_scale fp32 [M], x_scale_f16 [M] or None)."""
+    torch = _torch()
+    if x.dtype != torch.float16 or x.dim() != 2 or not x.is_contiguous():
+        raise McvError("w8a8_quantize x must be contiguous fp16 [M, K]")
+    M, K = x.shape
+    if x_int8 is None:
+        x_int8 = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if x_scale is None:
+        x_scale = torch.empty(M, dtype=torch.float32, device=x.device)
+    _check(lib().mcv_w8a8_quantize_act(_dev(x), M, K, _dev(x_int8), _dev(x_scale),
+                                       _dev(x_scale_f16) if x_scale_f16 is not None else 0, _stream(stream)),
+           "w8a8_quantize")
+    return x_int8, x_scale, x_scale_f16
+
+
+def matmul_w8a8_i32(x_int8, w_int8, out=None, layout: int = W8_KN, stream=None):
+    """acc[M, N] int32 = x_int8 . w (ops.cpp:1097-1133 generalised to M rows)."""
+    torch = _torch()
+    M, K = x_int8.shape
+    N = w_int8.shape[1] if layout == W8_KN else w_int8.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.int32, device=x_int8.device)
+    _check(lib().mcv_w8a8_gemm_i32(_dev(x_int8), M, K, N, _dev(w_int8), layout, _dev(out), _stream(stream)),
+           "matmul_w8a8_i32")
+    return out
+
+
+def _scale_dtype(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return MCV_F32
+    if t.dtype == torch.float16:
+        return MCV_F16
+    raise McvError(f"scale dtype must be fp32 or fp16, got {t.dtype}")
+
+
+def w8a8_dequant(acc, x_scale, w_scale, out=None, stream=None):
+    """out = fp16 RNE((acc * w_scale[n]) * x_scale[m]) (ops.cpp:1173-1210)."""
+    torch = _torch()
+    M, N = acc.shape
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=acc.device)
+    _check(lib().mcv_w8a8_dequant(_dev(acc), _dev(x_scale), _scale_dtype(x_scale), _dev(w_scale), _scale_dtype(w_scale),
+                                  M, N, _dev(out), _stream(stream)), "w8a8_dequant")
+    return out
+
+
+def matmul_w8a8(x_int8, x_scale, w: W8A8QuantizedWeight, out=None, use_f32_scale=True, stream=None):
+    """Fused int8 GEMM + dequant epilogue; bit-identical to matmul_w8a8_i32 + w8a8_dequant."""
+    torch = _torch()
+    M, K = x_int8.shape
+    if out is None:
+        out = torch.empty((M, w.N), dtype=torch.float16, device=x_int8.device)
+    ws = w.w_scale_f32 if use_f32_scale else w.w_scale
+    _check(lib().mcv_w8a8_gemm_f16(_dev(x_int8), _dev(x_scale), _scale_dtype(x_scale), M, K, w.N, _dev(w.w_int8),
+                                   w.layout, _dev(ws), _scale_dtype(ws), _dev(out), _stream(stream)), "matmul_w8a8")
+    return out
+
+
+# ------------------------------------------------------------- elementwise -- #
+def silu_mul(gate, up, out=None, stream=None):
+    """out = silu(gate) * up in fp32, RNE to fp16 (ops.cpp:437-456)."""
+    torch = _torch()
+    if gate.shape != up.shape or gate.dtype != torch.float16 or up.dtype != torch.float16:
+        raise McvError("silu_mul requires fp16 tensors of one shape")
+    if out is None:
+        out = torch.empty_like(gate)
+    _check(lib().mcv_silu_mul(_dev(gate), _dev(up), _dev(out), gate.numel(), _stream(stream)), "silu_mul")
+    return out
+
+
+def argmax_last_dim(x, out=None, stream=None):
+    """Per-row first-maximum argmax of fp16 [M, N] -> int64 [M]."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    if out is None:
+        out = torch.empty(x2.shape[0], dtype=torch.int64, device=x.device)
+    _check(lib().mcv_argmax_f16(_dev(x2), x2.shape[0], x2.shape[1], _dev(out), _stream(stream)), "argmax")
+    return out
+
+
+def version() -> str:
+    return lib().mcv_version().decode()

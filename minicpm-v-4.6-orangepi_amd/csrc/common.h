@@ -1,0 +1,88 @@
+// common.h -- shared helpers for the gfx950 quantized-matmul library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "mcv_quant.h"
+
+namespace mcv {
+
+constexpr int kGroup = 128;       // quantisation group along K
+constexpr int kSlab = 64;         // output columns per slab (one per lane)
+constexpr int kChunkK = 32;       // k per 16-byte lane chunk
+
+// Last error message of this thread, returned by mcv_last_error().
+std::string& last_error();
+
+// Records a formatted message and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+inline int ok() { return MCV_OK; }
+
+// Checks the launch that was just issued; HIP launch errors become MCV_ERR_HIP.
+int check_launch(const char* what);
+
+// Returns MCV_ERR_NO_DEVICE unless the current device is a gfx950 (the only
+// target the code objects are built for); cached per device id.
+int require_device();
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------ device helpers --
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef int int4_t __attribute__((ext_vector_type(4)));
+typedef int int16_t_v __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+// fp32 -> fp16 with IEEE round-to-nearest-even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Order-preserving 16-bit key of an fp16 value for the greedy argmax: fp16
+// subnormals and -0 map to +0 (the reference decodes logits with subnormals
+// flushed, language_model.cpp:444-459, and compares with '>'); NaN and -inf
+// return 0, a key no candidate has, because they can never win the scan.
+__device__ __forceinline__ uint32_t argmax_key16(uint16_t h) {
+    const uint32_t e = (h >> 10) & 0x1fu;
+    if (e == 0x1f) {                       // inf or NaN
+        if ((h & 0x3ffu) != 0 || (h & 0x8000u)) return 0u;
+        return 0xfc00u | 0x8000u;          // +inf
+    }
+    if (e == 0) h = 0;                     // subnormal or zero -> +0
+    return (h & 0x8000u) ? (~static_cast<uint32_t>(h) & 0xffffu) : (static_cast<uint32_t>(h) | 0x8000u);
+}
+
+// 64-bit argmax key: larger value first, then smaller index.  0 = no candidate.
+__device__ __forceinline__ unsigned long long argmax_key64(uint32_t key16, uint32_t idx) {
+    if (key16 == 0) return 0ull;
+    return (static_cast<unsigned long long>(key16) << 32) | static_cast<unsigned long long>(0xffffffffu - idx);
+}
+__device__ __host__ __forceinline__ int64_t argmax_index(unsigned long long key) {
+    if (key == 0ull) return 0;
+    return static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(key & 0xffffffffull));
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        unsigned long long o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+}  // namespace mcv

@@ -1,0 +1,366 @@
+// w4a16_gemv.hip -- W4A16 decode kernels for gfx950.
+//
+// Streaming GEMV over the slab-64 layout (see include/mcv_quant.h): each lane
+// owns one output column and walks K in 16-byte chunks, so every wave-wide
+// 128-bit load is one contiguous 1 KiB line.  Nibbles are widened in registers
+// with the fp16 exponent-bias identity: bits 0x6400 | q form the fp16 value
+// 1024 + q, and 0x6400 | (q << 4) the value 1024 + 16 q; subtracting
+// 1024 + z (or 1024 + 16 z) leaves the exact q - z (or 16 (q - z)).  Pairs of
+// consecutive k then go through v_dot2_f32_f16 against the activation pairs,
+// accumulating in fp32.  The activation row is wave-uniform and is read with
+// scalar loads.  Waves of a workgroup split K; partial sums meet in LDS.
+//
+// Replaces the NPU kernel src/csrc/custom_ops/op_kernel/matmul_w4a16_custom.cpp
+// (8 AICore blocks, int8 tiles, fp16 Axpy accumulation) and its host wrapper
+// src/csrc/lib/ops.cpp:1030-1095.
+#include <cstdlib>
+
+#include "common.h"
+
+namespace mcv {
+namespace {
+
+struct LmHeadWs {
+    unsigned long long key;  // running max of argmax_key64 over finished workgroups
+    unsigned int count;      // finished workgroups
+    unsigned int pad;
+};
+
+// (a & mask) | magic in one v_and_or_b32.  gfx9 VOP3 encodings take no
+// literal and at most one SGPR, so the mask rides in an SGPR and the magic
+// exponent pattern in a VGPR; left to itself the compiler emits v_and + v_or.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t smask, uint32_t vmagic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(smask), "v"(vmagic));
+    return r;
+}
+
+// Adds the contribution of one quantisation group (four 16-byte chunks of this
+// lane's column) to `acc`.
+__device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t* __restrict__ xw, int g,
+                                           uint32_t z, float scale, float acc, uint32_t vmagic) {
+    const uint32_t zlo = (0x6400u + z) * 0x10001u;          // half2(1024 + z)
+    const uint32_t zhi = (0x6400u + (z << 4)) * 0x10001u;   // half2(1024 + 16 z)
+    const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+    const uint32_t mhi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
+    float alo = 0.f, ahi = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t words[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int kw = (g * kGroup + c * kChunkK + w * 8) >> 1;   // half2 index into x
+            const uint32_t q = words[w];
+            const uint32_t q8 = q >> 8;
+            const half2_t p0 = as_h2(and_or(q, mlo, vmagic)) - as_h2(zlo);    // k+0, k+1
+            const half2_t p1 = as_h2(and_or(q, mhi, vmagic)) - as_h2(zhi);    // k+2, k+3 (x16)
+            const half2_t p2 = as_h2(and_or(q8, mlo, vmagic)) - as_h2(zlo);   // k+4, k+5
+            const half2_t p3 = as_h2(and_or(q8, mhi, vmagic)) - as_h2(zhi);   // k+6, k+7 (x16)
+            alo = __builtin_amdgcn_fdot2(p0, as_h2(xw[kw + 0]), alo, false);
+            ahi = __builtin_amdgcn_fdot2(p1, as_h2(xw[kw + 1]), ahi, false);
+            alo = __builtin_amdgcn_fdot2(p2, as_h2(xw[kw + 2]), alo, false);
+            ahi = __builtin_amdgcn_fdot2(p3, as_h2(xw[kw + 3]), ahi, false);
+        }
+    }
+    return fmaf(alo + ahi * 0.0625f, scale, acc);
+}
+
+// grid = (Nslab, M), block = 64 * KSPLIT.  Wave w handles groups
+// {w*GPW + r*KSPLIT*GPW + i : i < GPW}.  ARGMAX (M == 1 only) also folds the
+// workgroup's fp16 logits into the running argmax in `ws`; the last workgroup
+// to finish writes the token and re-zeroes `ws`.
+template <int KSPLIT, int GPW, bool ARGMAX>
+__global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
+    const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int K, int N,
+    int Npad, LmHeadWs* __restrict__ ws, int64_t* __restrict__ token) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: keeps x loads scalar
+    const int slab = blockIdx.x;
+    const int m = blockIdx.y;
+    const int n = slab * kSlab + lane;
+    const int G = K / kGroup;
+    uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
+    const int C = K / kChunkK;
+    const uint4* __restrict__ wp = qw + static_cast<size_t>(slab) * C * kSlab + lane;
+    const uint32_t* __restrict__ xw = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(m) * K);
+    const uint16_t* __restrict__ sp = scales + n;
+    const uint32_t* __restrict__ zp = zeros + (n >> 3);
+    const uint32_t zshift = (n & 7) * 4;
+    const int zstride = Npad >> 3;
+
+    float acc = 0.f;
+    for (int gb = wave * GPW; gb < G; gb += KSPLIT * GPW) {
+        uint4 wv[GPW][4];
+        uint16_t sv[GPW];
+        uint32_t zv[GPW];
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            const int g = gb + i;
+            if (g < G) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) wv[i][c] = wp[static_cast<size_t>(g * 4 + c) * kSlab];
+                sv[i] = sp[static_cast<size_t>(g) * Npad];
+                zv[i] = zp[static_cast<size_t>(g) * zstride];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < GPW; ++i) {
+            const int g = gb + i;
+            if (g < G) acc = group_dot(wv[i], xw, g, ((zv[i] >> zshift) & 15u) + zero_bias, h2f(sv[i]), acc, vmagic);
+        }
+    }
+
+    if constexpr (KSPLIT > 1) {
+        __shared__ float red[KSPLIT][kSlab];
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        acc = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < KSPLIT; ++w) acc += red[w][lane];
+    }
+
+    const uint16_t h = f2h(acc);
+    if (out != nullptr && n < N) out[static_cast<size_t>(m) * N + n] = h;
+    if constexpr (ARGMAX) {
+        unsigned long long key = n < N ? argmax_key64(argmax_key16(h), static_cast<uint32_t>(n)) : 0ull;
+        key = wave_max_u64(key);
+        if (lane == 0) {
+            if (key != 0ull) atomicMax(&ws->key, key);
+            __threadfence();
+            const unsigned int done = atomicAdd(&ws->count, 1u);
+            if (done == gridDim.x - 1) {
+                __threadfence();
+                const unsigned long long fin = atomicAdd(&ws->key, 0ull);
+                *token = argmax_index(fin);
+                atomicExch(&ws->key, 0ull);
+                atomicExch(&ws->count, 0u);
+            }
+        }
+    }
+}
+
+template <bool ARGMAX>
+using GemvFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int,
+                        int, int, LmHeadWs*, int64_t*);
+
+template <bool ARGMAX, int KS>
+GemvFn<ARGMAX> pick_gpw(int gpw) {
+    switch (gpw) {
+        case 1: return w4a16_gemv_kernel<KS, 1, ARGMAX>;
+        case 2: return w4a16_gemv_kernel<KS, 2, ARGMAX>;
+        case 4: return w4a16_gemv_kernel<KS, 4, ARGMAX>;
+        default: return w4a16_gemv_kernel<KS, 8, ARGMAX>;
+    }
+}
+
+template <bool ARGMAX>
+GemvFn<ARGMAX> pick_kernel(int ks, int gpw) {
+    switch (ks) {
+        case 1: return pick_gpw<ARGMAX, 1>(gpw);
+        case 2: return pick_gpw<ARGMAX, 2>(gpw);
+        case 4: return pick_gpw<ARGMAX, 4>(gpw);
+        case 8: return pick_gpw<ARGMAX, 8>(gpw);
+        default: return pick_gpw<ARGMAX, 16>(gpw);
+    }
+}
+
+struct GemvCfg {
+    int ksplit;
+    int gpw;
+};
+
+int env_int(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    if (v == nullptr || *v == '\0') return fallback;
+    return std::atoi(v);
+}
+
+// Split K over enough waves to put ~16 waves on each of the 256 CUs, keep
+// each wave's groups unrolled (<= 8 groups = 32 outstanding 16-byte loads).
+// MCV_GEMV_KSPLIT / MCV_GEMV_GPW override the choice (tuning sweeps).
+GemvCfg choose_gemv(int64_t G, int64_t blocks) {
+    int ks = 1;
+    while (ks < 16 && blocks * ks < 4096 && ks * 2 <= G) ks *= 2;
+    int need = static_cast<int>(ceil_div(G, ks));
+    int gpw = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+    GemvCfg c{env_int("MCV_GEMV_KSPLIT", ks), env_int("MCV_GEMV_GPW", gpw)};
+    if (c.ksplit != 1 && c.ksplit != 2 && c.ksplit != 4 && c.ksplit != 8 && c.ksplit != 16) c.ksplit = ks;
+    if (c.gpw != 1 && c.gpw != 2 && c.gpw != 4 && c.gpw != 8) c.gpw = gpw;
+    return c;
+}
+
+bool w4_args_ok(const void* qw, const void* scales, const void* zeros, int zero_bias, int64_t K, int64_t N,
+                const char* who, int* rc) {
+    if (!qw || !scales || !zeros) { *rc = fail(MCV_ERR_INVALID_ARG, "%s: null weight pointer", who); return false; }
+    if (zero_bias != 0 && zero_bias != 1) { *rc = fail(MCV_ERR_INVALID_ARG, "%s: zero_bias must be 0 or 1", who); return false; }
+    if (K <= 0 || K % kGroup != 0 || K > (int64_t(1) << 24)) {
+        *rc = fail(MCV_ERR_SHAPE, "%s: K must be a positive multiple of 128 (K=%lld)", who, (long long)K);
+        return false;
+    }
+    if (N <= 0 || N > (int64_t(1) << 30)) {
+        *rc = fail(MCV_ERR_SHAPE, "%s: N out of range (N=%lld)", who, (long long)N);
+        return false;
+    }
+    return true;
+}
+
+// ------------------------------------------------------------- dequant --
+// grid = (Nslab, K/32), block = 64: lane -> column, blockIdx.y -> chunk.
+__global__ __launch_bounds__(64) void w4a16_dequant_kernel(const uint4* __restrict__ qw,
+                                                           const uint16_t* __restrict__ scales,
+                                                           const uint32_t* __restrict__ zeros, uint32_t zero_bias,
+                                                           int K, int N, int Npad, uint16_t* __restrict__ wf,
+                                                           int8_t* __restrict__ w8) {
+    const int lane = threadIdx.x;
+    const int slab = blockIdx.x;
+    const int c = blockIdx.y;
+    const int n = slab * kSlab + lane;
+    if (n >= N) return;
+    const int C = K / kChunkK;
+    const int g = c / 4;
+    const uint4 v = qw[(static_cast<size_t>(slab) * C + c) * kSlab + lane];
+    const float s = h2f(scales[static_cast<size_t>(g) * Npad + n]);
+    const int z = static_cast<int>(((zeros[static_cast<size_t>(g) * (Npad >> 3) + (n >> 3)] >> ((n & 7) * 4)) & 15u) + zero_bias);
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+    constexpr int kSlotOfK[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = c * kChunkK + w * 8 + j;
+            const int d = static_cast<int>((words[w] >> (4 * kSlotOfK[j])) & 15u) - z;
+            const size_t o = static_cast<size_t>(k) * N + n;
+            if (w8) w8[o] = static_cast<int8_t>(d);
+            if (wf) wf[o] = f2h(static_cast<float>(d) * s);   // exact product, one RNE
+        }
+    }
+}
+
+// ------------------------------------------- reference int8 tile format --
+// The reference's own device format (quantized_weight.cpp:41-73): int8 (q - z)
+// in [128][tileLen] tiles ordered (group, block b of 8, tile, k, i).  One thread
+// per output column; consecutive threads read consecutive bytes of a tile row.
+__global__ __launch_bounds__(256) void w4a16_tiled_i8_kernel(const uint16_t* __restrict__ x,
+                                                             const int8_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ scales,
+                                                             uint16_t* __restrict__ out, int K, int N, int blockLen,
+                                                             int tileLen, int tilesPerBlock) {
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    const int b = n / blockLen;
+    const int r = n - b * blockLen;
+    const int t = r / tileLen;
+    const int i = r - t * tileLen;
+    const int G = K / kGroup;
+    float acc = 0.f;
+    for (int g = 0; g < G; ++g) {
+        const int8_t* tp = w + (((static_cast<size_t>(g) * 8 + b) * tilesPerBlock + t) * kGroup) * tileLen + i;
+        float partial = 0.f;
+        for (int kk = 0; kk < kGroup; ++kk)
+            partial = fmaf(h2f(x[g * kGroup + kk]), static_cast<float>(tp[static_cast<size_t>(kk) * tileLen]), partial);
+        acc = fmaf(partial, h2f(scales[static_cast<size_t>(g) * N + n]), acc);
+    }
+    out[n] = f2h(acc);
+}
+
+}  // namespace
+
+// Internal entry used by the dispatcher in w4a16_gemm.hip.
+int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
+                      const void* zeros, int zero_bias, void* out, hipStream_t stream) {
+    int rc = MCV_OK;
+    if (!w4_args_ok(qw, scales, zeros, zero_bias, K, N, "mcv_w4a16_gemv", &rc)) return rc;
+    if (!x || !out) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemv: null x/out");
+    if (M <= 0 || M > 65535) return fail(MCV_ERR_SHAPE, "mcv_w4a16_gemv: M must be in [1, 65535] (M=%lld)", (long long)M);
+    if ((rc = require_device()) != MCV_OK) return rc;
+    const int64_t nslab = ceil_div(N, kSlab);
+    const GemvCfg cfg = choose_gemv(K / kGroup, nslab * M);
+    auto fn = pick_kernel<false>(cfg.ksplit, cfg.gpw);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(M)), dim3(64 * cfg.ksplit), 0,
+                       stream, static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
+                       static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
+                       static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(out), static_cast<int>(K),
+                       static_cast<int>(N), static_cast<int>(nslab * kSlab), nullptr, nullptr);
+    return check_launch("w4a16_gemv_kernel");
+}
+
+}  // namespace mcv
+
+using namespace mcv;
+
+extern "C" {
+
+int mcv_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
+                   const void* zeros, int zero_bias, void* out, mcv_stream_t stream) {
+    return launch_w4a16_gemv(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
+}
+
+int64_t mcv_lm_head_workspace_bytes(void) { return 256; }
+
+int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, const void* qw, const void* scales,
+                             const void* zeros, int zero_bias, void* logits, int64_t* token, void* workspace,
+                             mcv_stream_t stream) {
+    int rc = MCV_OK;
+    if (!w4_args_ok(qw, scales, zeros, zero_bias, K, N, "mcv_w4a16_lm_head_argmax", &rc)) return rc;
+    if (!x || !token || !workspace) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: null x/token/workspace");
+    if (V <= 0 || V > N) return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax: need 0 < V <= N (V=%lld N=%lld)",
+                                     (long long)V, (long long)N);
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: workspace must be 16-byte aligned");
+    if ((rc = require_device()) != MCV_OK) return rc;
+    // Only the slabs holding columns < V run; the scale/zero row stride is the
+    // packed width of the weight (N), not of V.
+    const int64_t nslab = ceil_div(V, kSlab);
+    const int64_t npad = ceil_div(N, kSlab) * kSlab;
+    const GemvCfg cfg = choose_gemv(K / kGroup, nslab);
+    auto fn = pick_kernel<true>(cfg.ksplit, cfg.gpw);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), 1u), dim3(64 * cfg.ksplit), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
+                       static_cast<const uint4*>(qw), static_cast<const uint16_t*>(scales),
+                       static_cast<const uint32_t*>(zeros), static_cast<uint32_t>(zero_bias),
+                       static_cast<uint16_t*>(logits), static_cast<int>(K), static_cast<int>(V),
+                       static_cast<int>(npad), static_cast<LmHeadWs*>(workspace), token);
+    return check_launch("w4a16_gemv_kernel<argmax>");
+}
+
+int mcv_w4a16_dequant(const void* qw, const void* scales, const void* zeros, int zero_bias, int64_t K, int64_t N,
+                      void* w_f16, int8_t* w8, mcv_stream_t stream) {
+    int rc = MCV_OK;
+    if (!w4_args_ok(qw, scales, zeros, zero_bias, K, N, "mcv_w4a16_dequant", &rc)) return rc;
+    if (!w_f16 && !w8) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_dequant: no output");
+    if ((rc = require_device()) != MCV_OK) return rc;
+    const int64_t nslab = ceil_div(N, kSlab);
+    hipLaunchKernelGGL(w4a16_dequant_kernel, dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(K / kChunkK)),
+                       dim3(64), 0, static_cast<hipStream_t>(stream), static_cast<const uint4*>(qw),
+                       static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
+                       static_cast<uint32_t>(zero_bias), static_cast<int>(K), static_cast<int>(N),
+                       static_cast<int>(nslab * kSlab), static_cast<uint16_t*>(w_f16), w8);
+    return check_launch("w4a16_dequant_kernel");
+}
+
+int mcv_w4a16_gemv_tiled_i8(const void* x, int64_t K, int64_t N, int64_t tile_len, int64_t packed_rows,
+                            const int8_t* w, const void* scales, void* out, mcv_stream_t stream) {
+    if (!x || !w || !scales || !out) return fail(MCV_ERR_INVALID_ARG, "matmul_w4a16: null pointer");
+    // Same constraints as src/csrc/lib/ops.cpp:1058-1079.
+    if (tile_len <= 0 || tile_len > 448 || tile_len % 16 != 0)
+        return fail(MCV_ERR_SHAPE, "matmul_w4a16 tile_len must be a multiple of 16 and <= 448");
+    if (K <= 0 || N <= 0 || K % kGroup != 0 || N % 128 != 0)
+        return fail(MCV_ERR_SHAPE, "matmul_w4a16 K and N must be multiples of 128");
+    const int64_t blockLen = (N + 7) / 8;
+    const int64_t tilesPerBlock = (blockLen + tile_len - 1) / tile_len;
+    if (packed_rows != (K / kGroup) * 8 * tilesPerBlock * kGroup)
+        return fail(MCV_ERR_SHAPE, "matmul_w4a16 w packed_rows mismatch");
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    hipLaunchKernelGGL(w4a16_tiled_i8_kernel, dim3(static_cast<unsigned>(ceil_div(N, 256))), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), w,
+                       static_cast<const uint16_t*>(scales), static_cast<uint16_t*>(out), static_cast<int>(K),
+                       static_cast<int>(N), static_cast<int>(blockLen), static_cast<int>(tile_len),
+                       static_cast<int>(tilesPerBlock));
+    return check_launch("w4a16_tiled_i8_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,295 @@
+// w8a8.hip -- W8A8 kernels for gfx950: per-row activation quantiser, int8 MFMA
+// GEMM with int32 accumulation and an optional fused fp16 dequant epilogue,
+// and the standalone dequant epilogue.
+//
+// Replaces the NPU operators w8a8_quantize_custom, matmul_w8a8_i32_custom and
+// w8a8_dequant_custom (src/csrc/custom_ops/op_kernel/*.cpp) and their host
+// wrappers (src/csrc/lib/ops.cpp:1097-1210).
+#include "common.h"
+
+namespace mcv {
+namespace {
+
+// ------------------------------------------------------ activation quant --
+// One workgroup per row.  scale = max|x| / 127 (floor 1e-8), inv = 1 / scale,
+// q = trunc(clamp(x * inv, -128, 127) +- 0.5): the closed form of
+// op_kernel/w8a8_quantize_custom.cpp:25-41 and quantized_weight.cpp:197-202,
+// every operation an explicitly rounded IEEE fp32 operation (no contraction).
+__global__ __launch_bounds__(256) void w8a8_quant_act_kernel(const uint16_t* __restrict__ x, int K,
+                                                             int8_t* __restrict__ xq, float* __restrict__ s32,
+                                                             uint16_t* __restrict__ s16) {
+    const int row = blockIdx.x;
+    const uint16_t* xr = x + static_cast<size_t>(row) * K;
+    float m = 0.f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        float v = fabsf(h2f(xr[k]));
+        m = v > m ? v : m;                      // NaN never becomes the maximum
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    __shared__ float wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = wmax[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) m = wmax[w] > m ? wmax[w] : m;
+    float scale = __fdiv_rn(m, 127.0f);
+    if (scale < 0.00000001f) scale = 0.00000001f;
+    const float inv = __fdiv_rn(1.0f, scale);
+    int8_t* qr = xq + static_cast<size_t>(row) * K;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        float v = __fmul_rn(h2f(xr[k]), inv);
+        v = v > 127.0f ? 127.0f : v;
+        v = v < -128.0f ? -128.0f : v;
+        const float r = v >= 0.0f ? __fadd_rn(v, 0.5f) : __fsub_rn(v, 0.5f);
+        qr[k] = static_cast<int8_t>(static_cast<int>(r));
+    }
+    if (threadIdx.x == 0) {
+        s32[row] = scale;
+        if (s16) s16[row] = f2h(scale);
+    }
+}
+
+// ------------------------------------------------------------- int8 GEMM --
+constexpr int BM = 128, BN = 128, BK = 128;
+constexpr int LST = BK + 16;   // bytes per LDS row
+constexpr int NT = 256;
+
+// 4x4 byte transpose: rows a, b, c, d (4 bytes each, columns 0..3) -> out[j]
+// = (a_j, b_j, c_j, d_j).
+__device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&o)[4]) {
+    const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);   // a0 b0 a1 b1
+    const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);   // a2 b2 a3 b3
+    const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);   // c0 d0 c1 d1
+    const uint32_t cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);   // c2 d2 c3 d3
+    o[0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);           // a0 b0 c0 d0
+    o[1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);           // a1 b1 c1 d1
+    o[2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
+}
+
+// OUT_F16: fused epilogue fp16 RNE(((float)acc * ws[n]) * xs[m]); otherwise int32.
+// W_KN: weight is [K][N] (the reference's layout), else [N][K].
+template <bool W_KN, bool OUT_F16>
+__global__ __launch_bounds__(NT) void w8a8_gemm_kernel(const int8_t* __restrict__ xq, const int8_t* __restrict__ w,
+                                                       int M, int K, int N, void* __restrict__ out,
+                                                       const void* __restrict__ xs, int xs16,
+                                                       const void* __restrict__ ws, int ws16) {
+    __shared__ __attribute__((aligned(16))) int8_t As[BM * LST];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[BN * LST];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const int KT = (K + BK - 1) / BK;
+
+    const int a_row = tid >> 3;            // + 32 p
+    const int a_col = (tid & 7) * 16;
+    const int b_kq = tid >> 3;             // [K][N]: k rows 4*b_kq .. +3
+    const int b_nb = (tid & 7) * 16;       //          columns b_nb .. +15
+
+    uint4 ra[4], rb[4];
+    auto load_tile = [&](int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int row = m0 + a_row + 32 * p;
+            const int k = k0 + a_col;
+            ra[p] = (row < M && k < K) ? *reinterpret_cast<const uint4*>(xq + static_cast<size_t>(row) * K + k)
+                                       : make_uint4(0, 0, 0, 0);
+        }
+        if constexpr (W_KN) {
+            const int n = n0 + b_nb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int k = k0 + 4 * b_kq + r;
+                rb[r] = (k < K && n < N) ? *reinterpret_cast<const uint4*>(w + static_cast<size_t>(k) * N + n)
+                                         : make_uint4(0, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int n = n0 + a_row + 32 * p;
+                const int k = k0 + a_col;
+                rb[p] = (n < N && k < K) ? *reinterpret_cast<const uint4*>(w + static_cast<size_t>(n) * K + k)
+                                         : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) *reinterpret_cast<uint4*>(&As[(a_row + 32 * p) * LST + a_col]) = ra[p];
+        if constexpr (W_KN) {
+            const uint32_t r0[4] = {rb[0].x, rb[0].y, rb[0].z, rb[0].w};
+            const uint32_t r1[4] = {rb[1].x, rb[1].y, rb[1].z, rb[1].w};
+            const uint32_t r2[4] = {rb[2].x, rb[2].y, rb[2].z, rb[2].w};
+            const uint32_t r3[4] = {rb[3].x, rb[3].y, rb[3].z, rb[3].w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                uint32_t t[4];
+                transpose4x4(r0[d], r1[d], r2[d], r3[d], t);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    *reinterpret_cast<uint32_t*>(&Bs[(b_nb + 4 * d + j) * LST + 4 * b_kq]) = t[j];
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) *reinterpret_cast<uint4*>(&Bs[(a_row + 32 * p) * LST + a_col]) = rb[p];
+        }
+    };
+
+    const int wm = (wave >> 1) * 64;
+    const int wn = (wave & 1) * 64;
+    int16_t_v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    load_tile(0);
+    for (int kt = 0; kt < KT; ++kt) {
+        __syncthreads();
+        store_tile();
+        __syncthreads();
+        if (kt + 1 < KT) load_tile(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            const int kk = ks * 32 + (lane >> 5) * 16;
+            int4_t af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const int4_t*>(&As[(wm + 32 * i + (lane & 31)) * LST + kk]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const int4_t*>(&Bs[(wn + 32 * j + (lane & 31)) * LST + kk]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn + 32 * j + (lane & 31);
+            if (col >= N) continue;
+            float wsv = 0.f;
+            if constexpr (OUT_F16) wsv = ws16 ? h2f(static_cast<const uint16_t*>(ws)[col]) : static_cast<const float*>(ws)[col];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row >= M) continue;
+                if constexpr (OUT_F16) {
+                    const float xsv = xs16 ? h2f(static_cast<const uint16_t*>(xs)[row]) : static_cast<const float*>(xs)[row];
+                    const float v = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][r]), wsv), xsv);
+                    static_cast<uint16_t*>(out)[static_cast<size_t>(row) * N + col] = f2h(v);
+                } else {
+                    static_cast<int32_t*>(out)[static_cast<size_t>(row) * N + col] = acc[i][j][r];
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------- dequant epilogue --
+// out = fp16 RNE(((float)acc * ws[n]) * xs[m]): op_kernel/w8a8_dequant_custom.cpp:55-62.
+__global__ __launch_bounds__(256) void w8a8_dequant_kernel(const int32_t* __restrict__ acc, const void* __restrict__ xs,
+                                                           int xs16, const void* __restrict__ ws, int ws16, int M, int N,
+                                                           uint16_t* __restrict__ out) {
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    const int m = blockIdx.y;
+    if (n >= N || m >= M) return;
+    const float wsv = ws16 ? h2f(static_cast<const uint16_t*>(ws)[n]) : static_cast<const float*>(ws)[n];
+    const float xsv = xs16 ? h2f(static_cast<const uint16_t*>(xs)[m]) : static_cast<const float*>(xs)[m];
+    const size_t o = static_cast<size_t>(m) * N + n;
+    out[o] = f2h(__fmul_rn(__fmul_rn(static_cast<float>(acc[o]), wsv), xsv));
+}
+
+int check_gemm_args(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, int w_layout, const void* out,
+                    const char* who) {
+    if (!xq || !w || !out) return fail(MCV_ERR_INVALID_ARG, "%s: null pointer", who);
+    if (w_layout != MCV_W8_KN && w_layout != MCV_W8_NK) return fail(MCV_ERR_INVALID_ARG, "%s: bad w_layout %d", who, w_layout);
+    if (M <= 0 || K <= 0 || N <= 0 || M > (int64_t(1) << 30) || N > (int64_t(1) << 30) || K > (int64_t(1) << 17))
+        return fail(MCV_ERR_SHAPE, "%s: bad shape M=%lld K=%lld N=%lld (K <= 131072 keeps int32 exact)", who,
+                    (long long)M, (long long)K, (long long)N);
+    if (K % 16 != 0) return fail(MCV_ERR_SHAPE, "%s: K must be a multiple of 16 (K=%lld)", who, (long long)K);
+    if (w_layout == MCV_W8_KN && N % 16 != 0)
+        return fail(MCV_ERR_SHAPE, "%s: [K, N] weights need N %% 16 == 0 (N=%lld)", who, (long long)N);
+    if ((reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(w)) % 16 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "%s: x and w must be 16-byte aligned", who);
+    if (ceil_div(M, BM) > 65535) return fail(MCV_ERR_SHAPE, "%s: M too large", who);
+    return MCV_OK;
+}
+
+template <bool OUT_F16>
+int launch_gemm(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, int w_layout, void* out,
+                const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream) {
+    dim3 grid(static_cast<unsigned>(ceil_div(N, BN)), static_cast<unsigned>(ceil_div(M, BM)));
+    if (w_layout == MCV_W8_KN)
+        hipLaunchKernelGGL((w8a8_gemm_kernel<true, OUT_F16>), grid, dim3(NT), 0, stream, xq, w, (int)M, (int)K, (int)N,
+                           out, xs, xs16, ws, ws16);
+    else
+        hipLaunchKernelGGL((w8a8_gemm_kernel<false, OUT_F16>), grid, dim3(NT), 0, stream, xq, w, (int)M, (int)K, (int)N,
+                           out, xs, xs16, ws, ws16);
+    return check_launch("w8a8_gemm_kernel");
+}
+
+bool dtype_ok(int d) { return d == MCV_F32 || d == MCV_F16; }
+
+}  // namespace
+}  // namespace mcv
+
+using namespace mcv;
+
+extern "C" {
+
+int mcv_w8a8_quantize_act(const void* x, int64_t M, int64_t K, int8_t* xq, float* s32, void* s16, mcv_stream_t stream) {
+    if (!x || !xq || !s32) return fail(MCV_ERR_INVALID_ARG, "w8a8_quantize: null pointer");
+    if (M <= 0 || K <= 0 || M > 0x7fffffff || K > 0x7fffffff)
+        return fail(MCV_ERR_SHAPE, "w8a8_quantize: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    hipLaunchKernelGGL(w8a8_quant_act_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<int>(K), xq, s32, static_cast<uint16_t*>(s16));
+    return check_launch("w8a8_quant_act_kernel");
+}
+
+int mcv_w8a8_gemm_i32(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, int w_layout, int32_t* acc,
+                      mcv_stream_t stream) {
+    int rc = check_gemm_args(xq, M, K, N, w, w_layout, acc, "matmul_w8a8_i32");
+    if (rc != MCV_OK) return rc;
+    if ((rc = require_device()) != MCV_OK) return rc;
+    return launch_gemm<false>(xq, M, K, N, w, w_layout, acc, nullptr, 0, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+int mcv_w8a8_gemm_f16(const int8_t* xq, const void* xs, int xs_dtype, int64_t M, int64_t K, int64_t N, const int8_t* w,
+                      int w_layout, const void* ws, int ws_dtype, void* out, mcv_stream_t stream) {
+    int rc = check_gemm_args(xq, M, K, N, w, w_layout, out, "matmul_w8a8");
+    if (rc != MCV_OK) return rc;
+    if (!xs || !ws) return fail(MCV_ERR_INVALID_ARG, "matmul_w8a8: null scale");
+    if (!dtype_ok(xs_dtype) || !dtype_ok(ws_dtype)) return fail(MCV_ERR_INVALID_ARG, "matmul_w8a8: bad scale dtype");
+    if ((rc = require_device()) != MCV_OK) return rc;
+    return launch_gemm<true>(xq, M, K, N, w, w_layout, out, xs, xs_dtype == MCV_F16, ws, ws_dtype == MCV_F16,
+                             static_cast<hipStream_t>(stream));
+}
+
+int mcv_w8a8_dequant(const int32_t* acc, const void* xs, int xs_dtype, const void* ws, int ws_dtype, int64_t M, int64_t N,
+                     void* out, mcv_stream_t stream) {
+    if (!acc || !xs || !ws || !out) return fail(MCV_ERR_INVALID_ARG, "w8a8_dequant: null pointer");
+    if (!dtype_ok(xs_dtype) || !dtype_ok(ws_dtype)) return fail(MCV_ERR_INVALID_ARG, "w8a8_dequant: bad scale dtype");
+    if (M <= 0 || N <= 0 || M > 65535 || N > 0x7fffffff)
+        return fail(MCV_ERR_SHAPE, "w8a8_dequant: bad shape M=%lld N=%lld", (long long)M, (long long)N);
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    hipLaunchKernelGGL(w8a8_dequant_kernel, dim3(static_cast<unsigned>(ceil_div(N, 256)), static_cast<unsigned>(M)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), acc, xs, xs_dtype == MCV_F16, ws, ws_dtype == MCV_F16,
+                       static_cast<int>(M), static_cast<int>(N), static_cast<uint16_t*>(out));
+    return check_launch("w8a8_dequant_kernel");
+}
+
+}  // extern "C"

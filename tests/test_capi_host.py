@@ -1,0 +1,143 @@
+"""CPU tests of the C-ABI library: it loads, exports every entry point that
+include/*.h declares, and its host-side functions (packers, quantisers,
+validation) agree with the pinned oracle.  No kernel is launched here."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import ROOT, f16_normal, synth_w4a16
+
+
+def _declared_functions():
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(mcv_[a-z0-9_]+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol(mcv):
+    names = _declared_functions()
+    assert len(names) >= 20
+    L = mcv.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(mcv._SIGS), set(names) ^ set(mcv._SIGS)
+    assert b"gfx950" in L.mcv_version()
+
+
+def test_packed_sizes(mcv):
+    assert mcv.packed_sizes(1024, 248094) == (3877 * 64 * 512, 8 * 3877 * 64 * 2, 8 * 3877 * 64 // 2)
+    assert mcv.packed_sizes(1000, 64) == (0, 0, 0)
+
+
+def test_layout_known_answer(mcv):
+    # one nibble set at (k, n): its byte position must follow the documented formula
+    K, N = 256, 136
+    for (k, n, v) in [(0, 0, 1), (1, 0, 2), (2, 0, 3), (7, 5, 9), (37, 70, 15), (255, 135, 6)]:
+        q = np.zeros((K, N), np.uint8)
+        q[k, n] = v
+        order = [0, 2, 4, 6, 1, 3, 5, 7]
+        qweight = np.zeros((K, N // 8), np.uint32)
+        for j in range(N // 8):
+            for s in range(8):
+                qweight[:, j] |= q[:, 8 * j + order[s]].astype(np.uint32) << (4 * s)
+        qw, sc, zr = mcv.pack_awq(qweight.view(np.int32), np.zeros((K // 128, N // 8), np.int32),
+                                  np.zeros((K // 128, N), np.uint16))
+        words = qw.view(np.uint32)
+        slab, lane, c, w = n // 64, n % 64, k // 32, (k % 32) // 8
+        slot = [0, 4, 1, 5, 2, 6, 3, 7][k % 8]
+        idx = ((slab * (K // 32) + c) * 64 + lane) * 4 + w
+        assert words[idx] == v << (4 * slot)
+        assert np.count_nonzero(words) == 1
+
+
+def test_awq_pack_roundtrip_vs_oracle(mcv, oracle):
+    rng = np.random.default_rng(20)
+    for K, N in [(128, 8), (256, 64), (384, 200), (1024, 520)]:
+        _, qweight, qzeros, scales = synth_w4a16(rng, K, N)
+        qw, sc, zr = mcv.pack_awq(qweight, qzeros, scales)
+        q, zeff, s = mcv.unpack(qw, sc, zr, 0, K, N)
+        w8 = q.astype(np.int16) - np.repeat(zeff, 128, axis=0).astype(np.int16)
+        assert np.array_equal(w8.astype(np.int8), oracle.unpack_awq(qweight, qzeros))
+        assert np.array_equal(s, scales)
+        npad = -(-N // 64) * 64
+        assert (sc.reshape(K // 128, npad)[:, N:] == 0).all()
+
+
+def test_gptq_pack_roundtrip_vs_oracle(mcv, oracle):
+    rng = np.random.default_rng(21)
+    K, N, G = 384, 72, 3
+    qweight = rng.integers(0, 2**32, (K // 8, N), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    qzeros = rng.integers(0, 2**32, (G, N // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    scales = f16_normal(rng, (G, N), 0.01)
+    g_idx = (np.arange(K) // 128).astype(np.int32)
+    qw, sc, zr = mcv.pack_gptq(qweight, qzeros, g_idx, scales)
+    q, zeff, s = mcv.unpack(qw, sc, zr, 1, K, N)
+    w8 = q.astype(np.int16) - np.repeat(zeff, 128, axis=0).astype(np.int16)
+    assert np.array_equal(w8.astype(np.int8), oracle.unpack_gptq(qweight, qzeros, g_idx, G))
+    assert zeff.min() >= 1 and zeff.max() <= 16
+    # g_idx omitted is the same as trivial g_idx
+    qw2, _, _ = mcv.pack_gptq(qweight, qzeros, None, scales)
+    assert np.array_equal(qw, qw2)
+
+
+def test_gptq_act_order_rejected(mcv):
+    K, N = 256, 8
+    g_idx = (np.arange(K) // 128).astype(np.int32)[::-1].copy()
+    with pytest.raises(mcv.McvError, match="act-order"):
+        mcv.pack_gptq(np.zeros((K // 8, N), np.int32), np.zeros((2, 1), np.int32), g_idx,
+                      np.zeros((2, N), np.uint16))
+
+
+def test_product_quantizer_matches_oracle(mcv, oracle):
+    rng = np.random.default_rng(22)
+    for K, N in [(128, 8), (256, 136), (1024, 1000)]:
+        w = f16_normal(rng, (K, N), 0.02)
+        w[:, 1] = 0
+        for nt in (1, 4):
+            a = mcv.quantize_int4(w, nthreads=nt)
+            b = oracle.quantize_int4_awq(w)
+            for x, y in zip(a, b):
+                assert np.array_equal(x.view(np.uint8), y.view(np.uint8))
+
+
+def test_w8a8_host_quantizer_matches_oracle(mcv, oracle):
+    rng = np.random.default_rng(23)
+    w = f16_normal(rng, (320, 96), 0.02)
+    w[:, 7] = 0
+    q_o, s32_o, s16_o = oracle.w8a8_quantize_weight(w)
+    q, s32, s16 = mcv.quantize_w8a8_weight_host(w, mcv.W8_KN)
+    assert np.array_equal(q, q_o) and np.array_equal(s32.view(np.uint32), s32_o.view(np.uint32))
+    assert np.array_equal(s16, s16_o)
+    qt, _, _ = mcv.quantize_w8a8_weight_host(w, mcv.W8_NK)
+    assert np.array_equal(qt, q_o.T)
+
+
+def test_validation_errors_without_device(mcv):
+    L = mcv.lib()
+    # null pointers and bad shapes are rejected on the host before any HIP call
+    assert L.mcv_w4a16_gemm(None, 1, 1024, 64, None, None, None, 0, None, None) == 1
+    assert b"null" in L.mcv_last_error()
+    fake = ctypes.c_void_p(0x1000)
+    assert L.mcv_w4a16_gemv(fake, 1, 1000, 64, fake, fake, fake, 0, fake, None) == 2
+    assert b"multiple of 128" in L.mcv_last_error()
+    assert L.mcv_w4a16_gemv(fake, 1, 1024, 64, fake, fake, fake, 2, fake, None) == 1
+    assert L.mcv_w8a8_gemm_i32(fake, 1, 1000, 64, fake, 0, fake, None) == 2        # K % 16
+    assert L.mcv_w8a8_gemm_i32(fake, 1, 1024, 72, fake, 0, fake, None) == 2        # [K,N] needs N % 16
+    assert L.mcv_w4a16_gemv_tiled_i8(fake, 1024, 3584, 450, 0, fake, fake, fake, None) == 2
+    assert b"tile_len" in L.mcv_last_error()
+    assert L.mcv_silu_mul(fake, fake, fake, 0, None) == 2
+
+
+def test_device_entry_fails_loudly_without_gpu(mcv):
+    from helpers import gpu_available
+    if gpu_available():
+        pytest.skip("a GPU is present")
+    L = mcv.lib()
+    fake = ctypes.c_void_p(0x1000)
+    rc = L.mcv_w4a16_gemm(fake, 1, 1024, 64, fake, fake, fake, 0, fake, None)
+    assert rc == 5, L.mcv_last_error()

@@ -1,0 +1,131 @@
+"""GPU parity of the W8A8 kernels: activation quantiser, int8 MFMA GEMM
+(int32 accumulators bit-exact), dequant epilogue and the fused path (bit-exact
+against the oracle's epilogue).  Config 5: M in {1, 256, 1024}, K=1024, N=3584."""
+import numpy as np
+import pytest
+
+from helpers import f16_normal
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _f16_dev(a_u16):
+    torch = _torch()
+    return torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16)).cuda().view(torch.float16)
+
+
+def _u16(t):
+    torch = _torch()
+    return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("M,K", [(1, 1024), (256, 1024), (1024, 1024), (3, 3584), (2, 1040), (1, 16)])
+def test_quantize_act_bit_exact(mcv, oracle, cuda, M, K):
+    torch = _torch()
+    rng = np.random.default_rng(M * 10 + K)
+    x = f16_normal(rng, (M, K), 1.0)
+    if M > 2:
+        x[1] = 0                                 # all-zero row -> scale floor
+        x[2, :7] = np.float16(0.5).view(np.uint16)
+    s16 = torch.empty(M, dtype=torch.float16, device="cuda")
+    xq, s32, _ = mcv.w8a8_quantize(_f16_dev(x), x_scale_f16=s16)
+    q_o, s32_o, s16_o = oracle.w8a8_quantize_act(x)
+    assert np.array_equal(xq.cpu().numpy(), q_o)
+    assert np.array_equal(s32.cpu().numpy().view(np.uint32), s32_o.view(np.uint32))
+    assert np.array_equal(_u16(s16), s16_o)
+
+
+def test_quantize_act_ties(mcv, oracle, cuda):
+    # values whose x * inv lands on k + 0.5 exactly: max|x| = 127 -> scale 1, inv 1
+    x = np.array([[127.0, 2.5, -2.5, 0.5, -0.5, 126.5, -127.0, 3.5]], np.float16).view(np.uint16)
+    xq, _, _ = mcv.w8a8_quantize(_f16_dev(x))
+    assert xq.cpu().numpy().tolist() == oracle.w8a8_quantize_act(x)[0].tolist()
+    assert xq.cpu().numpy().tolist() == [[127, 3, -3, 1, -1, 127, -127, 4]]
+
+
+def _int8_case(rng, M, K, N):
+    x = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    w = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    return x, w
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 3584), (256, 1024, 3584), (5, 1040, 208), (130, 256, 144)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_gemm_i32_bit_exact(mcv, oracle, cuda, M, K, N, layout):
+    torch = _torch()
+    rng = np.random.default_rng(M + K + N)
+    x, w = _int8_case(rng, M, K, N)
+    wl = mcv.W8_KN if layout == "kn" else mcv.W8_NK
+    wdev = torch.from_numpy(w if layout == "kn" else np.ascontiguousarray(w.T)).cuda()
+    acc = mcv.matmul_w8a8_i32(torch.from_numpy(x).cuda(), wdev, layout=wl)
+    assert np.array_equal(acc.cpu().numpy(), oracle.gemm_i32(x, w))
+
+
+def test_gemm_i32_full_size_exact(mcv, cuda):
+    # config 5 at M=1024 with extreme values: fp64 product is exact at this size
+    torch = _torch()
+    rng = np.random.default_rng(55)
+    M, K, N = 1024, 1024, 3584
+    x, w = _int8_case(rng, M, K, N)
+    x[0, :] = -128
+    w[:, 0] = -128                               # |acc| = 2^24 at (0, 0)
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    acc = mcv.matmul_w8a8_i32(xd, wd)
+    ref = (xd.double() @ wd.double()).to(torch.int64)
+    assert torch.equal(acc.to(torch.int64), ref)
+    assert int(acc[0, 0]) == 1 << 24
+
+
+def test_dequant_reference_vectors(mcv, oracle, cuda):
+    torch = _torch()
+    N = 3584
+    acc = (np.arange(N) - 1024).astype(np.int32)[None, :]
+    ws16 = oracle.f2h_trunc(np.float32(0.01) + (np.arange(N) % 7).astype(np.float32) * np.float32(0.001))
+    xs16 = oracle.f2h_trunc(np.array([0.02], np.float32))
+    out = mcv.w8a8_dequant(torch.from_numpy(acc).cuda(), _f16_dev(xs16), _f16_dev(ws16))
+    want = oracle.w8a8_dequant(acc, oracle.h2f(xs16), oracle.h2f(ws16))
+    assert np.array_equal(_u16(out), want)
+
+
+@pytest.mark.parametrize("M", [1, 256, 1024])
+def test_config5_end_to_end(mcv, oracle, cuda, M):
+    """fp16 x -> per-token int8 + fp32 scale; fp16 W -> per-channel int8 + fp32
+    scale; fused GEMM + epilogue.  Every stage bit-exact against the oracle."""
+    torch = _torch()
+    K, N = 1024, 3584
+    rng = np.random.default_rng(500 + M)
+    x = f16_normal(rng, (M, K), 1.0)
+    wf = f16_normal(rng, (K, N), 0.02)
+    wq = mcv.quantize_dense_weight_w8a8(_f16_dev(wf))
+    xq, xs, _ = mcv.w8a8_quantize(_f16_dev(x))
+    out = mcv.matmul_w8a8(xq, xs, wq)                    # fp32 scales
+    q_o, s_o, _ = oracle.w8a8_quantize_act(x)
+    wq_o, ws_o, ws16_o = oracle.w8a8_quantize_weight(wf)
+    assert np.array_equal(wq.w_int8.cpu().numpy(), wq_o)
+    rows = np.arange(M) if M <= 256 else np.arange(0, M, 8)
+    acc_o = oracle.gemm_i32(q_o[rows], wq_o)
+    want = oracle.w8a8_dequant(acc_o, s_o[rows], ws_o)
+    assert np.array_equal(_u16(out)[rows], want)
+    # fused == two-kernel path, with the reference's fp16 scales too
+    acc = mcv.matmul_w8a8_i32(xq, wq.w_int8)
+    assert torch.equal(mcv.w8a8_dequant(acc, xs, wq.w_scale_f32), out)
+    xs16 = xs.half()
+    assert torch.equal(mcv.matmul_w8a8(xq, xs16, wq, use_f32_scale=False),
+                       mcv.w8a8_dequant(acc, xs16, wq.w_scale))
+
+
+def test_nk_layout_fused(mcv, cuda):
+    torch = _torch()
+    rng = np.random.default_rng(77)
+    K, N, M = 1024, 3584, 64
+    wf = f16_normal(rng, (K, N), 0.02)
+    a = mcv.quantize_dense_weight_w8a8(_f16_dev(wf), layout=mcv.W8_KN)
+    b = mcv.quantize_dense_weight_w8a8(_f16_dev(wf), layout=mcv.W8_NK)
+    xq, xs, _ = mcv.w8a8_quantize(_f16_dev(f16_normal(rng, (M, K), 1.0)))
+    assert torch.equal(mcv.matmul_w8a8(xq, xs, a), mcv.matmul_w8a8(xq, xs, b))
