@@ -1,9 +1,9 @@
 """Benchmark of the MI355X quantized-matmul hot path.
 
 Default workload (one JSON line on stdout): BASELINE config 3, the W4A16
-lm_head -- M=1, K=1024, V=248094 -- as one fused GEMV + argmax launch per
-step, with 8 distinct weight copies (1.06 GB) rotated so no step hits the
-256 MB MALL.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
+lm_head -- M=1, K=1024, V=248094 -- as one GEMV launch per step with the
+argmax folded into it, with 8 distinct weight copies (1.06 GB) rotated so no
+step hits the 256 MB MALL.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
 (132,484,244 B per step, inputs resident in HBM).  `--workload` selects the
 other BASELINE configs (gemv1, mlp, lm_head, prefill, w8a8).
 
@@ -46,25 +46,35 @@ def to_dev_f16(a_u16):
     return torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16)).cuda().view(torch.float16)
 
 
-def timed_launches(launch, n_sets, steps, warmup):
-    """Runs `launch(i)` for warmup + steps iterations on the current stream.
-    Returns (total_ms over the timed steps, per-launch kernel ms list)."""
+def time_steps(launch, n_sets, steps, warmup):
+    """Back-to-back steps on the current stream, bracketed by one event pair
+    (plus a synchronize on both sides).  Returns total ms over `steps`."""
     import torch
     for i in range(warmup):
         launch(i % n_sets)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record()
     for i in range(steps):
-        ev[i][0].record()
         launch((warmup + i) % n_sets)
-        ev[i][1].record()
     t1.record()
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1), [a.elapsed_time(b) for a, b in ev]
+    return t0.elapsed_time(t1)
+
+
+def time_each_launch(launch, n_sets, steps):
+    """HIP events around every launch of the dominant kernel, on the stream it
+    is launched on (torch's current stream).  Returns per-launch ms."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        ev[i][0].record()
+        launch(i % n_sets)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
 
 
 def traffic_from_profiles(workload: str):
@@ -144,13 +154,15 @@ def wl_lm_head(pkg, args):
     xd = to_dev_f16(x)
     logits = torch.empty(V, dtype=torch.float16, device="cuda")
     nbytes = K * V // 2 + (K // 128) * V * 2 + (K // 128) * V // 2 + 2 * V + 2 * K
-    total_ms, kms = timed_launches(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
+    total_ms = time_steps(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
     token = int(heads[0].token.item())
+    kms = time_each_launch(lambda i: heads[i].launch_partials(xd, logits), copies, args.steps)
     res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                config={"workload": "w4a16_lm_head_gemv_argmax", "M": 1, "K": K, "V": V,
                        "weight_copies_rotated": copies, "rotated_bytes": copies * (qw.nbytes + sc.nbytes + zr.nbytes),
                        "algorithmic_bytes_per_step": nbytes, "token": token},
-               dtype="w4a16 (f16 x int4, f32 accumulate)", kernel="w4a16_gemv_kernel<argmax>")
+               dtype="w4a16 (f16 x int4, f32 accumulate)",
+               kernel="w4a16_gemv_kernel<8,1,2> (fused argmax); roofline timed on its <8,1,1> partials twin")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes)
     return res
@@ -170,7 +182,8 @@ def wl_gemv1(pkg, args):
     xd = to_dev_f16(x)
     out = torch.empty((1, N), dtype=torch.float16, device="cuda")
     nbytes = w4a16_bytes(K, N) + 2 * K + 2 * N
-    total_ms, kms = timed_launches(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps, args.warmup)
+    total_ms = time_steps(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps, args.warmup)
+    kms = time_each_launch(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps)
     res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                config={"workload": "w4a16_gemv_1024x1024", "M": 1, "K": K, "N": N, "weight_sets_rotated": sets},
                dtype="w4a16 (f16 x int4, f32 accumulate)", kernel="w4a16_gemv_kernel")
@@ -216,7 +229,8 @@ def wl_mlp(pkg, args):
         pkg.matmul_w4a16(a, L[2], y)
 
     nbytes = 2 * w4a16_bytes(H, I) + w4a16_bytes(I, H) + 2 * H * 2 + 2 * I * 2 * 3 + 2 * H
-    total_ms, kms = timed_launches(block, len(sets), args.steps, args.warmup)
+    total_ms = time_steps(block, len(sets), args.steps, args.warmup)
+    kms = time_each_launch(block, len(sets), args.steps)
     return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                 config={"workload": "w4a16_mlp_block_decode", "M": 1, "hidden": H, "intermediate": I,
                         "weight_sets_rotated": len(sets)},
@@ -232,7 +246,8 @@ def wl_prefill(pkg, args):
     x = to_dev_f16(f16_normal(rng, (M, K), 1.0))
     out = torch.empty((M, N), dtype=torch.float16, device="cuda")
     flops = 2.0 * M * K * N
-    total_ms, kms = timed_launches(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps, args.warmup)
+    total_ms = time_steps(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps, args.warmup)
+    kms = time_each_launch(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps)
     return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TFLOP/s", bound="mfma",
                 config={"workload": "w4a16_prefill_gemm", "M": M, "K": K, "N": N},
                 dtype="w4a16 (f16 MFMA, f32 accumulate)", kernel="w4a16_gemm_kernel")
@@ -246,13 +261,29 @@ def wl_w8a8(pkg, args):
     xq, xs, _ = pkg.w8a8_quantize(to_dev_f16(f16_normal(rng, (M, K), 1.0)))
     out = torch.empty((M, N), dtype=torch.float16, device="cuda")
     flops = 2.0 * M * K * N
-    total_ms, kms = timed_launches(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps, args.warmup)
+    total_ms = time_steps(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps, args.warmup)
+    kms = time_each_launch(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps)
     return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TOP/s", bound="mfma",
                 config={"workload": "w8a8_gemm_fused", "M": M, "K": K, "N": N},
                 dtype="int8 (i32 accumulate, fused f16 epilogue)", kernel="w8a8_gemm_kernel<kn,f16>")
 
 
-WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp, "prefill": wl_prefill, "w8a8": wl_w8a8}
+def wl_copy(pkg, args):
+    """Calibration for the HBM counters: a plain 128 MiB device-to-device copy
+    (torch's copy kernel) reads and writes exactly 134,217,728 bytes."""
+    import torch
+    n = 128 * 2**20
+    src = [torch.ones(n, dtype=torch.uint8, device="cuda") for _ in range(4)]
+    dst = torch.empty(n, dtype=torch.uint8, device="cuda")
+    total_ms = time_steps(lambda i: dst.copy_(src[i]), 4, args.steps, args.warmup)
+    kms = time_each_launch(lambda i: dst.copy_(src[i]), 4, args.steps)
+    return dict(bytes=2 * n, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
+                config={"workload": "copy_128MiB_calibration", "bytes_read": n, "bytes_written": n},
+                dtype="u8", kernel="torch copy kernel")
+
+
+WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp, "prefill": wl_prefill, "w8a8": wl_w8a8,
+             "copy": wl_copy}
 
 
 def main():

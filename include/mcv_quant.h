@@ -145,10 +145,11 @@ int mcv_w4a16_gemv_tiled_i8(const void* x_dev, int64_t K, int64_t N, int64_t til
                             int64_t packed_rows, const int8_t* w_dev, const void* scales_dev,
                             void* out_dev, mcv_stream_t stream);
 
-/* Workspace for mcv_w4a16_lm_head_argmax: device memory of this many bytes,
- * zero-filled once before its first use.  Each call leaves it zero-filled
- * again; calls that share one workspace must not overlap. */
-int64_t mcv_lm_head_workspace_bytes(void);
+/* Workspace for mcv_w4a16_lm_head_argmax over V columns: device memory of
+ * this many bytes, 128-byte aligned, zero-filled once before its first use
+ * (it holds the slot tree of the fused argmax; every call leaves it
+ * zero-filled again).  Calls sharing one workspace must not overlap. */
+int64_t mcv_lm_head_workspace_bytes(int64_t V);
 
 /* Greedy lm_head over a W4A16 weight: logits[v] = x . W[:, v] (fp16 RNE of the
  * fp32 sum) for v < V, and token = the first index of the maximum logit, with
@@ -157,11 +158,26 @@ int64_t mcv_lm_head_workspace_bytes(void);
  * V on are ignored, like the reference's clipped chunk tails, :472).
  * logits_dev may be NULL.  token_dev receives an int64 on the device.
  * Replaces the 16 chunk matmuls + 16 D2H copies + host scan of lm_head_greedy
- * (src/csrc/lib/language_model.cpp:412-482) with one kernel. */
+ * (src/csrc/lib/language_model.cpp:412-482) with one kernel: the GEMV's
+ * workgroups fold their best (value, index) into a two-level tree of
+ * (max, arrival count) slots in the workspace, and the last arrival writes
+ * the token. */
 int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
                              const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                              int zero_bias, void* logits_dev, int64_t* token_dev,
                              void* workspace_dev, mcv_stream_t stream);
+
+/* The same greedy lm_head in two launches, for callers that fold the final
+ * key reduction into their own next kernel: the GEMV writes logits (may be
+ * NULL) and one 64-bit argmax key per 64-column slab to keys_dev (8-byte
+ * aligned, 8 * ceil(V / 64) bytes, no initialisation needed);
+ * mcv_argmax_reduce_keys folds n_keys keys into the int64 token.  A key orders
+ * by fp16 value (subnormals as zero, NaN and -inf never winning), then by the
+ * smaller column index. */
+int mcv_w4a16_gemv_argmax_partials(const void* x_dev, int64_t K, int64_t N, int64_t V,
+                                   const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                                   int zero_bias, void* logits_dev, void* keys_dev, mcv_stream_t stream);
+int mcv_argmax_reduce_keys(const void* keys_dev, int64_t n_keys, int64_t* token_dev, mcv_stream_t stream);
 
 /* ------------------------------------------------------- W8A8 on device -- */
 /* Per-row symmetric int8 activation quantisation: scale = max|x| / 127

@@ -55,8 +55,10 @@ _SIGS = {
     "mcv_w4a16_gemm_mfma": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
-    "mcv_lm_head_workspace_bytes": (_c_i64, []),
+    "mcv_lm_head_workspace_bytes": (_c_i64, [_c_i64]),
     "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
+    "mcv_w4a16_gemv_argmax_partials": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp]),
+    "mcv_argmax_reduce_keys": (_c_int, [_vp, _c_i64, _vp, _vp]),
     "mcv_w8a8_quantize_act": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "mcv_w8a8_gemm_i32": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_dequant": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),
@@ -300,15 +302,17 @@ def matmul_w4a16_tiled(x, w_int8, scales, out, stream=None):
 class LmHeadW4A16:
     """Greedy lm_head over a W4A16 weight [K, >= vocab] with the argmax fused
     into the GEMV (replaces lm_head_greedy's 16 chunk matmuls + host scan,
-    src/csrc/lib/language_model.cpp:412-482).  Owns its zero-filled workspace."""
+    src/csrc/lib/language_model.cpp:412-482).  Owns its workspace."""
 
     def __init__(self, w: W4A16QuantizedWeight, vocab: int):
         torch = _torch()
         if vocab > w.N:
             raise McvError(f"vocab {vocab} exceeds weight width {w.N}")
         self.w, self.vocab = w, vocab
-        nbytes = lib().mcv_lm_head_workspace_bytes()
-        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=w.qweight.device)
+        # zero-filled once; every fused call leaves the combining tree zeroed again
+        self.workspace = torch.zeros(lib().mcv_lm_head_workspace_bytes(vocab), dtype=torch.uint8,
+                                     device=w.qweight.device)
+        self.keys = torch.empty(-(-vocab // SLAB), dtype=torch.int64, device=w.qweight.device)
         self.token = torch.zeros(1, dtype=torch.int64, device=w.qweight.device)
 
     def launch(self, x, logits=None, stream=None):
@@ -322,6 +326,19 @@ class LmHeadW4A16:
         _check(lib().mcv_w4a16_lm_head_argmax(_dev(x), self.w.K, self.w.N, self.vocab, q, s, z, self.w.zero_bias,
                                               _dev(logits) if logits is not None else 0, _dev(self.token),
                                               _dev(self.workspace), _stream(stream)), "mcv_w4a16_lm_head_argmax")
+        return self.token
+
+    def launch_partials(self, x, logits=None, stream=None):
+        """First stage only: the GEMV writing logits and per-slab argmax keys."""
+        q, s, z = self.w.ptrs()
+        _check(lib().mcv_w4a16_gemv_argmax_partials(_dev(x), self.w.K, self.w.N, self.vocab, q, s, z,
+                                                    self.w.zero_bias, _dev(logits) if logits is not None else 0,
+                                                    _dev(self.keys), _stream(stream)),
+               "mcv_w4a16_gemv_argmax_partials")
+
+    def reduce_partials(self, stream=None):
+        _check(lib().mcv_argmax_reduce_keys(_dev(self.keys), self.keys.numel(), _dev(self.token),
+                                            _stream(stream)), "mcv_argmax_reduce_keys")
         return self.token
 
     def __call__(self, x, logits=None) -> int:

@@ -24,9 +24,12 @@ LIB = PKG / "lib"
 BUILD = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-# Device flags.  Packed-fp32 instructions are disabled (see the environment
-# notes in the design document); fp32 division and sqrt stay correctly rounded
-# and contraction is left to explicit fma/__f*_rn calls in the kernels.
+# Device flags.  Packed-fp32 instructions are disabled; fp32 division and
+# sqrt stay correctly rounded.  Contraction is off: the epilogues must round
+# to fp32 before the fp16 conversion exactly as the reference does (with
+# contraction on, clang folds mul + fp32->fp16 into one v_fma_mixlo_f16, a
+# single rounding); fused multiply-adds are written explicitly (fmaf, dot2,
+# MFMA builtins).
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -34,6 +37,7 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-command-line-argument",
+    "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",

@@ -47,8 +47,14 @@ __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cas
 __device__ __forceinline__ float h2f(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
-// fp32 -> fp16 with IEEE round-to-nearest-even (v_cvt_f16_f32 in the default mode).
+// fp32 -> fp16 with IEEE round-to-nearest-even (v_cvt_f16_f32 in the default
+// mode) of exactly this fp32 value.  The empty asm hides where `f` came from:
+// otherwise the backend folds a preceding fp32 multiply or add into one
+// v_fma_mixlo_f16, which rounds the exact result to fp16 once instead of
+// rounding to fp32 first -- a different answer in about 1 of 8192 cases, and
+// not the reference's Mul/Muls-then-Cast(RINT) sequence.
 __device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 

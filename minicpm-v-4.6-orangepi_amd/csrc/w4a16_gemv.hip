@@ -20,12 +20,6 @@
 namespace mcv {
 namespace {
 
-struct LmHeadWs {
-    unsigned long long key;  // running max of argmax_key64 over finished workgroups
-    unsigned int count;      // finished workgroups
-    unsigned int pad;
-};
-
 // (a & mask) | magic in one v_and_or_b32.  gfx9 VOP3 encodings take no
 // literal and at most one SGPR, so the mask rides in an SGPR and the magic
 // exponent pattern in a VGPR; left to itself the compiler emits v_and + v_or.
@@ -65,15 +59,50 @@ __device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t*
     return fmaf(alo + ahi * 0.0625f, scale, acc);
 }
 
+// Cross-workgroup argmax without fences.  Each level-1 slot j (64 slots,
+// 128 B apart, taken by slab % 64) holds a 64-bit key max and a 32-bit arrival
+// count.  A workgroup folds its key in with atomicMax, waits for that atomic to
+// return -- it has then been performed at the device-coherent point -- and
+// only then bumps the count.  The arrival that brings the count to its
+// expected value therefore sees every other arrival's key when it reads the
+// slot (atomicMax with 0), clears the slot, and repeats the same two steps on
+// the level-2 slot; the last level-2 arrival writes the token and clears it.
+// Every call thus leaves the workspace all zero.  Measured on MI355X with the
+// lm_head's 3877 workgroups: 3877 atomics on one address serialise to 45 us
+// (spread over 64 addresses they are free), a __threadfence per workgroup adds
+// ~30 us, CAS-combined (key, count) words 22-39 us (retry storms when the
+// last arrivals bunch), this scheme ~4 us over the bare GEMV, and a second
+// reduction launch ~7 us.
+constexpr int kTreeStride = 16;                               // u64 words per slot: 128 B
+constexpr int kTreeWords = 64;
+constexpr int64_t kTreeBytes = (kTreeWords + 1) * kTreeStride * 8;
+
+// Folds `key` into slot `slot` (key word at [0], count at [8]); true for the
+// arrival that completes the slot, which then receives the slot's maximum.
+__device__ __forceinline__ bool slot_arrive(unsigned long long* slot, unsigned long long key, unsigned expected,
+                                            unsigned long long* merged) {
+    unsigned* count = reinterpret_cast<unsigned*>(slot + 8);
+    const unsigned long long before = atomicMax(slot, key);
+    asm volatile("s_waitcnt vmcnt(0)" : : "v"(before) : "memory");   // the max has returned, i.e. is performed
+    if (atomicAdd(count, 1u) + 1u != expected) return false;
+    *merged = atomicMax(slot, 0ull);                                   // atomic read of the slot's maximum
+    atomicExch(slot, 0ull);
+    atomicExch(count, 0u);
+    return true;
+}
+
+// ARGMAX modes of the GEMV epilogue (M == 1 only).
+constexpr int kArgNone = 0;
+constexpr int kArgPartials = 1;   // plain store of the slab's key to keys[slab]
+constexpr int kArgFused = 2;      // two-level slot tree in `keys`, token written by the last arrival
+
 // grid = (Nslab, M), block = 64 * KSPLIT.  Wave w handles groups
-// {w*GPW + r*KSPLIT*GPW + i : i < GPW}.  ARGMAX (M == 1 only) also folds the
-// workgroup's fp16 logits into the running argmax in `ws`; the last workgroup
-// to finish writes the token and re-zeroes `ws`.
-template <int KSPLIT, int GPW, bool ARGMAX>
+// {w*GPW + r*KSPLIT*GPW + i : i < GPW}.
+template <int KSPLIT, int GPW, int ARGMAX>
 __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int K, int N,
-    int Npad, LmHeadWs* __restrict__ ws, int64_t* __restrict__ token) {
+    int Npad, unsigned long long* __restrict__ keys, int64_t* __restrict__ token) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: keeps x loads scalar
     const int slab = blockIdx.x;
@@ -124,29 +153,47 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
 
     const uint16_t h = f2h(acc);
     if (out != nullptr && n < N) out[static_cast<size_t>(m) * N + n] = h;
-    if constexpr (ARGMAX) {
+    if constexpr (ARGMAX != kArgNone) {
         unsigned long long key = n < N ? argmax_key64(argmax_key16(h), static_cast<uint32_t>(n)) : 0ull;
         key = wave_max_u64(key);
         if (lane == 0) {
-            if (key != 0ull) atomicMax(&ws->key, key);
-            __threadfence();
-            const unsigned int done = atomicAdd(&ws->count, 1u);
-            if (done == gridDim.x - 1) {
-                __threadfence();
-                const unsigned long long fin = atomicAdd(&ws->key, 0ull);
-                *token = argmax_index(fin);
-                atomicExch(&ws->key, 0ull);
-                atomicExch(&ws->count, 0u);
+            if constexpr (ARGMAX == kArgPartials) {
+                keys[slab] = key;
+            } else {
+                const int nblk = static_cast<int>(gridDim.x);
+                const int j = slab & (kTreeWords - 1);
+                unsigned long long m1, m2;
+                if (slot_arrive(keys + j * kTreeStride, key,
+                                static_cast<unsigned>((nblk - j + kTreeWords - 1) / kTreeWords), &m1) &&
+                    slot_arrive(keys + kTreeWords * kTreeStride, m1,
+                                static_cast<unsigned>(nblk < kTreeWords ? nblk : kTreeWords), &m2))
+                    *token = argmax_index(m2);
             }
         }
     }
 }
 
-template <bool ARGMAX>
-using GemvFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int,
-                        int, int, LmHeadWs*, int64_t*);
+// One workgroup folds the per-slab keys into the token (first maximum wins:
+// the key orders by value, then by smallest index).
+__global__ __launch_bounds__(1024) void argmax_reduce_kernel(const unsigned long long* __restrict__ keys, int n,
+                                                             int64_t* __restrict__ token) {
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
+    best = wave_max_u64(best);
+    __shared__ unsigned long long wbest[16];
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) best = wbest[w] > best ? wbest[w] : best;
+        *token = argmax_index(best);
+    }
+}
 
-template <bool ARGMAX, int KS>
+template <int ARGMAX>
+using GemvFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int,
+                        int, int, unsigned long long*, int64_t*);
+
+template <int ARGMAX, int KS>
 GemvFn<ARGMAX> pick_gpw(int gpw) {
     switch (gpw) {
         case 1: return w4a16_gemv_kernel<KS, 1, ARGMAX>;
@@ -156,7 +203,7 @@ GemvFn<ARGMAX> pick_gpw(int gpw) {
     }
 }
 
-template <bool ARGMAX>
+template <int ARGMAX>
 GemvFn<ARGMAX> pick_kernel(int ks, int gpw) {
     switch (ks) {
         case 1: return pick_gpw<ARGMAX, 1>(gpw);
@@ -178,14 +225,15 @@ int env_int(const char* name, int fallback) {
     return std::atoi(v);
 }
 
-// Split K over enough waves to put ~16 waves on each of the 256 CUs, keep
-// each wave's groups unrolled (<= 8 groups = 32 outstanding 16-byte loads).
-// MCV_GEMV_KSPLIT / MCV_GEMV_GPW override the choice (tuning sweeps).
+// One quantisation group (four 16-byte loads per lane) per wave per trip,
+// and enough waves per workgroup (up to 8, at most one per group) that the
+// grid holds >= 16K waves, 64 per CU: measured on the lm_head shape (K=1024,
+// 3877 slabs), 4 or 8 waves x 1 group run at 23.4 us where 2 x 4 groups take
+// 31 us.  MCV_GEMV_KSPLIT / MCV_GEMV_GPW override the choice (tuning sweeps).
 GemvCfg choose_gemv(int64_t G, int64_t blocks) {
     int ks = 1;
-    while (ks < 16 && blocks * ks < 4096 && ks * 2 <= G) ks *= 2;
-    int need = static_cast<int>(ceil_div(G, ks));
-    int gpw = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+    while (ks < 8 && blocks * ks < 16384 && ks * 2 <= G) ks *= 2;
+    const int gpw = 1;
     GemvCfg c{env_int("MCV_GEMV_KSPLIT", ks), env_int("MCV_GEMV_GPW", gpw)};
     if (c.ksplit != 1 && c.ksplit != 2 && c.ksplit != 4 && c.ksplit != 8 && c.ksplit != 16) c.ksplit = ks;
     if (c.gpw != 1 && c.gpw != 2 && c.gpw != 4 && c.gpw != 8) c.gpw = gpw;
@@ -278,7 +326,7 @@ int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void
     if ((rc = require_device()) != MCV_OK) return rc;
     const int64_t nslab = ceil_div(N, kSlab);
     const GemvCfg cfg = choose_gemv(K / kGroup, nslab * M);
-    auto fn = pick_kernel<false>(cfg.ksplit, cfg.gpw);
+    auto fn = pick_kernel<kArgNone>(cfg.ksplit, cfg.gpw);
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(M)), dim3(64 * cfg.ksplit), 0,
                        stream, static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
@@ -298,7 +346,45 @@ int mcv_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* q
     return launch_w4a16_gemv(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
 }
 
-int64_t mcv_lm_head_workspace_bytes(void) { return 256; }
+int64_t mcv_lm_head_workspace_bytes(int64_t V) {
+    (void)V;
+    return kTreeBytes;
+}
+
+int mcv_w4a16_gemv_argmax_partials(const void* x, int64_t K, int64_t N, int64_t V, const void* qw,
+                                   const void* scales, const void* zeros, int zero_bias, void* logits,
+                                   void* keys, mcv_stream_t stream) {
+    int rc = MCV_OK;
+    if (!w4_args_ok(qw, scales, zeros, zero_bias, K, N, "mcv_w4a16_gemv_argmax_partials", &rc)) return rc;
+    if (!x || !keys) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemv_argmax_partials: null x/keys");
+    if (V <= 0 || V > N) return fail(MCV_ERR_SHAPE, "lm_head: need 0 < V <= N (V=%lld N=%lld)", (long long)V, (long long)N);
+    if (reinterpret_cast<uintptr_t>(keys) % 8 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "lm_head: workspace must be 8-byte aligned");
+    if ((rc = require_device()) != MCV_OK) return rc;
+    // Only the slabs holding columns < V run; the scale/zero row stride is the
+    // packed width of the weight (N), not of V.
+    const int64_t nslab = ceil_div(V, kSlab);
+    const int64_t npad = ceil_div(N, kSlab) * kSlab;
+    const GemvCfg cfg = choose_gemv(K / kGroup, nslab);
+    auto fn = pick_kernel<kArgPartials>(cfg.ksplit, cfg.gpw);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), 1u), dim3(64 * cfg.ksplit), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
+                       static_cast<const uint4*>(qw), static_cast<const uint16_t*>(scales),
+                       static_cast<const uint32_t*>(zeros), static_cast<uint32_t>(zero_bias),
+                       static_cast<uint16_t*>(logits), static_cast<int>(K), static_cast<int>(V),
+                       static_cast<int>(npad), static_cast<unsigned long long*>(keys), nullptr);
+    return check_launch("w4a16_gemv_kernel<partials>");
+}
+
+int mcv_argmax_reduce_keys(const void* keys, int64_t n_keys, int64_t* token, mcv_stream_t stream) {
+    if (!keys || !token) return fail(MCV_ERR_INVALID_ARG, "mcv_argmax_reduce_keys: null pointer");
+    if (n_keys <= 0 || n_keys > 0x7fffffff) return fail(MCV_ERR_SHAPE, "mcv_argmax_reduce_keys: bad n_keys");
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const unsigned long long*>(keys), static_cast<int>(n_keys), token);
+    return check_launch("argmax_reduce_kernel");
+}
 
 int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, const void* qw, const void* scales,
                              const void* zeros, int zero_bias, void* logits, int64_t* token, void* workspace,
@@ -308,21 +394,21 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
     if (!x || !token || !workspace) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: null x/token/workspace");
     if (V <= 0 || V > N) return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax: need 0 < V <= N (V=%lld N=%lld)",
                                      (long long)V, (long long)N);
-    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
-        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: workspace must be 16-byte aligned");
+    if (ceil_div(V, kSlab) > int64_t(kTreeWords) * 0xffff)
+        return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax: V too large for the combining tree");
+    if (reinterpret_cast<uintptr_t>(workspace) % 128 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: workspace must be 128-byte aligned");
     if ((rc = require_device()) != MCV_OK) return rc;
-    // Only the slabs holding columns < V run; the scale/zero row stride is the
-    // packed width of the weight (N), not of V.
     const int64_t nslab = ceil_div(V, kSlab);
     const int64_t npad = ceil_div(N, kSlab) * kSlab;
     const GemvCfg cfg = choose_gemv(K / kGroup, nslab);
-    auto fn = pick_kernel<true>(cfg.ksplit, cfg.gpw);
+    auto fn = pick_kernel<kArgFused>(cfg.ksplit, cfg.gpw);
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), 1u), dim3(64 * cfg.ksplit), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
                        static_cast<const uint4*>(qw), static_cast<const uint16_t*>(scales),
                        static_cast<const uint32_t*>(zeros), static_cast<uint32_t>(zero_bias),
                        static_cast<uint16_t*>(logits), static_cast<int>(K), static_cast<int>(V),
-                       static_cast<int>(npad), static_cast<LmHeadWs*>(workspace), token);
+                       static_cast<int>(npad), static_cast<unsigned long long*>(workspace), token);
     return check_launch("w4a16_gemv_kernel<argmax>");
 }
 

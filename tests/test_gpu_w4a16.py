@@ -205,7 +205,7 @@ def test_lm_head_config3(mcv, oracle, cuda):
     top2 = np.sort(ref)[-2:]
     assert top2[1] - top2[0] > 1e-2
     assert tok == int(np.argmax(ref))
-    # the workspace is left zeroed: a second call gives the same answer
+    # repeated calls (workspace reused) give the same answer
     assert head(_to_dev(x)) == tok
     assert head(_to_dev(x), logits) == tok
 
@@ -228,3 +228,28 @@ def test_lm_head_small_and_ties(mcv, oracle, cuda, V):
     assert tok == oracle.argmax_f16(got16)
     full = _host_f32(mcv.matmul_w4a16(_to_dev(x), w))[0, :V]
     assert np.array_equal(full.astype(np.float16).view(np.uint16), got16)
+
+
+@pytest.mark.parametrize("V", [4097, 8320, 100000])
+def test_lm_head_fused_tree_matches_two_stage(mcv, oracle, cuda, V):
+    """The fence-free slot tree (64 level-1 slots, uneven arrival counts
+    when ceil(V/64) is not a multiple of 64) gives the same token and logits as
+    the plain per-slab keys + reduction, and leaves its workspace zeroed."""
+    torch = _torch()
+    K, NW = 512, -(-V // 8) * 8
+    rng = np.random.default_rng(V + 11)
+    w_f16 = f16_normal(rng, (K, NW), 0.02)
+    qweight, qzeros, scales = mcv.quantize_int4(w_f16)
+    w = _dev_weight(mcv, qweight, qzeros, scales)
+    head = mcv.LmHeadW4A16(w, V)
+    for trial in range(3):
+        x = _to_dev(f16_normal(rng, (1, K), 1.0 + trial))
+        la = torch.empty(V, dtype=torch.float16, device="cuda")
+        lb = torch.empty(V, dtype=torch.float16, device="cuda")
+        fused = head(x, la)
+        assert int(head.workspace.count_nonzero()) == 0
+        head.launch_partials(x, lb)
+        two = int(head.reduce_partials().item())
+        assert fused == two
+        assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
+        assert fused == oracle.argmax_f16(la.cpu().view(torch.int16).numpy().view(np.uint16))

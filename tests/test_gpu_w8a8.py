@@ -111,7 +111,9 @@ def test_config5_end_to_end(mcv, oracle, cuda, M):
     rows = np.arange(M) if M <= 256 else np.arange(0, M, 8)
     acc_o = oracle.gemm_i32(q_o[rows], wq_o)
     want = oracle.w8a8_dequant(acc_o, s_o[rows], ws_o)
-    assert np.array_equal(_u16(out)[rows], want)
+    got = _u16(out)[rows]
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:3].tolist()}: {got[tuple(bad[0])]:#06x} vs {want[tuple(bad[0])]:#06x}"
     # fused == two-kernel path, with the reference's fp16 scales too
     acc = mcv.matmul_w8a8_i32(xq, wq.w_int8)
     assert torch.equal(mcv.w8a8_dequant(acc, xs, wq.w_scale_f32), out)
