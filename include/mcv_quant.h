@@ -184,8 +184,8 @@ int mcv_argmax_reduce_keys(const void* keys_dev, int64_t n_keys, int64_t* token_
  * (floor 1e-8), q = trunc(clamp(x * (1/scale), -128, 127) +- 0.5).
  * Replaces w8a8_quantize (src/csrc/lib/ops.cpp:1135-1171, kernel
  * op_kernel/w8a8_quantize_custom.cpp:18-47), which accepts M = 1 only.
- * x_scale_f32_dev [M] receives the fp32 scale; x_scale_f16_dev [M] (may be
- * NULL) its fp16 RNE encoding, the reference's stored form. */
+ * x_scale_f32_dev [M] receives the fp32 scale and x_scale_f16_dev [M] its fp16
+ * RNE encoding, the reference's stored form; either (not both) may be NULL. */
 int mcv_w8a8_quantize_act(const void* x_dev, int64_t M, int64_t K, int8_t* xq_dev,
                           float* x_scale_f32_dev, void* x_scale_f16_dev, mcv_stream_t stream);
 
@@ -231,6 +231,13 @@ int mcv_silu_mul(const void* gate_dev, const void* up_dev, void* out_dev, int64_
  * (src/csrc/lib/language_model.cpp:473-479). */
 int mcv_argmax_f16(const void* x_dev, int64_t M, int64_t N, int64_t* idx_dev,
                    mcv_stream_t stream);
+
+/* Row-wise RMSNorm of fp16 [M][H]: y = fp16 RNE((x * rstd) * gamma) with
+ * rstd = 1 / sqrt(mean(x^2) + eps) in fp32.  The final norm that
+ * lm_head_greedy applies before the vocabulary projection
+ * (src/csrc/lib/language_model.cpp:424, an aclnn builtin in the reference). */
+int mcv_rms_norm(const void* x_dev, const void* gamma_dev, int64_t M, int64_t H, double eps, void* out_dev,
+                 mcv_stream_t stream);
 
 #ifdef __cplusplus
 }

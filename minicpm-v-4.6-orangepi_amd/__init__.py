@@ -66,6 +66,7 @@ _SIGS = {
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
     "mcv_argmax_f16": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp]),
+    "mcv_rms_norm": (_c_int, [_vp, _vp, _c_i64, _c_i64, ctypes.c_double, _vp, _vp]),
 }
 
 
@@ -451,6 +452,19 @@ def argmax_last_dim(x, out=None, stream=None):
     if out is None:
         out = torch.empty(x2.shape[0], dtype=torch.int64, device=x.device)
     _check(lib().mcv_argmax_f16(_dev(x2), x2.shape[0], x2.shape[1], _dev(out), _stream(stream)), "argmax")
+    return out
+
+
+def rms_norm(x, gamma, eps: float, out=None, stream=None):
+    """Row-wise RMSNorm of fp16 [M, H] with fp16 gamma [H] (fp32 arithmetic)."""
+    torch = _torch()
+    if x.dtype != torch.float16 or gamma.dtype != torch.float16 or x.shape[-1] != gamma.numel():
+        raise McvError("rms_norm requires fp16 x [M, H] and gamma [H]")
+    x2 = x.reshape(-1, x.shape[-1])
+    if out is None:
+        out = torch.empty_like(x)
+    _check(lib().mcv_rms_norm(_dev(x2), _dev(gamma), x2.shape[0], x2.shape[1], float(eps), _dev(out), _stream(stream)),
+           "rms_norm")
     return out
 
 

@@ -93,7 +93,7 @@ def build_cpp_layer(jobs: int | None = None) -> Path:
     out = LIB / "libminicpmv_ops.so"
     tmp = LIB / "libminicpmv_ops.so.tmp"
     _run(["g++", "-shared", "-o", str(tmp), *map(str, objs), f"-L{LIB}", "-lmcv_quant",
-          "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"])
+          "-L/opt/rocm/lib", "-lamdhip64", "-lrocblas", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(tmp, out)
     return out
 
@@ -103,7 +103,7 @@ def build_cpp_tests(jobs: int | None = None) -> list[Path]:
     tdir = ROOT / "tests" / "cpp"
     srcs = sorted(tdir.glob("test_*.cpp"))
     bindir = tdir / "bin"
-    bindir.mkdir(exist_ok=True)
+    bindir.mkdir(parents=True, exist_ok=True)
 
     def one(src: Path) -> Path:
         exe = bindir / src.stem

@@ -1,0 +1,65 @@
+// ops.h -- quantized-matmul operators (hot-path subset of the reference's ops.h).
+//
+// Same names and argument order as src/csrc/include/minicpmv/ops.h:41,95-126
+// with aclrtStream -> hipStream_t.  Every operator validates shapes and dtypes
+// on the host (std::runtime_error on mismatch, as ops.cpp:1037-1079) and then
+// enqueues hand-written gfx950 kernels on `stream` through the C-ABI.  Unlike
+// the reference (which synchronises after every op, ops.cpp:374) the calls are
+// stream-ordered and asynchronous; Tensor::copy_to_host orders after them.
+//
+// Generalisations: the M = 1 restriction of matmul_w4a16 / matmul_w8a8_i32 /
+// w8a8_quantize / w8a8_dequant (ops.cpp:1049,1110,1148,1182) is lifted to any
+// M; scales may be fp16 or fp32.
+#pragma once
+
+#include "minicpmv/quantized_weight.h"
+#include "minicpmv/tensor.h"
+
+#include <hip/hip_runtime_api.h>
+
+namespace minicpmv {
+
+// out = silu(gate) * up in fp32, RNE to fp16.  gate, up, out: fp16, one shape.
+void silu_mul(const Tensor& gate, const Tensor& up, Tensor& out, hipStream_t stream);
+
+// Per-row argmax of fp16 [..., N] into Int64 [rows]; the first maximum wins.
+void argmax_last_dim(const Tensor& self, Tensor& out, hipStream_t stream);
+
+// The reference's W4A16 format, M = 1:
+//   x fp16 [1, K]; w_int8 int8 [(K/128)*8*tilesPerBlock*128, tile_len] holding
+//   (q - z) tile-packed by pack_w4a16_weight; scales fp16 [K/128, N]; out [1, N].
+void matmul_w4a16(const Tensor& x, const Tensor& w_int8, const Tensor& scales, Tensor& out, hipStream_t stream);
+
+// x fp16 [M, K] . dequant(w) -> out fp16 [M, N], any M (GEMV for small M,
+// LDS-dequant fp16 MFMA GEMM otherwise).
+void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream);
+
+// int32 out [M, N] = int8 x [M, K] . int8 w [K, N], exact.
+void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream);
+
+// Per-row symmetric int8 quantisation of fp16 x [M, K]; x_scale is [M]
+// (or [1] for M = 1, as the reference) in fp16 or fp32.
+void w8a8_quantize(const Tensor& x, Tensor& x_int8, Tensor& x_scale, hipStream_t stream);
+
+// out fp16 [M, N] = RNE((acc * w_scale[n]) * x_scale[m]); scales fp16 or fp32.
+void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream);
+
+// Fused int8 GEMM + dequant epilogue (the int32 accumulator stays on chip);
+// bit-identical to matmul_w8a8_i32 + w8a8_dequant with the same scales.
+// Uses w.w_scale_f32 when x_scale is fp32, the fp16 w.w_scale otherwise.
+void matmul_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8QuantizedWeight& w, Tensor& out,
+                 hipStream_t stream);
+
+// Materialises dequantised weights: w_f16 [K, N] fp16 and/or w_i8 [K, N] int8
+// (q - z); either pointer may be null.
+void w4a16_dequant(const W4A16QuantizedWeight& w, Tensor* w_f16, Tensor* w_i8, hipStream_t stream);
+
+// Dense fp16 fallback of the decode dispatcher: out [M, N] = a [M, K] . b,
+// b given as [N, K] or [K, N] (src/csrc/lib/ops.cpp:159-322 semantics).  A
+// plain library GEMM (rocBLAS, fp32 accumulation).
+void matmul_b_transposed(const Tensor& a, const Tensor& b, Tensor& out, hipStream_t stream);
+
+// y = fp16(x / sqrt(mean(x^2) + eps) * gamma) per row, fp32 in between.
+void rms_norm(const Tensor& x, const Tensor& gamma, Tensor& out, double epsilon, hipStream_t stream);
+
+}  // namespace minicpmv

@@ -1,0 +1,55 @@
+// quantized_weight.h -- W4A16 / W8A8 weight objects and their loaders.
+//
+// Mirrors src/csrc/include/minicpmv/quantized_weight.h:11-28.  Additive
+// changes, all behind the same names:
+//   - W4A16QuantizedWeight keeps the int4 nibbles packed on the device in the
+//     gfx950 slab-64 layout (include/mcv_quant.h) instead of widening them to
+//     int8 (q - z): `w_int8` holds those packed bytes, and the zero-points
+//     travel as `zeros` (+ `zero_bias`) rather than being folded in.
+//   - W8A8QuantizedWeight also keeps the fp32 per-channel scale; `w_scale` is
+//     the reference's truncated fp16 copy (quantized_weight.cpp:253).
+//   - N need not be a multiple of 128 (the reference's load requires it,
+//     quantized_weight.cpp:215-217); AutoAWQ/GPTQ packing needs N % 8 == 0.
+#pragma once
+
+#include "minicpmv/tensor.h"
+#include "minicpmv/weights.h"
+
+#include <cstdint>
+#include <string>
+
+namespace minicpmv {
+
+struct W4A16QuantizedWeight {
+    Tensor w_int8;          // UInt8 [packed bytes]: slab-64 nibbles
+    Tensor scales;          // Float16 [K/128, Npad]
+    Tensor zeros;           // Int32 [K/128, Npad/8]: 4-bit zero-points
+    int64_t K{0};
+    int64_t N{0};
+    int64_t group_size{128};
+    int zero_bias{0};       // 0: AutoAWQ / synthetic, 1: GPTQ v1 (stored zero - 1)
+};
+
+struct W8A8QuantizedWeight {
+    Tensor w_int8;          // Int8 [K, N]
+    Tensor w_scale;         // Float16 [N], truncating encode of the fp32 scale
+    Tensor w_scale_f32;     // Float32 [N]
+    int64_t K{0};
+    int64_t N{0};
+};
+
+bool has_w4a16_quantized_weight(const WeightsIndex& index, const std::string& base);
+W4A16QuantizedWeight load_w4a16_quantized_weight(const WeightsIndex& index, const std::string& base);
+W8A8QuantizedWeight quantize_dense_weight_w8a8(const Tensor& weight_kn);
+
+// Host tensors -> device weight (no device round trip).
+W4A16QuantizedWeight pack_w4a16_awq(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                                    int64_t K, int64_t N);
+W4A16QuantizedWeight pack_w4a16_gptq(const int32_t* qweight, const int32_t* qzeros, const int32_t* g_idx,
+                                     const uint16_t* scales, int64_t K, int64_t N, int64_t groups);
+// Build-defined synthetic int4 quantiser (mcv_w4a16_quantize_host) applied to
+// fp16 [K, N] host weights, then packed.
+W4A16QuantizedWeight quantize_w4a16_synthetic(const uint16_t* w_kn, int64_t K, int64_t N);
+W8A8QuantizedWeight quantize_w8a8_host(const uint16_t* w_kn, int64_t K, int64_t N);
+
+}  // namespace minicpmv

@@ -1,0 +1,192 @@
+// ops.cpp -- host-side validation + launch of the quantized-matmul operators.
+//
+// Validation mirrors the reference's host wrappers (src/csrc/lib/ops.cpp:
+// 437-456, 1030-1210): a mismatch throws std::runtime_error before anything is
+// enqueued.  The launches go through the C-ABI (include/mcv_quant.h).
+#include "minicpmv/ops.h"
+
+#include "mcv_quant.h"
+#include "minicpmv/hip_context.h"
+
+#include <rocblas/rocblas.h>
+
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+
+namespace minicpmv {
+namespace {
+
+void require(bool ok, const std::string& msg) {
+    if (!ok) throw std::runtime_error(msg);
+}
+
+int scale_dtype(const Tensor& t, const char* what) {
+    if (t.dtype() == DType::Float32) return MCV_F32;
+    if (t.dtype() == DType::Float16) return MCV_F16;
+    throw std::runtime_error(std::string(what) + " must be fp16 or fp32");
+}
+
+}  // namespace
+
+void silu_mul(const Tensor& gate, const Tensor& up, Tensor& out, hipStream_t stream) {
+    require(gate.dtype() == DType::Float16 && up.dtype() == DType::Float16 && out.dtype() == DType::Float16,
+            "silu_mul requires fp16 tensors");
+    require(gate.shape() == up.shape() && gate.shape() == out.shape(), "silu_mul shape mismatch");
+    check_mcv(mcv_silu_mul(gate.data(), up.data(), out.data(), static_cast<int64_t>(gate.numel()), stream), "silu_mul");
+}
+
+void argmax_last_dim(const Tensor& self, Tensor& out, hipStream_t stream) {
+    require(!self.shape().empty(), "argmax input must have rank >= 1");
+    require(self.dtype() == DType::Float16, "argmax input must be fp16");
+    require(out.dtype() == DType::Int64, "argmax output must be int64");
+    const int64_t n = self.shape().back();
+    const int64_t rows = n > 0 ? static_cast<int64_t>(self.numel()) / n : 0;
+    require(static_cast<int64_t>(out.numel()) == rows, "argmax output must hold one index per row");
+    check_mcv(mcv_argmax_f16(self.data(), rows, n, static_cast<int64_t*>(out.data()), stream), "argmax_last_dim");
+}
+
+void matmul_w4a16(const Tensor& x, const Tensor& w_int8, const Tensor& scales, Tensor& out, hipStream_t stream) {
+    require(x.dtype() == DType::Float16, "matmul_w4a16 x must be fp16");
+    require(w_int8.dtype() == DType::Int8, "matmul_w4a16 w must be int8 (pre-unpacked from GPTQ)");
+    require(scales.dtype() == DType::Float16, "matmul_w4a16 scales must be fp16");
+    require(out.dtype() == DType::Float16, "matmul_w4a16 out must be fp16");
+    require(x.shape().size() == 2 && x.shape()[0] == 1, "matmul_w4a16 x must be [1, K]");
+    require(scales.shape().size() == 2, "matmul_w4a16 scales must be 2D");
+    require(w_int8.shape().size() == 2, "matmul_w4a16 w must be [packed_rows, tile_len]");
+    const int64_t K = x.shape()[1], N = scales.shape()[1];
+    require(scales.shape() == std::vector<int64_t>{K / 128, N}, "matmul_w4a16 scales must be [K/128, N]");
+    require(out.shape() == std::vector<int64_t>{1, N}, "matmul_w4a16 out must be [1, N]");
+    check_mcv(mcv_w4a16_gemv_tiled_i8(x.data(), K, N, w_int8.shape()[1], w_int8.shape()[0],
+                                      static_cast<const int8_t*>(w_int8.data()), scales.data(), out.data(), stream),
+              "matmul_w4a16");
+}
+
+void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream) {
+    require(x.dtype() == DType::Float16 && out.dtype() == DType::Float16, "matmul_w4a16 x and out must be fp16");
+    require(x.shape().size() == 2 && x.shape()[1] == w.K, "matmul_w4a16 x must be [M, K]");
+    require(out.shape() == std::vector<int64_t>{x.shape()[0], w.N}, "matmul_w4a16 out must be [M, N]");
+    require(w.w_int8.data() && w.scales.data() && w.zeros.data(), "matmul_w4a16 weight is not loaded");
+    check_mcv(mcv_w4a16_gemm(x.data(), x.shape()[0], w.K, w.N, w.w_int8.data(), w.scales.data(), w.zeros.data(),
+                             w.zero_bias, out.data(), stream),
+              "matmul_w4a16");
+}
+
+void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream) {
+    require(x.dtype() == DType::Int8, "matmul_w8a8_i32 x must be int8");
+    require(w_int8.dtype() == DType::Int8, "matmul_w8a8_i32 w must be int8");
+    require(out.dtype() == DType::Int32, "matmul_w8a8_i32 out must be int32");
+    require(x.shape().size() == 2, "matmul_w8a8_i32 x must be [M, K]");
+    require(w_int8.shape().size() == 2 && w_int8.shape()[0] == x.shape()[1], "matmul_w8a8_i32 w must be [K, N]");
+    require(out.shape() == std::vector<int64_t>{x.shape()[0], w_int8.shape()[1]}, "matmul_w8a8_i32 out must be [M, N]");
+    check_mcv(mcv_w8a8_gemm_i32(static_cast<const int8_t*>(x.data()), x.shape()[0], x.shape()[1], w_int8.shape()[1],
+                                static_cast<const int8_t*>(w_int8.data()), MCV_W8_KN, static_cast<int32_t*>(out.data()),
+                                stream),
+              "matmul_w8a8_i32");
+}
+
+void w8a8_quantize(const Tensor& x, Tensor& x_int8, Tensor& x_scale, hipStream_t stream) {
+    require(x.dtype() == DType::Float16, "w8a8_quantize x must be fp16");
+    require(x_int8.dtype() == DType::Int8, "w8a8_quantize x_int8 must be int8");
+    require(x.shape().size() == 2, "w8a8_quantize x must be [M, K]");
+    require(x_int8.shape() == x.shape(), "w8a8_quantize x_int8 must match x shape");
+    const int64_t M = x.shape()[0], K = x.shape()[1];
+    require(static_cast<int64_t>(x_scale.numel()) == M, "w8a8_quantize x_scale must be [M] ([1] for M = 1)");
+    const bool f32 = x_scale.dtype() == DType::Float32;
+    require(f32 || x_scale.dtype() == DType::Float16, "w8a8_quantize x_scale must be fp16 or fp32");
+    check_mcv(mcv_w8a8_quantize_act(x.data(), M, K, static_cast<int8_t*>(x_int8.data()),
+                                    f32 ? static_cast<float*>(x_scale.data()) : nullptr, f32 ? nullptr : x_scale.data(),
+                                    stream),
+              "w8a8_quantize");
+}
+
+void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream) {
+    require(acc.dtype() == DType::Int32 && out.dtype() == DType::Float16, "w8a8_dequant requires int32 acc and fp16 out");
+    require(acc.shape().size() == 2, "w8a8_dequant acc must be [M, N]");
+    const int64_t M = acc.shape()[0], N = acc.shape()[1];
+    require(static_cast<int64_t>(x_scale.numel()) == M, "w8a8_dequant x_scale must be [M]");
+    require(w_scale.shape() == std::vector<int64_t>{N}, "w8a8_dequant w_scale must be [N]");
+    require(out.shape() == acc.shape(), "w8a8_dequant out must be [M, N]");
+    check_mcv(mcv_w8a8_dequant(static_cast<const int32_t*>(acc.data()), x_scale.data(), scale_dtype(x_scale, "x_scale"),
+                               w_scale.data(), scale_dtype(w_scale, "w_scale"), M, N, out.data(), stream),
+              "w8a8_dequant");
+}
+
+void matmul_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8QuantizedWeight& w, Tensor& out,
+                 hipStream_t stream) {
+    require(x_int8.dtype() == DType::Int8 && out.dtype() == DType::Float16, "matmul_w8a8 needs int8 x and fp16 out");
+    require(x_int8.shape().size() == 2 && x_int8.shape()[1] == w.K, "matmul_w8a8 x must be [M, K]");
+    const int64_t M = x_int8.shape()[0];
+    require(out.shape() == std::vector<int64_t>{M, w.N}, "matmul_w8a8 out must be [M, N]");
+    require(static_cast<int64_t>(x_scale.numel()) == M, "matmul_w8a8 x_scale must be [M]");
+    const int xs = scale_dtype(x_scale, "x_scale");
+    const Tensor& ws = (xs == MCV_F32 && w.w_scale_f32.data() != nullptr) ? w.w_scale_f32 : w.w_scale;
+    check_mcv(mcv_w8a8_gemm_f16(static_cast<const int8_t*>(x_int8.data()), x_scale.data(), xs, M, w.K, w.N,
+                                static_cast<const int8_t*>(w.w_int8.data()), MCV_W8_KN, ws.data(),
+                                scale_dtype(ws, "w_scale"), out.data(), stream),
+              "matmul_w8a8");
+}
+
+void w4a16_dequant(const W4A16QuantizedWeight& w, Tensor* w_f16, Tensor* w_i8, hipStream_t stream) {
+    const std::vector<int64_t> kn{w.K, w.N};
+    if (w_f16) require(w_f16->dtype() == DType::Float16 && w_f16->shape() == kn, "w4a16_dequant f16 out must be [K, N]");
+    if (w_i8) require(w_i8->dtype() == DType::Int8 && w_i8->shape() == kn, "w4a16_dequant i8 out must be [K, N]");
+    check_mcv(mcv_w4a16_dequant(w.w_int8.data(), w.scales.data(), w.zeros.data(), w.zero_bias, w.K, w.N,
+                                w_f16 ? w_f16->data() : nullptr, w_i8 ? static_cast<int8_t*>(w_i8->data()) : nullptr,
+                                stream),
+              "w4a16_dequant");
+}
+
+void rms_norm(const Tensor& x, const Tensor& gamma, Tensor& out, double epsilon, hipStream_t stream) {
+    require(x.dtype() == DType::Float16 && gamma.dtype() == DType::Float16 && out.dtype() == DType::Float16,
+            "rms_norm requires fp16 tensors");
+    require(!x.shape().empty() && out.shape() == x.shape(), "rms_norm out must match x");
+    const int64_t H = x.shape().back();
+    require(gamma.shape() == std::vector<int64_t>{H}, "rms_norm gamma must be [H]");
+    check_mcv(mcv_rms_norm(x.data(), gamma.data(), static_cast<int64_t>(x.numel()) / H, H, epsilon, out.data(), stream),
+              "rms_norm");
+}
+
+// Row-major out[M, N] = a[M, K] . B.  In rocBLAS's column-major terms that is
+// out^T (N x M) = B^T (N x K) . a^T (K x M): B stored [K, N] row-major is a
+// column-major N x K matrix (no transpose), B stored [N, K] needs one.
+void matmul_b_transposed(const Tensor& a, const Tensor& b, Tensor& out, hipStream_t stream) {
+    require(a.shape().size() == 2 && b.shape().size() == 2 && out.shape().size() == 2, "matmul tensors must be 2D");
+    require(a.dtype() == DType::Float16 && b.dtype() == DType::Float16 && out.dtype() == DType::Float16,
+            "matmul_b_transposed requires fp16 tensors");
+    const int64_t M = a.shape()[0], K = a.shape()[1], N = out.shape()[1];
+    require(out.shape()[0] == M, "matmul out rows mismatch");
+    bool kn;
+    if (b.shape() == std::vector<int64_t>{N, K}) kn = false;
+    else if (b.shape() == std::vector<int64_t>{K, N}) kn = true;
+    else throw std::runtime_error("matmul_b_transposed weight must be [N, K] or [K, N]");
+    static std::mutex mu;
+    static std::unordered_map<int, rocblas_handle> handles;
+    rocblas_handle h;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        int dev = 0;
+        check_hip(hipGetDevice(&dev), "hipGetDevice");
+        auto it = handles.find(dev);
+        if (it == handles.end()) {
+            rocblas_handle nh;
+            if (rocblas_create_handle(&nh) != rocblas_status_success) throw std::runtime_error("rocblas_create_handle failed");
+            it = handles.emplace(dev, nh).first;
+        }
+        h = it->second;
+        if (rocblas_set_stream(h, stream) != rocblas_status_success) throw std::runtime_error("rocblas_set_stream failed");
+        const float alpha = 1.0f, beta = 0.0f;
+        const rocblas_status st = rocblas_gemm_ex(
+            h, kn ? rocblas_operation_none : rocblas_operation_transpose, rocblas_operation_none,
+            static_cast<rocblas_int>(N), static_cast<rocblas_int>(M), static_cast<rocblas_int>(K), &alpha, b.data(),
+            rocblas_datatype_f16_r, static_cast<rocblas_int>(kn ? N : K), a.data(), rocblas_datatype_f16_r,
+            static_cast<rocblas_int>(K), &beta, out.data(), rocblas_datatype_f16_r, static_cast<rocblas_int>(N),
+            out.data(), rocblas_datatype_f16_r, static_cast<rocblas_int>(N), rocblas_datatype_f32_r,
+            rocblas_gemm_algo_standard, 0, 0);
+        if (st != rocblas_status_success)
+            throw std::runtime_error("rocblas_gemm_ex failed with status " + std::to_string(static_cast<int>(st)));
+    }
+}
+
+}  // namespace minicpmv

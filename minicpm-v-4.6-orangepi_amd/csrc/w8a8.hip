@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void w8a8_quant_act_kernel(const uint16_t* __r
         qr[k] = static_cast<int8_t>(static_cast<int>(r));
     }
     if (threadIdx.x == 0) {
-        s32[row] = scale;
+        if (s32) s32[row] = scale;
         if (s16) s16[row] = f2h(scale);
     }
 }
@@ -249,7 +249,7 @@ using namespace mcv;
 extern "C" {
 
 int mcv_w8a8_quantize_act(const void* x, int64_t M, int64_t K, int8_t* xq, float* s32, void* s16, mcv_stream_t stream) {
-    if (!x || !xq || !s32) return fail(MCV_ERR_INVALID_ARG, "w8a8_quantize: null pointer");
+    if (!x || !xq || (!s32 && !s16)) return fail(MCV_ERR_INVALID_ARG, "w8a8_quantize: null pointer");
     if (M <= 0 || K <= 0 || M > 0x7fffffff || K > 0x7fffffff)
         return fail(MCV_ERR_SHAPE, "w8a8_quantize: bad shape M=%lld K=%lld", (long long)M, (long long)K);
     int rc = require_device();

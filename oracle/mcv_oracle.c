@@ -420,3 +420,19 @@ int64_t or_argmax_f16(const uint16_t* logits, int64_t n) {
     }
     return best;
 }
+
+/* RMSNorm before the vocabulary projection: lm_head_greedy calls rms_norm
+ * (src/csrc/lib/language_model.cpp:424 -> ops.cpp rms_norm -> aclnnRmsNorm, a
+ * CANN builtin whose internal rounding is not vendored).  Restated from the
+ * definition: y = x / sqrt(mean(x^2) + eps) * gamma, fp32 with a sequential sum. */
+void or_rms_norm(const uint16_t* x, const uint16_t* gamma, int64_t M, int64_t H, float eps, uint16_t* out) {
+    for (int64_t m = 0; m < M; ++m) {
+        float ss = 0.0f;
+        for (int64_t i = 0; i < H; ++i) {
+            float v = or_h2f(x[m * H + i]);
+            ss += v * v;
+        }
+        float rstd = 1.0f / sqrtf(ss / (float)H + eps);
+        for (int64_t i = 0; i < H; ++i) out[m * H + i] = or_f2h_rne((or_h2f(x[m * H + i]) * rstd) * or_h2f(gamma[i]));
+    }
+}

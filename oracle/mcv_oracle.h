@@ -29,6 +29,9 @@
  *   or_silu_mul -- float64 silu rounded to fp16, within 1 fp16 ulp.
  *   or_argmax_f16 -- numpy argmax (first maximum) over the flushed values and the
  *       reference's modular-pattern lm_head test (tests/test_lm_head_pipeline.cpp).
+ *   or_rms_norm -- float64 numpy RMSNorm rounded to fp16, within 1 fp16 ulp.
+ *       The reference computes it with a CANN builtin (aclnnRmsNorm, not vendored):
+ *       its rounding is parity unpinned; the formula is the definition.
  */
 #ifndef MCV_ORACLE_H
 #define MCV_ORACLE_H
@@ -77,6 +80,7 @@ void or_w8a8_dequant(const int32_t* acc, const float* x_scale, const float* w_sc
 /* elementwise and argmax */
 void or_silu_mul(const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* out);
 int64_t or_argmax_f16(const uint16_t* logits, int64_t n);
+void or_rms_norm(const uint16_t* x, const uint16_t* gamma, int64_t M, int64_t H, float eps, uint16_t* out);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,135 @@
+// Loader: AutoAWQ and GPTQ checkpoints written to a safetensors file load
+// through load_w4a16_quantized_weight (GPTQ chosen by the presence of g_idx,
+// quantized_weight.cpp:212-214), and the loaded weight multiplies like the CPU
+// reference formula on the unpacked (q - z).  Also checks the dequantised
+// int8 values bit for bit against a host unpack.
+#include "minicpmv/hip_context.h"
+#include "minicpmv/ops.h"
+#include "minicpmv/quantized_weight.h"
+#include "test_common.h"
+
+#include <cmath>
+#include <random>
+
+using namespace minicpmv;
+
+static int check(HipContext& ctx, const W4A16QuantizedWeight& w, const std::vector<int8_t>& w8,
+                 const std::vector<uint16_t>& scales, const char* what) {
+    const int64_t K = w.K, N = w.N;
+    std::mt19937 rng(7);
+    std::normal_distribution<float> nd(0.f, 1.f);
+    std::vector<uint16_t> hx(static_cast<size_t>(K));
+    for (auto& v : hx) v = t::f2h_rne(nd(rng));
+    Tensor x({1, K}, DType::Float16);
+    x.copy_from_host(hx.data(), hx.size() * 2);
+    Tensor out({1, N}, DType::Float16);
+    out.allocate();
+    matmul_w4a16(x, w, out, ctx.stream());
+    std::vector<uint16_t> ho(static_cast<size_t>(N));
+    out.copy_to_host(ho.data(), ho.size() * 2);
+    double num = 0, den = 0, max_abs = 0;
+    for (int64_t n = 0; n < N; ++n) {
+        float ref = 0.f;
+        for (int64_t g = 0; g < K / 128; ++g) {
+            float part = 0.f;
+            for (int64_t kk = 0; kk < 128; ++kk) part += t::h2f(hx[g * 128 + kk]) * static_cast<float>(w8[(g * 128 + kk) * N + n]);
+            ref += part * t::h2f(scales[g * N + n]);
+        }
+        const double d = std::fabs(ref - t::h2f(ho[n]));
+        max_abs = std::max(max_abs, d);
+        num += d * d;
+        den += double(ref) * ref;
+    }
+    Tensor wi8({K, N}, DType::Int8);
+    wi8.allocate();
+    w4a16_dequant(w, nullptr, &wi8, ctx.stream());
+    std::vector<int8_t> hw8(static_cast<size_t>(K * N));
+    wi8.copy_to_host(hw8.data(), hw8.size());
+    const bool exact = hw8 == w8;
+    std::printf("%s K=%lld N=%lld max_abs=%.2e rel_l2=%.2e dequant_exact=%d\n", what, (long long)K, (long long)N, max_abs,
+                std::sqrt(num / den), int(exact));
+    return (max_abs <= 2e-2 && std::sqrt(num / den) <= 1e-3 && exact) ? 0 : 1;
+}
+
+int main(int argc, char** argv) {
+    HipContext ctx(0);
+    const std::string dir = argc > 1 ? argv[1] : "/tmp";
+    constexpr int64_t K = 512, N = 200, G = K / 128;
+    constexpr int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    std::mt19937 rng(3);
+    std::uniform_int_distribution<int> nib(0, 15);
+    std::uniform_real_distribution<float> sd(0.001f, 0.01f);
+    std::vector<uint8_t> q(static_cast<size_t>(K * N)), z(static_cast<size_t>(G * N));
+    for (auto& v : q) v = static_cast<uint8_t>(nib(rng));
+    for (auto& v : z) v = static_cast<uint8_t>(nib(rng));
+    std::vector<uint16_t> scales(static_cast<size_t>(G * N));
+    for (auto& v : scales) v = t::f2h_rne(sd(rng));
+    int rc = 0;
+
+    // AutoAWQ: qweight [K, N/8], qzeros [G, N/8], column order within a word
+    std::vector<int32_t> aq(static_cast<size_t>(K * N / 8)), az(static_cast<size_t>(G * N / 8));
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t j = 0; j < N / 8; ++j) {
+            uint32_t w = 0;
+            for (int s = 0; s < 8; ++s) w |= uint32_t(q[k * N + j * 8 + order[s]]) << (4 * s);
+            aq[k * (N / 8) + j] = static_cast<int32_t>(w);
+        }
+    for (int64_t g = 0; g < G; ++g)
+        for (int64_t j = 0; j < N / 8; ++j) {
+            uint32_t w = 0;
+            for (int s = 0; s < 8; ++s) w |= uint32_t(z[g * N + j * 8 + order[s]]) << (4 * s);
+            az[g * (N / 8) + j] = static_cast<int32_t>(w);
+        }
+    std::vector<int8_t> w8(static_cast<size_t>(K * N));
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) w8[k * N + n] = static_cast<int8_t>(int(q[k * N + n]) - int(z[(k / 128) * N + n]));
+    const std::string pa = dir + "/mcv_awq.safetensors";
+    t::write_safetensors(pa, {{"m.proj.qweight", "I32", {K, N / 8}, t::bytes_of(aq)},
+                              {"m.proj.qzeros", "I32", {G, N / 8}, t::bytes_of(az)},
+                              {"m.proj.scales", "F16", {G, N}, t::bytes_of(scales)}});
+    WeightsIndex ia(pa);
+    if (!has_w4a16_quantized_weight(ia, "m.proj") || has_w4a16_quantized_weight(ia, "m.other")) rc = 1;
+    rc |= check(ctx, load_w4a16_quantized_weight(ia, "m.proj"), w8, scales, "AWQ");
+
+    // GPTQ v1: qweight [K/8, N] along K, qzeros [G, N/8] natural order storing zero - 1
+    std::vector<int32_t> gq(static_cast<size_t>(K / 8 * N)), gz(static_cast<size_t>(G * N / 8));
+    for (int64_t k0 = 0; k0 < K / 8; ++k0)
+        for (int64_t n = 0; n < N; ++n) {
+            uint32_t w = 0;
+            for (int i = 0; i < 8; ++i) w |= uint32_t(q[(k0 * 8 + i) * N + n]) << (4 * i);
+            gq[k0 * N + n] = static_cast<int32_t>(w);
+        }
+    for (int64_t g = 0; g < G; ++g)
+        for (int64_t j = 0; j < N / 8; ++j) {
+            uint32_t w = 0;
+            for (int s = 0; s < 8; ++s) w |= uint32_t(z[g * N + j * 8 + s] & 15u) << (4 * s);
+            gz[g * (N / 8) + j] = static_cast<int32_t>(w);
+        }
+    std::vector<int8_t> w8g(static_cast<size_t>(K * N));
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) w8g[k * N + n] = static_cast<int8_t>(int(q[k * N + n]) - (int(z[(k / 128) * N + n]) + 1));
+    std::vector<int32_t> gidx(static_cast<size_t>(K));
+    for (int64_t k = 0; k < K; ++k) gidx[k] = static_cast<int32_t>(k / 128);
+    const std::string pg = dir + "/mcv_gptq.safetensors";
+    t::write_safetensors(pg, {{"m.proj.qweight", "I32", {K / 8, N}, t::bytes_of(gq)},
+                              {"m.proj.qzeros", "I32", {G, N / 8}, t::bytes_of(gz)},
+                              {"m.proj.g_idx", "I32", {K}, t::bytes_of(gidx)},
+                              {"m.proj.scales", "F16", {G, N}, t::bytes_of(scales)}});
+    WeightsIndex ig(pg);
+    rc |= check(ctx, load_w4a16_quantized_weight(ig, "m.proj"), w8g, scales, "GPTQ");
+
+    // act-order g_idx is refused with a clear message
+    std::swap(gidx[0], gidx[K - 1]);
+    t::write_safetensors(pg, {{"m.proj.qweight", "I32", {K / 8, N}, t::bytes_of(gq)},
+                              {"m.proj.qzeros", "I32", {G, N / 8}, t::bytes_of(gz)},
+                              {"m.proj.g_idx", "I32", {K}, t::bytes_of(gidx)},
+                              {"m.proj.scales", "F16", {G, N}, t::bytes_of(scales)}});
+    try {
+        WeightsIndex ig2(pg);
+        (void)load_w4a16_quantized_weight(ig2, "m.proj");
+        rc = 1;
+    } catch (const std::runtime_error& e) {
+        std::printf("act-order refused: %s\n", e.what());
+    }
+    return rc;
+}

@@ -71,6 +71,7 @@ class Oracle:
             "or_w8a8_dequant": (None, [vp, vp, vp, _i64, _i64, vp]),
             "or_silu_mul": (None, [vp, vp, _i64, vp]),
             "or_argmax_f16": (_i64, [vp, _i64]),
+            "or_rms_norm": (None, [vp, vp, _i64, _i64, ctypes.c_float, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -196,6 +197,15 @@ class Oracle:
     def argmax_f16(self, logits_u16):
         x = np.ascontiguousarray(logits_u16, np.uint16)
         return int(self.L.or_argmax_f16(self._p(x), x.size))
+
+
+    def rms_norm(self, x_u16, gamma_u16, eps):
+        x = np.ascontiguousarray(x_u16, np.uint16)
+        g = np.ascontiguousarray(gamma_u16, np.uint16)
+        M, H = x.shape
+        out = np.empty((M, H), np.uint16)
+        self.L.or_rms_norm(self._p(x), self._p(g), M, H, float(eps), self._p(out))
+        return out
 
 
 _ORACLE = None

@@ -78,3 +78,16 @@ def test_reference_lm_head_pipeline_patterns(oracle):
             assert oracle.argmax_f16(logits16) == best
     ref64 = [int(np.argmax(hf[n].astype(np.float64) @ wf.astype(np.float64))) for n in range(N)]
     assert tokens == ref64
+
+
+def test_rms_norm_vs_float64(oracle):
+    rng = np.random.default_rng(16)
+    x = f16_normal(rng, (4, 1024), 1.0)
+    x[2] = 0
+    g = f16_normal(rng, 1024, 0.5)
+    got = oracle.rms_norm(x, g, 1e-6).view(np.float16).astype(np.float64)
+    xf = x.view(np.float16).astype(np.float64)
+    ref = (xf / np.sqrt((xf ** 2).mean(axis=1, keepdims=True) + 1e-6) * g.view(np.float16).astype(np.float64)).astype(np.float16)
+    ulp = np.abs(np.spacing(ref)).astype(np.float64)
+    assert (np.abs(got - ref.astype(np.float64)) <= ulp + 1e-12).all()
+    assert (got[2] == 0).all()
