@@ -3,7 +3,8 @@
 Default workload (one JSON line on stdout): BASELINE config 3, the W4A16
 lm_head -- M=1, K=1024, V=248094 -- as one GEMV launch per step with the
 argmax folded into it, with 8 distinct weight copies (1.06 GB) rotated so no
-step hits the 256 MB MALL.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
+step hits the 256 MB MALL.  Steps are replayed from captured HIP graphs, so
+back-to-back kernels are not gated by the host's launch rate.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
 (132,484,244 B per step, inputs resident in HBM).  `--workload` selects the
 other BASELINE configs (gemv1, mlp, lm_head, prefill, w8a8).
 
@@ -46,35 +47,64 @@ def to_dev_f16(a_u16):
     return torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16)).cuda().view(torch.float16)
 
 
+GRAPH_CHUNK = 100     # launches per captured graph
+
+
+def _capture(launch, first, count, n_sets):
+    """A HIP graph holding `count` launches (weight sets rotating from
+    `first`), captured on a side stream; replayed, the kernels run back to back
+    with no host launch cost between them."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(count):
+                launch((first + i) % n_sets)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    return g
+
+
 def time_steps(launch, n_sets, steps, warmup):
-    """Back-to-back steps on the current stream, bracketed by one event pair
-    (plus a synchronize on both sides).  Returns total ms over `steps`."""
+    """`steps` back-to-back steps replayed from HIP graphs on torch's current
+    stream, bracketed by one event pair (and a synchronize on both sides).
+    The warmup steps run eagerly first, then once more as a graph replay.
+    Returns (total ms over `steps`, per-step ms of every graph chunk)."""
     import torch
     for i in range(warmup):
         launch(i % n_sets)
     torch.cuda.synchronize()
+    chunks = []
+    done = 0
+    while done < steps:
+        n = min(GRAPH_CHUNK, steps - done)
+        chunks.append((n, _capture(launch, warmup + done, n, n_sets)))
+        done += n
+    chunks[0][1].replay()                      # graph warmup
+    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chunks]
     t0.record()
-    for i in range(steps):
-        launch((warmup + i) % n_sets)
+    for (n, g), (a, b) in zip(chunks, ev):
+        a.record()
+        g.replay()
+        b.record()
     t1.record()
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1)
+    per_chunk = [a.elapsed_time(b) / n for (n, _), (a, b) in zip(chunks, ev)]
+    return t0.elapsed_time(t1), per_chunk
 
 
 def time_each_launch(launch, n_sets, steps):
-    """HIP events around every launch of the dominant kernel, on the stream it
-    is launched on (torch's current stream).  Returns per-launch ms."""
-    import torch
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    torch.cuda.synchronize()
-    for i in range(steps):
-        ev[i][0].record()
-        launch(i % n_sets)
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in ev]
+    """Average duration of the dominant kernel: `steps` launches of it alone,
+    replayed back to back from HIP graphs between HIP events recorded on the
+    stream they run on (torch's current stream).  Returns per-launch ms, one
+    value per graph chunk."""
+    _, per = time_steps(launch, n_sets, steps, 2)
+    return per
 
 
 def traffic_from_profiles(workload: str):
@@ -154,15 +184,16 @@ def wl_lm_head(pkg, args):
     xd = to_dev_f16(x)
     logits = torch.empty(V, dtype=torch.float16, device="cuda")
     nbytes = K * V // 2 + (K // 128) * V * 2 + (K // 128) * V // 2 + 2 * V + 2 * K
-    total_ms = time_steps(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
+    # one step = one launch of the fused GEMV + argmax kernel, so the step
+    # timing is also the dominant kernel's average launch duration
+    total_ms, kms = time_steps(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
     token = int(heads[0].token.item())
-    kms = time_each_launch(lambda i: heads[i].launch_partials(xd, logits), copies, args.steps)
     res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                config={"workload": "w4a16_lm_head_gemv_argmax", "M": 1, "K": K, "V": V,
                        "weight_copies_rotated": copies, "rotated_bytes": copies * (qw.nbytes + sc.nbytes + zr.nbytes),
                        "algorithmic_bytes_per_step": nbytes, "token": token},
                dtype="w4a16 (f16 x int4, f32 accumulate)",
-               kernel="w4a16_gemv_kernel<8,1,2> (fused argmax); roofline timed on its <8,1,1> partials twin")
+               kernel="w4a16_gemv_kernel<8,1,2> (GEMV + fused argmax)")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes)
     return res
@@ -182,7 +213,7 @@ def wl_gemv1(pkg, args):
     xd = to_dev_f16(x)
     out = torch.empty((1, N), dtype=torch.float16, device="cuda")
     nbytes = w4a16_bytes(K, N) + 2 * K + 2 * N
-    total_ms = time_steps(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps, args.warmup)
+    total_ms, _ = time_steps(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps, args.warmup)
     kms = time_each_launch(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps)
     res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                config={"workload": "w4a16_gemv_1024x1024", "M": 1, "K": K, "N": N, "weight_sets_rotated": sets},
@@ -229,7 +260,7 @@ def wl_mlp(pkg, args):
         pkg.matmul_w4a16(a, L[2], y)
 
     nbytes = 2 * w4a16_bytes(H, I) + w4a16_bytes(I, H) + 2 * H * 2 + 2 * I * 2 * 3 + 2 * H
-    total_ms = time_steps(block, len(sets), args.steps, args.warmup)
+    total_ms, _ = time_steps(block, len(sets), args.steps, args.warmup)
     kms = time_each_launch(block, len(sets), args.steps)
     return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                 config={"workload": "w4a16_mlp_block_decode", "M": 1, "hidden": H, "intermediate": I,
@@ -246,7 +277,7 @@ def wl_prefill(pkg, args):
     x = to_dev_f16(f16_normal(rng, (M, K), 1.0))
     out = torch.empty((M, N), dtype=torch.float16, device="cuda")
     flops = 2.0 * M * K * N
-    total_ms = time_steps(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps, args.warmup)
+    total_ms, _ = time_steps(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps, args.warmup)
     kms = time_each_launch(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps)
     return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TFLOP/s", bound="mfma",
                 config={"workload": "w4a16_prefill_gemm", "M": M, "K": K, "N": N},
@@ -261,7 +292,7 @@ def wl_w8a8(pkg, args):
     xq, xs, _ = pkg.w8a8_quantize(to_dev_f16(f16_normal(rng, (M, K), 1.0)))
     out = torch.empty((M, N), dtype=torch.float16, device="cuda")
     flops = 2.0 * M * K * N
-    total_ms = time_steps(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps, args.warmup)
+    total_ms, _ = time_steps(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps, args.warmup)
     kms = time_each_launch(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps)
     return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TOP/s", bound="mfma",
                 config={"workload": "w8a8_gemm_fused", "M": M, "K": K, "N": N},
@@ -275,7 +306,7 @@ def wl_copy(pkg, args):
     n = 128 * 2**20
     src = [torch.ones(n, dtype=torch.uint8, device="cuda") for _ in range(4)]
     dst = torch.empty(n, dtype=torch.uint8, device="cuda")
-    total_ms = time_steps(lambda i: dst.copy_(src[i]), 4, args.steps, args.warmup)
+    total_ms, _ = time_steps(lambda i: dst.copy_(src[i]), 4, args.steps, args.warmup)
     kms = time_each_launch(lambda i: dst.copy_(src[i]), 4, args.steps)
     return dict(bytes=2 * n, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                 config={"workload": "copy_128MiB_calibration", "bytes_read": n, "bytes_written": n},

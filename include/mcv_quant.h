@@ -33,6 +33,15 @@
  *   Zeros: uint32 [K/128][Npad/8], nibble s of word j holding column 8j + s.
  *   Effective zero = nibble + zero_bias (0 for AWQ/synthetic, 1 for GPTQ v1).
  *   Dequantised value w[k][n] = (q - (z + zero_bias)) * s[k/128][n].
+ *
+ * W8A8 weight layout MCV_W8_TILED
+ *   A K x N int8 weight is padded with zeros to Np = 64 * ceil(N / 64)
+ *   columns and Kp = 128 * ceil(K / 128) rows and stored as 1 KiB operand
+ *   lines of 32 columns x 32 k: byte offset of w[k][n] =
+ *     ((((n / 64) * (Kp / 32) + k / 32) * 2 + (n % 64) / 32) * 64 + l) * 16 + (k % 16),
+ *   l = (n % 32) + 32 * ((k % 32) / 16): the operand order of
+ *   v_mfma_i32_32x32x32_i8, so a wave loads each operand with one coalesced
+ *   128-bit load.  Size: mcv_w8a8_tiled_bytes(K, N) = Np * Kp.
  */
 #ifndef MCV_QUANT_H
 #define MCV_QUANT_H
@@ -56,7 +65,11 @@ enum mcv_status {
 };
 
 enum mcv_dtype { MCV_F32 = 0, MCV_F16 = 1 };
-enum mcv_w8_layout { MCV_W8_KN = 0 /* [K][N], the reference's layout */, MCV_W8_NK = 1 /* [N][K] */ };
+enum mcv_w8_layout {
+    MCV_W8_KN = 0,    /* [K][N] row-major, the reference's layout */
+    MCV_W8_NK = 1,    /* [N][K] row-major */
+    MCV_W8_TILED = 2  /* MFMA operand tiles, see below */
+};
 
 #define MCV_W4_GROUP 128
 #define MCV_W4_LAYOUT_SLAB64 1
@@ -191,7 +204,9 @@ int mcv_w8a8_quantize_act(const void* x_dev, int64_t M, int64_t K, int8_t* xq_de
 
 /* acc[M][N] int32 = xq[M][K] . W exactly.  W is int8 in layout w_layout.
  * Replaces matmul_w8a8_i32 (src/csrc/lib/ops.cpp:1097-1133, kernel
- * op_kernel/matmul_w8a8_i32_custom.cpp:15-48), which accepts M = 1 only. */
+ * op_kernel/matmul_w8a8_i32_custom.cpp:15-48), which accepts M = 1 only.
+ * MCV_W8_TILED runs the operand-line GEMM (M > 4) or GEMV (M <= 4); the
+ * KN / NK layouts a slower kernel that transposes through LDS. */
 int mcv_w8a8_gemm_i32(const int8_t* xq_dev, int64_t M, int64_t K, int64_t N,
                       const int8_t* w_dev, int w_layout, int32_t* acc_dev, mcv_stream_t stream);
 
@@ -211,9 +226,17 @@ int mcv_w8a8_gemm_f16(const int8_t* xq_dev, const void* x_scale_dev, int x_scale
                       const void* w_scale_dev, int w_scale_dtype, void* out_dev,
                       mcv_stream_t stream);
 
+/* Bytes of a K x N weight in MCV_W8_TILED (0 on bad shape). */
+int64_t mcv_w8a8_tiled_bytes(int64_t K, int64_t N);
+
+/* Re-lays an int8 [K][N] weight (the reference's w_int8 layout) into
+ * MCV_W8_TILED on the host; tiled_host holds mcv_w8a8_tiled_bytes(K, N). */
+int mcv_w8a8_pack_tiled_host(const int8_t* q_kn_host, int64_t K, int64_t N, int8_t* tiled_host);
+
 /* Host-side per-output-channel weight quantiser: replaces
  * quantize_dense_weight_w8a8 (src/csrc/lib/quantized_weight.cpp:231-268) minus
- * its device round trip.  w_kn_host fp16 [K][N]; q_host int8 in out_layout;
+ * its device round trip.  w_kn_host fp16 [K][N]; q_host int8 in out_layout
+ * (MCV_W8_TILED: mcv_w8a8_tiled_bytes(K, N) bytes);
  * scale_f32_host [N]; scale_f16_host [N] (truncating encode, :253), may be NULL. */
 int mcv_w8a8_quantize_weight_host(const uint16_t* w_kn_host, int64_t K, int64_t N,
                                   int8_t* q_host, int out_layout, float* scale_f32_host,

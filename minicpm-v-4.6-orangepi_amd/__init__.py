@@ -26,7 +26,7 @@ GROUP = 128
 SLAB = 64
 
 MCV_F32, MCV_F16 = 0, 1
-W8_KN, W8_NK = 0, 1
+W8_KN, W8_NK, W8_TILED = 0, 1, 2
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -64,6 +64,8 @@ _SIGS = {
     "mcv_w8a8_dequant": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),
     "mcv_w8a8_gemm_f16": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
+    "mcv_w8a8_tiled_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "mcv_w8a8_pack_tiled_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
     "mcv_argmax_f16": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp]),
     "mcv_rms_norm": (_c_int, [_vp, _vp, _c_i64, _c_i64, ctypes.c_double, _vp, _vp]),
@@ -163,11 +165,27 @@ def quantize_int4(w_kn_f16: np.ndarray, nthreads: int = 0):
     return qweight, qzeros, scales
 
 
+def w8a8_tiled_bytes(K: int, N: int) -> int:
+    return lib().mcv_w8a8_tiled_bytes(K, N)
+
+
+def pack_w8a8_tiled(q_kn: np.ndarray) -> np.ndarray:
+    """int8 [K, N] (the reference's w_int8 layout) -> MCV_W8_TILED bytes."""
+    q_kn = np.ascontiguousarray(q_kn, np.int8)
+    K, N = q_kn.shape
+    out = np.empty(w8a8_tiled_bytes(K, N), np.int8)
+    _check(lib().mcv_w8a8_pack_tiled_host(_np_ptr(q_kn), K, N, _np_ptr(out)), "mcv_w8a8_pack_tiled_host")
+    return out
+
+
 def quantize_w8a8_weight_host(w_kn_f16: np.ndarray, layout: int = W8_KN):
     """Per-channel int8 weight quantiser (quantized_weight.cpp:231-268) -> (q, scale f32 [N], scale f16 bits [N])."""
     w = np.ascontiguousarray(w_kn_f16).view(np.uint16)
     K, N = w.shape
-    q = np.empty((K, N) if layout == W8_KN else (N, K), np.int8)
+    if layout == W8_TILED:
+        q = np.empty(w8a8_tiled_bytes(K, N), np.int8)
+    else:
+        q = np.empty((K, N) if layout == W8_KN else (N, K), np.int8)
     s32 = np.empty(N, np.float32)
     s16 = np.empty(N, np.uint16)
     _check(lib().mcv_w8a8_quantize_weight_host(_np_ptr(w), K, N, _np_ptr(q), layout, _np_ptr(s32), _np_ptr(s16)),
@@ -352,15 +370,15 @@ class LmHeadW4A16:
 class W8A8QuantizedWeight:
     """Mirrors W8A8QuantizedWeight (quantized_weight.h:19-24) plus the fp32 scale."""
 
-    w_int8: "object"       # torch.int8, [K, N] (W8_KN) or [N, K] (W8_NK)
+    w_int8: "object"       # torch.int8, [K, N] (W8_KN), [N, K] (W8_NK) or flat MFMA tiles (W8_TILED)
     w_scale: "object"      # torch.float16 [N] (truncating encode, the reference's stored form)
     w_scale_f32: "object"  # torch.float32 [N]
     K: int
     N: int
-    layout: int = W8_KN
+    layout: int = W8_TILED
 
 
-def quantize_dense_weight_w8a8(weight_kn, layout: int = W8_KN) -> W8A8QuantizedWeight:
+def quantize_dense_weight_w8a8(weight_kn, layout: int = W8_TILED) -> W8A8QuantizedWeight:
     """quantized_weight.cpp:231-268 without the device round trip: fp16 [K, N] -> int8 + scales."""
     torch = _torch()
     w_np = weight_kn.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16) \
@@ -389,11 +407,18 @@ def w8a8_quantize(x, x_int8=None, x_scale=None, x_scale_f16=None, stream=None):
     return x_int8, x_scale, x_scale_f16
 
 
-def matmul_w8a8_i32(x_int8, w_int8, out=None, layout: int = W8_KN, stream=None):
-    """acc[M, N] int32 = x_int8 . w (ops.cpp:1097-1133 generalised to M rows)."""
+def matmul_w8a8_i32(x_int8, w_int8, out=None, layout: int = W8_KN, stream=None, N: int = 0):
+    """acc[M, N] int32 = x_int8 . w (ops.cpp:1097-1133 generalised to M rows).
+    `w_int8` may also be a W8A8QuantizedWeight (its layout and N are used)."""
     torch = _torch()
     M, K = x_int8.shape
-    N = w_int8.shape[1] if layout == W8_KN else w_int8.shape[0]
+    if isinstance(w_int8, W8A8QuantizedWeight):
+        layout, N, w_int8 = w_int8.layout, w_int8.N, w_int8.w_int8
+    elif layout == W8_TILED:
+        if N <= 0:
+            raise McvError("matmul_w8a8_i32: N is required for a tiled weight tensor")
+    else:
+        N = w_int8.shape[1] if layout == W8_KN else w_int8.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=torch.int32, device=x_int8.device)
     _check(lib().mcv_w8a8_gemm_i32(_dev(x_int8), M, K, N, _dev(w_int8), layout, _dev(out), _stream(stream)),

@@ -36,6 +36,9 @@ void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, h
 
 // int32 out [M, N] = int8 x [M, K] . int8 w [K, N], exact.
 void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream);
+// The same over a quantized weight object, in whatever layout it holds
+// (MCV_W8_TILED: operand-line GEMM / GEMV kernels).
+void matmul_w8a8_i32(const Tensor& x, const W8A8QuantizedWeight& w, Tensor& out, hipStream_t stream);
 
 // Per-row symmetric int8 quantisation of fp16 x [M, K]; x_scale is [M]
 // (or [1] for M = 1, as the reference) in fp16 or fp32.

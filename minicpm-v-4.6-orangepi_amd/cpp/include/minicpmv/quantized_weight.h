@@ -7,11 +7,14 @@
 //     int8 (q - z): `w_int8` holds those packed bytes, and the zero-points
 //     travel as `zeros` (+ `zero_bias`) rather than being folded in.
 //   - W8A8QuantizedWeight also keeps the fp32 per-channel scale; `w_scale` is
-//     the reference's truncated fp16 copy (quantized_weight.cpp:253).
+//     the reference's truncated fp16 copy (quantized_weight.cpp:253).  Its
+//     `w_int8` is stored in `layout`: MCV_W8_TILED (MFMA operand lines, what
+//     quantize_dense_weight_w8a8 produces) or the reference's [K, N].
 //   - N need not be a multiple of 128 (the reference's load requires it,
 //     quantized_weight.cpp:215-217); AutoAWQ/GPTQ packing needs N % 8 == 0.
 #pragma once
 
+#include "mcv_quant.h"
 #include "minicpmv/tensor.h"
 #include "minicpmv/weights.h"
 
@@ -31,11 +34,12 @@ struct W4A16QuantizedWeight {
 };
 
 struct W8A8QuantizedWeight {
-    Tensor w_int8;          // Int8 [K, N]
+    Tensor w_int8;          // Int8: [K, N] (MCV_W8_KN) or flat MCV_W8_TILED bytes
     Tensor w_scale;         // Float16 [N], truncating encode of the fp32 scale
     Tensor w_scale_f32;     // Float32 [N]
     int64_t K{0};
     int64_t N{0};
+    int layout{MCV_W8_KN};  // mcv_w8_layout
 };
 
 bool has_w4a16_quantized_weight(const WeightsIndex& index, const std::string& base);
@@ -50,6 +54,7 @@ W4A16QuantizedWeight pack_w4a16_gptq(const int32_t* qweight, const int32_t* qzer
 // Build-defined synthetic int4 quantiser (mcv_w4a16_quantize_host) applied to
 // fp16 [K, N] host weights, then packed.
 W4A16QuantizedWeight quantize_w4a16_synthetic(const uint16_t* w_kn, int64_t K, int64_t N);
-W8A8QuantizedWeight quantize_w8a8_host(const uint16_t* w_kn, int64_t K, int64_t N);
+// `layout` MCV_W8_TILED (default) or MCV_W8_KN.
+W8A8QuantizedWeight quantize_w8a8_host(const uint16_t* w_kn, int64_t K, int64_t N, int layout = MCV_W8_TILED);
 
 }  // namespace minicpmv

@@ -86,6 +86,17 @@ void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStre
               "matmul_w8a8_i32");
 }
 
+void matmul_w8a8_i32(const Tensor& x, const W8A8QuantizedWeight& w, Tensor& out, hipStream_t stream) {
+    require(x.dtype() == DType::Int8 && out.dtype() == DType::Int32, "matmul_w8a8_i32 needs int8 x and int32 out");
+    require(x.shape().size() == 2 && x.shape()[1] == w.K, "matmul_w8a8_i32 x must be [M, K]");
+    require(out.shape() == std::vector<int64_t>{x.shape()[0], w.N}, "matmul_w8a8_i32 out must be [M, N]");
+    require(w.w_int8.data() != nullptr, "matmul_w8a8_i32 weight is not loaded");
+    check_mcv(mcv_w8a8_gemm_i32(static_cast<const int8_t*>(x.data()), x.shape()[0], w.K, w.N,
+                                static_cast<const int8_t*>(w.w_int8.data()), w.layout, static_cast<int32_t*>(out.data()),
+                                stream),
+              "matmul_w8a8_i32");
+}
+
 void w8a8_quantize(const Tensor& x, Tensor& x_int8, Tensor& x_scale, hipStream_t stream) {
     require(x.dtype() == DType::Float16, "w8a8_quantize x must be fp16");
     require(x_int8.dtype() == DType::Int8, "w8a8_quantize x_int8 must be int8");
@@ -123,7 +134,7 @@ void matmul_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8Quantize
     const int xs = scale_dtype(x_scale, "x_scale");
     const Tensor& ws = (xs == MCV_F32 && w.w_scale_f32.data() != nullptr) ? w.w_scale_f32 : w.w_scale;
     check_mcv(mcv_w8a8_gemm_f16(static_cast<const int8_t*>(x_int8.data()), x_scale.data(), xs, M, w.K, w.N,
-                                static_cast<const int8_t*>(w.w_int8.data()), MCV_W8_KN, ws.data(),
+                                static_cast<const int8_t*>(w.w_int8.data()), w.layout, ws.data(),
                                 scale_dtype(ws, "w_scale"), out.data(), stream),
               "matmul_w8a8");
 }

@@ -109,18 +109,22 @@ W4A16QuantizedWeight quantize_w4a16_synthetic(const uint16_t* w_kn, int64_t K, i
     return pack_w4a16_awq(qweight.data(), qzeros.data(), scales.data(), K, N);
 }
 
-W8A8QuantizedWeight quantize_w8a8_host(const uint16_t* w_kn, int64_t K, int64_t N) {
+W8A8QuantizedWeight quantize_w8a8_host(const uint16_t* w_kn, int64_t K, int64_t N, int layout) {
     if (K <= 0 || N <= 0 || (N % 16) != 0)
         throw std::runtime_error("W8A8 dense weight shape must have positive K and N multiple of 16");
-    std::vector<int8_t> q(static_cast<size_t>(K * N));
+    if (layout != MCV_W8_TILED && layout != MCV_W8_KN)
+        throw std::runtime_error("quantize_dense_weight_w8a8: layout must be MCV_W8_TILED or MCV_W8_KN");
+    const int64_t bytes = layout == MCV_W8_TILED ? mcv_w8a8_tiled_bytes(K, N) : K * N;
+    std::vector<int8_t> q(static_cast<size_t>(bytes));
     std::vector<float> s32(static_cast<size_t>(N));
     std::vector<uint16_t> s16(static_cast<size_t>(N));
-    check_mcv(mcv_w8a8_quantize_weight_host(w_kn, K, N, q.data(), MCV_W8_KN, s32.data(), s16.data()),
+    check_mcv(mcv_w8a8_quantize_weight_host(w_kn, K, N, q.data(), layout, s32.data(), s16.data()),
               "quantize_dense_weight_w8a8");
     W8A8QuantizedWeight out;
     out.K = K;
     out.N = N;
-    out.w_int8 = Tensor({K, N}, DType::Int8);
+    out.layout = layout;
+    out.w_int8 = layout == MCV_W8_TILED ? Tensor({bytes}, DType::Int8) : Tensor({K, N}, DType::Int8);
     out.w_int8.copy_from_host(q.data(), q.size());
     out.w_scale = Tensor({N}, DType::Float16);
     out.w_scale.copy_from_host(s16.data(), s16.size() * 2);

@@ -267,12 +267,39 @@ int8_t quantize_i8_host(float v, float inv) {
 
 }  // namespace
 
+namespace {
+// Byte offset of w[k][n] in MCV_W8_TILED for a weight with Kp / 32 k-blocks
+// per 64-column slab (include/mcv_quant.h).
+inline int64_t tiled_offset(int64_t k, int64_t n, int64_t kblocks) {
+    const int64_t l = (n % 32) + 32 * ((k % 32) / 16);
+    return ((((n / 64) * kblocks + k / 32) * 2 + (n % 64) / 32) * 64 + l) * 16 + (k % 16);
+}
+}  // namespace
+
+extern "C" int64_t mcv_w8a8_tiled_bytes(int64_t K, int64_t N) {
+    if (K <= 0 || N <= 0 || K > (int64_t(1) << 30) || N > (int64_t(1) << 30)) return 0;
+    return ceil_div(N, kSlab) * kSlab * ceil_div(K, 128) * 128;
+}
+
+extern "C" int mcv_w8a8_pack_tiled_host(const int8_t* q_kn, int64_t K, int64_t N, int8_t* tiled) {
+    if (!q_kn || !tiled) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_pack_tiled_host: null pointer");
+    const int64_t bytes = mcv_w8a8_tiled_bytes(K, N);
+    if (bytes == 0) return fail(MCV_ERR_SHAPE, "mcv_w8a8_pack_tiled_host: bad shape K=%lld N=%lld", (long long)K, (long long)N);
+    std::memset(tiled, 0, static_cast<size_t>(bytes));
+    const int64_t kblocks = ceil_div(K, 128) * 4;
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) tiled[tiled_offset(k, n, kblocks)] = q_kn[k * N + n];
+    return MCV_OK;
+}
+
 extern "C" int mcv_w8a8_quantize_weight_host(const uint16_t* w_kn, int64_t K, int64_t N, int8_t* q,
                                              int out_layout, float* scale_f32, uint16_t* scale_f16) {
     if (!w_kn || !q || !scale_f32) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_host: null pointer");
     if (K <= 0 || N <= 0) return fail(MCV_ERR_SHAPE, "mcv_w8a8_quantize_weight_host: K and N must be positive");
-    if (out_layout != MCV_W8_KN && out_layout != MCV_W8_NK)
+    if (out_layout != MCV_W8_KN && out_layout != MCV_W8_NK && out_layout != MCV_W8_TILED)
         return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_host: bad layout %d", out_layout);
+    const int64_t kblocks = ceil_div(K, 128) * 4;
+    if (out_layout == MCV_W8_TILED) std::memset(q, 0, static_cast<size_t>(mcv_w8a8_tiled_bytes(K, N)));
     for (int64_t n = 0; n < N; ++n) {
         float max_abs = 0.0f;
         for (int64_t k = 0; k < K; ++k) max_abs = std::max(max_abs, std::fabs(h2f_host(w_kn[k * N + n])));
@@ -284,7 +311,8 @@ extern "C" int mcv_w8a8_quantize_weight_host(const uint16_t* w_kn, int64_t K, in
         for (int64_t k = 0; k < K; ++k) {
             const int8_t v = quantize_i8_host(h2f_host(w_kn[k * N + n]), inv);
             if (out_layout == MCV_W8_KN) q[k * N + n] = v;
-            else q[n * K + k] = v;
+            else if (out_layout == MCV_W8_NK) q[n * K + k] = v;
+            else q[tiled_offset(k, n, kblocks)] = v;
         }
     }
     return MCV_OK;

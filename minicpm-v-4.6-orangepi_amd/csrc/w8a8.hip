@@ -8,6 +8,10 @@
 #include "common.h"
 
 namespace mcv {
+
+int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
+                      const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
+
 namespace {
 
 // ------------------------------------------------------ activation quant --
@@ -213,7 +217,8 @@ __global__ __launch_bounds__(256) void w8a8_dequant_kernel(const int32_t* __rest
 int check_gemm_args(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, int w_layout, const void* out,
                     const char* who) {
     if (!xq || !w || !out) return fail(MCV_ERR_INVALID_ARG, "%s: null pointer", who);
-    if (w_layout != MCV_W8_KN && w_layout != MCV_W8_NK) return fail(MCV_ERR_INVALID_ARG, "%s: bad w_layout %d", who, w_layout);
+    if (w_layout != MCV_W8_KN && w_layout != MCV_W8_NK && w_layout != MCV_W8_TILED)
+        return fail(MCV_ERR_INVALID_ARG, "%s: bad w_layout %d", who, w_layout);
     if (M <= 0 || K <= 0 || N <= 0 || M > (int64_t(1) << 30) || N > (int64_t(1) << 30) || K > (int64_t(1) << 17))
         return fail(MCV_ERR_SHAPE, "%s: bad shape M=%lld K=%lld N=%lld (K <= 131072 keeps int32 exact)", who,
                     (long long)M, (long long)K, (long long)N);
@@ -229,6 +234,7 @@ int check_gemm_args(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int
 template <bool OUT_F16>
 int launch_gemm(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, int w_layout, void* out,
                 const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream) {
+    if (w_layout == MCV_W8_TILED) return launch_w8a8_tiled(xq, M, K, N, w, out, OUT_F16, xs, xs16, ws, ws16, stream);
     dim3 grid(static_cast<unsigned>(ceil_div(N, BN)), static_cast<unsigned>(ceil_div(M, BM)));
     if (w_layout == MCV_W8_KN)
         hipLaunchKernelGGL((w8a8_gemm_kernel<true, OUT_F16>), grid, dim3(NT), 0, stream, xq, w, (int)M, (int)K, (int)N,

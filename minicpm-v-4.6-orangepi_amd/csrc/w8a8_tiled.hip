@@ -1,0 +1,445 @@
+// w8a8_tiled.hip -- W8A8 GEMM and GEMV over the MFMA-tiled int8 weight layout
+// (MCV_W8_TILED, include/mcv_quant.h), gfx950.
+//
+// acc[m][n] = sum_k xq[m][k] * w[k][n] in int32 (exact), optionally followed
+// by the fused epilogue out = fp16 RNE((float(acc) * ws[n]) * xs[m]).
+//
+// The tiled layout stores every 32-column x 32-k block of the weight as one
+// contiguous 1 KiB line in the operand order of v_mfma_i32_32x32x32_i8 (lane
+// l: column l%32, k-half l/32, 16 bytes).  A wave therefore loads its weight
+// operands straight from HBM into registers -- one coalesced 128-bit load per
+// operand, no LDS, no VALU -- and only the activations go through LDS.
+//
+// GEMM: each wave owns one 64-column slab and TM rows (TM/32 x 2 blocks of
+// 32x32 int32 accumulators); WN waves side by side share the x rows through a
+// double-buffered LDS ring, KS k-parts split K inside the workgroup.  The
+// weight operands of a stage are loaded two stages ahead into a ring of three
+// register sets; the x vectors of a stage two stages ahead too, spread over
+// the k32 steps of the stage being computed.  The MFMA computes the transposed
+// tile (weights as the row operand), so a lane ends up with four consecutive
+// output columns per register quad: int32 results leave as 16-byte stores,
+// fp16 results as 16-byte stores after one v_permlane32_swap per pair.
+//
+// GEMV (M <= 4): one workgroup per slab, eight waves splitting K, v_dot4
+// int8 dot products on the same operand lines, partial sums meeting in LDS.
+//
+// Replaces matmul_w8a8_i32_custom + w8a8_dequant_custom and their host
+// wrappers (src/csrc/lib/ops.cpp:1097-1133, 1173-1210) for weights packed by
+// quantize_dense_weight_w8a8 (src/csrc/lib/quantized_weight.cpp:231-268).
+#include <cstdlib>
+
+#include "common.h"
+
+namespace mcv {
+namespace {
+
+constexpr int kW8Block = 1024;        // bytes of one 32-column x 32-k operand line
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ int xcd_tile(int b, int total) {
+    const int per = total >> 3, rem = total & 7, x = b & 7, i = b >> 3;
+    return x * per + (x < rem ? x : rem) + i;
+}
+
+__device__ __forceinline__ float scale_at(const void* p, int is16, int idx) {
+    return is16 ? h2f(static_cast<const uint16_t*>(p)[idx]) : static_cast<const float*>(p)[idx];
+}
+
+template <int TM, int WN, int KS>
+struct Cfg8 {
+    static constexpr int NW = WN * KS;
+    static constexpr int NT = 64 * NW;
+    static_assert(NW == 4, "four waves");
+    static constexpr int MB = TM / 32;
+    static constexpr int BK = 128;                              // k bytes per stage (4 MFMA k32 steps)
+    static constexpr int NSTEP = BK / 32;
+    static constexpr int PITCH = BK + 16;                       // bytes per LDS row of the x tile
+    static constexpr int kAThreads = 64 * WN;
+    static constexpr int kAVec = TM * (BK / 16) / kAThreads;    // 16-byte x vectors per thread per stage
+    static_assert(kAVec >= 1 && kAVec <= 8, "x staging registers");
+    static constexpr int kBVec = 2 * NSTEP;                     // weight operand lines per wave per stage
+    static constexpr int kAStage = TM * PITCH;
+    static constexpr int kLdsBytes = KS * 2 * kAStage;
+    // KS > 1: k-parts 1..KS-1 hand one 32-row block at a time to k-part 0
+    static constexpr int kRedBytes = (KS - 1) * WN * 32 * 64 * 4;
+    static constexpr int kLdsAlloc = kLdsBytes > kRedBytes ? kLdsBytes : kRedBytes;
+};
+
+template <int TM, int WN, int KS, bool OUT_F16>
+__global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
+    const int8_t* __restrict__ xq, const int8_t* __restrict__ w, int M, int K, int N, int KB, void* __restrict__ out,
+    const void* __restrict__ xs, int xs16, const void* __restrict__ ws, int ws16, int nslab, int n_tiles,
+    int total_tiles, int KT) {
+    using C = Cfg8<TM, WN, KS>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[C::kLdsAlloc];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kp = wave / WN;
+    const int wn = wave - kp * WN;
+    const int tile = xcd_tile(static_cast<int>(blockIdx.x), total_tiles);
+    const int tm = tile / n_tiles;
+    const int tn = tile - tm * n_tiles;
+    const int m0 = tm * TM;
+    const int slab = tn * WN + wn;
+    const int kt0 = kp * KT;                   // first stage of this k-part
+
+    uint8_t* As = lds + kp * 2 * C::kAStage;
+
+    // x rows m0.. through a range-checked buffer: rows past M read as zero;
+    // k past K within a row reads the next row, which meets zero weights.
+    const int rows_here = M - m0 < TM ? M - m0 : TM;
+    const __amdgpu_buffer_rsrc_t xr = rsrc(xq + static_cast<size_t>(m0) * K, static_cast<uint32_t>(rows_here) * K);
+    // Weights: slabs past the end read as zero.
+    const __amdgpu_buffer_rsrc_t wr = rsrc(w, static_cast<uint32_t>(nslab) * KB * 2 * kW8Block);
+    const uint32_t wbase = (static_cast<uint32_t>(slab) * KB * 2) * kW8Block + lane * 16u;
+    const int at = wn * 64 + lane;
+    constexpr int kVecPerRow = C::BK / 16;
+
+    struct Set {
+        uint4 a[C::kAVec];
+        int4_t b[C::kBVec];     // [k32 step][half]
+    };
+    constexpr int kItems = C::kAVec + C::kBVec;
+    auto load_item = [&](int kt, Set& st, int it) {
+        const int k0 = (kt0 + kt) * C::BK;
+        if (it < C::kAVec) {
+            const int idx = at + it * C::kAThreads;
+            const uint32_t off = static_cast<uint32_t>((idx / kVecPerRow) * K + k0 + (idx % kVecPerRow) * 16);
+            st.a[it] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        } else {
+            const int b = it - C::kAVec;       // step * 2 + half
+            const uint32_t off = wbase + static_cast<uint32_t>((k0 / 32 + (b >> 1)) * 2 + (b & 1)) * kW8Block;
+            st.b[b] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+        }
+    };
+    auto store_a = [&](int buf, const Set& st, int it) {
+        const int idx = at + it * C::kAThreads;
+        *reinterpret_cast<uint4*>(As + buf * C::kAStage + (idx / kVecPerRow) * C::PITCH + (idx % kVecPerRow) * 16) =
+            st.a[it];
+    };
+
+    int16_t_v acc[C::MB][2];
+#pragma unroll
+    for (int i = 0; i < C::MB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    // Stage kt: weights from `cur`, x from LDS buffer kt&1.  During its k32
+    // steps the x vectors of stage kt+1 (`nxt`, loaded a stage ago) move to
+    // the other LDS buffer and stage kt+2 is loaded into `fut`.
+    auto step = [&](int kt, Set& cur, Set& nxt, Set& fut) {
+        const int kn = kt + 2 < KT ? kt + 2 : KT - 1;
+        const bool store = kt + 1 < KT;
+        const uint8_t* A = As + (kt & 1) * C::kAStage + (lane & 31) * C::PITCH + (lane >> 5) * 16;
+        int4_t af[2][C::MB];
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) af[0][i] = *reinterpret_cast<const int4_t*>(A + i * 32 * C::PITCH);
+#pragma unroll
+        for (int s = 0; s < C::NSTEP; ++s) {
+            const int c = s & 1, n = c ^ 1;
+            if (s + 1 < C::NSTEP) {
+#pragma unroll
+                for (int i = 0; i < C::MB; ++i)
+                    af[n][i] = *reinterpret_cast<const int4_t*>(A + i * 32 * C::PITCH + (s + 1) * 32);
+            }
+#pragma unroll
+            for (int i = 0; i < C::MB; ++i) {
+                acc[i][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.b[2 * s], af[c][i], acc[i][0], 0, 0, 0);
+                acc[i][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.b[2 * s + 1], af[c][i], acc[i][1], 0, 0, 0);
+            }
+#pragma unroll
+            for (int it = s * kItems / C::NSTEP; it < (s + 1) * kItems / C::NSTEP; ++it) {
+                if (it < C::kAVec && store) store_a((kt + 1) & 1, nxt, it);
+                load_item(kn, fut, it);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+    };
+
+    Set s0, s1, s2;
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) load_item(0, s0, it);
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) load_item(KT > 1 ? 1 : 0, s1, it);
+#pragma unroll
+    for (int it = 0; it < C::kAVec; ++it) store_a(0, s0, it);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 2 < KT; kt += 3) {
+        step(kt, s0, s1, s2);
+        step(kt + 1, s1, s2, s0);
+        step(kt + 2, s2, s0, s1);
+    }
+    if (kt < KT) step(kt, s0, s1, s2);
+    if (kt + 1 < KT) step(kt + 1, s1, s2, s0);
+
+    if constexpr (KS > 1) {
+        int* red = reinterpret_cast<int*>(lds);
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) {
+            if (kp > 0) {
+                int* dst = red + ((kp - 1) * WN + wn) * 2 * 16 * 64 + lane;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dst[(j * 16 + r) * 64] = acc[i][j][r];
+            }
+            __syncthreads();
+            if (kp == 0) {
+#pragma unroll
+                for (int p = 1; p < KS; ++p) {
+                    const int* src = red + ((p - 1) * WN + wn) * 2 * 16 * 64 + lane;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] += src[(j * 16 + r) * 64];
+                }
+            }
+            __syncthreads();
+        }
+        if (kp > 0) return;
+    }
+
+    // Transposed blocks: register r of lane l holds row 32 i + l%32 and
+    // column 32 j + 8 (r/4) + 4 (l/32) + r%4.
+    const int h = lane >> 5;
+    if constexpr (!OUT_F16) {
+        int32_t* o = static_cast<int32_t*>(out);
+        const bool vec_ok = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) {
+            const int row = m0 + 32 * i + (lane & 31);
+            if (row >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int col = slab * kSlab + 32 * j + 8 * g + 4 * h;
+                    if (col >= N) continue;
+                    int32_t* dst = o + static_cast<size_t>(row) * N + col;
+                    if (vec_ok) {
+                        *reinterpret_cast<int4_t*>(dst) = int4_t{acc[i][j][4 * g], acc[i][j][4 * g + 1],
+                                                                 acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (col + e < N) dst[e] = acc[i][j][4 * g + e];
+                    }
+                }
+        }
+    } else {
+        uint16_t* o = static_cast<uint16_t*>(out);
+        const bool vec_ok = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+        // the lane's 32 columns' weight scales (zero past N)
+        float wsv[2][4][4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int col = slab * kSlab + 32 * j + 8 * g + 4 * h + e;
+                    wsv[j][g][e] = col < N ? scale_at(ws, ws16, col) : 0.f;
+                }
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) {
+            const int row = m0 + 32 * i + (lane & 31);
+            const float xsv = row < M ? scale_at(xs, xs16, row) : 0.f;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; g += 2) {
+                    uint32_t p[4];
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        auto deq = [&](int gg, int e) {
+                            return f2h(__fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][4 * gg + e]), wsv[j][gg][e]), xsv));
+                        };
+                        const uint32_t x0 = deq(g, 2 * d) | (uint32_t(deq(g, 2 * d + 1)) << 16);
+                        const uint32_t x1 = deq(g + 1, 2 * d) | (uint32_t(deq(g + 1, 2 * d + 1)) << 16);
+                        const auto sw = __builtin_amdgcn_permlane32_swap(x0, x1, false, false);
+                        p[d] = sw[0];
+                        p[2 + d] = sw[1];
+                    }
+                    const int col = slab * kSlab + 32 * j + 8 * g + 8 * h;
+                    if (row >= M || col >= N) continue;
+                    uint16_t* dst = o + static_cast<size_t>(row) * N + col;
+                    if (vec_ok) {
+                        *reinterpret_cast<uint4*>(dst) = make_uint4(p[0], p[1], p[2], p[3]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (col + e < N) dst[e] = static_cast<uint16_t>(p[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ GEMV --
+// grid = nslab, block = 512 (eight waves).  Wave v walks k-blocks v, v+8, ...
+// Lane l of half j accumulates column 64 slab + 32 j + l%32 over its k-half
+// l/32 with v_dot4_i32_i8 (exact int32).
+template <int MR, bool OUT_F16>
+__global__ __launch_bounds__(512) void w8a8_tiled_gemv_kernel(const int8_t* __restrict__ xq,
+                                                              const int8_t* __restrict__ w, int M, int K, int N,
+                                                              int KB, void* __restrict__ out,
+                                                              const void* __restrict__ xs, int xs16,
+                                                              const void* __restrict__ ws, int ws16, int nslab) {
+    __shared__ int red[8][MR][2][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int slab = blockIdx.x;
+    const int h = lane >> 5;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(w, static_cast<uint32_t>(nslab) * KB * 2 * kW8Block);
+    const __amdgpu_buffer_rsrc_t xr = rsrc(xq, static_cast<uint32_t>(M) * K);
+    int acc[MR][2];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0;
+    for (int kb = wave; kb < KB; kb += 8) {
+        int4_t wv[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            wv[j] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   wr, ((static_cast<uint32_t>(slab) * KB + kb) * 2 + j) * kW8Block + lane * 16u, 0, 0));
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            // k past K in a row meets zero weights; rows past M are not used
+            const int4_t xv = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             xr, static_cast<uint32_t>(m * K + kb * 32 + h * 16), 0, 0));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[m][j] = __builtin_amdgcn_sdot4(wv[j][q], xv[q], acc[m][j], false);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) red[wave][m][j][lane] = acc[m][j];
+    __syncthreads();
+    // thread t < 64 * MR finishes (row t/64, column 64 slab + t%64)
+    const int t = threadIdx.x;
+    if (t >= 64 * MR) return;
+    const int m = t >> 6, c = t & 63, j = c >> 5, l = c & 31;
+    int sum = 0;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) sum += red[v][m][j][l] + red[v][m][j][l + 32];
+    const int n = slab * kSlab + c;
+    if (m >= M || n >= N) return;
+    if constexpr (OUT_F16) {
+        const float v = __fmul_rn(__fmul_rn(static_cast<float>(sum), scale_at(ws, ws16, n)), scale_at(xs, xs16, m));
+        static_cast<uint16_t*>(out)[static_cast<size_t>(m) * N + n] = f2h(v);
+    } else {
+        static_cast<int32_t*>(out)[static_cast<size_t>(m) * N + n] = sum;
+    }
+}
+
+struct Shape8 {
+    int tm, wn, ks;
+};
+
+template <bool F16>
+using Gemm8Fn = void (*)(const int8_t*, const int8_t*, int, int, int, int, void*, const void*, int, const void*, int,
+                         int, int, int, int);
+
+template <bool F16>
+Gemm8Fn<F16> pick8(const Shape8& s) {
+    if (s.tm == 128 && s.wn == 2) return w8a8_tiled_gemm_kernel<128, 2, 2, F16>;
+    if (s.tm == 128 && s.wn == 4) return w8a8_tiled_gemm_kernel<128, 4, 1, F16>;
+    if (s.tm == 64 && s.wn == 4) return w8a8_tiled_gemm_kernel<64, 4, 1, F16>;
+    if (s.tm == 64 && s.wn == 2) return w8a8_tiled_gemm_kernel<64, 2, 2, F16>;
+    if (s.tm == 32 && s.wn == 2) return w8a8_tiled_gemm_kernel<32, 2, 2, F16>;
+    if (s.tm == 32 && s.wn == 1) return w8a8_tiled_gemm_kernel<32, 1, 4, F16>;
+    return nullptr;
+}
+
+// Preference order from a sweep on MI355X (K=1024, N=3584): 64-row waves side
+// by side win from M=1024 up; smaller M needs the k-split shapes to fill the
+// chip.
+constexpr Shape8 kShapes8[] = {{64, 4, 1}, {64, 2, 2}, {32, 2, 2}, {32, 1, 4}, {128, 4, 1}, {128, 2, 2}};
+
+// The first listed shape whose grid covers most of the 256 CUs, else the one
+// with the most workgroups; MCV_W8GEMM_SHAPE="TM,WN,KS" overrides it.
+Shape8 choose8(int64_t M, int64_t KT, int64_t nslab) {
+    if (const char* e = std::getenv("MCV_W8GEMM_SHAPE")) {
+        Shape8 s{0, 0, 0};
+        if (std::sscanf(e, "%d,%d,%d", &s.tm, &s.wn, &s.ks) == 3 && pick8<true>(s) && KT % s.ks == 0) return s;
+    }
+    Shape8 best{0, 0, 0};
+    int64_t best_tiles = -1;
+    for (const Shape8& s : kShapes8) {
+        if (KT % s.ks != 0) continue;
+        const int64_t t = ceil_div(M, s.tm) * ceil_div(nslab, s.wn);
+        if (t >= 200) return s;
+        if (t > best_tiles) {
+            best_tiles = t;
+            best = s;
+        }
+    }
+    return best;
+}
+
+}  // namespace
+
+// Columns pad to 64 (a slab), k to 128 (a GEMM stage); padding is zero.
+int64_t w8a8_tiled_bytes(int64_t K, int64_t N) {
+    if (K <= 0 || N <= 0) return 0;
+    return ceil_div(N, kSlab) * kSlab * ceil_div(K, 128) * 128;
+}
+
+// xq [M][K] int8 (16-byte aligned rows not required), w tiled; out int32 or
+// fp16 [M][N].  Shapes were validated by the caller.
+int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
+                      const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream) {
+    const int64_t nslab = ceil_div(N, kSlab);
+    const int64_t KB = ceil_div(K, 128) * 4;            // 32-k blocks per slab (padded to whole stages)
+    if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 32) || M * K >= (int64_t(1) << 32))
+        return fail(MCV_ERR_SHAPE, "w8a8 tiled: weight or activation exceeds 4 GiB");
+    if (M <= 4) {
+        const dim3 grid(static_cast<unsigned>(nslab)), block(512);
+        const int iM = static_cast<int>(M), iK = static_cast<int>(K), iN = static_cast<int>(N), iKB = static_cast<int>(KB);
+        const int ns = static_cast<int>(nslab);
+#define MCV_GEMV8(R)                                                                                                  \
+    if (f16)                                                                                                          \
+        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, true>), grid, block, 0, stream, xq, w, iM, iK, iN, iKB, out, xs, \
+                           xs16, ws, ws16, ns);                                                                       \
+    else                                                                                                              \
+        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, false>), grid, block, 0, stream, xq, w, iM, iK, iN, iKB, out,   \
+                           xs, xs16, ws, ws16, ns);
+        switch (M) {
+            case 1: MCV_GEMV8(1) break;
+            case 2: MCV_GEMV8(2) break;
+            case 3: MCV_GEMV8(3) break;
+            default: MCV_GEMV8(4) break;
+        }
+#undef MCV_GEMV8
+        return check_launch("w8a8_tiled_gemv_kernel");
+    }
+    const int64_t KT_all = KB / 4;                      // 128-k stages over the padded K
+    const Shape8 s = choose8(M, KT_all, nslab);
+    const int64_t n_tiles = ceil_div(nslab, s.wn);
+    const int64_t total = ceil_div(M, s.tm) * n_tiles;
+    if (total > 0x7fffffff) return fail(MCV_ERR_SHAPE, "w8a8 tiled: too many tiles");
+    const int KT = static_cast<int>(KT_all / s.ks);
+    const int KBs = static_cast<int>(KB);
+    if (f16)
+        hipLaunchKernelGGL(pick8<true>(s), dim3(static_cast<unsigned>(total)), dim3(256), 0, stream, xq, w,
+                           static_cast<int>(M), static_cast<int>(K), static_cast<int>(N), KBs, out, xs, xs16, ws, ws16,
+                           static_cast<int>(nslab), static_cast<int>(n_tiles), static_cast<int>(total), KT);
+    else
+        hipLaunchKernelGGL(pick8<false>(s), dim3(static_cast<unsigned>(total)), dim3(256), 0, stream, xq, w,
+                           static_cast<int>(M), static_cast<int>(K), static_cast<int>(N), KBs, out, xs, xs16, ws, ws16,
+                           static_cast<int>(nslab), static_cast<int>(n_tiles), static_cast<int>(total), KT);
+    return check_launch("w8a8_tiled_gemm_kernel");
+}
+
+}  // namespace mcv

@@ -115,6 +115,38 @@ def test_w8a8_host_quantizer_matches_oracle(mcv, oracle):
     assert np.array_equal(s16, s16_o)
     qt, _, _ = mcv.quantize_w8a8_weight_host(w, mcv.W8_NK)
     assert np.array_equal(qt, q_o.T)
+    qtile, _, _ = mcv.quantize_w8a8_weight_host(w, mcv.W8_TILED)
+    assert np.array_equal(qtile, mcv.pack_w8a8_tiled(q_o))
+
+
+def _tiled_reference(q_kn):
+    """MCV_W8_TILED restated from its definition in include/mcv_quant.h: pad
+    to 64 columns / 128 k, then [slab][k-block of 32][half of 32 columns]
+    [lane = column%32 + 32 * (k%32 >= 16)][k%16]."""
+    K, N = q_kn.shape
+    Np, Kp = -(-N // 64) * 64, -(-K // 128) * 128
+    p = np.zeros((Kp, Np), np.int8)
+    p[:K, :N] = q_kn
+    # k = 32 kb + 16 kh + b ; n = 64 s + 32 j + c
+    t = p.reshape(Kp // 32, 2, 16, Np // 64, 2, 32)          # kb, kh, b, s, j, c
+    t = t.transpose(3, 0, 4, 1, 5, 2)                         # s, kb, j, kh, c, b
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+@pytest.mark.parametrize("K,N", [(128, 64), (1024, 3584), (16, 80), (1040, 208), (256, 1)])
+def test_w8a8_tiled_layout(mcv, K, N):
+    rng = np.random.default_rng(K + N)
+    q = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    tiled = mcv.pack_w8a8_tiled(q)
+    assert tiled.nbytes == mcv.w8a8_tiled_bytes(K, N) == (-(-N // 64) * 64) * (-(-K // 128) * 128)
+    assert np.array_equal(tiled, _tiled_reference(q))
+    # a hand-placed known answer: w[k=17][n=70] sits in slab 1, k-block 0,
+    # half 0, lane 6 + 32, byte 1
+    q2 = np.zeros((128, 128), np.int8)
+    q2[17, 70] = 5
+    t2 = mcv.pack_w8a8_tiled(q2)
+    off = ((((1 * 4 + 0) * 2 + 0) * 64) + 38) * 16 + 1
+    assert t2[off] == 5 and np.count_nonzero(t2) == 1
 
 
 def test_validation_errors_without_device(mcv):

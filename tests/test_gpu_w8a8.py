@@ -54,17 +54,47 @@ def _int8_case(rng, M, K, N):
     return x, w
 
 
+def _dev_weight(mcv, w, layout):
+    """int8 [K, N] -> device tensor in `layout` (kn / nk / tiled)."""
+    torch = _torch()
+    if layout == "kn":
+        return torch.from_numpy(w).cuda(), mcv.W8_KN
+    if layout == "nk":
+        return torch.from_numpy(np.ascontiguousarray(w.T)).cuda(), mcv.W8_NK
+    return torch.from_numpy(mcv.pack_w8a8_tiled(w)).cuda(), mcv.W8_TILED
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 3584), (256, 1024, 3584), (5, 1040, 208), (130, 256, 144)],
                          ids=lambda v: str(v))
-@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("layout", ["kn", "nk", "tiled"])
 def test_gemm_i32_bit_exact(mcv, oracle, cuda, M, K, N, layout):
     torch = _torch()
     rng = np.random.default_rng(M + K + N)
     x, w = _int8_case(rng, M, K, N)
-    wl = mcv.W8_KN if layout == "kn" else mcv.W8_NK
-    wdev = torch.from_numpy(w if layout == "kn" else np.ascontiguousarray(w.T)).cuda()
-    acc = mcv.matmul_w8a8_i32(torch.from_numpy(x).cuda(), wdev, layout=wl)
+    wdev, wl = _dev_weight(mcv, w, layout)
+    acc = mcv.matmul_w8a8_i32(torch.from_numpy(x).cuda(), wdev, layout=wl, N=N)
     assert np.array_equal(acc.cpu().numpy(), oracle.gemm_i32(x, w))
+
+
+# The tiled path's GEMV (M <= 4) and every GEMM tile shape, ragged K and N
+# (K padded to 128 with zero weights, N to 64), extreme values.
+@pytest.mark.parametrize("M,K,N", [(2, 1024, 3584), (3, 208, 80), (4, 2048, 1000), (6, 1024, 3584),
+                                   (64, 16, 64), (100, 1040, 3584), (1024, 1024, 3584), (300, 3584, 1024)],
+                         ids=lambda v: str(v))
+def test_tiled_gemm_i32_bit_exact(mcv, oracle, cuda, M, K, N):
+    torch = _torch()
+    rng = np.random.default_rng(7 * M + K + N)
+    x, w = _int8_case(rng, M, K, N)
+    x[0, :] = -128
+    w[:, 0] = -128
+    wdev, _ = _dev_weight(mcv, w, "tiled")
+    acc = mcv.matmul_w8a8_i32(torch.from_numpy(x).cuda(), wdev, layout=mcv.W8_TILED, N=N)
+    if M * K * N <= 300 * 1024 * 1024:
+        assert np.array_equal(acc.cpu().numpy(), oracle.gemm_i32(x, w))
+    else:
+        ref = (torch.from_numpy(x).cuda().double() @ torch.from_numpy(w).cuda().double()).to(torch.int64)
+        assert torch.equal(acc.to(torch.int64), ref)
+    assert int(acc[0, 0]) == K * 128 * 128
 
 
 def test_gemm_i32_full_size_exact(mcv, cuda):
@@ -76,10 +106,12 @@ def test_gemm_i32_full_size_exact(mcv, cuda):
     x[0, :] = -128
     w[:, 0] = -128                               # |acc| = 2^24 at (0, 0)
     xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
-    acc = mcv.matmul_w8a8_i32(xd, wd)
     ref = (xd.double() @ wd.double()).to(torch.int64)
-    assert torch.equal(acc.to(torch.int64), ref)
-    assert int(acc[0, 0]) == 1 << 24
+    for layout in ("kn", "tiled"):
+        wdev, wl = _dev_weight(mcv, w, layout)
+        acc = mcv.matmul_w8a8_i32(xd, wdev, layout=wl, N=N)
+        assert torch.equal(acc.to(torch.int64), ref), layout
+        assert int(acc[0, 0]) == 1 << 24
 
 
 def test_dequant_reference_vectors(mcv, oracle, cuda):
@@ -107,7 +139,8 @@ def test_config5_end_to_end(mcv, oracle, cuda, M):
     out = mcv.matmul_w8a8(xq, xs, wq)                    # fp32 scales
     q_o, s_o, _ = oracle.w8a8_quantize_act(x)
     wq_o, ws_o, ws16_o = oracle.w8a8_quantize_weight(wf)
-    assert np.array_equal(wq.w_int8.cpu().numpy(), wq_o)
+    assert wq.layout == mcv.W8_TILED
+    assert np.array_equal(wq.w_int8.cpu().numpy(), mcv.pack_w8a8_tiled(wq_o))
     rows = np.arange(M) if M <= 256 else np.arange(0, M, 8)
     acc_o = oracle.gemm_i32(q_o[rows], wq_o)
     want = oracle.w8a8_dequant(acc_o, s_o[rows], ws_o)
@@ -115,7 +148,7 @@ def test_config5_end_to_end(mcv, oracle, cuda, M):
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:3].tolist()}: {got[tuple(bad[0])]:#06x} vs {want[tuple(bad[0])]:#06x}"
     # fused == two-kernel path, with the reference's fp16 scales too
-    acc = mcv.matmul_w8a8_i32(xq, wq.w_int8)
+    acc = mcv.matmul_w8a8_i32(xq, wq)
     assert torch.equal(mcv.w8a8_dequant(acc, xs, wq.w_scale_f32), out)
     xs16 = xs.half()
     assert torch.equal(mcv.matmul_w8a8(xq, xs16, wq, use_f32_scale=False),
@@ -129,5 +162,12 @@ def test_nk_layout_fused(mcv, cuda):
     wf = f16_normal(rng, (K, N), 0.02)
     a = mcv.quantize_dense_weight_w8a8(_f16_dev(wf), layout=mcv.W8_KN)
     b = mcv.quantize_dense_weight_w8a8(_f16_dev(wf), layout=mcv.W8_NK)
+    c = mcv.quantize_dense_weight_w8a8(_f16_dev(wf), layout=mcv.W8_TILED)
     xq, xs, _ = mcv.w8a8_quantize(_f16_dev(f16_normal(rng, (M, K), 1.0)))
-    assert torch.equal(mcv.matmul_w8a8(xq, xs, a), mcv.matmul_w8a8(xq, xs, b))
+    ref = mcv.matmul_w8a8(xq, xs, a)
+    assert torch.equal(ref, mcv.matmul_w8a8(xq, xs, b))
+    assert torch.equal(ref, mcv.matmul_w8a8(xq, xs, c))
+    # fp16 scales and the M <= 4 GEMV through the same epilogue
+    xs16 = xs.half()
+    assert torch.equal(mcv.matmul_w8a8(xq, xs16, a, use_f32_scale=False), mcv.matmul_w8a8(xq, xs16, c, use_f32_scale=False))
+    assert torch.equal(mcv.matmul_w8a8(xq[:3], xs[:3], a), mcv.matmul_w8a8(xq[:3], xs[:3], c))
