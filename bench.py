@@ -193,7 +193,7 @@ def wl_lm_head(pkg, args):
                        "weight_copies_rotated": copies, "rotated_bytes": copies * (qw.nbytes + sc.nbytes + zr.nbytes),
                        "algorithmic_bytes_per_step": nbytes, "token": token},
                dtype="w4a16 (f16 x int4, f32 accumulate)",
-               kernel="w4a16_gemv_kernel<8,1,2> (GEMV + fused argmax)")
+               kernel="w4a16_lm_head_kernel<4,1> (GEMV + fused argmax)")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes)
     return res

@@ -172,9 +172,9 @@ int64_t mcv_lm_head_workspace_bytes(int64_t V);
  * logits_dev may be NULL.  token_dev receives an int64 on the device.
  * Replaces the 16 chunk matmuls + 16 D2H copies + host scan of lm_head_greedy
  * (src/csrc/lib/language_model.cpp:412-482) with one kernel: the GEMV's
- * workgroups fold their best (value, index) into a two-level tree of
- * (max, arrival count) slots in the workspace, and the last arrival writes
- * the token. */
+ * workgroups fold their best (value, index) into 64 (max, arrival count)
+ * slots of the workspace; the arrivals completing a slot bump a global count,
+ * and the last of those reads the 64 slot maxima and writes the token. */
 int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
                              const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                              int zero_bias, void* logits_dev, int64_t* token_dev,

@@ -59,42 +59,55 @@ __device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t*
     return fmaf(alo + ahi * 0.0625f, scale, acc);
 }
 
-// Cross-workgroup argmax without fences.  Each level-1 slot j (64 slots,
-// 128 B apart, taken by slab % 64) holds a 64-bit key max and a 32-bit arrival
-// count.  A workgroup folds its key in with atomicMax, waits for that atomic to
-// return -- it has then been performed at the device-coherent point -- and
-// only then bumps the count.  The arrival that brings the count to its
-// expected value therefore sees every other arrival's key when it reads the
-// slot (atomicMax with 0), clears the slot, and repeats the same two steps on
-// the level-2 slot; the last level-2 arrival writes the token and clears it.
-// Every call thus leaves the workspace all zero.  Measured on MI355X with the
-// lm_head's 3877 workgroups: 3877 atomics on one address serialise to 45 us
-// (spread over 64 addresses they are free), a __threadfence per workgroup adds
-// ~30 us, CAS-combined (key, count) words 22-39 us (retry storms when the
-// last arrivals bunch), this scheme ~4 us over the bare GEMV, and a second
-// reduction launch ~7 us.
+// Cross-workgroup argmax without fences.  64 slots (128 B apart, slot j taken
+// by the slabs s with s % 64 == j) each hold a 64-bit key maximum and a 32-bit
+// arrival count; one more 128-byte line holds a global count.  A workgroup
+// folds its key into its slot with atomicMax and waits for that atomic to
+// return -- it has then been performed at the device-coherent point -- before
+// it bumps the slot's count.  The arrival that completes a slot bumps the
+// global count (only 64 such arrivals, so it never serialises); the arrival
+// that completes the global count knows every slot count completed after all
+// of that slot's maxima were performed, so one wave reads the 64 slot maxima
+// in a single parallel round of atomic reads, writes the token and clears the
+// workspace.  The last workgroup's tail is four device round trips.  Every
+// call leaves the workspace all zero.  Measured on MI355X with the lm_head's
+// 3877 workgroups: 3877 atomics on one address serialise to 45 us (spread over
+// 64 addresses they are free), a __threadfence per workgroup adds ~30 us,
+// CAS-combined (key, count) words 22-39 us (retry storms when the last
+// arrivals bunch).
 constexpr int kTreeStride = 16;                               // u64 words per slot: 128 B
 constexpr int kTreeWords = 64;
 constexpr int64_t kTreeBytes = (kTreeWords + 1) * kTreeStride * 8;
 
-// Folds `key` into slot `slot` (key word at [0], count at [8]); true for the
-// arrival that completes the slot, which then receives the slot's maximum.
-__device__ __forceinline__ bool slot_arrive(unsigned long long* slot, unsigned long long key, unsigned expected,
-                                            unsigned long long* merged) {
-    unsigned* count = reinterpret_cast<unsigned*>(slot + 8);
-    const unsigned long long before = atomicMax(slot, key);
-    asm volatile("s_waitcnt vmcnt(0)" : : "v"(before) : "memory");   // the max has returned, i.e. is performed
-    if (atomicAdd(count, 1u) + 1u != expected) return false;
-    *merged = atomicMax(slot, 0ull);                                   // atomic read of the slot's maximum
+// Run by one full wave of each workgroup after its columns are final; `key`
+// is the workgroup's best key (wave-uniform).
+__device__ __forceinline__ void argmax_arrive(unsigned long long* __restrict__ ws, unsigned long long key, int slab,
+                                              int nblk, int lane, int64_t* __restrict__ token) {
+    const int j = slab & (kTreeWords - 1);
+    const unsigned expected = static_cast<unsigned>((nblk - j + kTreeWords - 1) / kTreeWords);
+    const unsigned nslots = static_cast<unsigned>(nblk < kTreeWords ? nblk : kTreeWords);
+    unsigned* gcount = reinterpret_cast<unsigned*>(ws + kTreeWords * kTreeStride + 8);
+    int last = 0;
+    if (lane == 0) {
+        unsigned long long* slot = ws + j * kTreeStride;
+        const unsigned long long before = atomicMax(slot, key);
+        asm volatile("s_waitcnt vmcnt(0)" : : "v"(before) : "memory");   // the max has returned, i.e. is performed
+        if (atomicAdd(reinterpret_cast<unsigned*>(slot + 8), 1u) + 1u == expected)
+            last = atomicAdd(gcount, 1u) + 1u == nslots;
+    }
+    if (!__shfl(last, 0, 64)) return;
+    unsigned long long* slot = ws + lane * kTreeStride;
+    // atomic reads of the final slot maxima (atomicMax with 0 changes nothing)
+    const unsigned long long m = wave_max_u64(static_cast<unsigned>(lane) < nslots ? atomicMax(slot, 0ull) : 0ull);
+    if (lane == 0) *token = argmax_index(m);
     atomicExch(slot, 0ull);
-    atomicExch(count, 0u);
-    return true;
+    atomicExch(reinterpret_cast<unsigned*>(slot + 8), 0u);
+    if (lane == 0) atomicExch(gcount, 0u);
 }
 
 // ARGMAX modes of the GEMV epilogue (M == 1 only).
 constexpr int kArgNone = 0;
 constexpr int kArgPartials = 1;   // plain store of the slab's key to keys[slab]
-constexpr int kArgFused = 2;      // two-level slot tree in `keys`, token written by the last arrival
 
 // grid = (Nslab, M), block = 64 * KSPLIT.  Wave w handles groups
 // {w*GPW + r*KSPLIT*GPW + i : i < GPW}.
@@ -156,21 +169,62 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
     if constexpr (ARGMAX != kArgNone) {
         unsigned long long key = n < N ? argmax_key64(argmax_key16(h), static_cast<uint32_t>(n)) : 0ull;
         key = wave_max_u64(key);
-        if (lane == 0) {
-            if constexpr (ARGMAX == kArgPartials) {
-                keys[slab] = key;
-            } else {
-                const int nblk = static_cast<int>(gridDim.x);
-                const int j = slab & (kTreeWords - 1);
-                unsigned long long m1, m2;
-                if (slot_arrive(keys + j * kTreeStride, key,
-                                static_cast<unsigned>((nblk - j + kTreeWords - 1) / kTreeWords), &m1) &&
-                    slot_arrive(keys + kTreeWords * kTreeStride, m1,
-                                static_cast<unsigned>(nblk < kTreeWords ? nblk : kTreeWords), &m2))
-                    *token = argmax_index(m2);
-            }
+        if (lane == 0) keys[slab] = key;
+    }
+}
+
+// Greedy lm_head: the GEMV above with the argmax fused.  A workgroup may walk
+// SPW consecutive slabs (fewer arrivals at the cross-workgroup argmax); on the
+// lm_head shape one slab per workgroup measures best (graph-replayed, MI355X:
+// SPW 1/2/4/8 = 27.2/28.6/28.9/31.3 us against 26.4 us for the bare GEMV).
+// Waves split K as in the GEMV; their partial sums meet in a double-buffered
+// LDS array, so one barrier per slab suffices.
+template <int KSPLIT, int SPW>
+__global__ __launch_bounds__(64 * KSPLIT) void w4a16_lm_head_kernel(
+    const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
+    const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ logits, int K, int V, int Npad,
+    int nslab, unsigned long long* __restrict__ ws, int64_t* __restrict__ token) {
+    __shared__ float red[2][KSPLIT][kSlab];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = K / kGroup;
+    const int C = K / kChunkK;
+    const int zstride = Npad >> 3;
+    const uint32_t* __restrict__ xw = reinterpret_cast<const uint32_t*>(x);
+    uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
+    unsigned long long best = 0ull;
+    const int s0 = static_cast<int>(blockIdx.x) * SPW;
+#pragma unroll
+    for (int si = 0; si < SPW; ++si) {
+        const int slab = s0 + si;
+        if (slab >= nslab) break;                                       // workgroup-uniform
+        const int n = slab * kSlab + lane;
+        const uint4* __restrict__ wp = qw + static_cast<size_t>(slab) * C * kSlab + lane;
+        const uint32_t zshift = (n & 7) * 4;
+        float acc = 0.f;
+        for (int g = wave; g < G; g += KSPLIT) {
+            uint4 wv[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) wv[c] = wp[static_cast<size_t>(g * 4 + c) * kSlab];
+            const uint16_t sv = scales[static_cast<size_t>(g) * Npad + n];
+            const uint32_t zv = zeros[static_cast<size_t>(g) * zstride + (n >> 3)];
+            acc = group_dot(wv, xw, g, ((zv >> zshift) & 15u) + zero_bias, h2f(sv), acc, vmagic);
+        }
+        red[si & 1][wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            acc = red[si & 1][0][lane];
+#pragma unroll
+            for (int w = 1; w < KSPLIT; ++w) acc += red[si & 1][w][lane];
+            const uint16_t h = f2h(acc);
+            if (logits != nullptr && n < V) logits[n] = h;
+            const unsigned long long key = n < V ? argmax_key64(argmax_key16(h), static_cast<uint32_t>(n)) : 0ull;
+            best = key > best ? key : best;
         }
     }
+    if (wave != 0) return;
+    argmax_arrive(ws, wave_max_u64(best), static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token);
 }
 
 // One workgroup folds the per-slab keys into the token (first maximum wins:
@@ -227,12 +281,14 @@ int env_int(const char* name, int fallback) {
 
 // One quantisation group (four 16-byte loads per lane) per wave per trip,
 // and enough waves per workgroup (up to 8, at most one per group) that the
-// grid holds >= 16K waves, 64 per CU: measured on the lm_head shape (K=1024,
-// 3877 slabs), 4 or 8 waves x 1 group run at 23.4 us where 2 x 4 groups take
-// 31 us.  MCV_GEMV_KSPLIT / MCV_GEMV_GPW override the choice (tuning sweeps).
+// grid holds >= 8K waves, 32 per CU.  Measured on the lm_head shape (K=1024,
+// 3877 slabs) with graph-replayed launches: 4 waves x 1 group (two trips)
+// 25.4 us, 8 x 1 25.8 us, 4 x 2 27.1 us, 2 x 4 31.0 us; the decode is VALU
+// heavy, so more loads in flight per wave do not pay.  MCV_GEMV_KSPLIT /
+// MCV_GEMV_GPW override the choice (tuning sweeps).
 GemvCfg choose_gemv(int64_t G, int64_t blocks) {
     int ks = 1;
-    while (ks < 8 && blocks * ks < 16384 && ks * 2 <= G) ks *= 2;
+    while (ks < 8 && blocks * ks < 8192 && ks * 2 <= G) ks *= 2;
     const int gpw = 1;
     GemvCfg c{env_int("MCV_GEMV_KSPLIT", ks), env_int("MCV_GEMV_GPW", gpw)};
     if (c.ksplit != 1 && c.ksplit != 2 && c.ksplit != 4 && c.ksplit != 8 && c.ksplit != 16) c.ksplit = ks;
@@ -401,15 +457,27 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
     if ((rc = require_device()) != MCV_OK) return rc;
     const int64_t nslab = ceil_div(V, kSlab);
     const int64_t npad = ceil_div(N, kSlab) * kSlab;
-    const GemvCfg cfg = choose_gemv(K / kGroup, nslab);
-    auto fn = pick_kernel<kArgFused>(cfg.ksplit, cfg.gpw);
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), 1u), dim3(64 * cfg.ksplit), 0,
-                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
-                       static_cast<const uint4*>(qw), static_cast<const uint16_t*>(scales),
-                       static_cast<const uint32_t*>(zeros), static_cast<uint32_t>(zero_bias),
-                       static_cast<uint16_t*>(logits), static_cast<int>(K), static_cast<int>(V),
-                       static_cast<int>(npad), static_cast<unsigned long long*>(workspace), token);
-    return check_launch("w4a16_gemv_kernel<argmax>");
+    // 4 waves per slab and one slab per workgroup, as measured best on the
+    // lm_head shape; MCV_LMHEAD_SPW overrides the latter for sweeps.
+    int spw = env_int("MCV_LMHEAD_SPW", 1);
+    if (spw != 1 && spw != 2 && spw != 4 && spw != 8) spw = 1;
+    const int ks = K / kGroup >= 4 ? 4 : static_cast<int>(K / kGroup);
+    using LmFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int,
+                          int, int, unsigned long long*, int64_t*);
+    LmFn fn = nullptr;
+#define MCV_LM(KS_, SPW_) \
+    if (ks == KS_ && spw == SPW_) fn = w4a16_lm_head_kernel<KS_, SPW_>;
+    MCV_LM(4, 1) MCV_LM(4, 2) MCV_LM(4, 4) MCV_LM(4, 8) MCV_LM(2, 1) MCV_LM(2, 2) MCV_LM(2, 4) MCV_LM(2, 8)
+    MCV_LM(1, 1) MCV_LM(1, 2) MCV_LM(1, 4) MCV_LM(1, 8)
+#undef MCV_LM
+    const int64_t nblk = ceil_div(nslab, spw);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nblk)), dim3(64 * ks), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
+                       static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
+                       static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(logits), static_cast<int>(K),
+                       static_cast<int>(V), static_cast<int>(npad), static_cast<int>(nslab),
+                       static_cast<unsigned long long*>(workspace), token);
+    return check_launch("w4a16_lm_head_kernel");
 }
 
 int mcv_w4a16_dequant(const void* qw, const void* scales, const void* zeros, int zero_bias, int64_t K, int64_t N,
