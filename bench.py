@@ -229,8 +229,10 @@ def wl_gemv1(pkg, args):
     return res
 
 
-def wl_mlp(pkg, args):
-    """Config 2: gate/up 1024->3584, silu*mul, down 3584->1024, 24 layer sets x 4 copies."""
+def wl_mlp(pkg, args, fused=True):
+    """Config 2: gate/up 1024->3584, silu*mul, down 3584->1024, 24 layer sets x 4 copies.
+    Fused (default): one gate+up+silu*mul launch and the down GEMV; unfused: the
+    reference's four launches (gate, up, silu_mul, down)."""
     import torch
     H, I = 1024, 3584
     nsets, reps = 24, args.copies or 4
@@ -254,18 +256,22 @@ def wl_mlp(pkg, args):
 
     def block(i):
         L = sets[i]
-        pkg.matmul_w4a16(x, L[0], g)
-        pkg.matmul_w4a16(x, L[1], u)
-        pkg.silu_mul(g, u, a)
+        if fused:
+            pkg.mlp_gate_up_silu_w4a16(x, L[0], L[1], a)
+        else:
+            pkg.matmul_w4a16(x, L[0], g)
+            pkg.matmul_w4a16(x, L[1], u)
+            pkg.silu_mul(g, u, a)
         pkg.matmul_w4a16(a, L[2], y)
 
     nbytes = 2 * w4a16_bytes(H, I) + w4a16_bytes(I, H) + 2 * H * 2 + 2 * I * 2 * 3 + 2 * H
     total_ms, _ = time_steps(block, len(sets), args.steps, args.warmup)
     kms = time_each_launch(block, len(sets), args.steps)
     return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
-                config={"workload": "w4a16_mlp_block_decode", "M": 1, "hidden": H, "intermediate": I,
-                        "weight_sets_rotated": len(sets)},
-                dtype="w4a16 (f16 x int4, f32 accumulate)", kernel="mlp block (4 launches)")
+                config={"workload": "w4a16_mlp_block_decode" + ("" if fused else "_unfused"), "M": 1, "hidden": H,
+                        "intermediate": I, "weight_sets_rotated": len(sets)},
+                dtype="w4a16 (f16 x int4, f32 accumulate)",
+                kernel="mlp block (gate+up+silu launch, down GEMV)" if fused else "mlp block (4 launches)")
 
 
 def wl_prefill(pkg, args):
@@ -313,7 +319,8 @@ def wl_copy(pkg, args):
                 dtype="u8", kernel="torch copy kernel")
 
 
-WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp, "prefill": wl_prefill, "w8a8": wl_w8a8,
+WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
+             "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, fused=False), "prefill": wl_prefill, "w8a8": wl_w8a8,
              "copy": wl_copy}
 
 

@@ -143,6 +143,17 @@ int mcv_w4a16_gemm_mfma(const void* x_dev, int64_t M, int64_t K, int64_t N,
                         const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                         int zero_bias, void* out_dev, mcv_stream_t stream);
 
+/* Decode MLP front half in one launch: act[M][N] = silu(x . Wgate) * (x . Wup)
+ * with gate and up rounded to fp16 first, exactly as two mcv_w4a16_gemv calls
+ * followed by mcv_silu_mul produce it (bit-identical).  Both weights are K x N
+ * slab-64.  Replaces the gate matmul + up matmul + silu_mul sequence of the
+ * decoder layers' MLP (src/csrc/lib/decoder_layer.cpp:1029-1046, silu_mul
+ * src/csrc/lib/ops.cpp:437-456).  Meant for decode-sized M (GEMV kernel). */
+int mcv_w4a16_gate_up_silu(const void* x_dev, int64_t M, int64_t K, int64_t N,
+                           const void* qw_gate_dev, const void* scales_gate_dev, const void* zeros_gate_dev,
+                           int zero_bias_gate, const void* qw_up_dev, const void* scales_up_dev,
+                           const void* zeros_up_dev, int zero_bias_up, void* act_dev, mcv_stream_t stream);
+
 /* Materialise dequantised weights: w_f16_kn [K][N] = fp16 RNE((q - z) * s)
  * and/or w8_kn [K][N] = q - z (int8), either may be NULL.  The int8 form is
  * the reference's unpacked w_int8 (src/csrc/lib/quantized_weight.cpp:155). */

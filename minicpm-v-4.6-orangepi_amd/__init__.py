@@ -54,6 +54,8 @@ _SIGS = {
     "mcv_w4a16_gemv": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_gemm_mfma": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "mcv_w4a16_gate_up_silu": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp,
+                                        _vp]),
     "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "mcv_lm_head_workspace_bytes": (_c_i64, [_c_i64]),
     "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
@@ -290,6 +292,26 @@ def matmul_w4a16_gemv(x, w, out=None, stream=None):
 
 def matmul_w4a16_mfma(x, w, out=None, stream=None):
     return _w4_call("mcv_w4a16_gemm_mfma", x, w, out, stream)
+
+
+def mlp_gate_up_silu_w4a16(x, w_gate: W4A16QuantizedWeight, w_up: W4A16QuantizedWeight, out=None, stream=None):
+    """act[M, N] = silu(x . gate) * (x . up), one launch; bit-identical to two
+    matmul_w4a16 calls and silu_mul (decoder_layer.cpp:1029-1046)."""
+    torch = _torch()
+    if x.dtype != torch.float16 or x.dim() != 2 or x.shape[1] != w_gate.K or not x.is_contiguous():
+        raise McvError(f"mlp_gate_up_silu: x must be contiguous fp16 [M, {w_gate.K}]")
+    if (w_up.K, w_up.N) != (w_gate.K, w_gate.N):
+        raise McvError("mlp_gate_up_silu: gate and up weights must have the same shape")
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, w_gate.N), dtype=torch.float16, device=x.device)
+    if out.dtype != torch.float16 or tuple(out.shape) != (M, w_gate.N) or not out.is_contiguous():
+        raise McvError(f"mlp_gate_up_silu: out must be contiguous fp16 [{M}, {w_gate.N}]")
+    qg, sg, zg = w_gate.ptrs()
+    qu, su, zu = w_up.ptrs()
+    _check(lib().mcv_w4a16_gate_up_silu(_dev(x), M, w_gate.K, w_gate.N, qg, sg, zg, w_gate.zero_bias, qu, su, zu,
+                                        w_up.zero_bias, _dev(out), _stream(stream)), "mcv_w4a16_gate_up_silu")
+    return out
 
 
 def w4a16_dequant(w: W4A16QuantizedWeight, f16=True, i8=False, stream=None):

@@ -34,6 +34,12 @@ void matmul_w4a16(const Tensor& x, const Tensor& w_int8, const Tensor& scales, T
 // LDS-dequant fp16 MFMA GEMM otherwise).
 void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream);
 
+// Decode MLP front half in one launch: act [M, I] = silu(x . gate) * (x . up),
+// gate/up rounded to fp16 first -- bit-identical to two matmul_w4a16 calls and
+// silu_mul (the reference's sequence, decoder_layer.cpp:1029-1046).
+void mlp_gate_up_silu_w4a16(const Tensor& x, const W4A16QuantizedWeight& gate, const W4A16QuantizedWeight& up,
+                            Tensor& act, hipStream_t stream);
+
 // int32 out [M, N] = int8 x [M, K] . int8 w [K, N], exact.
 void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream);
 // The same over a quantized weight object, in whatever layout it holds

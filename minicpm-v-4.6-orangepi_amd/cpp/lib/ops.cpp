@@ -73,6 +73,18 @@ void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, h
               "matmul_w4a16");
 }
 
+void mlp_gate_up_silu_w4a16(const Tensor& x, const W4A16QuantizedWeight& gate, const W4A16QuantizedWeight& up,
+                            Tensor& act, hipStream_t stream) {
+    require(x.dtype() == DType::Float16 && act.dtype() == DType::Float16, "mlp_gate_up_silu x and act must be fp16");
+    require(x.shape().size() == 2 && x.shape()[1] == gate.K, "mlp_gate_up_silu x must be [M, K]");
+    require(up.K == gate.K && up.N == gate.N, "mlp_gate_up_silu gate and up must have the same shape");
+    require(act.shape() == std::vector<int64_t>{x.shape()[0], gate.N}, "mlp_gate_up_silu act must be [M, N]");
+    check_mcv(mcv_w4a16_gate_up_silu(x.data(), x.shape()[0], gate.K, gate.N, gate.w_int8.data(), gate.scales.data(),
+                                     gate.zeros.data(), gate.zero_bias, up.w_int8.data(), up.scales.data(),
+                                     up.zeros.data(), up.zero_bias, act.data(), stream),
+              "mlp_gate_up_silu");
+}
+
 void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream) {
     require(x.dtype() == DType::Int8, "matmul_w8a8_i32 x must be int8");
     require(w_int8.dtype() == DType::Int8, "matmul_w8a8_i32 w must be int8");

@@ -82,6 +82,18 @@ __device__ __host__ __forceinline__ int64_t argmax_index(unsigned long long key)
     return static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(key & 0xffffffffull));
 }
 
+// fp16 RNE((g / (1 + exp(-g))) * u) with every step in fp32: the operation
+// sequence of src/csrc/custom_ops/op_kernel/silu_mul_custom.cpp:59-75.  Shared
+// by silu_mul_kernel and the fused gate/up GEMV so both round identically.
+__device__ __forceinline__ uint16_t silu_mul_f16(uint16_t g, uint16_t u) {
+    const float gv = h2f(g);
+    float t = expf(-gv);
+    t = __fadd_rn(t, 1.0f);
+    t = __fdiv_rn(gv, t);
+    t = __fmul_rn(t, h2f(u));
+    return f2h(t);
+}
+
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

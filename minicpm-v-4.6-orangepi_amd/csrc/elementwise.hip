@@ -4,19 +4,12 @@
 namespace mcv {
 namespace {
 
-// out = fp16 RNE((g / (1 + exp(-g))) * u), fp32 in between: the operation
-// sequence of src/csrc/custom_ops/op_kernel/silu_mul_custom.cpp:59-75.
+// out = silu_mul_f16(g, u) elementwise (common.h).
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
                                                        uint16_t* __restrict__ out, int64_t n) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const float gv = h2f(g[i]);
-        float t = expf(-gv);
-        t = __fadd_rn(t, 1.0f);
-        t = __fdiv_rn(gv, t);
-        t = __fmul_rn(t, h2f(u[i]));
-        out[i] = f2h(t);
-    }
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        out[i] = silu_mul_f16(g[i], u[i]);
 }
 
 // One workgroup per row: 64-bit keys (value, then lowest index) reduced with

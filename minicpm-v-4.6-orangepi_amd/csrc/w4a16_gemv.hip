@@ -227,6 +227,60 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_lm_head_kernel(
     argmax_arrive(ws, wave_max_u64(best), static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token);
 }
 
+// Decode MLP front half in one launch: act = silu(x . Wgate) * (x . Wup).
+// Each workgroup owns one 64-column slab of both weights; its waves split K
+// exactly like the GEMV (the same group_dot per weight), the two partial sums
+// meet in LDS, and wave 0 rounds gate and up to fp16 -- as the separate GEMV
+// launches store them -- before silu_mul_f16, so the result is bit-identical
+// to gate GEMV + up GEMV + silu_mul.  grid = (Nslab, M).
+template <int KSPLIT>
+__global__ __launch_bounds__(64 * KSPLIT) void w4a16_gate_up_silu_kernel(
+    const uint16_t* __restrict__ x, const uint4* __restrict__ qg, const uint16_t* __restrict__ sg,
+    const uint32_t* __restrict__ zg, uint32_t zbg, const uint4* __restrict__ qu, const uint16_t* __restrict__ su,
+    const uint32_t* __restrict__ zu, uint32_t zbu, uint16_t* __restrict__ act, int K, int N, int Npad) {
+    __shared__ float red[2][KSPLIT][kSlab];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slab = blockIdx.x;
+    const int m = blockIdx.y;
+    const int n = slab * kSlab + lane;
+    const int G = K / kGroup;
+    const int C = K / kChunkK;
+    const int zstride = Npad >> 3;
+    const uint32_t zshift = (n & 7) * 4;
+    const uint32_t* __restrict__ xw = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(m) * K);
+    const size_t wofs = static_cast<size_t>(slab) * C * kSlab + lane;
+    uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
+    float ag = 0.f, au = 0.f;
+    for (int g = wave; g < G; g += KSPLIT) {
+        uint4 wgv[4], wuv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wgv[c] = qg[wofs + static_cast<size_t>(g * 4 + c) * kSlab];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wuv[c] = qu[wofs + static_cast<size_t>(g * 4 + c) * kSlab];
+        const uint16_t sgv = sg[static_cast<size_t>(g) * Npad + n], suv = su[static_cast<size_t>(g) * Npad + n];
+        const uint32_t zgv = zg[static_cast<size_t>(g) * zstride + (n >> 3)];
+        const uint32_t zuv = zu[static_cast<size_t>(g) * zstride + (n >> 3)];
+        ag = group_dot(wgv, xw, g, ((zgv >> zshift) & 15u) + zbg, h2f(sgv), ag, vmagic);
+        au = group_dot(wuv, xw, g, ((zuv >> zshift) & 15u) + zbu, h2f(suv), au, vmagic);
+    }
+    if constexpr (KSPLIT > 1) {
+        red[0][wave][lane] = ag;
+        red[1][wave][lane] = au;
+        __syncthreads();
+        if (wave != 0) return;
+        ag = red[0][0][lane];
+        au = red[1][0][lane];
+#pragma unroll
+        for (int w = 1; w < KSPLIT; ++w) {
+            ag += red[0][w][lane];
+            au += red[1][w][lane];
+        }
+    }
+    if (n < N) act[static_cast<size_t>(m) * N + n] = silu_mul_f16(f2h(ag), f2h(au));
+}
+
 // One workgroup folds the per-slab keys into the token (first maximum wins:
 // the key orders by value, then by smallest index).
 __global__ __launch_bounds__(1024) void argmax_reduce_kernel(const unsigned long long* __restrict__ keys, int n,
@@ -478,6 +532,36 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
                        static_cast<int>(V), static_cast<int>(npad), static_cast<int>(nslab),
                        static_cast<unsigned long long*>(workspace), token);
     return check_launch("w4a16_lm_head_kernel");
+}
+
+int mcv_w4a16_gate_up_silu(const void* x, int64_t M, int64_t K, int64_t N, const void* qw_gate,
+                           const void* scales_gate, const void* zeros_gate, int zero_bias_gate, const void* qw_up,
+                           const void* scales_up, const void* zeros_up, int zero_bias_up, void* act,
+                           mcv_stream_t stream) {
+    int rc = MCV_OK;
+    if (!w4_args_ok(qw_gate, scales_gate, zeros_gate, zero_bias_gate, K, N, "mcv_w4a16_gate_up_silu", &rc) ||
+        !w4_args_ok(qw_up, scales_up, zeros_up, zero_bias_up, K, N, "mcv_w4a16_gate_up_silu", &rc))
+        return rc;
+    if (!x || !act) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gate_up_silu: null x/act");
+    if (M <= 0 || M > 65535) return fail(MCV_ERR_SHAPE, "mcv_w4a16_gate_up_silu: M must be in [1, 65535] (M=%lld)", (long long)M);
+    if ((rc = require_device()) != MCV_OK) return rc;
+    const int64_t nslab = ceil_div(N, kSlab);
+    const GemvCfg cfg = choose_gemv(K / kGroup, nslab * M);
+    using Fn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, const uint4*,
+                        const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int, int);
+    Fn fn = cfg.ksplit >= 8 ? w4a16_gate_up_silu_kernel<8>
+          : cfg.ksplit == 4 ? w4a16_gate_up_silu_kernel<4>
+          : cfg.ksplit == 2 ? w4a16_gate_up_silu_kernel<2> : w4a16_gate_up_silu_kernel<1>;
+    const int ks = cfg.ksplit >= 8 ? 8 : cfg.ksplit;
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(M)), dim3(64 * ks), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
+                       static_cast<const uint4*>(qw_gate), static_cast<const uint16_t*>(scales_gate),
+                       static_cast<const uint32_t*>(zeros_gate), static_cast<uint32_t>(zero_bias_gate),
+                       static_cast<const uint4*>(qw_up), static_cast<const uint16_t*>(scales_up),
+                       static_cast<const uint32_t*>(zeros_up), static_cast<uint32_t>(zero_bias_up),
+                       static_cast<uint16_t*>(act), static_cast<int>(K), static_cast<int>(N),
+                       static_cast<int>(nslab * kSlab));
+    return check_launch("w4a16_gate_up_silu_kernel");
 }
 
 int mcv_w4a16_dequant(const void* qw, const void* scales, const void* zeros, int zero_bias, int64_t K, int64_t N,

@@ -253,3 +253,27 @@ def test_lm_head_fused_tree_matches_two_stage(mcv, oracle, cuda, V):
         assert fused == two
         assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
         assert fused == oracle.argmax_f16(la.cpu().view(torch.int16).numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 3584), (2, 1024, 3584), (1, 2048, 6144), (3, 1024, 520), (1, 128, 64)],
+                         ids=lambda v: str(v))
+def test_gate_up_silu_fused(mcv, oracle, cuda, M, K, N):
+    """One launch == gate GEMV, up GEMV, silu_mul (bit-identical), and within
+    tolerance of the oracle's gate/up formula + silu*mul."""
+    torch = _torch()
+    rng = np.random.default_rng(900 + M + K + N)
+    _, qg, zg, sg = synth_w4a16(rng, K, N)
+    _, qu, zu, su = synth_w4a16(rng, K, N)
+    x = f16_normal(rng, (M, K), 1.0)
+    wg, wu = _dev_weight(mcv, qg, zg, sg), _dev_weight(mcv, qu, zu, su)
+    xd = _to_dev(x)
+    fused = mcv.mlp_gate_up_silu_w4a16(xd, wg, wu)
+    g = mcv.matmul_w4a16_gemv(xd, wg)
+    u = mcv.matmul_w4a16_gemv(xd, wu)
+    three = mcv.silu_mul(g, u)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), three.view(torch.int16))
+    g_o = oracle.w4a16_matmul(x, oracle.unpack_awq(qg, zg), sg)
+    u_o = oracle.w4a16_matmul(x, oracle.unpack_awq(qu, zu), su)
+    a_o = oracle.silu_mul(oracle.f2h_rne(g_o), oracle.f2h_rne(u_o))
+    _check(_host_f32(fused), a_o.view(np.float16).astype(np.float32), f"gate_up_silu M={M} K={K} N={N}")
