@@ -334,15 +334,17 @@ int env_int(const char* name, int fallback) {
 }
 
 // One quantisation group (four 16-byte loads per lane) per wave per trip,
-// and enough waves per workgroup (up to 8, at most one per group) that the
+// and enough waves per workgroup (up to 16, at most one per group) that the
 // grid holds >= 8K waves, 32 per CU.  Measured on the lm_head shape (K=1024,
 // 3877 slabs) with graph-replayed launches: 4 waves x 1 group (two trips)
 // 25.4 us, 8 x 1 25.8 us, 4 x 2 27.1 us, 2 x 4 31.0 us; the decode is VALU
-// heavy, so more loads in flight per wave do not pay.  MCV_GEMV_KSPLIT /
-// MCV_GEMV_GPW override the choice (tuning sweeps).
+// heavy, so more loads in flight per wave do not pay.  On the decoder's
+// narrow projections the grid is tiny and the serial trips per wave set the
+// time: K=3584 N=1024 8 x 1 6.45 us, 16 x 1 5.39 us; K=2048 N=1024 4.56 us
+// vs 4.07 us.  MCV_GEMV_KSPLIT / MCV_GEMV_GPW override the choice.
 GemvCfg choose_gemv(int64_t G, int64_t blocks) {
     int ks = 1;
-    while (ks < 8 && blocks * ks < 8192 && ks * 2 <= G) ks *= 2;
+    while (ks < 16 && blocks * ks < 8192 && ks * 2 <= G) ks *= 2;
     const int gpw = 1;
     GemvCfg c{env_int("MCV_GEMV_KSPLIT", ks), env_int("MCV_GEMV_GPW", gpw)};
     if (c.ksplit != 1 && c.ksplit != 2 && c.ksplit != 4 && c.ksplit != 8 && c.ksplit != 16) c.ksplit = ks;
@@ -549,10 +551,12 @@ int mcv_w4a16_gate_up_silu(const void* x, int64_t M, int64_t K, int64_t N, const
     const GemvCfg cfg = choose_gemv(K / kGroup, nslab * M);
     using Fn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, const uint4*,
                         const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int, int);
-    Fn fn = cfg.ksplit >= 8 ? w4a16_gate_up_silu_kernel<8>
-          : cfg.ksplit == 4 ? w4a16_gate_up_silu_kernel<4>
-          : cfg.ksplit == 2 ? w4a16_gate_up_silu_kernel<2> : w4a16_gate_up_silu_kernel<1>;
-    const int ks = cfg.ksplit >= 8 ? 8 : cfg.ksplit;
+    // Same k-split as the GEMV so the fp32 partial sums add in the same order.
+    const int ks = cfg.ksplit;
+    Fn fn = ks >= 16 ? w4a16_gate_up_silu_kernel<16>
+          : ks == 8 ? w4a16_gate_up_silu_kernel<8>
+          : ks == 4 ? w4a16_gate_up_silu_kernel<4>
+          : ks == 2 ? w4a16_gate_up_silu_kernel<2> : w4a16_gate_up_silu_kernel<1>;
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(M)), dim3(64 * ks), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
                        static_cast<const uint4*>(qw_gate), static_cast<const uint16_t*>(scales_gate),

@@ -171,3 +171,23 @@ def test_nk_layout_fused(mcv, cuda):
     xs16 = xs.half()
     assert torch.equal(mcv.matmul_w8a8(xq, xs16, a, use_f32_scale=False), mcv.matmul_w8a8(xq, xs16, c, use_f32_scale=False))
     assert torch.equal(mcv.matmul_w8a8(xq[:3], xs[:3], a), mcv.matmul_w8a8(xq[:3], xs[:3], c))
+
+
+# Every projection of one decode step (K, N): qkv, z, out, gate/up, down of the
+# linear-attention layers and q, k/v, o of the full-attention layers.
+@pytest.mark.parametrize("K,N", [(1024, 6144), (1024, 2048), (2048, 1024), (1024, 3584), (3584, 1024),
+                                 (1024, 4096), (1024, 512), (1024, 16)], ids=lambda v: str(v))
+def test_decode_shapes_fused(mcv, oracle, cuda, K, N):
+    torch = _torch()
+    rng = np.random.default_rng(K * 3 + N)
+    x = f16_normal(rng, (1, K), 1.0)
+    wf = f16_normal(rng, (K, N), 0.02)
+    wq = mcv.quantize_dense_weight_w8a8(_f16_dev(wf))
+    xq, xs, _ = mcv.w8a8_quantize(_f16_dev(x))
+    out = mcv.matmul_w8a8(xq, xs, wq)
+    acc = mcv.matmul_w8a8_i32(xq, wq)
+    q_o, s_o, _ = oracle.w8a8_quantize_act(x)
+    wq_o, ws_o, _ = oracle.w8a8_quantize_weight(wf)
+    acc_o = oracle.gemm_i32(q_o, wq_o)
+    assert np.array_equal(acc.cpu().numpy(), acc_o)
+    assert np.array_equal(_u16(out), oracle.w8a8_dequant(acc_o, s_o, ws_o))
