@@ -186,14 +186,20 @@ def wl_lm_head(pkg, args):
     nbytes = K * V // 2 + (K // 128) * V * 2 + (K // 128) * V // 2 + 2 * V + 2 * K
     # one step = one launch of the fused GEMV + argmax kernel, so the step
     # timing is also the dominant kernel's average launch duration
-    total_ms, kms = time_steps(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
-    token = int(heads[0].token.item())
+    if args.argmax == "slots":
+        # host-finished route: the step is the GEMV leaving tagged slot maxima
+        # (the 64-way fold happens on the host after the copy it makes anyway)
+        total_ms, kms = time_steps(lambda i: heads[i].launch_slots(xd, logits), copies, args.steps, args.warmup)
+        token = heads[0](xd)
+    else:
+        total_ms, kms = time_steps(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
+        token = int(heads[0].token.item())
     res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
-               config={"workload": "w4a16_lm_head_gemv_argmax", "M": 1, "K": K, "V": V,
+               config={"workload": "w4a16_lm_head_gemv_argmax", "M": 1, "K": K, "V": V, "argmax": args.argmax,
                        "weight_copies_rotated": copies, "rotated_bytes": copies * (qw.nbytes + sc.nbytes + zr.nbytes),
                        "algorithmic_bytes_per_step": nbytes, "token": token},
                dtype="w4a16 (f16 x int4, f32 accumulate)",
-               kernel="w4a16_lm_head_kernel<4,1> (GEMV + fused argmax)")
+               kernel=f"w4a16_lm_head_kernel<16,{'kLmSlots' if args.argmax == 'slots' else 'kLmTree'}> (GEMV + fused argmax)")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes)
     return res
@@ -335,6 +341,8 @@ def main():
     ap.add_argument("--K", type=int, default=0)
     ap.add_argument("--N", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--argmax", default="tree", choices=["tree", "slots"],
+                    help="lm_head: token on the device (tree) or host-finished tagged slots")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

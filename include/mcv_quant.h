@@ -191,6 +191,30 @@ int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
                              int zero_bias, void* logits_dev, int64_t* token_dev,
                              void* workspace_dev, mcv_stream_t stream);
 
+/* The greedy lm_head with the last step of the argmax left to the reader of
+ * the token, for callers that copy the token to the host anyway (the
+ * reference's lm_head_greedy returns it to the host, language_model.cpp:
+ * 464-481).  The kernel is the one above, but each workgroup ends with one
+ * fire-and-forget atomicMax of a key tagged with `tag` into one of
+ * MCV_LM_SLOTS slots (MCV_LM_SLOT_STRIDE u64 words apart) of slots_dev
+ * (mcv_lm_head_slots_bytes() bytes, 128-byte aligned), so no workgroup waits
+ * on a device round trip.  Copy the slots to the host and call
+ * mcv_lm_head_slots_token(slots, tag) for the token (same value and tie rule
+ * as mcv_w4a16_lm_head_argmax).  Tags: zero-fill the slots once, then give
+ * every call a tag in [1, MCV_LM_SLOT_TAG_MAX] larger than any tag used since
+ * the last zero-fill (zero-fill again before wrapping).  V < 2^24.  Calls
+ * sharing one slots buffer must not overlap. */
+#define MCV_LM_SLOTS 64
+#define MCV_LM_SLOT_STRIDE 16
+#define MCV_LM_SLOT_TAG_MAX 0xffffffu
+int64_t mcv_lm_head_slots_bytes(void);
+int mcv_w4a16_lm_head_argmax_slots(const void* x_dev, int64_t K, int64_t N, int64_t V,
+                                   const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                                   int zero_bias, void* logits_dev, void* slots_dev, uint32_t tag,
+                                   mcv_stream_t stream);
+/* Host: the token from a host copy of the slots; never fails on valid slots. */
+int64_t mcv_lm_head_slots_token(const uint64_t* slots_host, uint32_t tag);
+
 /* The same greedy lm_head in two launches, for callers that fold the final
  * key reduction into their own next kernel: the GEMV writes logits (may be
  * NULL) and one 64-bit argmax key per 64-column slab to keys_dev (8-byte

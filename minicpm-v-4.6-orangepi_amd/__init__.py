@@ -59,6 +59,10 @@ _SIGS = {
     "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "mcv_lm_head_workspace_bytes": (_c_i64, [_c_i64]),
     "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
+    "mcv_lm_head_slots_bytes": (_c_i64, []),
+    "mcv_w4a16_lm_head_argmax_slots": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp,
+                                                ctypes.c_uint32, _vp]),
+    "mcv_lm_head_slots_token": (_c_i64, [_vp, ctypes.c_uint32]),
     "mcv_w4a16_gemv_argmax_partials": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp]),
     "mcv_argmax_reduce_keys": (_c_int, [_vp, _c_i64, _vp, _vp]),
     "mcv_w8a8_quantize_act": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
@@ -343,31 +347,63 @@ def matmul_w4a16_tiled(x, w_int8, scales, out, stream=None):
 class LmHeadW4A16:
     """Greedy lm_head over a W4A16 weight [K, >= vocab] with the argmax fused
     into the GEMV (replaces lm_head_greedy's 16 chunk matmuls + host scan,
-    src/csrc/lib/language_model.cpp:412-482).  Owns its workspace."""
+    src/csrc/lib/language_model.cpp:412-482).  Owns its workspaces.
+
+    Three routes to the same token: launch() writes it on the device (the
+    in-kernel arrival tree); launch_slots() + read_slots_token() -- what
+    __call__ uses, since it returns the token to the host anyway -- leave
+    call-tagged slot maxima that the host folds after its copy;
+    launch_partials() + reduce_partials() use a second kernel."""
+
+    TAG_MAX = 0xFFFFFF
+    N_SLOTS, SLOT_STRIDE = 64, 16
 
     def __init__(self, w: W4A16QuantizedWeight, vocab: int):
         torch = _torch()
         if vocab > w.N:
             raise McvError(f"vocab {vocab} exceeds weight width {w.N}")
         self.w, self.vocab = w, vocab
+        dev = w.qweight.device
         # zero-filled once; every fused call leaves the combining tree zeroed again
-        self.workspace = torch.zeros(lib().mcv_lm_head_workspace_bytes(vocab), dtype=torch.uint8,
-                                     device=w.qweight.device)
-        self.keys = torch.empty(-(-vocab // SLAB), dtype=torch.int64, device=w.qweight.device)
-        self.token = torch.zeros(1, dtype=torch.int64, device=w.qweight.device)
+        self.workspace = torch.zeros(lib().mcv_lm_head_workspace_bytes(vocab), dtype=torch.uint8, device=dev)
+        self.slots = torch.zeros(lib().mcv_lm_head_slots_bytes() // 8, dtype=torch.int64, device=dev)
+        self.tag = 0
+        self.keys = torch.empty(-(-vocab // SLAB), dtype=torch.int64, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int64, device=dev)
 
-    def launch(self, x, logits=None, stream=None):
-        """Stream-ordered: fills self.token (and logits if given); no sync."""
+    def _check_io(self, x, logits):
         torch = _torch()
         if x.dtype != torch.float16 or x.numel() != self.w.K or not x.is_contiguous():
             raise McvError(f"lm_head x must be contiguous fp16 [1, {self.w.K}]")
         if logits is not None and (logits.dtype != torch.float16 or logits.numel() != self.vocab):
             raise McvError(f"lm_head logits must be fp16 [{self.vocab}]")
+
+    def launch(self, x, logits=None, stream=None):
+        """Stream-ordered: fills self.token (and logits if given); no sync."""
+        self._check_io(x, logits)
         q, s, z = self.w.ptrs()
         _check(lib().mcv_w4a16_lm_head_argmax(_dev(x), self.w.K, self.w.N, self.vocab, q, s, z, self.w.zero_bias,
                                               _dev(logits) if logits is not None else 0, _dev(self.token),
                                               _dev(self.workspace), _stream(stream)), "mcv_w4a16_lm_head_argmax")
         return self.token
+
+    def launch_slots(self, x, logits=None, stream=None) -> int:
+        """Stream-ordered: leaves this call's tagged maxima in self.slots; returns the tag."""
+        self._check_io(x, logits)
+        if self.tag >= self.TAG_MAX:                  # tags must grow: start over from zero-filled slots
+            self.slots.zero_()
+            self.tag = 0
+        self.tag += 1
+        q, s, z = self.w.ptrs()
+        _check(lib().mcv_w4a16_lm_head_argmax_slots(_dev(x), self.w.K, self.w.N, self.vocab, q, s, z,
+                                                    self.w.zero_bias, _dev(logits) if logits is not None else 0,
+                                                    _dev(self.slots), self.tag, _stream(stream)),
+               "mcv_w4a16_lm_head_argmax_slots")
+        return self.tag
+
+    def read_slots_token(self, tag: int) -> int:
+        host = np.ascontiguousarray(self.slots.cpu().numpy())      # synchronising copy
+        return int(lib().mcv_lm_head_slots_token(_np_ptr(host), tag))
 
     def launch_partials(self, x, logits=None, stream=None):
         """First stage only: the GEMV writing logits and per-slab argmax keys."""
@@ -383,8 +419,7 @@ class LmHeadW4A16:
         return self.token
 
     def __call__(self, x, logits=None) -> int:
-        self.launch(x, logits)
-        return int(self.token.item())
+        return self.read_slots_token(self.launch_slots(x, logits))
 
 
 # ----------------------------------------------------------------- W8A8 ----- #

@@ -18,6 +18,8 @@ LmHeadW4A16 make_lm_head_w4a16(W4A16QuantizedWeight weight, int64_t vocab) {
     head.workspace.zero();
     head.token = Tensor({1}, DType::Int64);
     head.token.zero();
+    head.slots = Tensor({mcv_lm_head_slots_bytes()}, DType::UInt8);
+    head.slots.zero();
     return head;
 }
 
@@ -31,6 +33,33 @@ void lm_head_argmax_w4a16(const Tensor& hidden_1xH, LmHeadW4A16& head, Tensor* l
                                        w.zeros.data(), w.zero_bias, logits ? logits->data() : nullptr,
                                        static_cast<int64_t*>(head.token.data()), head.workspace.data(), stream),
               "lm_head_argmax_w4a16");
+}
+
+uint32_t lm_head_argmax_slots_w4a16(const Tensor& hidden_1xH, LmHeadW4A16& head, Tensor* logits, hipStream_t stream) {
+    const W4A16QuantizedWeight& w = head.weight;
+    if (hidden_1xH.dtype() != DType::Float16 || hidden_1xH.shape() != std::vector<int64_t>{1, w.K})
+        throw std::runtime_error("lm_head hidden must be fp16 [1, hidden_size]");
+    if (logits && (logits->dtype() != DType::Float16 || static_cast<int64_t>(logits->numel()) != head.vocab))
+        throw std::runtime_error("lm_head logits must be fp16 [1, vocab]");
+    if (head.tag >= MCV_LM_SLOT_TAG_MAX) {          // tags must grow: start over from zero-filled slots
+        check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        head.slots.zero();
+        head.tag = 0;
+    }
+    const uint32_t tag = ++head.tag;
+    check_mcv(mcv_w4a16_lm_head_argmax_slots(hidden_1xH.data(), w.K, w.N, head.vocab, w.w_int8.data(),
+                                             w.scales.data(), w.zeros.data(), w.zero_bias,
+                                             logits ? logits->data() : nullptr, head.slots.data(), tag, stream),
+              "lm_head_argmax_slots_w4a16");
+    return tag;
+}
+
+int64_t lm_head_read_slots_token(const LmHeadW4A16& head, uint32_t tag, hipStream_t stream) {
+    uint64_t host[MCV_LM_SLOTS * MCV_LM_SLOT_STRIDE];
+    check_hip(hipMemcpyAsync(host, head.slots.data(), sizeof(host), hipMemcpyDeviceToHost, stream),
+              "hipMemcpyAsync slots");
+    check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    return mcv_lm_head_slots_token(host, tag);
 }
 
 namespace {
@@ -57,8 +86,8 @@ int64_t lm_head_greedy_w4a16(const Tensor& last_hidden_1xH, const Tensor* final_
                              LmHeadW4A16& head, hipStream_t stream) {
     Tensor normed;
     const Tensor& x = maybe_norm(last_hidden_1xH, final_norm, rms_epsilon, normed, stream);
-    lm_head_argmax_w4a16(x, head, nullptr, stream);
-    return read_token(head.token, stream);
+    const uint32_t tag = lm_head_argmax_slots_w4a16(x, head, nullptr, stream);
+    return lm_head_read_slots_token(head, tag, stream);
 }
 
 int64_t lm_head_greedy_w8a8(const Tensor& last_hidden_1xH, const Tensor* final_norm, double rms_epsilon,

@@ -29,10 +29,23 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t smask, uint32_t 
     return r;
 }
 
+// The group's 128 activation values as 64 half2 words.  The index is
+// wave-uniform, so these become scalar loads into SGPRs.
+__device__ __forceinline__ void load_x_group(const uint32_t* __restrict__ xw, int g, uint32_t (&xs)[64]) {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) xs[i] = xw[g * 64 + i];
+}
+
+// Every load of one trip (weights, scale, zero word, activations) is issued
+// before the first wait: left alone, the scheduler sinks the scale and the
+// activation loads below the waits for the weight words, which costs each
+// trip a second full memory latency.
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 // Adds the contribution of one quantisation group (four 16-byte chunks of this
-// lane's column) to `acc`.
-__device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t* __restrict__ xw, int g,
-                                           uint32_t z, float scale, float acc, uint32_t vmagic) {
+// lane's column, activations `xs`) to `acc`.
+__device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t (&xs)[64], uint32_t z, float scale,
+                                           float acc, uint32_t vmagic) {
     const uint32_t zlo = (0x6400u + z) * 0x10001u;          // half2(1024 + z)
     const uint32_t zhi = (0x6400u + (z << 4)) * 0x10001u;   // half2(1024 + 16 z)
     const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
@@ -43,17 +56,17 @@ __device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t*
         const uint32_t words[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const int kw = (g * kGroup + c * kChunkK + w * 8) >> 1;   // half2 index into x
+            const int kw = (c * kChunkK + w * 8) >> 1;                // half2 index into xs
             const uint32_t q = words[w];
             const uint32_t q8 = q >> 8;
             const half2_t p0 = as_h2(and_or(q, mlo, vmagic)) - as_h2(zlo);    // k+0, k+1
             const half2_t p1 = as_h2(and_or(q, mhi, vmagic)) - as_h2(zhi);    // k+2, k+3 (x16)
             const half2_t p2 = as_h2(and_or(q8, mlo, vmagic)) - as_h2(zlo);   // k+4, k+5
             const half2_t p3 = as_h2(and_or(q8, mhi, vmagic)) - as_h2(zhi);   // k+6, k+7 (x16)
-            alo = __builtin_amdgcn_fdot2(p0, as_h2(xw[kw + 0]), alo, false);
-            ahi = __builtin_amdgcn_fdot2(p1, as_h2(xw[kw + 1]), ahi, false);
-            alo = __builtin_amdgcn_fdot2(p2, as_h2(xw[kw + 2]), alo, false);
-            ahi = __builtin_amdgcn_fdot2(p3, as_h2(xw[kw + 3]), ahi, false);
+            alo = __builtin_amdgcn_fdot2(p0, as_h2(xs[kw + 0]), alo, false);
+            ahi = __builtin_amdgcn_fdot2(p1, as_h2(xs[kw + 1]), ahi, false);
+            alo = __builtin_amdgcn_fdot2(p2, as_h2(xs[kw + 2]), alo, false);
+            ahi = __builtin_amdgcn_fdot2(p3, as_h2(xs[kw + 3]), ahi, false);
         }
     }
     return fmaf(alo + ahi * 0.0625f, scale, acc);
@@ -150,7 +163,12 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
 #pragma unroll
         for (int i = 0; i < GPW; ++i) {
             const int g = gb + i;
-            if (g < G) acc = group_dot(wv[i], xw, g, ((zv[i] >> zshift) & 15u) + zero_bias, h2f(sv[i]), acc, vmagic);
+            if (g < G) {
+                uint32_t xs[64];
+                load_x_group(xw, g, xs);
+                if (i == 0) issue_fence();
+                acc = group_dot(wv[i], xs, ((zv[i] >> zshift) & 15u) + zero_bias, h2f(sv[i]), acc, vmagic);
+            }
         }
     }
 
@@ -173,18 +191,39 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
     }
 }
 
-// Greedy lm_head: the GEMV above with the argmax fused.  A workgroup may walk
-// SPW consecutive slabs (fewer arrivals at the cross-workgroup argmax); on the
-// lm_head shape one slab per workgroup measures best (graph-replayed, MI355X:
-// SPW 1/2/4/8 = 27.2/28.6/28.9/31.3 us against 26.4 us for the bare GEMV).
-// Waves split K as in the GEMV; their partial sums meet in a double-buffered
-// LDS array, so one barrier per slab suffices.
-template <int KSPLIT, int SPW>
-__global__ __launch_bounds__(64 * KSPLIT) void w4a16_lm_head_kernel(
+// Greedy lm_head: the GEMV with the argmax folded in.  Eight waves per
+// workgroup, wave w owning quantisation groups w, w + 8, ...; a workgroup
+// walks SPW consecutive slabs.  When K <= 1024 (one group per wave) the
+// activation group stays in SGPRs for the whole workgroup and the next slab's
+// weight, scale and zero loads are issued before the current slab is
+// decoded.  Per-slab partial sums go to LDS and meet after one barrier (idle
+// waves contribute -0.0, the exact additive identity, so the sums equal the
+// GEMV's whenever that also gives each wave one group).  The best key then
+// leaves through one of two routes:
+//   kLmTree  -- the fence-free 64-slot arrival tree above; the last arrival
+//               writes the token (four device round trips after the last
+//               workgroup);
+//   kLmSlots -- one fire-and-forget atomicMax of a call-tagged key into one
+//               of 64 slots; whoever reads the token takes the maximum of the
+//               slots that carry this call's tag (the host, after the copy it
+//               makes anyway).  Slot key bits: 63..40 tag, 39..24 the fp16
+//               key, 23..0 the complement of the column index.
+// Measured on the lm_head shape (MI355X, 8 rotated weight copies, graph-
+// replayed): SPW 16 (243 workgroups) with the tree 26.9-27.2 us, with slots
+// 25.7-26.0 us; SPW 8 27.1-27.3 / 26.4-27.0 us; SPW 1-4 28-30 us; the former
+// one-slab, four-wave kernel ~27.9 us.  Direct launches run ~1 us faster.
+constexpr int kLmWaves = 8;
+constexpr int kLmTree = 0;
+constexpr int kLmSlots = 1;
+constexpr int kSlotStride = 16;                              // u64 words per slot: 128 B
+
+template <int SPW, int MODE>
+__global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ logits, int K, int V, int Npad,
-    int nslab, unsigned long long* __restrict__ ws, int64_t* __restrict__ token) {
-    __shared__ float red[2][KSPLIT][kSlab];
+    int nslab, unsigned long long* __restrict__ ws, int64_t* __restrict__ token, uint32_t tag) {
+    __shared__ float part[SPW][kLmWaves][kSlab];
+    __shared__ unsigned long long wbest[kLmWaves];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = K / kGroup;
@@ -193,38 +232,85 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_lm_head_kernel(
     const uint32_t* __restrict__ xw = reinterpret_cast<const uint32_t*>(x);
     uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
     asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
-    unsigned long long best = 0ull;
     const int s0 = static_cast<int>(blockIdx.x) * SPW;
+    const int ns = nslab - s0 < SPW ? nslab - s0 : SPW;                  // workgroup-uniform
+    const uint32_t zshift = (lane & 7) * 4;                              // slab bases are multiples of 8 columns
+    const uint4* __restrict__ wbase = qw + lane;
+    const uint16_t* __restrict__ sbase = scales + lane;
+    const uint32_t* __restrict__ zbase = zeros + (lane >> 3);
+    auto issue = [&](uint4 (&wv)[4], uint16_t& sv, uint32_t& zv, int slab, int g) {
+        const uint4* __restrict__ p = wbase + (static_cast<size_t>(slab) * C + g * 4) * kSlab;
 #pragma unroll
-    for (int si = 0; si < SPW; ++si) {
-        const int slab = s0 + si;
-        if (slab >= nslab) break;                                       // workgroup-uniform
-        const int n = slab * kSlab + lane;
-        const uint4* __restrict__ wp = qw + static_cast<size_t>(slab) * C * kSlab + lane;
-        const uint32_t zshift = (n & 7) * 4;
-        float acc = 0.f;
-        for (int g = wave; g < G; g += KSPLIT) {
-            uint4 wv[4];
+        for (int c = 0; c < 4; ++c) wv[c] = p[c * kSlab];
+        sv = sbase[static_cast<size_t>(g) * Npad + slab * kSlab];
+        zv = zbase[static_cast<size_t>(g) * zstride + slab * (kSlab / 8)];
+    };
+
+    if (G <= kLmWaves && ns == SPW) {
+        if (wave < G) {
+            uint32_t xs[64];
+            load_x_group(xw, wave, xs);
+            uint4 wv[2][4];
+            uint16_t sv[2];
+            uint32_t zv[2];
+            issue(wv[0], sv[0], zv[0], s0, wave);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) wv[c] = wp[static_cast<size_t>(g * 4 + c) * kSlab];
-            const uint16_t sv = scales[static_cast<size_t>(g) * Npad + n];
-            const uint32_t zv = zeros[static_cast<size_t>(g) * zstride + (n >> 3)];
-            acc = group_dot(wv, xw, g, ((zv >> zshift) & 15u) + zero_bias, h2f(sv), acc, vmagic);
+            for (int i = 0; i < SPW; ++i) {
+                if (i + 1 < SPW) issue(wv[(i + 1) & 1], sv[(i + 1) & 1], zv[(i + 1) & 1], s0 + i + 1, wave);
+                issue_fence();
+                part[i][wave][lane] = group_dot(wv[i & 1], xs, ((zv[i & 1] >> zshift) & 15u) + zero_bias,
+                                                h2f(sv[i & 1]), 0.f, vmagic);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < SPW; ++i) part[i][wave][lane] = -0.0f;
         }
-        red[si & 1][wave][lane] = acc;
-        __syncthreads();
-        if (wave == 0) {
-            acc = red[si & 1][0][lane];
-#pragma unroll
-            for (int w = 1; w < KSPLIT; ++w) acc += red[si & 1][w][lane];
-            const uint16_t h = f2h(acc);
-            if (logits != nullptr && n < V) logits[n] = h;
-            const unsigned long long key = n < V ? argmax_key64(argmax_key16(h), static_cast<uint32_t>(n)) : 0ull;
-            best = key > best ? key : best;
+    } else {
+        for (int i = 0; i < ns; ++i) {
+            float acc = -0.0f;
+            for (int g = wave; g < G; g += kLmWaves) {
+                uint4 wv[4];
+                uint16_t sv;
+                uint32_t zv;
+                issue(wv, sv, zv, s0 + i, g);
+                uint32_t xs[64];
+                load_x_group(xw, g, xs);
+                issue_fence();
+                acc = group_dot(wv, xs, ((zv >> zshift) & 15u) + zero_bias, h2f(sv), g == wave ? 0.f : acc, vmagic);
+            }
+            part[i][wave][lane] = acc;
         }
     }
+    __syncthreads();
+
+    unsigned long long best = 0ull;
+    for (int i = wave; i < ns; i += kLmWaves) {
+        float acc = part[i][0][lane];
+#pragma unroll
+        for (int w = 1; w < kLmWaves; ++w) acc += part[i][w][lane];
+        const int n = (s0 + i) * kSlab + lane;
+        const uint16_t h = f2h(acc);
+        if (logits != nullptr && n < V) logits[n] = h;
+        const unsigned long long key = n < V ? argmax_key64(argmax_key16(h), static_cast<uint32_t>(n)) : 0ull;
+        best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
     if (wave != 0) return;
-    argmax_arrive(ws, wave_max_u64(best), static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token);
+    best = wave_max_u64(lane < kLmWaves ? wbest[lane] : 0ull);
+    if constexpr (MODE == kLmTree) {
+        argmax_arrive(ws, best, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token);
+    } else {
+        if (lane == 0) {
+            // argmax_key64 -> slot key: the fp16 key moves to bits 39..24, the
+            // index complement keeps its low 24 bits (V < 2^24)
+            const unsigned long long k16 = best >> 32;
+            const unsigned long long idx = best & 0xffffffull;
+            atomicMax(ws + (blockIdx.x & (kTreeWords - 1)) * kSlotStride,
+                      (static_cast<unsigned long long>(tag) << 40) | (k16 << 24) | (k16 ? idx : 0ull));
+        }
+    }
 }
 
 // Decode MLP front half in one launch: act = silu(x . Wgate) * (x . Wup).
@@ -262,8 +348,11 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gate_up_silu_kernel(
         const uint16_t sgv = sg[static_cast<size_t>(g) * Npad + n], suv = su[static_cast<size_t>(g) * Npad + n];
         const uint32_t zgv = zg[static_cast<size_t>(g) * zstride + (n >> 3)];
         const uint32_t zuv = zu[static_cast<size_t>(g) * zstride + (n >> 3)];
-        ag = group_dot(wgv, xw, g, ((zgv >> zshift) & 15u) + zbg, h2f(sgv), ag, vmagic);
-        au = group_dot(wuv, xw, g, ((zuv >> zshift) & 15u) + zbu, h2f(suv), au, vmagic);
+        uint32_t xs[64];
+        load_x_group(xw, g, xs);
+        issue_fence();
+        ag = group_dot(wgv, xs, ((zgv >> zshift) & 15u) + zbg, h2f(sgv), ag, vmagic);
+        au = group_dot(wuv, xs, ((zuv >> zshift) & 15u) + zbu, h2f(suv), au, vmagic);
     }
     if constexpr (KSPLIT > 1) {
         red[0][wave][lane] = ag;
@@ -447,6 +536,34 @@ int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void
     return check_launch("w4a16_gemv_kernel");
 }
 
+// Shared launcher of both argmax routes.  SPW 16 measured best on the
+// lm_head shape; MCV_LMHEAD_SPW (1, 2, 4, 8, 16) overrides it for sweeps.
+int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* qw, const void* scales,
+                   const void* zeros, int zero_bias, void* logits, int64_t* token, void* ws, uint32_t tag, int mode,
+                   hipStream_t stream) {
+    const int64_t nslab = ceil_div(V, kSlab);
+    const int64_t npad = ceil_div(N, kSlab) * kSlab;
+    int spw = env_int("MCV_LMHEAD_SPW", 16);
+    if (spw != 1 && spw != 2 && spw != 4 && spw != 8 && spw != 16) spw = 16;
+    using LmFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int,
+                          int, int, unsigned long long*, int64_t*, uint32_t);
+    LmFn fn = nullptr;
+#define MCV_LM(SPW_)                                                                                  \
+    if (spw == SPW_)                                                                                  \
+        fn = mode == kLmTree ? w4a16_lm_head_kernel<SPW_, kLmTree> : w4a16_lm_head_kernel<SPW_, kLmSlots>;
+    MCV_LM(1) MCV_LM(2) MCV_LM(4) MCV_LM(8) MCV_LM(16)
+#undef MCV_LM
+    const int64_t nblk = ceil_div(nslab, spw);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nblk)), dim3(64 * kLmWaves), 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
+                       static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
+                       static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(logits), static_cast<int>(K),
+                       static_cast<int>(V), static_cast<int>(npad), static_cast<int>(nslab),
+                       static_cast<unsigned long long*>(ws), token, tag);
+    return check_launch("w4a16_lm_head_kernel");
+}
+
+
 }  // namespace mcv
 
 using namespace mcv;
@@ -511,29 +628,42 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
     if (reinterpret_cast<uintptr_t>(workspace) % 128 != 0)
         return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: workspace must be 128-byte aligned");
     if ((rc = require_device()) != MCV_OK) return rc;
-    const int64_t nslab = ceil_div(V, kSlab);
-    const int64_t npad = ceil_div(N, kSlab) * kSlab;
-    // 4 waves per slab and one slab per workgroup, as measured best on the
-    // lm_head shape; MCV_LMHEAD_SPW overrides the latter for sweeps.
-    int spw = env_int("MCV_LMHEAD_SPW", 1);
-    if (spw != 1 && spw != 2 && spw != 4 && spw != 8) spw = 1;
-    const int ks = K / kGroup >= 4 ? 4 : static_cast<int>(K / kGroup);
-    using LmFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int,
-                          int, int, unsigned long long*, int64_t*);
-    LmFn fn = nullptr;
-#define MCV_LM(KS_, SPW_) \
-    if (ks == KS_ && spw == SPW_) fn = w4a16_lm_head_kernel<KS_, SPW_>;
-    MCV_LM(4, 1) MCV_LM(4, 2) MCV_LM(4, 4) MCV_LM(4, 8) MCV_LM(2, 1) MCV_LM(2, 2) MCV_LM(2, 4) MCV_LM(2, 8)
-    MCV_LM(1, 1) MCV_LM(1, 2) MCV_LM(1, 4) MCV_LM(1, 8)
-#undef MCV_LM
-    const int64_t nblk = ceil_div(nslab, spw);
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nblk)), dim3(64 * ks), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
-                       static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
-                       static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(logits), static_cast<int>(K),
-                       static_cast<int>(V), static_cast<int>(npad), static_cast<int>(nslab),
-                       static_cast<unsigned long long*>(workspace), token);
-    return check_launch("w4a16_lm_head_kernel");
+    return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, token, workspace, 0u, kLmTree,
+                          static_cast<hipStream_t>(stream));
+}
+
+int64_t mcv_lm_head_slots_bytes(void) { return int64_t(kTreeWords) * kSlotStride * 8; }
+
+int mcv_w4a16_lm_head_argmax_slots(const void* x, int64_t K, int64_t N, int64_t V, const void* qw,
+                                   const void* scales, const void* zeros, int zero_bias, void* logits, void* slots,
+                                   uint32_t tag, mcv_stream_t stream) {
+    int rc = MCV_OK;
+    if (!w4_args_ok(qw, scales, zeros, zero_bias, K, N, "mcv_w4a16_lm_head_argmax_slots", &rc)) return rc;
+    if (!x || !slots) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax_slots: null x/slots");
+    if (V <= 0 || V > N) return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax_slots: need 0 < V <= N (V=%lld N=%lld)",
+                                     (long long)V, (long long)N);
+    if (V >= (int64_t(1) << 24))
+        return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax_slots: V must be below 2^24 (V=%lld)", (long long)V);
+    if (tag == 0 || tag > MCV_LM_SLOT_TAG_MAX)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax_slots: tag must be in [1, 2^24 - 1] (tag=%u)", tag);
+    if (reinterpret_cast<uintptr_t>(slots) % 128 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax_slots: slots must be 128-byte aligned");
+    if ((rc = require_device()) != MCV_OK) return rc;
+    return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, nullptr, slots, tag, kLmSlots,
+                          static_cast<hipStream_t>(stream));
+}
+
+int64_t mcv_lm_head_slots_token(const uint64_t* slots_host, uint32_t tag) {
+    if (!slots_host) return fail(MCV_ERR_INVALID_ARG, "mcv_lm_head_slots_token: null slots");
+    uint64_t best = 0;
+    for (int j = 0; j < kTreeWords; ++j) {
+        const uint64_t k = slots_host[static_cast<size_t>(j) * kSlotStride];
+        if ((k >> 40) != tag) continue;                                  // no workgroup of this call used slot j
+        const uint64_t v = k & 0xffffffffffull;
+        best = v > best ? v : best;
+    }
+    if ((best >> 24) == 0) return 0;                                    // no candidate (every logit NaN or -inf)
+    return static_cast<int64_t>(0xffffffu - static_cast<uint32_t>(best & 0xffffffu));
 }
 
 int mcv_w4a16_gate_up_silu(const void* x, int64_t M, int64_t K, int64_t N, const void* qw_gate,

@@ -173,3 +173,32 @@ def test_device_entry_fails_loudly_without_gpu(mcv):
     fake = ctypes.c_void_p(0x1000)
     rc = L.mcv_w4a16_gemm(fake, 1, 1024, 64, fake, fake, fake, 0, fake, None)
     assert rc == 5, L.mcv_last_error()
+
+
+def test_lm_head_slots_token_known_answer(mcv):
+    """Host fold of the tagged slot maxima: only this call's tag counts, the
+    larger fp16 key wins, ties go to the smaller column, no candidate -> 0."""
+    L = mcv.lib()
+    stride = 16
+    slots = np.zeros(64 * stride, np.uint64)
+
+    def key(tag, h16, n):
+        k16 = (h16 | 0x8000) if not (h16 & 0x8000) else (~h16 & 0xFFFF)
+        return np.uint64((tag << 40) | (k16 << 24) | (0xFFFFFF - n))
+
+    slots[3 * stride] = key(5, 0x3C00, 100)          # 1.0 at column 100
+    slots[7 * stride] = key(5, 0x3C00, 50)           # 1.0 at column 50: tie, smaller index wins
+    slots[9 * stride] = key(4, 0x4000, 7)            # 2.0, but an older call's tag
+    slots[11 * stride] = key(5, 0xBC00, 3)           # -1.0
+    assert L.mcv_lm_head_slots_token(slots.ctypes.data, 5) == 50
+    assert L.mcv_lm_head_slots_token(slots.ctypes.data, 4) == 7
+    assert L.mcv_lm_head_slots_token(slots.ctypes.data, 6) == 0      # no slot carries tag 6
+    empty = np.zeros(64 * stride, np.uint64)
+    empty[0] = np.uint64(9 << 40)                                    # present, but no candidate
+    assert L.mcv_lm_head_slots_token(empty.ctypes.data, 9) == 0
+    assert L.mcv_lm_head_slots_bytes() == 64 * stride * 8
+    fake = ctypes.c_void_p(0x1000)
+    assert L.mcv_w4a16_lm_head_argmax_slots(fake, 1024, 1024, 1024, fake, fake, fake, 0, None, fake, 0, None) == 1
+    assert b"tag" in L.mcv_last_error()
+    big = 1 << 24
+    assert L.mcv_w4a16_lm_head_argmax_slots(fake, 128, big, big, fake, fake, fake, 0, None, fake, 1, None) == 2

@@ -195,7 +195,7 @@ def test_lm_head_config3(mcv, oracle, cuda):
     w = _dev_weight(mcv, qweight, qzeros, scales)
     head = mcv.LmHeadW4A16(w, V)
     logits = torch.empty(V, dtype=torch.float16, device="cuda")
-    tok = head(_to_dev(x), logits)
+    tok = head(_to_dev(x), logits)                      # host-finished slots route
     got16 = logits.cpu().view(torch.int16).numpy().view(np.uint16)
     ref = oracle.w4a16_matmul(x, oracle.unpack_awq(qweight, qzeros), scales)[0, :V]
     _check(got16.view(np.float16).astype(np.float32), ref, "lm_head logits")
@@ -205,7 +205,12 @@ def test_lm_head_config3(mcv, oracle, cuda):
     top2 = np.sort(ref)[-2:]
     assert top2[1] - top2[0] > 1e-2
     assert tok == int(np.argmax(ref))
-    # repeated calls (workspace reused) give the same answer
+    # the device-token route: same token, same logits, workspace left zeroed
+    lt = torch.empty(V, dtype=torch.float16, device="cuda")
+    assert int(head.launch(_to_dev(x), lt).item()) == tok
+    assert torch.equal(lt.view(torch.int16), logits.view(torch.int16))
+    assert int(head.workspace.count_nonzero()) == 0
+    # repeated calls (slots and workspace reused) give the same answer
     assert head(_to_dev(x)) == tok
     assert head(_to_dev(x), logits) == tok
 
@@ -226,15 +231,38 @@ def test_lm_head_small_and_ties(mcv, oracle, cuda, V):
     tok = head(_to_dev(x), logits)
     got16 = logits.cpu().view(torch.int16).numpy().view(np.uint16)
     assert tok == oracle.argmax_f16(got16)
+    assert int(head.launch(_to_dev(x)).item()) == tok
     full = _host_f32(mcv.matmul_w4a16(_to_dev(x), w))[0, :V]
     assert np.array_equal(full.astype(np.float16).view(np.uint16), got16)
 
 
+# K = 2048 takes the generic path (two groups per wave); V = 1000 leaves the
+# last workgroup with a partial run of slabs; zero_bias = 1 is GPTQ's zero + 1.
+@pytest.mark.parametrize("K,V,zb", [(1024, 1000, 0), (2048, 1000, 0), (2048, 5000, 1), (128, 777, 1)])
+def test_lm_head_shapes(mcv, oracle, cuda, K, V, zb):
+    torch = _torch()
+    rng = np.random.default_rng(K + V + zb)
+    NW = -(-V // 8) * 8
+    _, qweight, qzeros, scales = synth_w4a16(rng, K, NW)
+    x = f16_normal(rng, (1, K), 1.0)
+    w = _dev_weight(mcv, qweight, qzeros, scales)
+    if zb:
+        w = mcv.W4A16QuantizedWeight(w.qweight, w.scales, w.zeros, K, NW, 1)
+    head = mcv.LmHeadW4A16(w, V)
+    logits = torch.empty(V, dtype=torch.float16, device="cuda")
+    tok = head(_to_dev(x), logits)
+    got16 = logits.cpu().view(torch.int16).numpy().view(np.uint16)
+    w8 = oracle.unpack_awq(qweight, qzeros) - np.int8(zb)
+    _check(got16.view(np.float16).astype(np.float32), oracle.w4a16_matmul(x, w8, scales)[0, :V], "lm_head")
+    assert tok == oracle.argmax_f16(got16)
+    assert int(head.launch(_to_dev(x)).item()) == tok
+
+
 @pytest.mark.parametrize("V", [4097, 8320, 100000])
-def test_lm_head_fused_tree_matches_two_stage(mcv, oracle, cuda, V):
-    """The fence-free slot tree (64 level-1 slots, uneven arrival counts
-    when ceil(V/64) is not a multiple of 64) gives the same token and logits as
-    the plain per-slab keys + reduction, and leaves its workspace zeroed."""
+def test_lm_head_routes_agree(mcv, oracle, cuda, V):
+    """The in-kernel arrival tree (64 level-1 slots, uneven arrival counts),
+    the host-finished tagged slots and the two-kernel keys + reduction give
+    the same token and logits; the tree leaves its workspace zeroed."""
     torch = _torch()
     K, NW = 512, -(-V // 8) * 8
     rng = np.random.default_rng(V + 11)
@@ -246,13 +274,33 @@ def test_lm_head_fused_tree_matches_two_stage(mcv, oracle, cuda, V):
         x = _to_dev(f16_normal(rng, (1, K), 1.0 + trial))
         la = torch.empty(V, dtype=torch.float16, device="cuda")
         lb = torch.empty(V, dtype=torch.float16, device="cuda")
-        fused = head(x, la)
+        lc = torch.empty(V, dtype=torch.float16, device="cuda")
+        tree = int(head.launch(x, la).item())
         assert int(head.workspace.count_nonzero()) == 0
         head.launch_partials(x, lb)
         two = int(head.reduce_partials().item())
-        assert fused == two
+        slots = head(x, lc)
+        assert tree == two == slots
         assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
-        assert fused == oracle.argmax_f16(la.cpu().view(torch.int16).numpy().view(np.uint16))
+        assert torch.equal(la.view(torch.int16), lc.view(torch.int16))
+        assert tree == oracle.argmax_f16(la.cpu().view(torch.int16).numpy().view(np.uint16))
+
+
+def test_lm_head_slot_tag_wrap(mcv, oracle, cuda):
+    """Tags grow call by call; at the wrap the slots are zero-filled again and
+    an older call's larger tag cannot leak into the next token."""
+    torch = _torch()
+    K, V = 256, 3000
+    rng = np.random.default_rng(42)
+    qweight, qzeros, scales = mcv.quantize_int4(f16_normal(rng, (K, V), 0.02))
+    head = mcv.LmHeadW4A16(_dev_weight(mcv, qweight, qzeros, scales), V)
+    xa, xb = (_to_dev(f16_normal(rng, (1, K), 1.0)) for _ in range(2))
+    ta, tb = int(head.launch(xa).item()), int(head.launch(xb).item())
+    assert ta != tb
+    head.tag = head.TAG_MAX - 1
+    assert head(xa) == ta and head.tag == head.TAG_MAX
+    assert head(xb) == tb and head.tag == 1
+    assert head(xa) == ta and head.tag == 2
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 3584), (2, 1024, 3584), (1, 2048, 6144), (3, 1024, 520), (1, 128, 64)],
