@@ -68,11 +68,11 @@ struct Cfg8 {
     static constexpr int kLdsAlloc = kLdsBytes > kRedBytes ? kLdsBytes : kRedBytes;
 };
 
-template <int TM, int WN, int KS, bool OUT_F16>
+template <int TM, int WN, int KS, int DEPTH, bool OUT_F16>
 __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
     const int8_t* __restrict__ xq, const int8_t* __restrict__ w, int M, int K, int N, int KB, void* __restrict__ out,
     const void* __restrict__ xs, int xs16, const void* __restrict__ ws, int ws16, int nslab, int n_tiles,
-    int total_tiles, int KT) {
+    int total_tiles, int KT, int col_major) {
     using C = Cfg8<TM, WN, KS>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[C::kLdsAlloc];
 
@@ -81,9 +81,13 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kp = wave / WN;
     const int wn = wave - kp * WN;
+    // Each XCD gets a contiguous run of tiles (xcd_tile); col_major orders
+    // that run down the columns of tiles, so an XCD's L2 holds a few weight
+    // slabs and re-reads of the smaller x operand cross XCDs instead.
     const int tile = xcd_tile(static_cast<int>(blockIdx.x), total_tiles);
-    const int tm = tile / n_tiles;
-    const int tn = tile - tm * n_tiles;
+    const int m_tiles = total_tiles / n_tiles;
+    const int tm = col_major ? tile % m_tiles : tile / n_tiles;
+    const int tn = col_major ? tile / m_tiles : tile - tm * n_tiles;
     const int m0 = tm * TM;
     const int slab = tn * WN + wn;
     const int kt0 = kp * KT;                   // first stage of this k-part
@@ -105,15 +109,22 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
         int4_t b[C::kBVec];     // [k32 step][half]
     };
     constexpr int kItems = C::kAVec + C::kBVec;
+    // Stages past this k-part's last are loaded from an offset beyond both
+    // buffers: the loads still issue (no branch, so the waits stay exact) but
+    // return zero without touching memory.
+    constexpr uint32_t kNowhere = 0xFFFFFF00u;
     auto load_item = [&](int kt, Set& st, int it) {
+        const bool live = kt < KT;
         const int k0 = (kt0 + kt) * C::BK;
         if (it < C::kAVec) {
             const int idx = at + it * C::kAThreads;
-            const uint32_t off = static_cast<uint32_t>((idx / kVecPerRow) * K + k0 + (idx % kVecPerRow) * 16);
+            const uint32_t off = live ? static_cast<uint32_t>((idx / kVecPerRow) * K + k0 + (idx % kVecPerRow) * 16)
+                                      : kNowhere;
             st.a[it] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
         } else {
             const int b = it - C::kAVec;       // step * 2 + half
-            const uint32_t off = wbase + static_cast<uint32_t>((k0 / 32 + (b >> 1)) * 2 + (b & 1)) * kW8Block;
+            const uint32_t off = live ? wbase + static_cast<uint32_t>((k0 / 32 + (b >> 1)) * 2 + (b & 1)) * kW8Block
+                                      : kNowhere;
             st.b[b] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
         }
     };
@@ -131,11 +142,36 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
+    // The fused epilogue's scales are loaded now, off the critical path: the
+    // lane's 32 columns' weight scales (zero past N) and its rows' x scales.
+    // Transposed blocks: register r of lane l holds row 32 i + l%32 and column
+    // 32 j + 8 (r/4) + 4 (l/32) + r%4.
+    const int h = lane >> 5;
+    float wsv[2][4][4];
+    float xsv_all[C::MB];
+    if constexpr (OUT_F16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int col = slab * kSlab + 32 * j + 8 * g + 4 * h + e;
+                    wsv[j][g][e] = col < N ? scale_at(ws, ws16, col) : 0.f;
+                }
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) {
+            const int row = m0 + 32 * i + (lane & 31);
+            xsv_all[i] = row < M ? scale_at(xs, xs16, row) : 0.f;
+        }
+    }
+
     // Stage kt: weights from `cur`, x from LDS buffer kt&1.  During its k32
-    // steps the x vectors of stage kt+1 (`nxt`, loaded a stage ago) move to
-    // the other LDS buffer and stage kt+2 is loaded into `fut`.
+    // steps the x vectors of stage kt+1 (`nxt`, loaded earlier) move to the
+    // other LDS buffer and stage kt+DEPTH is loaded into `fut`, the register
+    // set stage kt-1 has just released.
     auto step = [&](int kt, Set& cur, Set& nxt, Set& fut) {
-        const int kn = kt + 2 < KT ? kt + 2 : KT - 1;
+        const int kn = kt + DEPTH;
         const bool store = kt + 1 < KT;
         const uint8_t* A = As + (kt & 1) * C::kAStage + (lane & 31) * C::PITCH + (lane >> 5) * 16;
         int4_t af[2][C::MB];
@@ -164,22 +200,24 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
         __syncthreads();
     };
 
-    Set s0, s1, s2;
+    // A ring of DEPTH + 1 register sets: stage kt lives in set kt % (DEPTH + 1).
+    constexpr int R = DEPTH + 1;
+    Set sets[R];
 #pragma unroll
-    for (int it = 0; it < kItems; ++it) load_item(0, s0, it);
+    for (int d = 0; d < DEPTH; ++d)
 #pragma unroll
-    for (int it = 0; it < kItems; ++it) load_item(KT > 1 ? 1 : 0, s1, it);
+        for (int it = 0; it < kItems; ++it) load_item(d, sets[d], it);
 #pragma unroll
-    for (int it = 0; it < C::kAVec; ++it) store_a(0, s0, it);
+    for (int it = 0; it < C::kAVec; ++it) store_a(0, sets[0], it);
     __syncthreads();
     int kt = 0;
-    for (; kt + 2 < KT; kt += 3) {
-        step(kt, s0, s1, s2);
-        step(kt + 1, s1, s2, s0);
-        step(kt + 2, s2, s0, s1);
+    for (; kt + R <= KT; kt += R) {
+#pragma unroll
+        for (int u = 0; u < R; ++u) step(kt + u, sets[u], sets[(u + 1) % R], sets[(u + DEPTH) % R]);
     }
-    if (kt < KT) step(kt, s0, s1, s2);
-    if (kt + 1 < KT) step(kt + 1, s1, s2, s0);
+#pragma unroll
+    for (int u = 0; u < R - 1; ++u)
+        if (kt + u < KT) step(kt + u, sets[u], sets[(u + 1) % R], sets[(u + DEPTH) % R]);
 
     if constexpr (KS > 1) {
         int* red = reinterpret_cast<int*>(lds);
@@ -208,9 +246,6 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
         if (kp > 0) return;
     }
 
-    // Transposed blocks: register r of lane l holds row 32 i + l%32 and
-    // column 32 j + 8 (r/4) + 4 (l/32) + r%4.
-    const int h = lane >> 5;
     if constexpr (!OUT_F16) {
         int32_t* o = static_cast<int32_t*>(out);
         const bool vec_ok = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
@@ -238,21 +273,10 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
     } else {
         uint16_t* o = static_cast<uint16_t*>(out);
         const bool vec_ok = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-        // the lane's 32 columns' weight scales (zero past N)
-        float wsv[2][4][4];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int col = slab * kSlab + 32 * j + 8 * g + 4 * h + e;
-                    wsv[j][g][e] = col < N ? scale_at(ws, ws16, col) : 0.f;
-                }
 #pragma unroll
         for (int i = 0; i < C::MB; ++i) {
             const int row = m0 + 32 * i + (lane & 31);
-            const float xsv = row < M ? scale_at(xs, xs16, row) : 0.f;
+            const float xsv = xsv_all[i];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -344,37 +368,40 @@ __global__ __launch_bounds__(512) void w8a8_tiled_gemv_kernel(const int8_t* __re
 }
 
 struct Shape8 {
-    int tm, wn, ks;
+    int tm, wn, ks, depth;
 };
 
 template <bool F16>
 using Gemm8Fn = void (*)(const int8_t*, const int8_t*, int, int, int, int, void*, const void*, int, const void*, int,
-                         int, int, int, int);
+                         int, int, int, int, int);
 
 template <bool F16>
 Gemm8Fn<F16> pick8(const Shape8& s) {
-    if (s.tm == 128 && s.wn == 2) return w8a8_tiled_gemm_kernel<128, 2, 2, F16>;
-    if (s.tm == 128 && s.wn == 4) return w8a8_tiled_gemm_kernel<128, 4, 1, F16>;
-    if (s.tm == 64 && s.wn == 4) return w8a8_tiled_gemm_kernel<64, 4, 1, F16>;
-    if (s.tm == 64 && s.wn == 2) return w8a8_tiled_gemm_kernel<64, 2, 2, F16>;
-    if (s.tm == 32 && s.wn == 2) return w8a8_tiled_gemm_kernel<32, 2, 2, F16>;
-    if (s.tm == 32 && s.wn == 1) return w8a8_tiled_gemm_kernel<32, 1, 4, F16>;
+#define MCV_S8(TM_, WN_, KS_, D_) \
+    if (s.tm == TM_ && s.wn == WN_ && s.ks == KS_ && s.depth == D_) return w8a8_tiled_gemm_kernel<TM_, WN_, KS_, D_, F16>;
+    MCV_S8(128, 2, 2, 2) MCV_S8(128, 4, 1, 2) MCV_S8(64, 4, 1, 2) MCV_S8(64, 2, 2, 2) MCV_S8(32, 2, 2, 2)
+    MCV_S8(32, 1, 4, 2) MCV_S8(64, 4, 1, 3) MCV_S8(64, 4, 1, 4) MCV_S8(64, 2, 2, 3) MCV_S8(64, 2, 2, 4)
+    MCV_S8(32, 2, 2, 3) MCV_S8(32, 2, 2, 4) MCV_S8(32, 1, 4, 3) MCV_S8(128, 4, 1, 3) MCV_S8(128, 2, 2, 3)
+#undef MCV_S8
     return nullptr;
 }
 
-// Preference order from a sweep on MI355X (K=1024, N=3584): 64-row waves side
-// by side win from M=1024 up; smaller M needs the k-split shapes to fill the
-// chip.
-constexpr Shape8 kShapes8[] = {{64, 4, 1}, {64, 2, 2}, {32, 2, 2}, {32, 1, 4}, {128, 4, 1}, {128, 2, 2}};
+// Preference order from a sweep on MI355X (K=1024, N=3584, graph-replayed,
+// column-major tile order): M=2048 128x256 tiles 15.7 us (64x256: 18.2);
+// M=1024 64x256 10.0 us (128x256, 112 tiles: 13.4); M=256 the k-split 32x128
+// tiles 7.3 us (64x256: 9.0).  Prefetching three stages ahead instead of two
+// was 0.5-2 us slower at every size.
+constexpr Shape8 kShapes8[] = {{128, 4, 1, 2}, {64, 4, 1, 2}, {64, 2, 2, 2}, {32, 2, 2, 2}, {32, 1, 4, 2}, {128, 2, 2, 2}};
 
 // The first listed shape whose grid covers most of the 256 CUs, else the one
 // with the most workgroups; MCV_W8GEMM_SHAPE="TM,WN,KS" overrides it.
 Shape8 choose8(int64_t M, int64_t KT, int64_t nslab) {
     if (const char* e = std::getenv("MCV_W8GEMM_SHAPE")) {
-        Shape8 s{0, 0, 0};
-        if (std::sscanf(e, "%d,%d,%d", &s.tm, &s.wn, &s.ks) == 3 && pick8<true>(s) && KT % s.ks == 0) return s;
+        Shape8 s{0, 0, 0, 2};
+        if (std::sscanf(e, "%d,%d,%d,%d", &s.tm, &s.wn, &s.ks, &s.depth) >= 3 && pick8<true>(s) && KT % s.ks == 0)
+            return s;
     }
-    Shape8 best{0, 0, 0};
+    Shape8 best{0, 0, 0, 2};
     int64_t best_tiles = -1;
     for (const Shape8& s : kShapes8) {
         if (KT % s.ks != 0) continue;
@@ -431,14 +458,18 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
     if (total > 0x7fffffff) return fail(MCV_ERR_SHAPE, "w8a8 tiled: too many tiles");
     const int KT = static_cast<int>(KT_all / s.ks);
     const int KBs = static_cast<int>(KB);
+    // Down the tile columns when x is the smaller operand (M < N); along the
+    // tile rows otherwise.  MCV_W8GEMM_ORDER=0/1 overrides (tuning sweeps).
+    int col_major = M < N ? 1 : 0;
+    if (const char* e = std::getenv("MCV_W8GEMM_ORDER")) col_major = std::atoi(e) ? 1 : 0;
     if (f16)
         hipLaunchKernelGGL(pick8<true>(s), dim3(static_cast<unsigned>(total)), dim3(256), 0, stream, xq, w,
                            static_cast<int>(M), static_cast<int>(K), static_cast<int>(N), KBs, out, xs, xs16, ws, ws16,
-                           static_cast<int>(nslab), static_cast<int>(n_tiles), static_cast<int>(total), KT);
+                           static_cast<int>(nslab), static_cast<int>(n_tiles), static_cast<int>(total), KT, col_major);
     else
         hipLaunchKernelGGL(pick8<false>(s), dim3(static_cast<unsigned>(total)), dim3(256), 0, stream, xq, w,
                            static_cast<int>(M), static_cast<int>(K), static_cast<int>(N), KBs, out, xs, xs16, ws, ws16,
-                           static_cast<int>(nslab), static_cast<int>(n_tiles), static_cast<int>(total), KT);
+                           static_cast<int>(nslab), static_cast<int>(n_tiles), static_cast<int>(total), KT, col_major);
     return check_launch("w8a8_tiled_gemm_kernel");
 }
 
