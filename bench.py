@@ -6,7 +6,8 @@ argmax folded into it, with 8 distinct weight copies (1.06 GB) rotated so no
 step hits the 256 MB MALL.  Steps are replayed from captured HIP graphs, so
 back-to-back kernels are not gated by the host's launch rate.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
 (132,484,244 B per step, inputs resident in HBM).  `--workload` selects the
-other BASELINE configs (gemv1, mlp, lm_head, prefill, w8a8).
+other BASELINE configs (gemv1, mlp, lm_head, prefill, w8a8) and the vendor library's dense
+GEMM at the same shapes (vendor_f16, vendor_int8) as a yardstick.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload lm_head]
 """
@@ -296,6 +297,32 @@ def wl_prefill(pkg, args):
                 dtype="w4a16 (f16 MFMA, f32 accumulate)", kernel="w4a16_gemm_kernel")
 
 
+def wl_vendor(pkg, args, int8=False):
+    """The vendor library's dense GEMM at the same shape (torch.matmul -> hipBLASLt
+    for fp16, torch._int_mm for int8): the yardstick for the quantised GEMMs,
+    which do strictly more work (dequant, epilogue) per output."""
+    import torch
+    M, K, N = args.M or (1024 if int8 else 2048), args.K or 1024, args.N or 3584
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    if int8:
+        a = torch.randint(-128, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
+        b = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda", generator=g).t()
+        fn = lambda i: torch._int_mm(a, b)
+    else:
+        a = torch.randn(M, K, dtype=torch.float16, device="cuda", generator=g)
+        b = torch.randn(N, K, dtype=torch.float16, device="cuda", generator=g).t()   # column-major B
+        c = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        fn = lambda i: torch.matmul(a, b, out=c)
+    flops = 2.0 * M * K * N
+    total_ms, _ = time_steps(fn, 1, args.steps, args.warmup)
+    kms = time_each_launch(fn, 1, args.steps)
+    return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TOP/s" if int8 else "TFLOP/s", bound="mfma",
+                config={"workload": "vendor_int8_gemm" if int8 else "vendor_f16_gemm", "M": M, "K": K, "N": N},
+                dtype="int8 (i32 accumulate)" if int8 else "f16 (f32 accumulate)",
+                kernel="torch._int_mm" if int8 else "torch.matmul (hipBLASLt)")
+
+
 def wl_w8a8(pkg, args):
     import torch
     M, K, N = args.M or 1024, args.K or 1024, args.N or 3584
@@ -327,7 +354,7 @@ def wl_copy(pkg, args):
 
 WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
              "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, fused=False), "prefill": wl_prefill, "w8a8": wl_w8a8,
-             "copy": wl_copy}
+             "copy": wl_copy, "vendor_f16": wl_vendor, "vendor_int8": lambda pkg, args: wl_vendor(pkg, args, int8=True)}
 
 
 def main():
