@@ -277,6 +277,27 @@ int mcv_w8a8_quantize_weight_host(const uint16_t* w_kn_host, int64_t K, int64_t 
                                   int8_t* q_host, int out_layout, float* scale_f32_host,
                                   uint16_t* scale_f16_host);
 
+/* Source element type of a checkpoint tensor. */
+enum mcv_src_dtype {
+    MCV_SRC_F16 = 0,
+    MCV_SRC_BF16 = 1  /* converted as the reference loads bf16 (src/csrc/lib/weights.cpp:25-33) */
+};
+
+/* The same per-output-channel quantiser fed straight from a checkpoint's
+ * [N][K] (out, in) linear weight, fp16 or bf16, in one host pass: replaces
+ * the reference's bf16 load, host transpose and quantisation
+ * (load_matmul_weight_transposed, src/csrc/lib/language_model.cpp:84-105,
+ * then quantize_dense_weight_w8a8, quantized_weight.cpp:231-268), bit-identical
+ * to them.  Outputs as mcv_w8a8_quantize_weight_host. */
+int mcv_w8a8_quantize_weight_nk_host(const uint16_t* w_nk_host, int src_dtype, int64_t K, int64_t N,
+                                     int8_t* q_host, int out_layout, float* scale_f32_host,
+                                     uint16_t* scale_f16_host);
+
+/* Re-lays a pre-quantised int8 [N][K] checkpoint tensor (safetensors I8, no
+ * counterpart in the reference, whose loader has no I8 dtype,
+ * src/csrc/lib/weights.cpp:15-23) into MCV_W8_TILED on the host. */
+int mcv_w8a8_pack_tiled_nk_host(const int8_t* q_nk_host, int64_t K, int64_t N, int8_t* tiled_host);
+
 /* ------------------------------------------------------------ elementwise -- */
 /* out = fp16 RNE(silu(g) * u) in fp32, n elements.  Replaces silu_mul
  * (src/csrc/lib/ops.cpp:437-456, op_kernel/silu_mul_custom.cpp:38-89). */

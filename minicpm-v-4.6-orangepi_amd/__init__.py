@@ -27,6 +27,7 @@ SLAB = 64
 
 MCV_F32, MCV_F16 = 0, 1
 W8_KN, W8_NK, W8_TILED = 0, 1, 2
+SRC_F16, SRC_BF16 = 0, 1
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -72,6 +73,8 @@ _SIGS = {
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_tiled_bytes": (_c_i64, [_c_i64, _c_i64]),
     "mcv_w8a8_pack_tiled_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
+    "mcv_w8a8_quantize_weight_nk_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
+    "mcv_w8a8_pack_tiled_nk_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
     "mcv_argmax_f16": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp]),
     "mcv_rms_norm": (_c_int, [_vp, _vp, _c_i64, _c_i64, ctypes.c_double, _vp, _vp]),
@@ -196,6 +199,32 @@ def quantize_w8a8_weight_host(w_kn_f16: np.ndarray, layout: int = W8_KN):
     s16 = np.empty(N, np.uint16)
     _check(lib().mcv_w8a8_quantize_weight_host(_np_ptr(w), K, N, _np_ptr(q), layout, _np_ptr(s32), _np_ptr(s16)),
            "mcv_w8a8_quantize_weight_host")
+    return q, s32, s16
+
+
+def pack_w8a8_tiled_nk(q_nk: np.ndarray) -> np.ndarray:
+    """int8 [N, K] (a pre-quantised checkpoint tensor) -> MCV_W8_TILED bytes."""
+    q_nk = np.ascontiguousarray(q_nk, np.int8)
+    N, K = q_nk.shape
+    out = np.empty(w8a8_tiled_bytes(K, N), np.int8)
+    _check(lib().mcv_w8a8_pack_tiled_nk_host(_np_ptr(q_nk), K, N, _np_ptr(out)), "mcv_w8a8_pack_tiled_nk_host")
+    return out
+
+
+def quantize_w8a8_weight_nk_host(w_nk: np.ndarray, src_dtype: int = SRC_F16, layout: int = W8_TILED):
+    """The same quantiser straight from a checkpoint's [N, K] fp16 / bf16 bits
+    (the reference's bf16 load + host transpose + quantize_dense_weight_w8a8,
+    language_model.cpp:84-105, quantized_weight.cpp:231-268) -> (q, s32, s16)."""
+    w = np.ascontiguousarray(w_nk).view(np.uint16)
+    N, K = w.shape
+    if layout == W8_TILED:
+        q = np.empty(w8a8_tiled_bytes(K, N), np.int8)
+    else:
+        q = np.empty((K, N) if layout == W8_KN else (N, K), np.int8)
+    s32 = np.empty(N, np.float32)
+    s16 = np.empty(N, np.uint16)
+    _check(lib().mcv_w8a8_quantize_weight_nk_host(_np_ptr(w), src_dtype, K, N, _np_ptr(q), layout, _np_ptr(s32),
+                                                  _np_ptr(s16)), "mcv_w8a8_quantize_weight_nk_host")
     return q, s32, s16
 
 

@@ -57,4 +57,14 @@ W4A16QuantizedWeight quantize_w4a16_synthetic(const uint16_t* w_kn, int64_t K, i
 // `layout` MCV_W8_TILED (default) or MCV_W8_KN.
 W8A8QuantizedWeight quantize_w8a8_host(const uint16_t* w_kn, int64_t K, int64_t N, int layout = MCV_W8_TILED);
 
+// W8A8 weights straight from a checkpoint, no device round trip and no host
+// transpose: `base.weight` [N, K] either I8 with `base.weight_scale` ([N],
+// F32 / F16 / BF16; a pre-quantised checkpoint, which the reference cannot
+// read -- its loader has no I8, weights.cpp:15-23) or F16 / BF16 (quantised on
+// the host exactly as load_matmul_weight_transposed + quantize_dense_weight_w8a8
+// do, language_model.cpp:84-105,190-231).
+bool has_w8a8_quantized_weight(const WeightsIndex& index, const std::string& base);
+W8A8QuantizedWeight load_w8a8_quantized_weight(const WeightsIndex& index, const std::string& base,
+                                               int layout = MCV_W8_TILED);
+
 }  // namespace minicpmv

@@ -146,4 +146,111 @@ W8A8QuantizedWeight quantize_dense_weight_w8a8(const Tensor& weight_kn) {
     return quantize_w8a8_host(h.data(), K, N);
 }
 
+namespace {
+
+W8A8QuantizedWeight upload_w8a8(const std::vector<int8_t>& q, const std::vector<float>& s32,
+                                const std::vector<uint16_t>& s16, int64_t K, int64_t N, int layout) {
+    W8A8QuantizedWeight out;
+    out.K = K;
+    out.N = N;
+    out.layout = layout;
+    out.w_int8 = layout == MCV_W8_TILED ? Tensor({static_cast<int64_t>(q.size())}, DType::Int8) : Tensor({K, N}, DType::Int8);
+    out.w_int8.copy_from_host(q.data(), q.size());
+    out.w_scale = Tensor({N}, DType::Float16);
+    out.w_scale.copy_from_host(s16.data(), s16.size() * 2);
+    out.w_scale_f32 = Tensor({N}, DType::Float32);
+    out.w_scale_f32.copy_from_host(s32.data(), s32.size() * 4);
+    return out;
+}
+
+// IEEE fp16 -> fp32 bits (exact, subnormals included).
+uint32_t f16_to_f32_bits(uint16_t h) {
+    const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 0x1f) return sign | 0x7f800000u | (m << 13);
+    if (e == 0) {
+        if (m == 0) return sign;
+        e = 113;                                   // normalise the subnormal
+        while ((m & 0x400u) == 0) { m <<= 1; --e; }
+        return sign | (e << 23) | ((m & 0x3ffu) << 13);
+    }
+    return sign | ((e + 112u) << 23) | (m << 13);
+}
+
+// The reference's stored fp16 copy of a W8A8 scale: truncating encode,
+// underflow to signed zero (src/csrc/lib/quantized_weight.cpp:186-195).
+uint16_t f32_to_f16_trunc(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int32_t e = static_cast<int32_t>((x >> 23) & 0xffu) - 112;
+    if (e <= 0) return static_cast<uint16_t>(sign);
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | ((x & 0x7fffffu) >> 13));
+}
+
+float scale_value(const uint8_t* p, DType dt, int64_t i) {
+    uint32_t bits = 0;
+    uint16_t h = 0;
+    switch (dt) {
+        case DType::Float32: std::memcpy(&bits, p + 4 * i, 4); break;
+        case DType::BFloat16: std::memcpy(&h, p + 2 * i, 2); bits = static_cast<uint32_t>(h) << 16; break;
+        case DType::Float16: std::memcpy(&h, p + 2 * i, 2); bits = f16_to_f32_bits(h); break;
+        default: throw std::runtime_error("W8A8 weight_scale must be F32, F16 or BF16");
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+}  // namespace
+
+bool has_w8a8_quantized_weight(const WeightsIndex& index, const std::string& base) {
+    return index.contains(base + ".weight") && index.contains(base + ".weight_scale") &&
+           index.at(base + ".weight").dtype == DType::Int8;
+}
+
+W8A8QuantizedWeight load_w8a8_quantized_weight(const WeightsIndex& index, const std::string& base, int layout) {
+    if (layout != MCV_W8_TILED && layout != MCV_W8_KN)
+        throw std::runtime_error("load_w8a8_quantized_weight: layout must be MCV_W8_TILED or MCV_W8_KN");
+    const TensorInfo& wi = index.at(base + ".weight");
+    if (wi.shape.size() != 2) throw std::runtime_error("W8A8 weight " + base + " must be 2-D [N, K]");
+    const int64_t N = wi.shape[0], K = wi.shape[1];
+    if (K <= 0 || N <= 0 || (N % 16) != 0)
+        throw std::runtime_error("W8A8 weight " + base + " needs positive K and N multiple of 16");
+    const int64_t bytes = layout == MCV_W8_TILED ? mcv_w8a8_tiled_bytes(K, N) : K * N;
+    std::vector<int8_t> q(static_cast<size_t>(bytes));
+    std::vector<float> s32(static_cast<size_t>(N));
+    std::vector<uint16_t> s16(static_cast<size_t>(N));
+    const uint8_t* src = index.host_data(base + ".weight");
+    if (wi.dtype == DType::Int8) {
+        // pre-quantised: int8 [N, K] plus one scale per output channel
+        const TensorInfo& si = index.at(base + ".weight_scale");
+        int64_t sn = 1;
+        for (int64_t d : si.shape) sn *= d;
+        if (sn != N) throw std::runtime_error("W8A8 weight_scale of " + base + " must hold N values");
+        const uint8_t* sp = index.host_data(base + ".weight_scale");
+        for (int64_t n = 0; n < N; ++n) {
+            s32[n] = scale_value(sp, si.dtype, n);
+            s16[n] = f32_to_f16_trunc(s32[n]);
+        }
+        const int8_t* qn = reinterpret_cast<const int8_t*>(src);
+        if (layout == MCV_W8_TILED) {
+            check_mcv(mcv_w8a8_pack_tiled_nk_host(qn, K, N, q.data()), "load_w8a8_quantized_weight");
+        } else {
+            for (int64_t n = 0; n < N; ++n)
+                for (int64_t k = 0; k < K; ++k) q[k * N + n] = qn[n * K + k];
+        }
+    } else if (wi.dtype == DType::Float16 || wi.dtype == DType::BFloat16) {
+        // dense checkpoint weight: quantised in one host pass (no transpose, no device round trip)
+        check_mcv(mcv_w8a8_quantize_weight_nk_host(reinterpret_cast<const uint16_t*>(src),
+                                                   wi.dtype == DType::BFloat16 ? MCV_SRC_BF16 : MCV_SRC_F16, K, N,
+                                                   q.data(), layout, s32.data(), s16.data()),
+                  "load_w8a8_quantized_weight");
+    } else {
+        throw std::runtime_error("W8A8 weight " + base + " must be I8 (with weight_scale), F16 or BF16");
+    }
+    return upload_w8a8(q, s32, s16, K, N, layout);
+}
+
 }  // namespace minicpmv

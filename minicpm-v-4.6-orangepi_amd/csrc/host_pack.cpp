@@ -318,6 +318,92 @@ extern "C" int mcv_w8a8_quantize_weight_host(const uint16_t* w_kn, int64_t K, in
     return MCV_OK;
 }
 
+namespace {
+
+// bf16 -> fp16 exactly as the reference loads bf16 checkpoint tensors
+// (src/csrc/lib/weights.cpp:25-33): exponent rebias, top mantissa bits kept,
+// below the fp16 normal range -> signed zero, above it (NaN too) -> signed inf.
+uint16_t bf16_to_f16_trunc_host(uint16_t bf) {
+    const uint32_t x = static_cast<uint32_t>(bf) << 16;
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int32_t e = static_cast<int32_t>((x >> 23) & 0xffu) - 112;
+    if (e <= 0) return static_cast<uint16_t>(sign);
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | ((x & 0x7fffffu) >> 13));
+}
+
+// Runs fn(n0, n1) over [0, N) split into contiguous ranges on up to 16 threads.
+template <typename Fn>
+void parallel_columns(int64_t N, int64_t work_per_column, Fn fn) {
+    int nt = static_cast<int>(std::thread::hardware_concurrency());
+    if (nt < 1) nt = 1;
+    if (nt > 16) nt = 16;
+    if (N * work_per_column < (int64_t(1) << 18)) nt = 1;            // small: not worth the threads
+    if (nt == 1) {
+        fn(int64_t(0), N);
+        return;
+    }
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; ++t) {
+        const int64_t n0 = N * t / nt, n1 = N * (t + 1) / nt;
+        if (n1 > n0) th.emplace_back(fn, n0, n1);
+    }
+    for (auto& x : th) x.join();
+}
+
+}  // namespace
+
+extern "C" int mcv_w8a8_pack_tiled_nk_host(const int8_t* q_nk, int64_t K, int64_t N, int8_t* tiled) {
+    if (!q_nk || !tiled) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_pack_tiled_nk_host: null pointer");
+    const int64_t bytes = mcv_w8a8_tiled_bytes(K, N);
+    if (bytes == 0) return fail(MCV_ERR_SHAPE, "mcv_w8a8_pack_tiled_nk_host: bad shape K=%lld N=%lld", (long long)K, (long long)N);
+    std::memset(tiled, 0, static_cast<size_t>(bytes));
+    const int64_t kblocks = ceil_div(K, 128) * 4;
+    parallel_columns(N, K, [&](int64_t n0, int64_t n1) {
+        for (int64_t n = n0; n < n1; ++n)
+            for (int64_t k = 0; k < K; ++k) tiled[tiled_offset(k, n, kblocks)] = q_nk[n * K + k];
+    });
+    return MCV_OK;
+}
+
+extern "C" int mcv_w8a8_quantize_weight_nk_host(const uint16_t* w_nk, int src_dtype, int64_t K, int64_t N, int8_t* q,
+                                                int out_layout, float* scale_f32, uint16_t* scale_f16) {
+    if (!w_nk || !q || !scale_f32) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_nk_host: null pointer");
+    if (K <= 0 || N <= 0) return fail(MCV_ERR_SHAPE, "mcv_w8a8_quantize_weight_nk_host: K and N must be positive");
+    if (src_dtype != MCV_SRC_F16 && src_dtype != MCV_SRC_BF16)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_nk_host: bad source dtype %d", src_dtype);
+    if (out_layout != MCV_W8_KN && out_layout != MCV_W8_NK && out_layout != MCV_W8_TILED)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_nk_host: bad layout %d", out_layout);
+    const int64_t kblocks = ceil_div(K, 128) * 4;
+    if (out_layout == MCV_W8_TILED) std::memset(q, 0, static_cast<size_t>(mcv_w8a8_tiled_bytes(K, N)));
+    const bool bf = src_dtype == MCV_SRC_BF16;
+    // Output channel n is row n of the checkpoint's [N][K]: the same values,
+    // the same per-channel formula as the [K][N] quantiser above.
+    parallel_columns(N, K, [&](int64_t n0, int64_t n1) {
+        std::vector<float> row(static_cast<size_t>(K));
+        for (int64_t n = n0; n < n1; ++n) {
+            const uint16_t* src = w_nk + n * K;
+            float max_abs = 0.0f;
+            for (int64_t k = 0; k < K; ++k) {
+                row[k] = h2f_host(bf ? bf16_to_f16_trunc_host(src[k]) : src[k]);
+                max_abs = std::max(max_abs, std::fabs(row[k]));
+            }
+            float scale = max_abs / 127.0f;
+            if (scale < 0.00000001f) scale = 0.00000001f;
+            const float inv = 1.0f / scale;
+            scale_f32[n] = scale;
+            if (scale_f16) scale_f16[n] = f2h_trunc_host(scale);
+            for (int64_t k = 0; k < K; ++k) {
+                const int8_t v = quantize_i8_host(row[k], inv);
+                if (out_layout == MCV_W8_KN) q[k * N + n] = v;
+                else if (out_layout == MCV_W8_NK) q[n * K + k] = v;
+                else q[tiled_offset(k, n, kblocks)] = v;
+            }
+        }
+    });
+    return MCV_OK;
+}
+
 extern "C" int mcv_w4a16_quantize_host(const uint16_t* w_kn, int64_t K, int64_t N, int32_t* qweight, int32_t* qzeros,
                                        uint16_t* scales, int nthreads) {
     if (!w_kn || !qweight || !qzeros || !scales) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_quantize_host: null pointer");

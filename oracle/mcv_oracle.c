@@ -68,6 +68,24 @@ uint16_t or_f2h_trunc(float f) {
     return (uint16_t)(sign | ((uint32_t)e << 10) | (m >> 13));
 }
 
+/* bf16 -> fp16 as the reference loads bf16 checkpoint tensors
+ * (src/csrc/lib/weights.cpp:25-33): rebias the exponent, keep the top 10
+ * mantissa bits (bf16 has 7, so nothing is lost for fp16 normals), flush
+ * what falls below the fp16 normal range to signed zero and send what falls
+ * above it -- NaN included -- to signed infinity. */
+uint16_t or_bf16_to_f16_trunc(uint16_t bf) {
+    uint32_t x = (uint32_t)bf << 16;
+    uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t e = (int32_t)((x >> 23) & 0xffu) - 127 + 15;
+    if (e <= 0) return (uint16_t)sign;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint32_t)e << 10) | ((x & 0x7fffffu) >> 13));
+}
+
+void or_bf16_to_f16_trunc_array(const uint16_t* bf, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = or_bf16_to_f16_trunc(bf[i]);
+}
+
 /* IEEE-754 round-to-nearest-even encode with subnormals.  Build-defined: the
  * synthetic generators and the fp16 outputs of every kernel use this rounding
  * (the reference's AscendC casts use CAST_RINT, e.g.

@@ -13,6 +13,9 @@
  *   or_h2f / or_h2f_ftz / or_f2h_trunc / or_f2h_rne  -- exhaustive over all 65536
  *       fp16 bit patterns against numpy's IEEE conversions, and a brute-force
  *       "largest fp16 not above |f|" characterisation of truncation.
+ *   or_bf16_to_f16_trunc -- exhaustive over all 65536 bf16 patterns: exact (numpy
+ *       float32 -> float16) wherever the value is an fp16 normal, signed zero
+ *       below, signed infinity above and for NaN.
  *   or_unpack_awq / or_unpack_gptq  -- hand-built known-answer words, a vectorised
  *       numpy restatement written from the format description, and round trips.
  *   or_quantize_int4_awq  -- build-defined (the reference has no int4 quantizer);
@@ -47,6 +50,8 @@ float or_h2f(uint16_t h);
 float or_h2f_ftz(uint16_t h);
 uint16_t or_f2h_trunc(float f);
 uint16_t or_f2h_rne(float f);
+uint16_t or_bf16_to_f16_trunc(uint16_t bf);
+void or_bf16_to_f16_trunc_array(const uint16_t* bf, int64_t n, uint16_t* out);
 void or_h2f_array(const uint16_t* h, int64_t n, float* out);
 void or_f2h_rne_array(const float* f, int64_t n, uint16_t* out);
 void or_f2h_trunc_array(const float* f, int64_t n, uint16_t* out);

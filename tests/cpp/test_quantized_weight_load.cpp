@@ -2,13 +2,17 @@
 // through load_w4a16_quantized_weight (GPTQ chosen by the presence of g_idx,
 // quantized_weight.cpp:212-214), and the loaded weight multiplies like the CPU
 // reference formula on the unpacked (q - z).  Also checks the dequantised
-// int8 values bit for bit against a host unpack.
+// int8 values bit for bit against a host unpack.  W8A8: checkpoint [N, K]
+// F16 / BF16 weights quantise in one host pass to the same bytes as the
+// reference's transpose + quantize_dense_weight_w8a8, and pre-quantised I8
+// weights with F32 / F16 scales load to the tiled layout and multiply exactly.
 #include "minicpmv/hip_context.h"
 #include "minicpmv/ops.h"
 #include "minicpmv/quantized_weight.h"
 #include "test_common.h"
 
 #include <cmath>
+#include <cstring>
 #include <random>
 
 using namespace minicpmv;
@@ -49,6 +53,110 @@ static int check(HipContext& ctx, const W4A16QuantizedWeight& w, const std::vect
     std::printf("%s K=%lld N=%lld max_abs=%.2e rel_l2=%.2e dequant_exact=%d\n", what, (long long)K, (long long)N, max_abs,
                 std::sqrt(num / den), int(exact));
     return (max_abs <= 2e-2 && std::sqrt(num / den) <= 1e-3 && exact) ? 0 : 1;
+}
+
+
+// bf16 -> fp16 as the reference loads checkpoint tensors (weights.cpp:25-33)
+static uint16_t bf16_to_f16(uint16_t bf) {
+    const uint32_t x = static_cast<uint32_t>(bf) << 16;
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int32_t e = static_cast<int32_t>((x >> 23) & 0xffu) - 112;
+    if (e <= 0) return static_cast<uint16_t>(sign);
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | ((x & 0x7fffffu) >> 13));
+}
+
+template <typename T>
+static std::vector<T> host_copy(const Tensor& t) {
+    std::vector<T> v(t.size_bytes() / sizeof(T));
+    t.copy_to_host(v.data(), t.size_bytes());
+    return v;
+}
+
+static int check_w8a8(HipContext& ctx, const std::string& dir) {
+    constexpr int64_t N = 208, K = 384;
+    std::mt19937 rng(11);
+    std::normal_distribution<float> nd(0.f, 0.02f);
+    std::vector<uint16_t> w_nk(static_cast<size_t>(N * K)), bf_nk(static_cast<size_t>(N * K));
+    for (auto& v : w_nk) v = t::f2h_rne(nd(rng));
+    for (auto& v : bf_nk) {
+        const float f = nd(rng);
+        uint32_t bits;
+        std::memcpy(&bits, &f, 4);
+        v = static_cast<uint16_t>(bits >> 16);
+    }
+    std::uniform_int_distribution<int> qd(-128, 127);
+    std::vector<int8_t> q_nk(static_cast<size_t>(N * K));
+    for (auto& v : q_nk) v = static_cast<int8_t>(qd(rng));
+    std::vector<float> s_f32(static_cast<size_t>(N));
+    std::vector<uint16_t> s_f16(static_cast<size_t>(N));
+    for (int64_t n = 0; n < N; ++n) {
+        s_f32[n] = 0.001f + 0.0001f * static_cast<float>(n % 13);
+        s_f16[n] = t::f2h_rne(s_f32[n]);
+    }
+    const std::string p = dir + "/mcv_w8a8.safetensors";
+    t::write_safetensors(p, {{"a.weight", "F16", {N, K}, t::bytes_of(w_nk)},
+                             {"b.weight", "BF16", {N, K}, t::bytes_of(bf_nk)},
+                             {"c.weight", "I8", {N, K}, t::bytes_of(q_nk)},
+                             {"c.weight_scale", "F32", {N}, t::bytes_of(s_f32)},
+                             {"d.weight", "I8", {N, K}, t::bytes_of(q_nk)},
+                             {"d.weight_scale", "F16", {N, 1}, t::bytes_of(s_f16)}});
+    WeightsIndex idx(p);
+    int rc = 0;
+    if (has_w8a8_quantized_weight(idx, "a") || !has_w8a8_quantized_weight(idx, "c") ||
+        !has_w8a8_quantized_weight(idx, "d")) {
+        std::printf("has_w8a8_quantized_weight wrong\n");
+        rc = 1;
+    }
+    // dense sources: the same bytes and scales as transpose + quantize_dense_weight_w8a8
+    for (int src = 0; src < 2; ++src) {
+        std::vector<uint16_t> kn(static_cast<size_t>(K * N));
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t k = 0; k < K; ++k) kn[k * N + n] = src ? bf16_to_f16(bf_nk[n * K + k]) : w_nk[n * K + k];
+        const W8A8QuantizedWeight ref = quantize_w8a8_host(kn.data(), K, N, MCV_W8_TILED);
+        const W8A8QuantizedWeight got = load_w8a8_quantized_weight(idx, src ? "b" : "a");
+        const bool same = host_copy<int8_t>(ref.w_int8) == host_copy<int8_t>(got.w_int8) &&
+                          host_copy<uint32_t>(ref.w_scale_f32) == host_copy<uint32_t>(got.w_scale_f32) &&
+                          host_copy<uint16_t>(ref.w_scale) == host_copy<uint16_t>(got.w_scale) &&
+                          got.layout == MCV_W8_TILED && got.K == K && got.N == N;
+        std::printf("W8A8 %s checkpoint == transpose + quantize: %d\n", src ? "BF16" : "F16", int(same));
+        if (!same) rc = 1;
+        const W8A8QuantizedWeight kn_w = load_w8a8_quantized_weight(idx, src ? "b" : "a", MCV_W8_KN);
+        const W8A8QuantizedWeight kn_ref = quantize_w8a8_host(kn.data(), K, N, MCV_W8_KN);
+        if (host_copy<int8_t>(kn_w.w_int8) != host_copy<int8_t>(kn_ref.w_int8)) {
+            std::printf("W8A8 [K, N] layout differs\n");
+            rc = 1;
+        }
+    }
+    // pre-quantised I8: exact int32 products through the tiled GEMM and GEMV
+    for (const char* name : {"c", "d"}) {
+        const W8A8QuantizedWeight w = load_w8a8_quantized_weight(idx, name);
+        const std::vector<float> sc = host_copy<float>(w.w_scale_f32);
+        bool scales_ok = true;
+        for (int64_t n = 0; n < N; ++n)
+            scales_ok &= name[0] == 'c' ? sc[n] == s_f32[n] : sc[n] == t::h2f(s_f16[n]);
+        for (int64_t M : {3, 70}) {
+            std::vector<int8_t> hx(static_cast<size_t>(M * K));
+            for (auto& v : hx) v = static_cast<int8_t>(qd(rng));
+            Tensor x({M, K}, DType::Int8);
+            x.copy_from_host(hx.data(), hx.size());
+            Tensor acc({M, N}, DType::Int32);
+            acc.allocate();
+            matmul_w8a8_i32(x, w, acc, ctx.stream());
+            const std::vector<int32_t> ha = host_copy<int32_t>(acc);
+            bool exact = true;
+            for (int64_t m = 0; m < M; ++m)
+                for (int64_t n = 0; n < N; ++n) {
+                    int32_t r = 0;
+                    for (int64_t k = 0; k < K; ++k) r += int32_t(hx[m * K + k]) * int32_t(q_nk[n * K + k]);
+                    exact &= r == ha[m * N + n];
+                }
+            std::printf("W8A8 I8 checkpoint %s M=%lld: int32 exact %d, scales %d\n", name, (long long)M, int(exact),
+                        int(scales_ok));
+            if (!exact || !scales_ok) rc = 1;
+        }
+    }
+    return rc;
 }
 
 int main(int argc, char** argv) {
@@ -131,5 +239,6 @@ int main(int argc, char** argv) {
     } catch (const std::runtime_error& e) {
         std::printf("act-order refused: %s\n", e.what());
     }
+    rc |= check_w8a8(ctx, dir);
     return rc;
 }

@@ -59,6 +59,7 @@ class Oracle:
             "or_h2f_array": (None, [vp, _i64, vp]),
             "or_f2h_rne_array": (None, [vp, _i64, vp]),
             "or_f2h_trunc_array": (None, [vp, _i64, vp]),
+            "or_bf16_to_f16_trunc_array": (None, [vp, _i64, vp]),
             "or_unpack_awq": (ctypes.c_int, [vp, vp, _i64, _i64, vp]),
             "or_unpack_gptq": (ctypes.c_int, [vp, vp, vp, _i64, _i64, _i64, vp]),
             "or_quantize_int4_awq": (ctypes.c_int, [vp, _i64, _i64, vp, vp, vp]),
@@ -100,6 +101,12 @@ class Oracle:
         f = np.ascontiguousarray(f, np.float32)
         out = np.empty(f.shape, np.uint16)
         self.L.or_f2h_trunc_array(self._p(f), f.size, self._p(out))
+        return out
+
+    def bf16_to_f16_trunc(self, bf):
+        bf = np.ascontiguousarray(bf, np.uint16)
+        out = np.empty(bf.shape, np.uint16)
+        self.L.or_bf16_to_f16_trunc_array(self._p(bf), bf.size, self._p(out))
         return out
 
     def unpack_awq(self, qweight, qzeros):

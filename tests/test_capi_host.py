@@ -202,3 +202,33 @@ def test_lm_head_slots_token_known_answer(mcv):
     assert b"tag" in L.mcv_last_error()
     big = 1 << 24
     assert L.mcv_w4a16_lm_head_argmax_slots(fake, 128, big, big, fake, fake, fake, 0, None, fake, 1, None) == 2
+
+
+@pytest.mark.parametrize("K,N", [(1024, 3584), (200, 72), (2048, 1000)])
+def test_w8a8_checkpoint_quantiser(mcv, oracle, K, N):
+    """[N, K] checkpoint bits -> int8 + scales in one host pass, bit-identical
+    to the reference's load (bf16 -> fp16 truncating), host transpose and
+    per-channel quantiser, for fp16 and bf16 sources and every layout."""
+    rng = np.random.default_rng(K + N)
+    w_nk = f16_normal(rng, (N, K), 0.02)
+    w_nk[3, :] = 0                                      # all-zero channel -> scale floor
+    q_o, s_o, s16_o = oracle.w8a8_quantize_weight(np.ascontiguousarray(w_nk.T))
+    for layout in (mcv.W8_KN, mcv.W8_NK, mcv.W8_TILED):
+        q, s32, s16 = mcv.quantize_w8a8_weight_nk_host(w_nk, mcv.SRC_F16, layout)
+        want = {mcv.W8_KN: q_o, mcv.W8_NK: np.ascontiguousarray(q_o.T), mcv.W8_TILED: mcv.pack_w8a8_tiled(q_o)}[layout]
+        assert np.array_equal(q, want), layout
+        assert np.array_equal(s32.view(np.uint32), s_o.view(np.uint32))
+        assert np.array_equal(s16, s16_o)
+    # bf16 source: random bf16 patterns around N(0, 0.02), plus out-of-range ones
+    f = (rng.standard_normal((N, K)).astype(np.float32) * np.float32(0.02))
+    bf = (f.view(np.uint32) >> 16).astype(np.uint16)
+    bf[0, :4] = [0x0001, 0x8001, 0x3880, 0x387F]        # bf16 subnormal / f16-subnormal range -> signed zero
+    q, s32, s16 = mcv.quantize_w8a8_weight_nk_host(bf, mcv.SRC_BF16, mcv.W8_TILED)
+    as16 = np.ascontiguousarray(oracle.bf16_to_f16_trunc(bf).T)
+    q_o, s_o, s16_o = oracle.w8a8_quantize_weight(as16)
+    assert np.array_equal(q, mcv.pack_w8a8_tiled(q_o))
+    assert np.array_equal(s32.view(np.uint32), s_o.view(np.uint32))
+    assert np.array_equal(s16, s16_o)
+    # pre-quantised int8 [N, K] (safetensors I8) -> tiled
+    q_nk = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    assert np.array_equal(mcv.pack_w8a8_tiled_nk(q_nk), mcv.pack_w8a8_tiled(np.ascontiguousarray(q_nk.T)))

@@ -82,3 +82,25 @@ def test_f2h_trunc_is_largest_not_above(oracle):
 def test_f2h_trunc_nan_becomes_inf(oracle):
     # exponent field 255 maps to >= 31: the reference encodes NaN as infinity
     assert oracle.L.or_f2h_trunc(float("nan")) in (0x7C00, 0xFC00)
+
+
+def test_bf16_to_f16_trunc_exhaustive(oracle):
+    """All 65536 bf16 patterns: where the value is an fp16 normal the
+    conversion is exact (bf16's 7 mantissa bits fit in fp16's 10); below the
+    fp16 normal range it is signed zero (no subnormals), above it and for NaN
+    signed infinity (language_model loads, src/csrc/lib/weights.cpp:25-33)."""
+    bf = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.bf16_to_f16_trunc(bf)
+    val = (bf.astype(np.uint32) << 16).view(np.float32)
+    sign = (bf & 0x8000).astype(np.uint16)
+    a = np.abs(val)
+    normal = (a >= np.float32(2.0 ** -14)) & (a < np.float32(65536.0))
+    assert np.array_equal(got[normal], val[normal].astype(np.float16).view(np.uint16))
+    assert np.array_equal(got[normal].view(np.float16).astype(np.float32), val[normal])   # exact
+    low = a < np.float32(2.0 ** -14)
+    assert np.array_equal(got[low], sign[low])
+    high = ~normal & ~low                                         # >= 65536, inf, NaN
+    assert np.array_equal(got[high], sign[high] | np.uint16(0x7C00))
+    # known answers
+    assert oracle.bf16_to_f16_trunc(np.array([0x3F80, 0xC020, 0x4780, 0x7FC0, 0x3880, 0x387F], np.uint16)).tolist() == \
+        [0x3C00, 0xC100, 0x7C00, 0x7C00, 0x0400, 0x0000]
