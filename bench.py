@@ -297,6 +297,36 @@ def wl_prefill(pkg, args):
                 dtype="w4a16 (f16 MFMA, f32 accumulate)", kernel="w4a16_gemm_kernel")
 
 
+def wl_norm_quant(pkg, args, fused=True):
+    """Decode-time RMSNorm + W8A8 activation quantisation (M=1, H=1024 by
+    default): one fused launch, or rms_norm then w8a8_quantize."""
+    import torch
+    M, H = args.M or 1, args.K or 1024
+    rng = np.random.default_rng(1)
+    sets = 64
+    xs = [to_dev_f16(f16_normal(rng, (M, H), 1.0)) for _ in range(sets)]
+    g = to_dev_f16(f16_normal(rng, H, 1.0))
+    normed = torch.empty((M, H), dtype=torch.float16, device="cuda")
+    xq = torch.empty((M, H), dtype=torch.int8, device="cuda")
+    sc = torch.empty(M, dtype=torch.float32, device="cuda")
+    L = pkg.lib()
+    if fused:
+        fn = lambda i: L.mcv_rms_norm_w8a8_quantize(xs[i].data_ptr(), g.data_ptr(), M, H, 1e-6, normed.data_ptr(),
+                                                    xq.data_ptr(), sc.data_ptr(), None,
+                                                    torch.cuda.current_stream().cuda_stream)
+    else:
+        def fn(i):
+            L.mcv_rms_norm(xs[i].data_ptr(), g.data_ptr(), M, H, 1e-6, normed.data_ptr(),
+                           torch.cuda.current_stream().cuda_stream)
+            L.mcv_w8a8_quantize_act(normed.data_ptr(), M, H, xq.data_ptr(), sc.data_ptr(), None,
+                                    torch.cuda.current_stream().cuda_stream)
+    nbytes = M * (7 * H + 4) + 2 * H
+    total_ms, _ = time_steps(fn, sets, args.steps, args.warmup)
+    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=[total_ms / args.steps], unit="GB/s", bound="hbm",
+                config={"workload": "rms_norm_w8a8_quant" + ("" if fused else "_unfused"), "M": M, "H": H},
+                dtype="f16 -> int8", kernel="rms_norm_quant_kernel" if fused else "rms_norm_kernel + w8a8_quant_act_kernel")
+
+
 def wl_vendor(pkg, args, int8=False):
     """The vendor library's dense GEMM at the same shape (torch.matmul -> hipBLASLt
     for fp16, torch._int_mm for int8): the yardstick for the quantised GEMMs,
@@ -354,7 +384,8 @@ def wl_copy(pkg, args):
 
 WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
              "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, fused=False), "prefill": wl_prefill, "w8a8": wl_w8a8,
-             "copy": wl_copy, "vendor_f16": wl_vendor, "vendor_int8": lambda pkg, args: wl_vendor(pkg, args, int8=True)}
+             "copy": wl_copy, "norm_quant": wl_norm_quant,
+             "norm_quant_unfused": lambda pkg, args: wl_norm_quant(pkg, args, fused=False), "vendor_f16": wl_vendor, "vendor_int8": lambda pkg, args: wl_vendor(pkg, args, int8=True)}
 
 
 def main():

@@ -237,6 +237,16 @@ int mcv_argmax_reduce_keys(const void* keys_dev, int64_t n_keys, int64_t* token_
 int mcv_w8a8_quantize_act(const void* x_dev, int64_t M, int64_t K, int8_t* xq_dev,
                           float* x_scale_f32_dev, void* x_scale_f16_dev, mcv_stream_t stream);
 
+/* RMSNorm then per-row activation quantisation in one launch: the decode
+ * sequence rms_norm -> w8a8_quantize that precedes every W8A8 projection
+ * group (src/csrc/lib/decoder_layer.cpp:955-966, 1022-1032).  normed_dev
+ * [M][H] fp16 receives the normed row (as mcv_rms_norm; may be NULL when no
+ * fp16 consumer remains); xq_dev and the scales as mcv_w8a8_quantize_act of
+ * that row.  Bit-identical to mcv_rms_norm followed by mcv_w8a8_quantize_act. */
+int mcv_rms_norm_w8a8_quantize(const void* x_dev, const void* gamma_dev, int64_t M, int64_t H, double eps,
+                               void* normed_dev, int8_t* xq_dev, float* x_scale_f32_dev,
+                               void* x_scale_f16_dev, mcv_stream_t stream);
+
 /* acc[M][N] int32 = xq[M][K] . W exactly.  W is int8 in layout w_layout.
  * Replaces matmul_w8a8_i32 (src/csrc/lib/ops.cpp:1097-1133, kernel
  * op_kernel/matmul_w8a8_i32_custom.cpp:15-48), which accepts M = 1 only.

@@ -78,6 +78,7 @@ _SIGS = {
     "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
     "mcv_argmax_f16": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp]),
     "mcv_rms_norm": (_c_int, [_vp, _vp, _c_i64, _c_i64, ctypes.c_double, _vp, _vp]),
+    "mcv_rms_norm_w8a8_quantize": (_c_int, [_vp, _vp, _c_i64, _c_i64, ctypes.c_double, _vp, _vp, _vp, _vp, _vp]),
 }
 
 
@@ -577,6 +578,27 @@ def rms_norm(x, gamma, eps: float, out=None, stream=None):
     _check(lib().mcv_rms_norm(_dev(x2), _dev(gamma), x2.shape[0], x2.shape[1], float(eps), _dev(out), _stream(stream)),
            "rms_norm")
     return out
+
+
+def rms_norm_w8a8_quantize(x, gamma, eps: float, normed=None, want_normed: bool = True, x_scale_f16=None,
+                           stream=None):
+    """RMSNorm then per-row int8 quantisation in one launch (decoder_layer.cpp:955-966,
+    1022-1032); bit-identical to rms_norm + w8a8_quantize.  Returns
+    (normed fp16 [M, H] or None, x_int8 [M, H], x_scale fp32 [M], x_scale_f16 or None)."""
+    torch = _torch()
+    if x.dtype != torch.float16 or gamma.dtype != torch.float16 or x.dim() != 2 or not x.is_contiguous() \
+            or x.shape[1] != gamma.numel():
+        raise McvError("rms_norm_w8a8_quantize requires contiguous fp16 x [M, H] and gamma [H]")
+    M, H = x.shape
+    if normed is None and want_normed:
+        normed = torch.empty_like(x)
+    xq = torch.empty((M, H), dtype=torch.int8, device=x.device)
+    xs = torch.empty(M, dtype=torch.float32, device=x.device)
+    _check(lib().mcv_rms_norm_w8a8_quantize(_dev(x), _dev(gamma), M, H, float(eps),
+                                            _dev(normed) if normed is not None else 0, _dev(xq), _dev(xs),
+                                            _dev(x_scale_f16) if x_scale_f16 is not None else 0, _stream(stream)),
+           "rms_norm_w8a8_quantize")
+    return normed, xq, xs, x_scale_f16
 
 
 def version() -> str:

@@ -49,6 +49,11 @@ void matmul_w8a8_i32(const Tensor& x, const W8A8QuantizedWeight& w, Tensor& out,
 // Per-row symmetric int8 quantisation of fp16 x [M, K]; x_scale is [M]
 // (or [1] for M = 1, as the reference) in fp16 or fp32.
 void w8a8_quantize(const Tensor& x, Tensor& x_int8, Tensor& x_scale, hipStream_t stream);
+// rms_norm followed by w8a8_quantize of the normed row in one launch
+// (decoder_layer.cpp:955-966, 1022-1032), bit-identical to the pair; `normed`
+// may be null when nothing else reads the fp16 row.
+void rms_norm_w8a8_quantize(const Tensor& x, const Tensor& gamma, double epsilon, Tensor* normed, Tensor& x_int8,
+                            Tensor& x_scale, hipStream_t stream);
 
 // out fp16 [M, N] = RNE((acc * w_scale[n]) * x_scale[m]); scales fp16 or fp32.
 void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream);

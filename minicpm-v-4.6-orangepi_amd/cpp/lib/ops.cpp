@@ -124,6 +124,25 @@ void w8a8_quantize(const Tensor& x, Tensor& x_int8, Tensor& x_scale, hipStream_t
               "w8a8_quantize");
 }
 
+void rms_norm_w8a8_quantize(const Tensor& x, const Tensor& gamma, double epsilon, Tensor* normed, Tensor& x_int8,
+                            Tensor& x_scale, hipStream_t stream) {
+    require(x.dtype() == DType::Float16 && gamma.dtype() == DType::Float16, "rms_norm_w8a8_quantize needs fp16 x, gamma");
+    require(x.shape().size() == 2, "rms_norm_w8a8_quantize x must be [M, H]");
+    const int64_t M = x.shape()[0], H = x.shape()[1];
+    require(static_cast<int64_t>(gamma.numel()) == H, "rms_norm_w8a8_quantize gamma must be [H]");
+    require(!normed || (normed->dtype() == DType::Float16 && normed->shape() == x.shape()),
+            "rms_norm_w8a8_quantize normed must be fp16 [M, H]");
+    require(x_int8.dtype() == DType::Int8 && x_int8.shape() == x.shape(), "rms_norm_w8a8_quantize x_int8 must be int8 [M, H]");
+    require(static_cast<int64_t>(x_scale.numel()) == M, "rms_norm_w8a8_quantize x_scale must be [M]");
+    const bool f32 = x_scale.dtype() == DType::Float32;
+    require(f32 || x_scale.dtype() == DType::Float16, "rms_norm_w8a8_quantize x_scale must be fp16 or fp32");
+    check_mcv(mcv_rms_norm_w8a8_quantize(x.data(), gamma.data(), M, H, epsilon, normed ? normed->data() : nullptr,
+                                         static_cast<int8_t*>(x_int8.data()),
+                                         f32 ? static_cast<float*>(x_scale.data()) : nullptr,
+                                         f32 ? nullptr : x_scale.data(), stream),
+              "rms_norm_w8a8_quantize");
+}
+
 void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream) {
     require(acc.dtype() == DType::Int32 && out.dtype() == DType::Float16, "w8a8_dequant requires int32 acc and fp16 out");
     require(acc.shape().size() == 2, "w8a8_dequant acc must be [M, N]");

@@ -103,4 +103,67 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
     return v;
 }
 
+// ---- row kernels shared by RMSNorm, activation quantisation and their fusion
+// (one 256-thread workgroup per row; the same code in every kernel, so the
+// fused kernel is bit-identical to the two separate launches).
+
+// rstd = 1 / sqrt(mean(x^2) + eps): per-thread fp32 sums of squares over the
+// strided elements i = tid, tid + 256, ... in that order (`ss`), folded by a
+// wave shuffle tree and then across the four waves in order.
+__device__ __forceinline__ float block_rstd(float ss, int H, float eps) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    __shared__ float part[4];
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) tot += part[w];
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, static_cast<float>(H)), eps)));
+}
+
+__device__ __forceinline__ float row_rstd(const uint16_t* __restrict__ xr, int H, float eps) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const float v = h2f(xr[i]);
+        ss = fmaf(v, v, ss);
+    }
+    return block_rstd(ss, H, eps);
+}
+
+// fp16 RNE((x * rstd) * gamma), each product an IEEE fp32 multiply.
+__device__ __forceinline__ uint16_t rms_apply(uint16_t x, float rstd, uint16_t g) {
+    return f2h(__fmul_rn(__fmul_rn(h2f(x), rstd), h2f(g)));
+}
+
+// Workgroup maximum of per-thread |x| maxima (NaN never becomes the maximum).
+__device__ __forceinline__ float row_absmax(float m) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    __shared__ float wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = wmax[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) m = wmax[w] > m ? wmax[w] : m;
+    return m;
+}
+
+// scale = max / 127 floored at 1e-8 (op_kernel/w8a8_quantize_custom.cpp:25-41).
+__device__ __forceinline__ float act_scale(float absmax) {
+    const float scale = __fdiv_rn(absmax, 127.0f);
+    return scale < 0.00000001f ? 0.00000001f : scale;
+}
+
+// quantize_i8 (src/csrc/lib/quantized_weight.cpp:197-202): clamp, then
+// round half away from zero by truncating v +- 0.5.
+__device__ __forceinline__ int8_t act_quant(uint16_t x, float inv) {
+    float v = __fmul_rn(h2f(x), inv);
+    v = v > 127.0f ? 127.0f : v;
+    v = v < -128.0f ? -128.0f : v;
+    const float r = v >= 0.0f ? __fadd_rn(v, 0.5f) : __fsub_rn(v, 0.5f);
+    return static_cast<int8_t>(static_cast<int>(r));
+}
+
 }  // namespace mcv

@@ -33,27 +33,13 @@ __global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* __restrict_
 }
 
 // One workgroup per row: y = fp16((x * rstd) * gamma), rstd = 1 / sqrt(mean(x^2)
-// + eps), every step an IEEE fp32 operation; the sum of squares is a per-thread
-// strided sum folded by a wave shuffle tree and then across waves.
+// + eps), every step an IEEE fp32 operation (row_rstd, rms_apply).
 __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
                                                        int H, float eps, uint16_t* __restrict__ out) {
     const uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * H;
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        const float v = h2f(xr[i]);
-        ss = fmaf(v, v, ss);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    __shared__ float part[4];
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) tot += part[w];
-    const float rstd = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, static_cast<float>(H)), eps)));
+    const float rstd = row_rstd(xr, H, eps);
     uint16_t* orow = out + static_cast<size_t>(blockIdx.x) * H;
-    for (int i = threadIdx.x; i < H; i += blockDim.x)
-        orow[i] = f2h(__fmul_rn(__fmul_rn(h2f(xr[i]), rstd), h2f(gamma[i])));
+    for (int i = threadIdx.x; i < H; i += blockDim.x) orow[i] = rms_apply(xr[i], rstd, gamma[i]);
 }
 
 }  // namespace

@@ -26,31 +26,87 @@ __global__ __launch_bounds__(256) void w8a8_quant_act_kernel(const uint16_t* __r
     const uint16_t* xr = x + static_cast<size_t>(row) * K;
     float m = 0.f;
     for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        float v = fabsf(h2f(xr[k]));
-        m = v > m ? v : m;                      // NaN never becomes the maximum
+        const float v = fabsf(h2f(xr[k]));
+        m = v > m ? v : m;
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        float o = __shfl_xor(m, off, 64);
-        m = o > m ? o : m;
-    }
-    __shared__ float wmax[4];
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = wmax[0];
-    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) m = wmax[w] > m ? wmax[w] : m;
-    float scale = __fdiv_rn(m, 127.0f);
-    if (scale < 0.00000001f) scale = 0.00000001f;
+    const float scale = act_scale(row_absmax(m));
     const float inv = __fdiv_rn(1.0f, scale);
     int8_t* qr = xq + static_cast<size_t>(row) * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        float v = __fmul_rn(h2f(xr[k]), inv);
-        v = v > 127.0f ? 127.0f : v;
-        v = v < -128.0f ? -128.0f : v;
-        const float r = v >= 0.0f ? __fadd_rn(v, 0.5f) : __fsub_rn(v, 0.5f);
-        qr[k] = static_cast<int8_t>(static_cast<int>(r));
-    }
+    for (int k = threadIdx.x; k < K; k += blockDim.x) qr[k] = act_quant(xr[k], inv);
     if (threadIdx.x == 0) {
+        if (s32) s32[row] = scale;
+        if (s16) s16[row] = f2h(scale);
+    }
+}
+
+// RMSNorm and the activation quantisation in one pass over a row (the decode
+// sequence rms_norm -> w8a8_quantize of decoder_layer.cpp:955-966,
+// 1022-1032): the normed fp16 row is formed once, optionally stored (the
+// other projections of the step still read it), and quantised from the same
+// fp16 values -- bit-identical to rms_norm_kernel + w8a8_quant_act_kernel
+// (same element order per thread, same reductions).  Rows of up to 256 * PER
+// elements stay in registers, x and gamma loaded together up front; longer
+// rows take the strided loops (PER = 0).
+template <int PER>
+__global__ __launch_bounds__(256) void rms_norm_quant_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ gamma, int H, float eps,
+                                                             uint16_t* __restrict__ normed, int8_t* __restrict__ xq,
+                                                             float* __restrict__ s32, uint16_t* __restrict__ s16) {
+    const int row = blockIdx.x;
+    const int t = threadIdx.x;
+    const uint16_t* xr = x + static_cast<size_t>(row) * H;
+    uint16_t* nr = normed ? normed + static_cast<size_t>(row) * H : nullptr;
+    int8_t* qr = xq + static_cast<size_t>(row) * H;
+    float m = 0.f;
+    float inv;
+    float scale;
+    if constexpr (PER > 0) {
+        uint16_t xv[PER], gv[PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = t + 256 * j;
+            xv[j] = i < H ? xr[i] : uint16_t(0);
+            gv[j] = i < H ? gamma[i] : uint16_t(0);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            if (t + 256 * j < H) {
+                const float v = h2f(xv[j]);
+                ss = fmaf(v, v, ss);
+            }
+        }
+        const float rstd = block_rstd(ss, H, eps);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = t + 256 * j;
+            if (i < H) {
+                xv[j] = rms_apply(xv[j], rstd, gv[j]);                  // xv now holds the normed row
+                if (nr) nr[i] = xv[j];
+                const float v = fabsf(h2f(xv[j]));
+                m = v > m ? v : m;
+            }
+        }
+        scale = act_scale(row_absmax(m));
+        inv = __fdiv_rn(1.0f, scale);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int i = t + 256 * j;
+            if (i < H) qr[i] = act_quant(xv[j], inv);
+        }
+    } else {
+        const float rstd = row_rstd(xr, H, eps);
+        for (int i = t; i < H; i += blockDim.x) {
+            const uint16_t h = rms_apply(xr[i], rstd, gamma[i]);
+            if (nr) nr[i] = h;
+            const float v = fabsf(h2f(h));
+            m = v > m ? v : m;
+        }
+        scale = act_scale(row_absmax(m));
+        inv = __fdiv_rn(1.0f, scale);
+        for (int i = t; i < H; i += blockDim.x) qr[i] = act_quant(rms_apply(xr[i], rstd, gamma[i]), inv);
+    }
+    if (t == 0) {
         if (s32) s32[row] = scale;
         if (s16) s16[row] = f2h(scale);
     }
@@ -263,6 +319,20 @@ int mcv_w8a8_quantize_act(const void* x, int64_t M, int64_t K, int8_t* xq, float
     hipLaunchKernelGGL(w8a8_quant_act_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<const uint16_t*>(x), static_cast<int>(K), xq, s32, static_cast<uint16_t*>(s16));
     return check_launch("w8a8_quant_act_kernel");
+}
+
+int mcv_rms_norm_w8a8_quantize(const void* x, const void* gamma, int64_t M, int64_t H, double eps, void* normed,
+                               int8_t* xq, float* s32, void* s16, mcv_stream_t stream) {
+    if (!x || !gamma || !xq || (!s32 && !s16)) return fail(MCV_ERR_INVALID_ARG, "rms_norm_w8a8_quantize: null pointer");
+    if (M <= 0 || H <= 0 || M > 0x7fffffff || H > 0x7fffffff || !(eps >= 0.0))
+        return fail(MCV_ERR_SHAPE, "rms_norm_w8a8_quantize: bad shape M=%lld H=%lld or eps", (long long)M, (long long)H);
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    auto fn = H <= 1024 ? rms_norm_quant_kernel<4> : H <= 4096 ? rms_norm_quant_kernel<16> : rms_norm_quant_kernel<0>;
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(M)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(gamma), static_cast<int>(H),
+                       static_cast<float>(eps), static_cast<uint16_t*>(normed), xq, s32, static_cast<uint16_t*>(s16));
+    return check_launch("rms_norm_quant_kernel");
 }
 
 int mcv_w8a8_gemm_i32(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, int w_layout, int32_t* acc,
