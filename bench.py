@@ -281,6 +281,50 @@ def wl_mlp(pkg, args, fused=True):
                 kernel="mlp block (gate+up+silu launch, down GEMV)" if fused else "mlp block (4 launches)")
 
 
+def wl_mlp_w8a8(pkg, args, fused=True):
+    """The decode MLP block over W8A8 weights (gate/up 1024->3584, down
+    3584->1024), 32 layer sets (352 MB, past the MALL), from the normed fp16
+    row: fused = quantise x, one gate+up+silu*mul launch, quantise act, down;
+    unfused = the reference's quantise, gate, up, silu_mul, quantise, down."""
+    import torch
+    H, I = 1024, 3584
+    nsets = args.copies or 32
+    sets = []
+    for s in range(nsets):
+        rng = np.random.default_rng(200 + s)
+        sets.append([pkg.quantize_dense_weight_w8a8(to_dev_f16(f16_normal(rng, (K, N), 0.02)))
+                     for (K, N) in ((H, I), (H, I), (I, H))])
+    x = to_dev_f16(f16_normal(np.random.default_rng(1), (1, H), 1.0))
+    xq = torch.empty((1, H), dtype=torch.int8, device="cuda")
+    xs = torch.empty(1, dtype=torch.float32, device="cuda")
+    g = torch.empty((1, I), dtype=torch.float16, device="cuda")
+    u = torch.empty_like(g)
+    a = torch.empty_like(g)
+    aq = torch.empty((1, I), dtype=torch.int8, device="cuda")
+    asc = torch.empty(1, dtype=torch.float32, device="cuda")
+    y = torch.empty((1, H), dtype=torch.float16, device="cuda")
+
+    def block(i):
+        L = sets[i]
+        pkg.w8a8_quantize(x, xq, xs)
+        if fused:
+            pkg.mlp_gate_up_silu_w8a8(xq, xs, L[0], L[1], a)
+        else:
+            pkg.matmul_w8a8(xq, xs, L[0], g)
+            pkg.matmul_w8a8(xq, xs, L[1], u)
+            pkg.silu_mul(g, u, a)
+        pkg.w8a8_quantize(a, aq, asc)
+        pkg.matmul_w8a8(aq, asc, L[2], y)
+
+    nbytes = 3 * H * I + 2 * (2 * I + I) * 4 + (2 * H + H) + (2 * I + I) * 2 + 2 * H
+    total_ms, _ = time_steps(block, len(sets), args.steps, args.warmup)
+    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=[total_ms / args.steps], unit="GB/s", bound="hbm",
+                config={"workload": "w8a8_mlp_block_decode" + ("" if fused else "_unfused"), "M": 1, "hidden": H,
+                        "intermediate": I, "weight_sets_rotated": len(sets)},
+                dtype="int8 (i32 accumulate, fused f16 epilogue)",
+                kernel="w8a8 mlp block (" + ("4 launches)" if fused else "6 launches)"))
+
+
 def wl_prefill(pkg, args):
     import torch
     M, K, N = args.M or 2048, args.K or 1024, args.N or 3584
@@ -384,7 +428,8 @@ def wl_copy(pkg, args):
 
 WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
              "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, fused=False), "prefill": wl_prefill, "w8a8": wl_w8a8,
-             "copy": wl_copy, "norm_quant": wl_norm_quant,
+             "copy": wl_copy, "norm_quant": wl_norm_quant, "mlp_w8a8": wl_mlp_w8a8,
+             "mlp_w8a8_unfused": lambda pkg, args: wl_mlp_w8a8(pkg, args, fused=False),
              "norm_quant_unfused": lambda pkg, args: wl_norm_quant(pkg, args, fused=False), "vendor_f16": wl_vendor, "vendor_int8": lambda pkg, args: wl_vendor(pkg, args, int8=True)}
 
 

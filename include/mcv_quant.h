@@ -271,6 +271,17 @@ int mcv_w8a8_gemm_f16(const int8_t* xq_dev, const void* x_scale_dev, int x_scale
                       const void* w_scale_dev, int w_scale_dtype, void* out_dev,
                       mcv_stream_t stream);
 
+/* Decode MLP front half over W8A8 weights: act[M][N] fp16 = silu(gate) * up,
+ * gate and up each the fused epilogue of mcv_w8a8_gemm_f16 over the same
+ * quantised x (one activation quantisation shared by both, as
+ * decoder_layer.cpp:1029-1046 does).  Both weights MCV_W8_TILED [K][N], their
+ * scales in ws_dtype; M in [1, 4].  One launch, bit-identical to two
+ * mcv_w8a8_gemm_f16 calls and mcv_silu_mul. */
+int mcv_w8a8_gate_up_silu(const int8_t* xq_dev, const void* x_scale_dev, int x_scale_dtype, int64_t M,
+                          int64_t K, int64_t N, const int8_t* w_gate_dev, const void* w_scale_gate_dev,
+                          const int8_t* w_up_dev, const void* w_scale_up_dev, int w_scale_dtype, void* act_dev,
+                          mcv_stream_t stream);
+
 /* Bytes of a K x N weight in MCV_W8_TILED (0 on bad shape). */
 int64_t mcv_w8a8_tiled_bytes(int64_t K, int64_t N);
 

@@ -72,6 +72,8 @@ _SIGS = {
     "mcv_w8a8_gemm_f16": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_tiled_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "mcv_w8a8_gate_up_silu": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp,
+                                       _vp]),
     "mcv_w8a8_pack_tiled_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "mcv_w8a8_quantize_weight_nk_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_pack_tiled_nk_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
@@ -542,6 +544,22 @@ def matmul_w8a8(x_int8, x_scale, w: W8A8QuantizedWeight, out=None, use_f32_scale
     ws = w.w_scale_f32 if use_f32_scale else w.w_scale
     _check(lib().mcv_w8a8_gemm_f16(_dev(x_int8), _dev(x_scale), _scale_dtype(x_scale), M, K, w.N, _dev(w.w_int8),
                                    w.layout, _dev(ws), _scale_dtype(ws), _dev(out), _stream(stream)), "matmul_w8a8")
+    return out
+
+
+def mlp_gate_up_silu_w8a8(x_int8, x_scale, w_gate: W8A8QuantizedWeight, w_up: W8A8QuantizedWeight, out=None,
+                          use_f32_scale=True, stream=None):
+    """act = silu(gate) * up over one quantised x, tiled weights, M <= 4 (decoder_layer.cpp:1029-1046
+    + silu_mul): one launch, bit-identical to two matmul_w8a8 calls and silu_mul."""
+    torch = _torch()
+    M, K = x_int8.shape
+    if out is None:
+        out = torch.empty((M, w_gate.N), dtype=torch.float16, device=x_int8.device)
+    wsg = w_gate.w_scale_f32 if use_f32_scale else w_gate.w_scale
+    wsu = w_up.w_scale_f32 if use_f32_scale else w_up.w_scale
+    _check(lib().mcv_w8a8_gate_up_silu(_dev(x_int8), _dev(x_scale), _scale_dtype(x_scale), M, K, w_gate.N,
+                                       _dev(w_gate.w_int8), _dev(wsg), _dev(w_up.w_int8), _dev(wsu), _scale_dtype(wsg),
+                                       _dev(out), _stream(stream)), "mlp_gate_up_silu_w8a8")
     return out
 
 

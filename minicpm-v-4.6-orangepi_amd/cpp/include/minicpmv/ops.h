@@ -55,6 +55,12 @@ void w8a8_quantize(const Tensor& x, Tensor& x_int8, Tensor& x_scale, hipStream_t
 void rms_norm_w8a8_quantize(const Tensor& x, const Tensor& gamma, double epsilon, Tensor* normed, Tensor& x_int8,
                             Tensor& x_scale, hipStream_t stream);
 
+// W8A8 decode MLP front half: act = silu(gate) * up over one quantised x
+// (decoder_layer.cpp:1029-1046 + silu_mul), bit-identical to two matmul_w8a8
+// calls and silu_mul; one launch for M <= 4 with tiled weights.
+void mlp_gate_up_silu_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8QuantizedWeight& gate,
+                           const W8A8QuantizedWeight& up, Tensor& act, hipStream_t stream);
+
 // out fp16 [M, N] = RNE((acc * w_scale[n]) * x_scale[m]); scales fp16 or fp32.
 void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream);
 

@@ -170,6 +170,35 @@ void matmul_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8Quantize
               "matmul_w8a8");
 }
 
+void mlp_gate_up_silu_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8QuantizedWeight& gate,
+                           const W8A8QuantizedWeight& up, Tensor& act, hipStream_t stream) {
+    require(x_int8.dtype() == DType::Int8 && act.dtype() == DType::Float16, "mlp_gate_up_silu_w8a8 needs int8 x, fp16 act");
+    require(gate.K == up.K && gate.N == up.N, "mlp_gate_up_silu_w8a8 gate and up must have one shape");
+    require(x_int8.shape().size() == 2 && x_int8.shape()[1] == gate.K, "mlp_gate_up_silu_w8a8 x must be [M, K]");
+    const int64_t M = x_int8.shape()[0];
+    require(act.shape() == std::vector<int64_t>{M, gate.N}, "mlp_gate_up_silu_w8a8 act must be [M, N]");
+    require(static_cast<int64_t>(x_scale.numel()) == M, "mlp_gate_up_silu_w8a8 x_scale must be [M]");
+    const int xs = scale_dtype(x_scale, "x_scale");
+    const bool f32 = xs == MCV_F32 && gate.w_scale_f32.data() != nullptr && up.w_scale_f32.data() != nullptr;
+    const Tensor& wsg = f32 ? gate.w_scale_f32 : gate.w_scale;
+    const Tensor& wsu = f32 ? up.w_scale_f32 : up.w_scale;
+    if (M <= 4 && gate.layout == MCV_W8_TILED && up.layout == MCV_W8_TILED) {
+        check_mcv(mcv_w8a8_gate_up_silu(static_cast<const int8_t*>(x_int8.data()), x_scale.data(), xs, M, gate.K,
+                                        gate.N, static_cast<const int8_t*>(gate.w_int8.data()), wsg.data(),
+                                        static_cast<const int8_t*>(up.w_int8.data()), wsu.data(),
+                                        scale_dtype(wsg, "w_scale"), act.data(), stream),
+                  "mlp_gate_up_silu_w8a8");
+        return;
+    }
+    // prefill sizes or [K, N] weights: the two fused GEMMs and silu_mul
+    Tensor g({M, gate.N}, DType::Float16), u({M, gate.N}, DType::Float16);
+    g.allocate();
+    u.allocate();
+    matmul_w8a8(x_int8, x_scale, gate, g, stream);
+    matmul_w8a8(x_int8, x_scale, up, u, stream);
+    silu_mul(g, u, act, stream);
+}
+
 void w4a16_dequant(const W4A16QuantizedWeight& w, Tensor* w_f16, Tensor* w_i8, hipStream_t stream) {
     const std::vector<int64_t> kn{w.K, w.N};
     if (w_f16) require(w_f16->dtype() == DType::Float16 && w_f16->shape() == kn, "w4a16_dequant f16 out must be [K, N]");

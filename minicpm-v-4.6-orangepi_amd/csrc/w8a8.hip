@@ -9,6 +9,9 @@
 
 namespace mcv {
 
+int launch_w8a8_tiled_gate_up_silu(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* wg,
+                                   const void* wsg, const int8_t* wu, const void* wsu, int ws16, const void* xs,
+                                   int xs16, void* act, hipStream_t stream);
 int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
                       const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
 
@@ -19,21 +22,42 @@ namespace {
 // q = trunc(clamp(x * inv, -128, 127) +- 0.5): the closed form of
 // op_kernel/w8a8_quantize_custom.cpp:25-41 and quantized_weight.cpp:197-202,
 // every operation an explicitly rounded IEEE fp32 operation (no contraction).
+// Rows of up to 256 * PER elements are held in registers between the two
+// passes (PER = 0: strided reloads).
+template <int PER>
 __global__ __launch_bounds__(256) void w8a8_quant_act_kernel(const uint16_t* __restrict__ x, int K,
                                                              int8_t* __restrict__ xq, float* __restrict__ s32,
                                                              uint16_t* __restrict__ s16) {
     const int row = blockIdx.x;
+    const int t = threadIdx.x;
     const uint16_t* xr = x + static_cast<size_t>(row) * K;
-    float m = 0.f;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        const float v = fabsf(h2f(xr[k]));
-        m = v > m ? v : m;
-    }
-    const float scale = act_scale(row_absmax(m));
-    const float inv = __fdiv_rn(1.0f, scale);
     int8_t* qr = xq + static_cast<size_t>(row) * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) qr[k] = act_quant(xr[k], inv);
-    if (threadIdx.x == 0) {
+    float m = 0.f;
+    float scale;
+    if constexpr (PER > 0) {
+        uint16_t xv[PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) xv[j] = t + 256 * j < K ? xr[t + 256 * j] : uint16_t(0);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const float v = fabsf(h2f(xv[j]));                // padding contributes 0, never above the max
+            m = v > m ? v : m;
+        }
+        scale = act_scale(row_absmax(m));
+        const float inv = __fdiv_rn(1.0f, scale);
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (t + 256 * j < K) qr[t + 256 * j] = act_quant(xv[j], inv);
+    } else {
+        for (int k = t; k < K; k += blockDim.x) {
+            const float v = fabsf(h2f(xr[k]));
+            m = v > m ? v : m;
+        }
+        scale = act_scale(row_absmax(m));
+        const float inv = __fdiv_rn(1.0f, scale);
+        for (int k = t; k < K; k += blockDim.x) qr[k] = act_quant(xr[k], inv);
+    }
+    if (t == 0) {
         if (s32) s32[row] = scale;
         if (s16) s16[row] = f2h(scale);
     }
@@ -316,7 +340,8 @@ int mcv_w8a8_quantize_act(const void* x, int64_t M, int64_t K, int8_t* xq, float
         return fail(MCV_ERR_SHAPE, "w8a8_quantize: bad shape M=%lld K=%lld", (long long)M, (long long)K);
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    hipLaunchKernelGGL(w8a8_quant_act_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, static_cast<hipStream_t>(stream),
+    auto fn = K <= 1024 ? w8a8_quant_act_kernel<4> : K <= 4096 ? w8a8_quant_act_kernel<16> : w8a8_quant_act_kernel<0>;
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(M)), dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<const uint16_t*>(x), static_cast<int>(K), xq, s32, static_cast<uint16_t*>(s16));
     return check_launch("w8a8_quant_act_kernel");
 }
@@ -352,6 +377,21 @@ int mcv_w8a8_gemm_f16(const int8_t* xq, const void* xs, int xs_dtype, int64_t M,
     if ((rc = require_device()) != MCV_OK) return rc;
     return launch_gemm<true>(xq, M, K, N, w, w_layout, out, xs, xs_dtype == MCV_F16, ws, ws_dtype == MCV_F16,
                              static_cast<hipStream_t>(stream));
+}
+
+int mcv_w8a8_gate_up_silu(const int8_t* xq, const void* xs, int xs_dtype, int64_t M, int64_t K, int64_t N,
+                          const int8_t* w_gate, const void* ws_gate, const int8_t* w_up, const void* ws_up,
+                          int ws_dtype, void* act, mcv_stream_t stream) {
+    int rc = check_gemm_args(xq, M, K, N, w_gate, MCV_W8_TILED, act, "mcv_w8a8_gate_up_silu");
+    if (rc != MCV_OK) return rc;
+    if (!w_up || !xs || !ws_gate || !ws_up) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_gate_up_silu: null pointer");
+    if (reinterpret_cast<uintptr_t>(w_up) % 16 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_gate_up_silu: weights must be 16-byte aligned");
+    if (M > 4) return fail(MCV_ERR_SHAPE, "mcv_w8a8_gate_up_silu: decode entry point, M must be 1..4 (M=%lld)", (long long)M);
+    if (!dtype_ok(xs_dtype) || !dtype_ok(ws_dtype)) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_gate_up_silu: bad scale dtype");
+    if ((rc = require_device()) != MCV_OK) return rc;
+    return launch_w8a8_tiled_gate_up_silu(xq, M, K, N, w_gate, ws_gate, w_up, ws_up, ws_dtype == MCV_F16, xs,
+                                          xs_dtype == MCV_F16, act, static_cast<hipStream_t>(stream));
 }
 
 int mcv_w8a8_dequant(const int32_t* acc, const void* xs, int xs_dtype, const void* ws, int ws_dtype, int64_t M, int64_t N,

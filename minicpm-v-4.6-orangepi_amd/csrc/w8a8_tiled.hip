@@ -309,62 +309,137 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
 }
 
 // ------------------------------------------------------------------ GEMV --
-// grid = nslab, block = 512 (eight waves).  Wave v walks k-blocks v, v+8, ...
-// Lane l of half j accumulates column 64 slab + 32 j + l%32 over its k-half
-// l/32 with v_dot4_i32_i8 (exact int32).
-template <int MR, bool OUT_F16>
-__global__ __launch_bounds__(512) void w8a8_tiled_gemv_kernel(const int8_t* __restrict__ xq,
-                                                              const int8_t* __restrict__ w, int M, int K, int N,
-                                                              int KB, void* __restrict__ out,
-                                                              const void* __restrict__ xs, int xs16,
-                                                              const void* __restrict__ ws, int ws16, int nslab) {
-    __shared__ int red[8][MR][2][64];
+// M <= 4.  A workgroup owns HALVES 32-column halves of one 64-column slab
+// (grid (nslab, 2 / HALVES)); its NW waves split the 32-k blocks, wave v
+// taking kb = v, v + NW, ...  Each wave issues the loads of U k-blocks (weight
+// lines and x vectors) before it multiplies any of them; k-blocks past the end
+// read as zero through an out-of-range buffer offset, so no load is
+// conditional.  Lane l of a half accumulates column 32 j + l%32 over k-half
+// l/32 with v_dot4_i32_i8 (exact int32); the partial sums meet in LDS.  DUAL:
+// the same over a second weight (gate and up) with the fp16 epilogues of both
+// and silu_mul_f16 -- bit-identical to two GEMVs and silu_mul, since the int32
+// sums are exact and the epilogue code is shared.
+template <int MR, int NW, int HALVES, int U, bool OUT_F16, bool DUAL>
+__global__ __launch_bounds__(64 * NW) void w8a8_tiled_gemv_kernel(
+    const int8_t* __restrict__ xq, const int8_t* __restrict__ w, const int8_t* __restrict__ w2, int M, int K, int N,
+    int KB, void* __restrict__ out, const void* __restrict__ xs, int xs16, const void* __restrict__ ws,
+    const void* __restrict__ ws2, int ws16, int nslab) {
+    constexpr int NWT = DUAL ? 2 : 1;
+    __shared__ int red[NW][MR][NWT][HALVES][64];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slab = blockIdx.x;
+    const int j0 = HALVES == 2 ? 0 : static_cast<int>(blockIdx.y);
     const int h = lane >> 5;
-    const __amdgpu_buffer_rsrc_t wr = rsrc(w, static_cast<uint32_t>(nslab) * KB * 2 * kW8Block);
+    constexpr uint32_t kNowhere = 0xFFFFFF00u;
+    const uint32_t wbytes = static_cast<uint32_t>(nslab) * KB * 2 * kW8Block;
+    const __amdgpu_buffer_rsrc_t wr[2] = {rsrc(w, wbytes), rsrc(DUAL ? w2 : w, wbytes)};
     const __amdgpu_buffer_rsrc_t xr = rsrc(xq, static_cast<uint32_t>(M) * K);
-    int acc[MR][2];
+    int acc[MR][NWT][HALVES];
 #pragma unroll
-    for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0;
-    for (int kb = wave; kb < KB; kb += 8) {
-        int4_t wv[2];
+    for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            wv[j] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   wr, ((static_cast<uint32_t>(slab) * KB + kb) * 2 + j) * kW8Block + lane * 16u, 0, 0));
+        for (int t = 0; t < NWT; ++t)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            // k past K in a row meets zero weights; rows past M are not used
-            const int4_t xv = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             xr, static_cast<uint32_t>(m * K + kb * 32 + h * 16), 0, 0));
+            for (int jj = 0; jj < HALVES; ++jj) acc[m][t][jj] = 0;
+    for (int kb0 = wave; kb0 < KB; kb0 += NW * U) {
+        int4_t wv[U][NWT][HALVES];
+        int4_t xv[U][MR];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+        for (int u = 0; u < U; ++u) {
+            const int kb = kb0 + u * NW;
+            const bool live = kb < KB;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[m][j] = __builtin_amdgcn_sdot4(wv[j][q], xv[q], acc[m][j], false);
+            for (int t = 0; t < NWT; ++t)
+#pragma unroll
+                for (int jj = 0; jj < HALVES; ++jj) {
+                    const uint32_t off =
+                        live ? ((static_cast<uint32_t>(slab) * KB + kb) * 2 + j0 + jj) * kW8Block + lane * 16u : kNowhere;
+                    wv[u][t][jj] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(wr[t], off, 0, 0));
+                }
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                // k past K in a row meets zero weights; rows past M are not used
+                const uint32_t off = live ? static_cast<uint32_t>(m * K + kb * 32 + h * 16) : kNowhere;
+                xv[u][m] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            }
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int t = 0; t < NWT; ++t)
+#pragma unroll
+                    for (int jj = 0; jj < HALVES; ++jj)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            acc[m][t][jj] = __builtin_amdgcn_sdot4(wv[u][t][jj][q], xv[u][m][q], acc[m][t][jj], false);
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) red[wave][m][j][lane] = acc[m][j];
-    __syncthreads();
-    // thread t < 64 * MR finishes (row t/64, column 64 slab + t%64)
-    const int t = threadIdx.x;
-    if (t >= 64 * MR) return;
-    const int m = t >> 6, c = t & 63, j = c >> 5, l = c & 31;
-    int sum = 0;
+        for (int t = 0; t < NWT; ++t)
 #pragma unroll
-    for (int v = 0; v < 8; ++v) sum += red[v][m][j][l] + red[v][m][j][l + 32];
-    const int n = slab * kSlab + c;
-    if (m >= M || n >= N) return;
-    if constexpr (OUT_F16) {
-        const float v = __fmul_rn(__fmul_rn(static_cast<float>(sum), scale_at(ws, ws16, n)), scale_at(xs, xs16, m));
-        static_cast<uint16_t*>(out)[static_cast<size_t>(m) * N + n] = f2h(v);
-    } else {
-        static_cast<int32_t*>(out)[static_cast<size_t>(m) * N + n] = sum;
+            for (int jj = 0; jj < HALVES; ++jj) red[wave][m][t][jj][lane] = acc[m][t][jj];
+    __syncthreads();
+    // thread -> (row m, half jj, column l of the half)
+    const int tid = threadIdx.x;
+    if (tid >= 32 * HALVES * MR) return;
+    const int m = tid / (32 * HALVES), jj = (tid >> 5) % HALVES, l = tid & 31;
+    int sum[NWT];
+#pragma unroll
+    for (int t = 0; t < NWT; ++t) {
+        sum[t] = 0;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) sum[t] += red[v][m][t][jj][l] + red[v][m][t][jj][l + 32];
     }
+    const int n = slab * kSlab + 32 * (j0 + jj) + l;
+    if (m >= M || n >= N) return;
+    const size_t o = static_cast<size_t>(m) * N + n;
+    if constexpr (DUAL) {
+        const float xsv = scale_at(xs, xs16, m);
+        const uint16_t g16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[0]), scale_at(ws, ws16, n)), xsv));
+        const uint16_t u16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[1]), scale_at(ws2, ws16, n)), xsv));
+        static_cast<uint16_t*>(out)[o] = silu_mul_f16(g16, u16);
+    } else if constexpr (OUT_F16) {
+        const float v = __fmul_rn(__fmul_rn(static_cast<float>(sum[0]), scale_at(ws, ws16, n)), scale_at(xs, xs16, m));
+        static_cast<uint16_t*>(out)[o] = f2h(v);
+    } else {
+        static_cast<int32_t*>(out)[o] = sum[0];
+    }
+}
+
+// GEMV launch: narrow outputs (fewer than 128 slabs) get a workgroup per
+// 32-column half and 16 waves, wide ones a workgroup per slab and 8 waves;
+// every wave keeps 4 k-blocks of loads in flight.
+template <bool OUT_F16, bool DUAL>
+int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, const int8_t* w2, void* out,
+                     const void* xs, int xs16, const void* ws, const void* ws2, int ws16, hipStream_t stream) {
+    const int64_t nslab = ceil_div(N, kSlab);
+    const int64_t KB = ceil_div(K, 128) * 4;
+    if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 32) || M * K >= (int64_t(1) << 32))
+        return fail(MCV_ERR_SHAPE, "w8a8 tiled GEMV: weight or activation exceeds 4 GiB");
+    const bool narrow = nslab < 128;
+    const dim3 grid(static_cast<unsigned>(nslab), narrow ? 2u : 1u);
+    const dim3 block(narrow ? 1024 : 512);
+    const int iM = static_cast<int>(M), iK = static_cast<int>(K), iN = static_cast<int>(N), iKB = static_cast<int>(KB);
+    const int ns = static_cast<int>(nslab);
+#define MCV_GEMV8(R)                                                                                                 \
+    if (narrow)                                                                                                      \
+        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, 16, 1, 4, OUT_F16, DUAL>), grid, block, 0, stream, xq, w, w2, iM, \
+                           iK, iN, iKB, out, xs, xs16, ws, ws2, ws16, ns);                                             \
+    else                                                                                                             \
+        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, 8, 2, 4, OUT_F16, DUAL>), grid, block, 0, stream, xq, w, w2, iM,  \
+                           iK, iN, iKB, out, xs, xs16, ws, ws2, ws16, ns);
+    switch (M) {
+        case 1: MCV_GEMV8(1) break;
+        case 2: MCV_GEMV8(2) break;
+        case 3: MCV_GEMV8(3) break;
+        default: MCV_GEMV8(4) break;
+    }
+#undef MCV_GEMV8
+    return check_launch(DUAL ? "w8a8_tiled_gemv_kernel<gate_up_silu>" : "w8a8_tiled_gemv_kernel");
 }
 
 struct Shape8 {
@@ -432,24 +507,8 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
     if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 32) || M * K >= (int64_t(1) << 32))
         return fail(MCV_ERR_SHAPE, "w8a8 tiled: weight or activation exceeds 4 GiB");
     if (M <= 4) {
-        const dim3 grid(static_cast<unsigned>(nslab)), block(512);
-        const int iM = static_cast<int>(M), iK = static_cast<int>(K), iN = static_cast<int>(N), iKB = static_cast<int>(KB);
-        const int ns = static_cast<int>(nslab);
-#define MCV_GEMV8(R)                                                                                                  \
-    if (f16)                                                                                                          \
-        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, true>), grid, block, 0, stream, xq, w, iM, iK, iN, iKB, out, xs, \
-                           xs16, ws, ws16, ns);                                                                       \
-    else                                                                                                              \
-        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, false>), grid, block, 0, stream, xq, w, iM, iK, iN, iKB, out,   \
-                           xs, xs16, ws, ws16, ns);
-        switch (M) {
-            case 1: MCV_GEMV8(1) break;
-            case 2: MCV_GEMV8(2) break;
-            case 3: MCV_GEMV8(3) break;
-            default: MCV_GEMV8(4) break;
-        }
-#undef MCV_GEMV8
-        return check_launch("w8a8_tiled_gemv_kernel");
+        return f16 ? launch_w8a8_gemv<true, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream)
+                   : launch_w8a8_gemv<false, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream);
     }
     const int64_t KT_all = KB / 4;                      // 128-k stages over the padded K
     const Shape8 s = choose8(M, KT_all, nslab);
@@ -471,6 +530,13 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
                            static_cast<int>(M), static_cast<int>(K), static_cast<int>(N), KBs, out, xs, xs16, ws, ws16,
                            static_cast<int>(nslab), static_cast<int>(n_tiles), static_cast<int>(total), KT, col_major);
     return check_launch("w8a8_tiled_gemm_kernel");
+}
+
+// Shapes were validated by the caller; M in [1, 4], both weights tiled.
+int launch_w8a8_tiled_gate_up_silu(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* wg,
+                                   const void* wsg, const int8_t* wu, const void* wsu, int ws16, const void* xs,
+                                   int xs16, void* act, hipStream_t stream) {
+    return launch_w8a8_gemv<true, true>(xq, M, K, N, wg, wu, act, xs, xs16, wsg, wsu, ws16, stream);
 }
 
 }  // namespace mcv

@@ -24,7 +24,7 @@ def _u16(t):
     return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("M,K", [(1, 1024), (256, 1024), (1024, 1024), (3, 3584), (2, 1040), (1, 16)])
+@pytest.mark.parametrize("M,K", [(1, 1024), (256, 1024), (1024, 1024), (3, 3584), (2, 1040), (1, 16), (2, 5000), (1, 4096)])
 def test_quantize_act_bit_exact(mcv, oracle, cuda, M, K):
     torch = _torch()
     rng = np.random.default_rng(M * 10 + K)
@@ -191,3 +191,46 @@ def test_decode_shapes_fused(mcv, oracle, cuda, K, N):
     acc_o = oracle.gemm_i32(q_o, wq_o)
     assert np.array_equal(acc.cpu().numpy(), acc_o)
     assert np.array_equal(_u16(out), oracle.w8a8_dequant(acc_o, s_o, ws_o))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 3584), (2, 1024, 3584), (4, 2048, 6144), (3, 384, 208), (1, 128, 64)],
+                         ids=lambda v: str(v))
+def test_gate_up_silu_fused(mcv, oracle, cuda, M, K, N):
+    """One launch == gate and up fused GEMVs + silu_mul, bit for bit, with fp32
+    and with fp16 scales; and the oracle's composition of the same stages."""
+    torch = _torch()
+    rng = np.random.default_rng(M * 31 + K + N)
+    wg = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (K, N), 0.02)))
+    wu = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (K, N), 0.02)))
+    x = f16_normal(rng, (M, K), 1.0)
+    s16 = torch.empty(M, dtype=torch.float16, device="cuda")
+    xq, xs, _ = mcv.w8a8_quantize(_f16_dev(x), x_scale_f16=s16)
+    for f32 in (True, False):
+        xsc = xs if f32 else s16
+        fused = mcv.mlp_gate_up_silu_w8a8(xq, xsc, wg, wu, use_f32_scale=f32)
+        three = mcv.silu_mul(mcv.matmul_w8a8(xq, xsc, wg, use_f32_scale=f32),
+                             mcv.matmul_w8a8(xq, xsc, wu, use_f32_scale=f32))
+        assert torch.equal(fused.view(torch.int16), three.view(torch.int16)), f32
+    # oracle: int32 products, reference epilogue, silu*mul
+    q_o = xq.cpu().numpy()
+    s_o = xs.cpu().numpy()
+    g_o = oracle.w8a8_dequant(oracle.gemm_i32(q_o, _tiled_to_kn(mcv, wg)), s_o, wg.w_scale_f32.cpu().numpy())
+    u_o = oracle.w8a8_dequant(oracle.gemm_i32(q_o, _tiled_to_kn(mcv, wu)), s_o, wu.w_scale_f32.cpu().numpy())
+    want = oracle.silu_mul(g_o, u_o)
+    got = _u16(mcv.mlp_gate_up_silu_w8a8(xq, xs, wg, wu))
+    gv, wv = got.view(np.float16).astype(np.float64), want.view(np.float16).astype(np.float64)
+    ulp = np.abs(np.spacing(want.view(np.float16))).astype(np.float64)
+    assert (np.abs(gv - wv) <= ulp).all()                 # exp may differ by an fp32 ulp between libms
+    assert (got == want).mean() > 0.99
+
+
+def _tiled_to_kn(mcv, w):
+    """int8 [K, N] of a tiled weight, read back through the documented layout formula."""
+    t = w.w_int8.cpu().numpy()
+    K, N = w.K, w.N
+    kb = -(-K // 128) * 4
+    k = np.arange(K)[:, None]
+    n = np.arange(N)[None, :]
+    l = n % 32 + 32 * ((k % 32) // 16)
+    off = ((((n // 64) * kb + k // 32) * 2 + (n % 64) // 32) * 64 + l) * 16 + k % 16
+    return t[off]
