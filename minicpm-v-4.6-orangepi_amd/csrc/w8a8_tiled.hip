@@ -410,9 +410,13 @@ __global__ __launch_bounds__(64 * NW) void w8a8_tiled_gemv_kernel(
     }
 }
 
-// GEMV launch: narrow outputs (fewer than 128 slabs) get a workgroup per
-// 32-column half and 16 waves, wide ones a workgroup per slab and 8 waves;
-// every wave keeps 4 k-blocks of loads in flight.
+// GEMV launch.  Measured with rotated weights (graph-replayed, M=1): narrow
+// outputs (fewer than 128 slabs) want a workgroup per 32-column half -- 8
+// waves with 4 k-blocks in flight up to K=2048 (K=1024, N=3584: 3.5 us; one
+// workgroup per slab, 8 waves, one block at a time: 4.8 us), 16 waves with 2
+// for longer K (K=3584, N=1024: 5.4 us against 10.0); wide ones a workgroup
+// per slab with 16 waves and 2 blocks (N=248096: 40.7 us against 47).
+// MCV_W8GEMV="NW,HALVES,U" picks another instantiated variant (sweeps).
 template <bool OUT_F16, bool DUAL>
 int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, const int8_t* w2, void* out,
                      const void* xs, int xs16, const void* ws, const void* ws2, int ws16, hipStream_t stream) {
@@ -421,17 +425,25 @@ int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const in
     if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 32) || M * K >= (int64_t(1) << 32))
         return fail(MCV_ERR_SHAPE, "w8a8 tiled GEMV: weight or activation exceeds 4 GiB");
     const bool narrow = nslab < 128;
-    const dim3 grid(static_cast<unsigned>(nslab), narrow ? 2u : 1u);
-    const dim3 block(narrow ? 1024 : 512);
+    int nw = narrow && KB <= 64 ? 8 : 16, halves = narrow ? 1 : 2, u = narrow && KB <= 64 ? 4 : 2;
+    if (const char* e = std::getenv("MCV_W8GEMV")) {
+        int a = 0, b = 0, c = 0;
+        if (std::sscanf(e, "%d,%d,%d", &a, &b, &c) == 3) { nw = a; halves = b; u = c; }
+    }
+    const dim3 grid(static_cast<unsigned>(nslab), halves == 1 ? 2u : 1u);
+    const dim3 block(64 * nw);
     const int iM = static_cast<int>(M), iK = static_cast<int>(K), iN = static_cast<int>(N), iKB = static_cast<int>(KB);
     const int ns = static_cast<int>(nslab);
-#define MCV_GEMV8(R)                                                                                                 \
-    if (narrow)                                                                                                      \
-        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, 16, 1, 4, OUT_F16, DUAL>), grid, block, 0, stream, xq, w, w2, iM, \
-                           iK, iN, iKB, out, xs, xs16, ws, ws2, ws16, ns);                                             \
-    else                                                                                                             \
-        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, 8, 2, 4, OUT_F16, DUAL>), grid, block, 0, stream, xq, w, w2, iM,  \
-                           iK, iN, iKB, out, xs, xs16, ws, ws2, ws16, ns);
+    bool launched = false;
+#define MCV_GEMV8V(R, NW_, H_, U_)                                                                                \
+    if (!launched && nw == NW_ && halves == H_ && u == U_) {                                                      \
+        hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, NW_, H_, U_, OUT_F16, DUAL>), grid, block, 0, stream, xq, w, w2, \
+                           iM, iK, iN, iKB, out, xs, xs16, ws, ws2, ws16, ns);                                    \
+        launched = true;                                                                                           \
+    }
+#define MCV_GEMV8(R) \
+    MCV_GEMV8V(R, 16, 1, 4) MCV_GEMV8V(R, 8, 2, 4) MCV_GEMV8V(R, 8, 2, 1) MCV_GEMV8V(R, 16, 2, 2) MCV_GEMV8V(R, 8, 1, 4) \
+    MCV_GEMV8V(R, 16, 1, 2) MCV_GEMV8V(R, 8, 2, 2)
     switch (M) {
         case 1: MCV_GEMV8(1) break;
         case 2: MCV_GEMV8(2) break;
@@ -439,6 +451,8 @@ int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const in
         default: MCV_GEMV8(4) break;
     }
 #undef MCV_GEMV8
+#undef MCV_GEMV8V
+    if (!launched) return fail(MCV_ERR_INVALID_ARG, "w8a8 tiled GEMV: no variant %d,%d,%d", nw, halves, u);
     return check_launch(DUAL ? "w8a8_tiled_gemv_kernel<gate_up_silu>" : "w8a8_tiled_gemv_kernel");
 }
 
