@@ -187,18 +187,22 @@ def wl_lm_head(pkg, args):
     nbytes = K * V // 2 + (K // 128) * V * 2 + (K // 128) * V // 2 + 2 * V + 2 * K
     # one step = one launch of the fused GEMV + argmax kernel, so the step
     # timing is also the dominant kernel's average launch duration
-    if args.argmax == "slots":
-        # host-finished route: the step is the GEMV leaving tagged slot maxima
-        # (the 64-way fold happens on the host after the copy it makes anyway)
-        total_ms, kms = time_steps(lambda i: heads[i].launch_slots(xd, logits), copies, args.steps, args.warmup)
-        token = heads[0](xd)
-    else:
-        total_ms, kms = time_steps(lambda i: heads[i].launch(xd, logits), copies, args.steps, args.warmup)
-        token = int(heads[0].token.item())
+    tree = lambda i: heads[i].launch(xd, logits)
+    # host-finished route (what lm_head_greedy_w4a16 runs): the step is the GEMV
+    # leaving tagged slot maxima; the 64-way fold happens on the host after the
+    # copy it makes anyway
+    slots = lambda i: heads[i].launch_slots(xd, logits)
+    main, other = (slots, tree) if args.argmax == "slots" else (tree, slots)
+    total_ms, kms = time_steps(main, copies, args.steps, args.warmup)
+    alt_ms, _ = time_steps(other, copies, args.steps, args.warmup)
+    token = heads[0](xd) if args.argmax == "slots" else int(heads[0].launch(xd, logits).item())
+    alt_name = "tree" if args.argmax == "slots" else "slots"
     res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
                config={"workload": "w4a16_lm_head_gemv_argmax", "M": 1, "K": K, "V": V, "argmax": args.argmax,
                        "weight_copies_rotated": copies, "rotated_bytes": copies * (qw.nbytes + sc.nbytes + zr.nbytes),
                        "algorithmic_bytes_per_step": nbytes, "token": token},
+               alt={alt_name: {"us_per_call": round(alt_ms / args.steps * 1e3, 2),
+                               "value": round(nbytes / (alt_ms / args.steps / 1e3) / 1e9, 2)}},
                dtype="w4a16 (f16 x int4, f32 accumulate)",
                kernel=f"w4a16_lm_head_kernel<16,{'kLmSlots' if args.argmax == 'slots' else 'kLmTree'}> (GEMV + fused argmax)")
     if not args.no_cpu:
@@ -494,6 +498,8 @@ def main():
         },
         "cpu_baseline": r.get("cpu_baseline"),
     }
+    if "alt" in r:
+        line["alt_argmax_routes"] = r["alt"]
     print(json.dumps(line), flush=True)
 
 
