@@ -285,6 +285,41 @@ def wl_mlp(pkg, args, fused=True):
                 kernel="mlp block (gate+up+silu launch, down GEMV)" if fused else "mlp block (4 launches)")
 
 
+def wl_qkvz(pkg, args, fused=True):
+    """The linear-attention layer's input projections at decode (qkv
+    1024->6144 and z 1024->2048 from the same normed row), 64 rotated layer
+    sets: one multi-projection launch, or two GEMVs."""
+    import torch
+    H = 1024
+    nsets = args.copies or 64
+    sets = []
+    for s in range(nsets):
+        rng = np.random.default_rng(300 + s)
+        mats = []
+        for N in (6144, 2048):
+            qweight, qzeros, scales = pkg.quantize_int4(f16_normal(rng, (H, N), 0.02))
+            mats.append(pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales))
+        sets.append(mats)
+    x = to_dev_f16(f16_normal(np.random.default_rng(1), (1, H), 1.0))
+    outs = [torch.empty((1, 6144), dtype=torch.float16, device="cuda"),
+            torch.empty((1, 2048), dtype=torch.float16, device="cuda")]
+
+    def step(i):
+        if fused:
+            pkg.matmul_w4a16_multi(x, sets[i], outs)
+        else:
+            pkg.matmul_w4a16(x, sets[i][0], outs[0])
+            pkg.matmul_w4a16(x, sets[i][1], outs[1])
+
+    nbytes = w4a16_bytes(H, 6144) + w4a16_bytes(H, 2048) + 2 * H + 2 * (6144 + 2048)
+    total_ms, _ = time_steps(step, len(sets), args.steps, args.warmup)
+    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=[total_ms / args.steps], unit="GB/s", bound="hbm",
+                config={"workload": "w4a16_qkv_z_decode" + ("" if fused else "_unfused"), "M": 1, "K": H,
+                        "N": [6144, 2048], "weight_sets_rotated": len(sets)},
+                dtype="w4a16 (f16 x int4, f32 accumulate)",
+                kernel="w4a16_gemv_multi_kernel" if fused else "w4a16_gemv_kernel x2")
+
+
 def wl_mlp_w8a8(pkg, args, fused=True):
     """The decode MLP block over W8A8 weights (gate/up 1024->3584, down
     3584->1024), 32 layer sets (352 MB, past the MALL), from the normed fp16
@@ -432,7 +467,8 @@ def wl_copy(pkg, args):
 
 WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
              "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, fused=False), "prefill": wl_prefill, "w8a8": wl_w8a8,
-             "copy": wl_copy, "norm_quant": wl_norm_quant, "mlp_w8a8": wl_mlp_w8a8,
+             "copy": wl_copy, "norm_quant": wl_norm_quant, "mlp_w8a8": wl_mlp_w8a8, "qkvz": wl_qkvz,
+             "qkvz_unfused": lambda pkg, args: wl_qkvz(pkg, args, fused=False),
              "mlp_w8a8_unfused": lambda pkg, args: wl_mlp_w8a8(pkg, args, fused=False),
              "norm_quant_unfused": lambda pkg, args: wl_norm_quant(pkg, args, fused=False), "vendor_f16": wl_vendor, "vendor_int8": lambda pkg, args: wl_vendor(pkg, args, int8=True)}
 

@@ -169,6 +169,24 @@ int mcv_w4a16_gemv_tiled_i8(const void* x_dev, int64_t K, int64_t N, int64_t til
                             int64_t packed_rows, const int8_t* w_dev, const void* scales_dev,
                             void* out_dev, mcv_stream_t stream);
 
+/* One W4A16 projection of a shared activation row, for mcv_w4a16_gemv_multi. */
+typedef struct mcv_w4a16_part {
+    const void* qw_dev;        /* slab-64 nibbles of a K x N weight */
+    const void* scales_dev;
+    const void* zeros_dev;
+    int zero_bias;
+    int64_t N;
+    void* out_dev;             /* fp16 [M][N] */
+} mcv_w4a16_part;
+
+/* Up to four projections of the same x [M][K] in one launch: the decode
+ * step's q/k/v (src/csrc/lib/decoder_layer.cpp:970-972) or qkv and z
+ * (:1108-1110), which the reference dispatches one matmul_decode_dispatch at a
+ * time.  Each part's output equals mcv_w4a16_gemv on that weight when both
+ * split K the same way (every K = 1024 decode shape). */
+int mcv_w4a16_gemv_multi(const void* x_dev, int64_t M, int64_t K, const mcv_w4a16_part* parts, int n_parts,
+                         mcv_stream_t stream);
+
 /* Workspace for mcv_w4a16_lm_head_argmax over V columns: device memory of
  * this many bytes, 128-byte aligned, zero-filled once before its first use
  * (it holds the slot tree of the fused argmax; every call leaves it

@@ -40,6 +40,12 @@ class McvError(RuntimeError):
 
 _LIB: Optional[ctypes.CDLL] = None
 
+
+class _W4Part(ctypes.Structure):
+    """mcv_w4a16_part (include/mcv_quant.h)."""
+    _fields_ = [("qw", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("zeros", ctypes.c_void_p),
+                ("zero_bias", ctypes.c_int), ("N", ctypes.c_int64), ("out", ctypes.c_void_p)]
+
 # name -> (restype, argtypes) for every entry point of include/mcv_quant.h
 _SIGS = {
     "mcv_last_error": (ctypes.c_char_p, []),
@@ -57,6 +63,7 @@ _SIGS = {
     "mcv_w4a16_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mcv_w4a16_gate_up_silu": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp,
                                         _vp]),
+    "mcv_w4a16_gemv_multi": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp]),
     "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "mcv_lm_head_workspace_bytes": (_c_i64, [_c_i64]),
     "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
@@ -324,6 +331,28 @@ def matmul_w4a16(x, w: W4A16QuantizedWeight, out=None, stream=None):
 
 def matmul_w4a16_gemv(x, w, out=None, stream=None):
     return _w4_call("mcv_w4a16_gemv", x, w, out, stream)
+
+
+def matmul_w4a16_multi(x, weights, outs=None, stream=None):
+    """Up to four projections of the same x [M, K] in one launch (q/k/v or
+    qkv + z at decode, decoder_layer.cpp:970-972, 1108-1110); returns the outputs."""
+    torch = _torch()
+    if x.dtype != torch.float16 or x.dim() != 2 or not x.is_contiguous():
+        raise McvError("matmul_w4a16_multi x must be contiguous fp16 [M, K]")
+    M, K = x.shape
+    if outs is None:
+        outs = [torch.empty((M, w.N), dtype=torch.float16, device=x.device) for w in weights]
+    if len(outs) != len(weights) or not 1 <= len(weights) <= 4:
+        raise McvError("matmul_w4a16_multi takes 1..4 weights and as many outputs")
+    parts = (_W4Part * len(weights))()
+    for i, (w, o) in enumerate(zip(weights, outs)):
+        if w.K != K or tuple(o.shape) != (M, w.N) or o.dtype != torch.float16:
+            raise McvError(f"matmul_w4a16_multi part {i}: weight K or output shape mismatch")
+        q, sc, z = w.ptrs()
+        parts[i] = _W4Part(q, sc, z, w.zero_bias, w.N, _dev(o))
+    _check(lib().mcv_w4a16_gemv_multi(_dev(x), M, K, ctypes.cast(parts, ctypes.c_void_p), len(weights), _stream(stream)),
+           "matmul_w4a16_multi")
+    return outs
 
 
 def matmul_w4a16_mfma(x, w, out=None, stream=None):

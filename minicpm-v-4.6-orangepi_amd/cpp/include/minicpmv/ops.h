@@ -16,6 +16,7 @@
 #include "minicpmv/tensor.h"
 
 #include <hip/hip_runtime_api.h>
+#include <vector>
 
 namespace minicpmv {
 
@@ -54,6 +55,11 @@ void w8a8_quantize(const Tensor& x, Tensor& x_int8, Tensor& x_scale, hipStream_t
 // may be null when nothing else reads the fp16 row.
 void rms_norm_w8a8_quantize(const Tensor& x, const Tensor& gamma, double epsilon, Tensor* normed, Tensor& x_int8,
                             Tensor& x_scale, hipStream_t stream);
+
+// Up to four W4A16 projections of the same x [M, K] in one launch (q/k/v,
+// decoder_layer.cpp:970-972; qkv and z, :1108-1110).  outs[i] is fp16 [M, N_i].
+void matmul_w4a16_multi(const Tensor& x, const std::vector<const W4A16QuantizedWeight*>& weights,
+                        const std::vector<Tensor*>& outs, hipStream_t stream);
 
 // W8A8 decode MLP front half: act = silu(gate) * up over one quantised x
 // (decoder_layer.cpp:1029-1046 + silu_mul), bit-identical to two matmul_w8a8

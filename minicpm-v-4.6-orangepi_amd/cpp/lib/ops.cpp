@@ -170,6 +170,25 @@ void matmul_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8Quantize
               "matmul_w8a8");
 }
 
+void matmul_w4a16_multi(const Tensor& x, const std::vector<const W4A16QuantizedWeight*>& weights,
+                        const std::vector<Tensor*>& outs, hipStream_t stream) {
+    require(x.dtype() == DType::Float16 && x.shape().size() == 2, "matmul_w4a16_multi x must be fp16 [M, K]");
+    require(!weights.empty() && weights.size() <= 4 && weights.size() == outs.size(),
+            "matmul_w4a16_multi takes 1..4 weights and as many outputs");
+    const int64_t M = x.shape()[0], K = x.shape()[1];
+    std::vector<mcv_w4a16_part> parts(weights.size());
+    for (size_t i = 0; i < weights.size(); ++i) {
+        const W4A16QuantizedWeight& w = *weights[i];
+        Tensor& o = *outs[i];
+        require(w.K == K, "matmul_w4a16_multi weight K must match x");
+        require(o.dtype() == DType::Float16 && o.shape() == std::vector<int64_t>{M, w.N},
+                "matmul_w4a16_multi out must be fp16 [M, N]");
+        parts[i] = mcv_w4a16_part{w.w_int8.data(), w.scales.data(), w.zeros.data(), w.zero_bias, w.N, o.data()};
+    }
+    check_mcv(mcv_w4a16_gemv_multi(x.data(), M, K, parts.data(), static_cast<int>(parts.size()), stream),
+              "matmul_w4a16_multi");
+}
+
 void mlp_gate_up_silu_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8QuantizedWeight& gate,
                            const W8A8QuantizedWeight& up, Tensor& act, hipStream_t stream) {
     require(x_int8.dtype() == DType::Int8 && act.dtype() == DType::Float16, "mlp_gate_up_silu_w8a8 needs int8 x, fp16 act");

@@ -13,6 +13,7 @@
 // Replaces the NPU kernel src/csrc/custom_ops/op_kernel/matmul_w4a16_custom.cpp
 // (8 AICore blocks, int8 tiles, fp16 Axpy accumulation) and its host wrapper
 // src/csrc/lib/ops.cpp:1030-1095.
+#include <cstdint>
 #include <cstdlib>
 
 #include "common.h"
@@ -311,6 +312,80 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
                       (static_cast<unsigned long long>(tag) << 40) | (k16 << 24) | (k16 ? idx : 0ull));
         }
     }
+}
+
+// Several projections of one activation row in one launch (q/k/v,
+// decoder_layer.cpp:970-972; qkv and z, :1108-1110): the grid runs over the
+// concatenated slabs of up to kMaxParts weights, each workgroup picks its
+// weight from the running slab ends and then does exactly what the GEMV above
+// does with GPW = 1, so with the same k-split the outputs are bit-identical to
+// separate launches.
+constexpr int kMaxParts = 4;
+struct GemvPart {
+    const uint4* qw;
+    const uint16_t* scales;
+    const uint32_t* zeros;
+    uint16_t* out;
+    int N;
+    int Npad;
+    int slab_end;          // running total of slabs up to and including this part
+    uint32_t zero_bias;
+};
+struct GemvParts {
+    GemvPart p[kMaxParts];
+    int count;
+};
+
+template <int KSPLIT>
+__global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_multi_kernel(const uint16_t* __restrict__ x, GemvParts parts,
+                                                                        int K) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gslab = blockIdx.x;
+    const int m = blockIdx.y;
+    // the part this slab belongs to (constant indices only: the kernel
+    // arguments stay in SGPRs)
+    GemvPart P = parts.p[0];
+    int slab0 = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxParts; ++j) {
+        if (j < parts.count && gslab >= parts.p[j - 1].slab_end) {
+            P = parts.p[j];
+            slab0 = parts.p[j - 1].slab_end;
+        }
+    }
+    const int slab = gslab - slab0;
+    const int n = slab * kSlab + lane;
+    const int G = K / kGroup;
+    const int C = K / kChunkK;
+    uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
+    const uint4* __restrict__ wp = P.qw + static_cast<size_t>(slab) * C * kSlab + lane;
+    const uint32_t* __restrict__ xw = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(m) * K);
+    const uint32_t zshift = (n & 7) * 4;
+    const int zstride = P.Npad >> 3;
+    float acc = 0.f;
+    for (int g = wave; g < G; g += KSPLIT) {
+        uint4 wv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wv[c] = wp[static_cast<size_t>(g * 4 + c) * kSlab];
+        const uint16_t sv = P.scales[static_cast<size_t>(g) * P.Npad + n];
+        const uint32_t zv = P.zeros[static_cast<size_t>(g) * zstride + (n >> 3)];
+        uint32_t xs[64];
+        load_x_group(xw, g, xs);
+        issue_fence();
+        acc = group_dot(wv, xs, ((zv >> zshift) & 15u) + P.zero_bias, h2f(sv), acc, vmagic);
+    }
+    if constexpr (KSPLIT > 1) {
+        __shared__ float red[KSPLIT][kSlab];
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        acc = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < KSPLIT; ++w) acc += red[w][lane];
+    }
+    if (n < P.N) P.out[static_cast<size_t>(m) * P.N + n] = f2h(acc);
 }
 
 // Decode MLP front half in one launch: act = silu(x . Wgate) * (x . Wup).
@@ -664,6 +739,46 @@ int64_t mcv_lm_head_slots_token(const uint64_t* slots_host, uint32_t tag) {
     }
     if ((best >> 24) == 0) return 0;                                    // no candidate (every logit NaN or -inf)
     return static_cast<int64_t>(0xffffffu - static_cast<uint32_t>(best & 0xffffffu));
+}
+
+int mcv_w4a16_gemv_multi(const void* x, int64_t M, int64_t K, const mcv_w4a16_part* parts, int n_parts,
+                         mcv_stream_t stream) {
+    if (!x || !parts) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemv_multi: null x/parts");
+    if (n_parts < 1 || n_parts > kMaxParts)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemv_multi: 1..%d parts (got %d)", kMaxParts, n_parts);
+    if (M <= 0 || M > 65535) return fail(MCV_ERR_SHAPE, "mcv_w4a16_gemv_multi: M must be in [1, 65535] (M=%lld)", (long long)M);
+    GemvParts gp{};
+    int64_t total = 0;
+    int64_t min_slabs = INT64_MAX;
+    for (int i = 0; i < n_parts; ++i) {
+        const mcv_w4a16_part& q = parts[i];
+        int rc = MCV_OK;
+        if (!w4_args_ok(q.qw_dev, q.scales_dev, q.zeros_dev, q.zero_bias, K, q.N, "mcv_w4a16_gemv_multi", &rc)) return rc;
+        if (!q.out_dev) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemv_multi: null out for part %d", i);
+        const int64_t ns = ceil_div(q.N, kSlab);
+        total += ns;
+        min_slabs = ns < min_slabs ? ns : min_slabs;
+        if (total > 0x7fffffff) return fail(MCV_ERR_SHAPE, "mcv_w4a16_gemv_multi: too many columns");
+        gp.p[i] = GemvPart{static_cast<const uint4*>(q.qw_dev), static_cast<const uint16_t*>(q.scales_dev),
+                           static_cast<const uint32_t*>(q.zeros_dev), static_cast<uint16_t*>(q.out_dev),
+                           static_cast<int>(q.N), static_cast<int>(ns * kSlab), static_cast<int>(total),
+                           static_cast<uint32_t>(q.zero_bias)};
+    }
+    gp.count = n_parts;
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    // The k-split the smallest part would get on its own (the decode shapes
+    // with K = 1024 all get 8, so the outputs equal separate launches').
+    const GemvCfg cfg = choose_gemv(K / kGroup, min_slabs * M);
+    const int ks = cfg.ksplit;
+    using Fn = void (*)(const uint16_t*, GemvParts, int);
+    Fn fn = ks >= 16 ? w4a16_gemv_multi_kernel<16>
+          : ks == 8 ? w4a16_gemv_multi_kernel<8>
+          : ks == 4 ? w4a16_gemv_multi_kernel<4>
+          : ks == 2 ? w4a16_gemv_multi_kernel<2> : w4a16_gemv_multi_kernel<1>;
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(total), static_cast<unsigned>(M)), dim3(64 * ks), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), gp, static_cast<int>(K));
+    return check_launch("w4a16_gemv_multi_kernel");
 }
 
 int mcv_w4a16_gate_up_silu(const void* x, int64_t M, int64_t K, int64_t N, const void* qw_gate,

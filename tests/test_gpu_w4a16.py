@@ -325,3 +325,29 @@ def test_gate_up_silu_fused(mcv, oracle, cuda, M, K, N):
     u_o = oracle.w4a16_matmul(x, oracle.unpack_awq(qu, zu), su)
     a_o = oracle.silu_mul(oracle.f2h_rne(g_o), oracle.f2h_rne(u_o))
     _check(_host_f32(fused), a_o.view(np.float16).astype(np.float32), f"gate_up_silu M={M} K={K} N={N}")
+
+
+# The decode step's shared-input projections: linear attention qkv + z,
+# full attention q / k / v, a GPTQ-style part (zero_bias 1), ragged N, M = 2.
+@pytest.mark.parametrize("M,K,Ns", [(1, 1024, (6144, 2048)), (1, 1024, (4096, 512, 512)), (2, 1024, (3584, 3584)),
+                                    (1, 256, (200, 72, 1000, 8)), (3, 1024, (520,))], ids=lambda v: str(v))
+def test_gemv_multi(mcv, oracle, cuda, M, K, Ns):
+    torch = _torch()
+    rng = np.random.default_rng(M + K + sum(Ns))
+    x = f16_normal(rng, (M, K), 1.0)
+    xd = _to_dev(x)
+    ws, refs = [], []
+    for i, N in enumerate(Ns):
+        _, qw, qz, sc = synth_w4a16(rng, K, N)
+        w = _dev_weight(mcv, qw, qz, sc)
+        zb = 1 if i == 1 else 0
+        if zb:
+            w = mcv.W4A16QuantizedWeight(w.qweight, w.scales, w.zeros, K, N, 1)
+        ws.append(w)
+        refs.append(oracle.w4a16_matmul(x, oracle.unpack_awq(qw, qz) - np.int8(zb), sc))
+    outs = mcv.matmul_w4a16_multi(xd, ws)
+    torch.cuda.synchronize()
+    for w, o, ref in zip(ws, outs, refs):
+        single = mcv.matmul_w4a16_gemv(xd, w)
+        assert torch.equal(o.view(torch.int16), single.view(torch.int16))
+        _check(_host_f32(o), ref, f"multi N={w.N}")
