@@ -163,6 +163,21 @@ def test_validation_errors_without_device(mcv):
     assert L.mcv_w4a16_gemv_tiled_i8(fake, 1024, 3584, 450, 0, fake, fake, fake, None) == 2
     assert b"tile_len" in L.mcv_last_error()
     assert L.mcv_silu_mul(fake, fake, fake, 0, None) == 2
+    # the fused and multi-part entry points validate on the host too
+    assert L.mcv_w4a16_gemv_multi(fake, 1, 1024, fake, 0, None) == 1
+    assert b"parts" in L.mcv_last_error()
+    assert L.mcv_w4a16_gemv_multi(fake, 1, 1024, None, 2, None) == 1
+    parts = (mcv._W4Part * 2)(mcv._W4Part(0x1000, 0x1000, 0x1000, 0, 64, 0x1000),
+                              mcv._W4Part(0x1000, 0x1000, 0x1000, 0, 64, None))
+    assert L.mcv_w4a16_gemv_multi(fake, 1, 1024, ctypes.cast(parts, ctypes.c_void_p), 2, None) == 1
+    assert b"null out" in L.mcv_last_error()
+    assert L.mcv_w4a16_gemv_multi(fake, 1, 1000, ctypes.cast(parts, ctypes.c_void_p), 1, None) == 2
+    assert L.mcv_w8a8_gate_up_silu(fake, fake, 0, 5, 1024, 64, fake, fake, fake, fake, 0, fake, None) == 2
+    assert b"M must be 1..4" in L.mcv_last_error()
+    assert L.mcv_w8a8_gate_up_silu(fake, fake, 0, 1, 1024, 64, fake, fake, None, fake, 0, fake, None) == 1
+    assert L.mcv_rms_norm_w8a8_quantize(fake, fake, 1, 1024, 1e-6, None, None, None, None, None) == 1
+    assert L.mcv_rms_norm_w8a8_quantize(fake, fake, 0, 1024, 1e-6, None, fake, fake, None, None) == 2
+    assert L.mcv_w4a16_gate_up_silu(fake, 1, 1024, 64, fake, fake, fake, 0, fake, fake, fake, 2, fake, None) == 1
 
 
 def test_device_entry_fails_loudly_without_gpu(mcv):
