@@ -1,12 +1,12 @@
 """Benchmark of the MI355X quantized-matmul hot path.
 
-Default workload (one JSON line on stdout): BASELINE config 3, the W4A16
+Default workload (one JSON line on stdout): the headline configuration, the W4A16
 lm_head -- M=1, K=1024, V=248094 -- as one GEMV launch per step with the
 argmax folded into it, with 8 distinct weight copies (1.06 GB) rotated so no
 step hits the 256 MB MALL.  Steps are replayed from captured HIP graphs, so
 back-to-back kernels are not gated by the host's launch rate.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
 (132,484,244 B per step, inputs resident in HBM).  `--workload` selects the
-other BASELINE configs (gemv1, mlp, lm_head, prefill, w8a8) and the vendor library's dense
+other benchmark configurations (gemv1, mlp, lm_head, prefill, w8a8) and the vendor library's dense
 GEMM at the same shapes (vendor_f16, vendor_int8) as a yardstick.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload lm_head]
@@ -241,7 +241,7 @@ def wl_gemv1(pkg, args):
 
 
 def wl_mlp(pkg, args, fused=True):
-    """Config 2: gate/up 1024->3584, silu*mul, down 3584->1024, 24 layer sets x 4 copies.
+    """The decode MLP block: gate/up 1024->3584, silu*mul, down 3584->1024, 24 layer sets x 4 copies.
     Fused (default): one gate+up+silu*mul launch and the down GEMV; unfused: the
     reference's four launches (gate, up, silu_mul, down)."""
     import torch
@@ -490,7 +490,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: every box in this build has a single MI355X and the hot path "
-              "has no multi-GPU leg (see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+              "has no multi-GPU leg (it would shard the weights by output column). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():

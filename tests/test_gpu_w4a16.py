@@ -1,6 +1,6 @@
 """GPU parity of the W4A16 kernels against the CPU oracle.
 
-Bar (BASELINE.json north_star): dequantised values bit-exact; fp16 outputs
+Bar: dequantised values bit-exact; fp16 outputs
 within max_abs <= 2e-2 and rel-L2 <= 1e-3 of the reference CPU formula
 (tests/test_matmul_w4a16.cpp:217-227) on the same seeded inputs; the lm_head
 argmax bit-exact.  Full-size shapes that the oracle cannot finish quickly are
@@ -52,7 +52,7 @@ def _check(got, ref, what):
 
 
 @pytest.mark.parametrize("M,K,N", [
-    (1, 1024, 1024),      # config 1
+    (1, 1024, 1024),      # the K = N = 1024 benchmark GEMV
     (1, 1024, 3584),      # gate / up
     (1, 3584, 1024),      # down
     (1, 1024, 6144), (1, 1024, 2048), (1, 2048, 1024), (1, 1024, 4096), (1, 1024, 512), (1, 1024, 16),
@@ -68,7 +68,7 @@ def test_gemv_vs_oracle(mcv, oracle, cuda, M, K, N):
     _check(_host_f32(out), ref, f"gemv M={M} K={K} N={N}")
 
 
-def test_gemv_config1_tight(mcv, oracle, cuda):
+def test_gemv_1024_tight(mcv, oracle, cuda):
     # the fp32-accumulating kernel is far inside the bar; a dropped group or
     # misplaced nibble would be O(1) off
     x, qweight, qzeros, scales, _ = _case(1, 1, 1024, 1024)
@@ -108,7 +108,7 @@ def test_gemm_mfma_vs_oracle(mcv, oracle, cuda, M, K, N):
 
 @pytest.mark.parametrize("M,K,N", [(512, 1024, 3584), (2048, 1024, 3584), (2048, 3584, 1024)], ids=lambda v: str(v))
 def test_gemm_mfma_full_size(mcv, oracle, cuda, M, K, N):
-    # config 4 sizes: fp64 product of the oracle-exact dequantised weights
+    # prefill benchmark sizes: fp64 product of the oracle-exact dequantised weights
     torch = _torch()
     x, qweight, qzeros, scales, _ = _case(4000 + M + K, M, K, N)
     w = _dev_weight(mcv, qweight, qzeros, scales)
@@ -185,8 +185,8 @@ def test_reference_int8_tile_format(mcv, oracle, cuda, K, N):
     _check(_host_f32(out), oracle.w4a16_matmul(x, w8, scales), f"tiled K={K} N={N}")
 
 
-def test_lm_head_config3(mcv, oracle, cuda):
-    """Config 3: K=1024, V=248094 (weight padded to 248096 for AutoAWQ packing)."""
+def test_lm_head_full_vocab(mcv, oracle, cuda):
+    """The model's lm_head shape: K=1024, V=248094 (weight padded to 248096 for AutoAWQ packing)."""
     torch = _torch()
     K, V = 1024, 248094
     rng = np.random.default_rng(3)

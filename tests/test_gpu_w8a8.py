@@ -1,6 +1,6 @@
 """GPU parity of the W8A8 kernels: activation quantiser, int8 MFMA GEMM
 (int32 accumulators bit-exact), dequant epilogue and the fused path (bit-exact
-against the oracle's epilogue).  Config 5: M in {1, 256, 1024}, K=1024, N=3584."""
+against the oracle's epilogue).  Benchmark shapes: M in {1, 256, 1024}, K=1024, N=3584."""
 import numpy as np
 import pytest
 
@@ -98,7 +98,7 @@ def test_tiled_gemm_i32_bit_exact(mcv, oracle, cuda, M, K, N):
 
 
 def test_gemm_i32_full_size_exact(mcv, cuda):
-    # config 5 at M=1024 with extreme values: fp64 product is exact at this size
+    # M=1024, K=1024, N=3584 with extreme values: the fp64 product is exact at this size
     torch = _torch()
     rng = np.random.default_rng(55)
     M, K, N = 1024, 1024, 3584
@@ -126,7 +126,7 @@ def test_dequant_reference_vectors(mcv, oracle, cuda):
 
 
 @pytest.mark.parametrize("M", [1, 256, 1024])
-def test_config5_end_to_end(mcv, oracle, cuda, M):
+def test_w8a8_end_to_end(mcv, oracle, cuda, M):
     """fp16 x -> per-token int8 + fp32 scale; fp16 W -> per-channel int8 + fp32
     scale; fused GEMM + epilogue.  Every stage bit-exact against the oracle."""
     torch = _torch()
