@@ -528,11 +528,16 @@ int mcv_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const vo
     return launch_w4a16_gemm_mfma(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
 }
 
-// Decode-sized M streams the weights once per row through the GEMV; from
-// 8 rows on the MFMA kernel reuses each dequantised operand across its rows.
+// Decode-sized M streams the weights once per row through the GEMV; larger M
+// goes to the MFMA kernel, which reuses each dequantised operand across rows.
 int mcv_w4a16_gemm(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                    const void* zeros, int zero_bias, void* out, mcv_stream_t stream) {
-    if (M >= 1 && M < 8)
+    // Few rows: the GEMV streams the weights once per row and still beats the
+    // MFMA GEMM, whose tile count is M/TM * N/TN, until the output reaches
+    // about 64K elements (MI355X, graph-replayed, rotated weights: K=1024
+    // N=3584 M=16 5.7 us against 7.0; K=3584 N=1024 M=48 12.4 against 12.5;
+    // K=1024 N=6144 crosses over near M=11).
+    if (M >= 1 && (M < 8 || int64_t(M) * N < 65536))
         return launch_w4a16_gemv(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
     return launch_w4a16_gemm_mfma(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
 }
