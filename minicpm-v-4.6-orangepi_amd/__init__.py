@@ -462,6 +462,36 @@ class LmHeadW4A16:
                "mcv_w4a16_lm_head_argmax_slots")
         return self.tag
 
+    def bind(self, x, logits=None, stream=None, route: str = "tree"):
+        """A zero-argument launcher over fixed buffers, checked and resolved
+        once, for decode loops that re-launch the lm_head every token (about
+        4 us of host time per call).  route "tree": each call does launch();
+        "slots": each call does launch_slots() and returns the tag."""
+        self._check_io(x, logits)
+        q, s, z = self.w.ptrs()
+        head = (_dev(x), self.w.K, self.w.N, self.vocab, q, s, z, self.w.zero_bias,
+                _dev(logits) if logits is not None else 0)
+        st = _stream(stream)
+        if route == "tree":
+            fn, args = lib().mcv_w4a16_lm_head_argmax, head + (_dev(self.token), _dev(self.workspace), st)
+
+            def launch():
+                _check(fn(*args), "mcv_w4a16_lm_head_argmax")
+                return self.token
+            return launch
+        if route != "slots":
+            raise McvError(f"unknown lm_head route {route!r}")
+        fn, slots = lib().mcv_w4a16_lm_head_argmax_slots, _dev(self.slots)
+
+        def launch_slots():
+            if self.tag >= self.TAG_MAX:
+                self.slots.zero_()
+                self.tag = 0
+            self.tag += 1
+            _check(fn(*head, slots, self.tag, st), "mcv_w4a16_lm_head_argmax_slots")
+            return self.tag
+        return launch_slots
+
     def read_slots_token(self, tag: int) -> int:
         host = np.ascontiguousarray(self.slots.cpu().numpy())      # synchronising copy
         return int(lib().mcv_lm_head_slots_token(_np_ptr(host), tag))

@@ -351,3 +351,36 @@ def test_gemv_multi(mcv, oracle, cuda, M, K, Ns):
         single = mcv.matmul_w4a16_gemv(xd, w)
         assert torch.equal(o.view(torch.int16), single.view(torch.int16))
         _check(_host_f32(o), ref, f"multi N={w.N}")
+
+
+@pytest.mark.gpu
+def test_lm_head_bound_launchers(mcv, oracle, cuda):
+    """bind() resolves the arguments once; its launchers give the tokens and
+    logits of launch() / launch_slots() over the same buffers, tags keep
+    growing, and a bad route or buffer is refused up front."""
+    torch = _torch()
+    K, V = 1024, 9000
+    rng = np.random.default_rng(7)
+    qweight, qzeros, scales = mcv.quantize_int4(f16_normal(rng, (K, V), 0.02))
+    head = mcv.LmHeadW4A16(_dev_weight(mcv, qweight, qzeros, scales), V)
+    x = _to_dev(f16_normal(rng, (1, K), 1.0))
+    la = torch.empty(V, dtype=torch.float16, device="cuda")
+    lb = torch.empty(V, dtype=torch.float16, device="cuda")
+    want = int(head.launch(x, la).item())
+    tree = head.bind(x, lb)
+    for _ in range(3):
+        lb.fill_(0)
+        assert int(tree().item()) == want
+        assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
+    assert int(head.workspace.count_nonzero()) == 0
+    slots = head.bind(x, lb, route="slots")
+    t0 = head.tag
+    for i in range(3):
+        tag = slots()
+        assert tag == t0 + i + 1
+        assert head.read_slots_token(tag) == want
+    assert want == oracle.argmax_f16(la.cpu().view(torch.int16).numpy().view(np.uint16))
+    with pytest.raises(mcv.McvError):
+        head.bind(x, lb, route="both")
+    with pytest.raises(mcv.McvError):
+        head.bind(x, torch.empty(V - 1, dtype=torch.float16, device="cuda"))
