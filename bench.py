@@ -269,10 +269,11 @@ def wl_gemv1(pkg, args):
     return res
 
 
-def wl_mlp(pkg, args, fused=True):
+def wl_mlp(pkg, args, mode="block"):
     """The decode MLP block: gate/up 1024->3584, silu*mul, down 3584->1024, 24 layer sets x 4 copies.
-    Fused (default): one gate+up+silu*mul launch and the down GEMV; unfused: the
-    reference's four launches (gate, up, silu_mul, down)."""
+    block (default): the whole block in one launch (DecodeMlpW4A16); two: one
+    gate+up+silu*mul launch and the down GEMV; unfused: the reference's four
+    launches (gate, up, silu_mul, down)."""
     import torch
     H, I = 1024, 3584
     nsets, reps = 24, args.copies or 4
@@ -293,10 +294,14 @@ def wl_mlp(pkg, args, fused=True):
     u = torch.empty_like(g)
     a = torch.empty_like(g)
     y = torch.empty((1, H), dtype=torch.float16, device="cuda")
+    mlps = [pkg.DecodeMlpW4A16(*L) for L in sets] if mode == "block" else None
 
     def block(i):
         L = sets[i]
-        if fused:
+        if mode == "block":
+            mlps[i](x, y)
+            return
+        if mode == "two":
             pkg.mlp_gate_up_silu_w4a16(x, L[0], L[1], a)
         else:
             pkg.matmul_w4a16(x, L[0], g)
@@ -307,11 +312,15 @@ def wl_mlp(pkg, args, fused=True):
     nbytes = 2 * w4a16_bytes(H, I) + w4a16_bytes(I, H) + 2 * H * 2 + 2 * I * 2 * 3 + 2 * H
     total_ms, _ = time_steps(block, len(sets), args.steps, args.warmup)
     kms = time_each_launch(block, len(sets), args.steps)
+    if mlps is not None and any(m.act_wait_gave_up() for m in mlps):
+        raise RuntimeError("decode MLP: a wait for act words gave up")
+    suffix = {"block": "", "two": "_2launch", "unfused": "_unfused"}[mode]
+    kernel = {"block": "w4a16_mlp_kernel (whole block, one launch)",
+              "two": "mlp block (gate+up+silu launch, down GEMV)", "unfused": "mlp block (4 launches)"}[mode]
     return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
-                config={"workload": "w4a16_mlp_block_decode" + ("" if fused else "_unfused"), "M": 1, "hidden": H,
+                config={"workload": "w4a16_mlp_block_decode" + suffix, "M": 1, "hidden": H,
                         "intermediate": I, "weight_sets_rotated": len(sets)},
-                dtype="w4a16 (f16 x int4, f32 accumulate)",
-                kernel="mlp block (gate+up+silu launch, down GEMV)" if fused else "mlp block (4 launches)")
+                dtype="w4a16 (f16 x int4, f32 accumulate)", kernel=kernel)
 
 
 def wl_qkvz(pkg, args, fused=True):
@@ -495,7 +504,8 @@ def wl_copy(pkg, args):
 
 
 WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
-             "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, fused=False), "prefill": wl_prefill, "w8a8": wl_w8a8,
+             "mlp_2launch": lambda pkg, args: wl_mlp(pkg, args, mode="two"),
+             "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, mode="unfused"), "prefill": wl_prefill, "w8a8": wl_w8a8,
              "copy": wl_copy, "norm_quant": wl_norm_quant, "mlp_w8a8": wl_mlp_w8a8, "qkvz": wl_qkvz,
              "qkvz_unfused": lambda pkg, args: wl_qkvz(pkg, args, fused=False),
              "mlp_w8a8_unfused": lambda pkg, args: wl_mlp_w8a8(pkg, args, fused=False),

@@ -154,6 +154,29 @@ int mcv_w4a16_gate_up_silu(const void* x_dev, int64_t M, int64_t K, int64_t N,
                            int zero_bias_gate, const void* qw_up_dev, const void* scales_up_dev,
                            const void* zeros_up_dev, int zero_bias_up, void* act_dev, mcv_stream_t stream);
 
+/* The whole decode MLP block, M = 1, in one launch:
+ *   out[H] = (silu(x . Wgate) * (x . Wup)) . Wdown
+ * gate/up H x I and down I x H, all slab-64; bit-identical to
+ * mcv_w4a16_gate_up_silu followed by mcv_w4a16_gemm on its output.  Replaces
+ * the decoder layers' MLP sequence (src/csrc/lib/decoder_layer.cpp:1029-1046:
+ * gate and up matmul_w4a16, silu_mul, down matmul_w4a16).  H and I are
+ * multiples of 128 with I <= 4096 (at most two quantisation groups of the
+ * down projection per wave slot), and the launch must fit on the device all
+ * at once (MCV_ERR_SHAPE otherwise: use the two-launch sequence).  The act row
+ * and the down projection's partial sums pass between workgroups inside the
+ * kernel through `workspace_dev` (per-workgroup call counters and call-tagged
+ * words): mcv_w4a16_mlp_workspace_bytes(H, I) bytes, 256-byte aligned,
+ * zero-filled once before the first call; one workspace serves one (H, I)
+ * shape, and calls sharing it must not overlap.  The u32 at byte 0 of the
+ * workspace becomes non-zero if a wait for another workgroup's words ever gave
+ * up (after ~0.3 s; the output of that call is then undefined). */
+int64_t mcv_w4a16_mlp_workspace_bytes(int64_t H, int64_t I);
+int mcv_w4a16_mlp(const void* x_dev, int64_t H, int64_t I,
+                  const void* qw_gate_dev, const void* scales_gate_dev, const void* zeros_gate_dev, int zero_bias_gate,
+                  const void* qw_up_dev, const void* scales_up_dev, const void* zeros_up_dev, int zero_bias_up,
+                  const void* qw_down_dev, const void* scales_down_dev, const void* zeros_down_dev,
+                  int zero_bias_down, void* out_dev, void* workspace_dev, mcv_stream_t stream);
+
 /* Materialise dequantised weights: w_f16_kn [K][N] = fp16 RNE((q - z) * s)
  * and/or w8_kn [K][N] = q - z (int8), either may be NULL.  The int8 form is
  * the reference's unpacked w_int8 (src/csrc/lib/quantized_weight.cpp:155). */

@@ -64,6 +64,9 @@ _SIGS = {
     "mcv_w4a16_gate_up_silu": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp,
                                         _vp]),
     "mcv_w4a16_gemv_multi": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp]),
+    "mcv_w4a16_mlp_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "mcv_w4a16_mlp": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int,
+                               _vp, _vp, _vp]),
     "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "mcv_lm_head_workspace_bytes": (_c_i64, [_c_i64]),
     "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
@@ -377,6 +380,58 @@ def mlp_gate_up_silu_w4a16(x, w_gate: W4A16QuantizedWeight, w_up: W4A16Quantized
     _check(lib().mcv_w4a16_gate_up_silu(_dev(x), M, w_gate.K, w_gate.N, qg, sg, zg, w_gate.zero_bias, qu, su, zu,
                                         w_up.zero_bias, _dev(out), _stream(stream)), "mcv_w4a16_gate_up_silu")
     return out
+
+
+class DecodeMlpW4A16:
+    """The whole decode MLP block, M = 1, in one launch:
+    out[H] = (silu(x . gate) * (x . up)) . down -- bit-identical to
+    mlp_gate_up_silu_w4a16 followed by matmul_w4a16 (decoder_layer.cpp:1029-1046).
+    Owns the workspace through which the act row passes inside the kernel;
+    calls on one object must not overlap (one stream)."""
+
+    ERROR_WORD = 0             # u32 index of the give-up flag in the workspace
+
+    def __init__(self, gate: W4A16QuantizedWeight, up: W4A16QuantizedWeight, down: W4A16QuantizedWeight):
+        torch = _torch()
+        if (up.K, up.N) != (gate.K, gate.N) or (down.K, down.N) != (gate.N, gate.K):
+            raise McvError(f"decode MLP: gate/up must be [H, I] and down [I, H]; got gate {gate.K}x{gate.N}, "
+                           f"up {up.K}x{up.N}, down {down.K}x{down.N}")
+        self.gate, self.up, self.down = gate, up, down
+        self.H, self.I = gate.K, gate.N
+        nbytes = lib().mcv_w4a16_mlp_workspace_bytes(self.H, self.I)
+        if nbytes <= 0:
+            raise McvError(f"decode MLP: unsupported shape H={self.H} I={self.I}")
+        self.workspace = torch.zeros(nbytes // 4, dtype=torch.int32, device=gate.qweight.device)
+
+    def _args(self, x, out, stream):
+        torch = _torch()
+        if x.dtype != torch.float16 or x.numel() != self.H or not x.is_contiguous():
+            raise McvError(f"decode MLP: x must be contiguous fp16 [1, {self.H}]")
+        if out.dtype != torch.float16 or out.numel() != self.H or not out.is_contiguous():
+            raise McvError(f"decode MLP: out must be contiguous fp16 [1, {self.H}]")
+        g, u, d = self.gate, self.up, self.down
+        return ((_dev(x), self.H, self.I) + g.ptrs() + (g.zero_bias,) + u.ptrs() + (u.zero_bias,) + d.ptrs()
+                + (d.zero_bias, _dev(out), _dev(self.workspace), _stream(stream)))
+
+    def __call__(self, x, out=None, stream=None):
+        torch = _torch()
+        if out is None:
+            out = torch.empty((1, self.H), dtype=torch.float16, device=x.device)
+        _check(lib().mcv_w4a16_mlp(*self._args(x, out, stream)), "mcv_w4a16_mlp")
+        return out
+
+    def bind(self, x, out, stream=None):
+        """A zero-argument launcher over fixed buffers (arguments resolved once)."""
+        fn, args = lib().mcv_w4a16_mlp, self._args(x, out, stream)
+
+        def launch():
+            _check(fn(*args), "mcv_w4a16_mlp")
+        return launch
+
+    def act_wait_gave_up(self) -> bool:
+        """True if a wait for another workgroup's words in any earlier call
+        timed out (synchronises)."""
+        return bool(int(self.workspace[self.ERROR_WORD].item()))
 
 
 def w4a16_dequant(w: W4A16QuantizedWeight, f16=True, i8=False, stream=None):

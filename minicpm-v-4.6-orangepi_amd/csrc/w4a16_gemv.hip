@@ -17,61 +17,10 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "gemv_body.h"
 
 namespace mcv {
 namespace {
-
-// (a & mask) | magic in one v_and_or_b32.  gfx9 VOP3 encodings take no
-// literal and at most one SGPR, so the mask rides in an SGPR and the magic
-// exponent pattern in a VGPR; left to itself the compiler emits v_and + v_or.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t smask, uint32_t vmagic) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(smask), "v"(vmagic));
-    return r;
-}
-
-// The group's 128 activation values as 64 half2 words.  The index is
-// wave-uniform, so these become scalar loads into SGPRs.
-__device__ __forceinline__ void load_x_group(const uint32_t* __restrict__ xw, int g, uint32_t (&xs)[64]) {
-#pragma unroll
-    for (int i = 0; i < 64; ++i) xs[i] = xw[g * 64 + i];
-}
-
-// Every load of one trip (weights, scale, zero word, activations) is issued
-// before the first wait: left alone, the scheduler sinks the scale and the
-// activation loads below the waits for the weight words, which costs each
-// trip a second full memory latency.
-__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// Adds the contribution of one quantisation group (four 16-byte chunks of this
-// lane's column, activations `xs`) to `acc`.
-__device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t (&xs)[64], uint32_t z, float scale,
-                                           float acc, uint32_t vmagic) {
-    const uint32_t zlo = (0x6400u + z) * 0x10001u;          // half2(1024 + z)
-    const uint32_t zhi = (0x6400u + (z << 4)) * 0x10001u;   // half2(1024 + 16 z)
-    const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
-    const uint32_t mhi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
-    float alo = 0.f, ahi = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const uint32_t words[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const int kw = (c * kChunkK + w * 8) >> 1;                // half2 index into xs
-            const uint32_t q = words[w];
-            const uint32_t q8 = q >> 8;
-            const half2_t p0 = as_h2(and_or(q, mlo, vmagic)) - as_h2(zlo);    // k+0, k+1
-            const half2_t p1 = as_h2(and_or(q, mhi, vmagic)) - as_h2(zhi);    // k+2, k+3 (x16)
-            const half2_t p2 = as_h2(and_or(q8, mlo, vmagic)) - as_h2(zlo);   // k+4, k+5
-            const half2_t p3 = as_h2(and_or(q8, mhi, vmagic)) - as_h2(zhi);   // k+6, k+7 (x16)
-            alo = __builtin_amdgcn_fdot2(p0, as_h2(xs[kw + 0]), alo, false);
-            ahi = __builtin_amdgcn_fdot2(p1, as_h2(xs[kw + 1]), ahi, false);
-            alo = __builtin_amdgcn_fdot2(p2, as_h2(xs[kw + 2]), alo, false);
-            ahi = __builtin_amdgcn_fdot2(p3, as_h2(xs[kw + 3]), ahi, false);
-        }
-    }
-    return fmaf(alo + ahi * 0.0625f, scale, acc);
-}
 
 // Cross-workgroup argmax without fences.  64 slots (128 B apart, slot j taken
 // by the slabs s with s % 64 == j) each hold a 64-bit key maximum and a 32-bit
@@ -406,29 +355,12 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gate_up_silu_kernel(
     const int m = blockIdx.y;
     const int n = slab * kSlab + lane;
     const int G = K / kGroup;
-    const int C = K / kChunkK;
-    const int zstride = Npad >> 3;
-    const uint32_t zshift = (n & 7) * 4;
     const uint32_t* __restrict__ xw = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(m) * K);
-    const size_t wofs = static_cast<size_t>(slab) * C * kSlab + lane;
     uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
     asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
     float ag = 0.f, au = 0.f;
-    for (int g = wave; g < G; g += KSPLIT) {
-        uint4 wgv[4], wuv[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) wgv[c] = qg[wofs + static_cast<size_t>(g * 4 + c) * kSlab];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) wuv[c] = qu[wofs + static_cast<size_t>(g * 4 + c) * kSlab];
-        const uint16_t sgv = sg[static_cast<size_t>(g) * Npad + n], suv = su[static_cast<size_t>(g) * Npad + n];
-        const uint32_t zgv = zg[static_cast<size_t>(g) * zstride + (n >> 3)];
-        const uint32_t zuv = zu[static_cast<size_t>(g) * zstride + (n >> 3)];
-        uint32_t xs[64];
-        load_x_group(xw, g, xs);
-        issue_fence();
-        ag = group_dot(wgv, xs, ((zgv >> zshift) & 15u) + zbg, h2f(sgv), ag, vmagic);
-        au = group_dot(wuv, xs, ((zuv >> zshift) & 15u) + zbu, h2f(suv), au, vmagic);
-    }
+    gate_up_partials(xw, w4_column(qg, sg, zg, zbg, K, Npad, slab, lane), w4_column(qu, su, zu, zbu, K, Npad, slab, lane),
+                     wave, KSPLIT, G, ag, au, vmagic);
     if constexpr (KSPLIT > 1) {
         red[0][wave][lane] = ag;
         red[1][wave][lane] = au;
@@ -591,6 +523,10 @@ __global__ __launch_bounds__(256) void w4a16_tiled_i8_kernel(const uint16_t* __r
 }
 
 }  // namespace
+
+// The GEMV launchers' k-split, for kernels that must add in the same order
+// (decode_mlp.hip).
+int gemv_ksplit(int64_t G, int64_t blocks) { return choose_gemv(G, blocks).ksplit; }
 
 // Internal entry used by the dispatcher in w4a16_gemm.hip.
 int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,

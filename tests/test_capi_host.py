@@ -178,6 +178,19 @@ def test_validation_errors_without_device(mcv):
     assert L.mcv_rms_norm_w8a8_quantize(fake, fake, 1, 1024, 1e-6, None, None, None, None, None) == 1
     assert L.mcv_rms_norm_w8a8_quantize(fake, fake, 0, 1024, 1e-6, None, fake, fake, None, None) == 2
     assert L.mcv_w4a16_gate_up_silu(fake, 1, 1024, 64, fake, fake, fake, 0, fake, fake, fake, 2, fake, None) == 1
+    # the one-launch decode MLP: workspace size, shapes, pointers, alignment
+    assert L.mcv_w4a16_mlp_workspace_bytes(1024, 3584) == 4 * (64 + 1024) + 3584 * 4 + 16 * 16 * 64 * 8
+    assert L.mcv_w4a16_mlp_workspace_bytes(0, 3584) == 0
+    w3 = (fake, fake, fake, 0)
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, *w3, fake, None, None) == 1
+    assert b"workspace" in L.mcv_last_error()
+    assert L.mcv_w4a16_mlp(fake, 1000, 3584, *w3, *w3, *w3, fake, fake, None) == 2
+    assert L.mcv_w4a16_mlp(fake, 1024, 6144, *w3, *w3, *w3, fake, fake, None) == 2      # 48 groups over 16 slots
+    assert b"two groups" in L.mcv_last_error()
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, None, 0, fake, fake, None) == 1
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, fake, 2, fake, fake, None) == 1
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, *w3, fake, ctypes.c_void_p(0x1080), None) == 1
+    assert b"aligned" in L.mcv_last_error()
 
 
 def test_device_entry_fails_loudly_without_gpu(mcv):
