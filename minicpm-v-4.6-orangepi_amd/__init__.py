@@ -383,13 +383,15 @@ def mlp_gate_up_silu_w4a16(x, w_gate: W4A16QuantizedWeight, w_up: W4A16Quantized
 
 
 class DecodeMlpW4A16:
-    """The whole decode MLP block, M = 1, in one launch:
-    out[H] = (silu(x . gate) * (x . up)) . down -- bit-identical to
-    mlp_gate_up_silu_w4a16 followed by matmul_w4a16 (decoder_layer.cpp:1029-1046).
-    Owns the workspace through which the act row passes inside the kernel;
-    calls on one object must not overlap (one stream)."""
+    """The whole decode MLP block, M = 1: out[H] = (silu(x . gate) * (x . up)) . down
+    (decoder_layer.cpp:1029-1046), bit-identical to mlp_gate_up_silu_w4a16
+    followed by matmul_w4a16 -- in one launch (mcv_w4a16_mlp) where the shape
+    allows, else those two launches (one_launch turns False).  Owns the
+    workspace through which the act row passes inside the kernel; calls on one
+    object must not overlap (one stream)."""
 
     ERROR_WORD = 0             # u32 index of the give-up flag in the workspace
+    _ERR_SHAPE = 2
 
     def __init__(self, gate: W4A16QuantizedWeight, up: W4A16QuantizedWeight, down: W4A16QuantizedWeight):
         torch = _torch()
@@ -398,10 +400,11 @@ class DecodeMlpW4A16:
                            f"up {up.K}x{up.N}, down {down.K}x{down.N}")
         self.gate, self.up, self.down = gate, up, down
         self.H, self.I = gate.K, gate.N
+        dev = gate.qweight.device
         nbytes = lib().mcv_w4a16_mlp_workspace_bytes(self.H, self.I)
-        if nbytes <= 0:
-            raise McvError(f"decode MLP: unsupported shape H={self.H} I={self.I}")
-        self.workspace = torch.zeros(nbytes // 4, dtype=torch.int32, device=gate.qweight.device)
+        self.one_launch = nbytes > 0
+        self.workspace = torch.zeros(max(nbytes, 4) // 4, dtype=torch.int32, device=dev)
+        self.act = torch.empty((1, self.I), dtype=torch.float16, device=dev)
 
     def _args(self, x, out, stream):
         torch = _torch()
@@ -413,15 +416,29 @@ class DecodeMlpW4A16:
         return ((_dev(x), self.H, self.I) + g.ptrs() + (g.zero_bias,) + u.ptrs() + (u.zero_bias,) + d.ptrs()
                 + (d.zero_bias, _dev(out), _dev(self.workspace), _stream(stream)))
 
+    def _two_launches(self, x, out, stream):
+        mlp_gate_up_silu_w4a16(x.view(1, self.H), self.gate, self.up, self.act, stream)
+        matmul_w4a16(self.act, self.down, out.view(1, self.H), stream)
+
     def __call__(self, x, out=None, stream=None):
         torch = _torch()
         if out is None:
             out = torch.empty((1, self.H), dtype=torch.float16, device=x.device)
-        _check(lib().mcv_w4a16_mlp(*self._args(x, out, stream)), "mcv_w4a16_mlp")
+        args = self._args(x, out, stream)
+        if self.one_launch:
+            rc = lib().mcv_w4a16_mlp(*args)
+            if rc != self._ERR_SHAPE:
+                _check(rc, "mcv_w4a16_mlp")
+                return out
+            self.one_launch = False            # this shape or device cannot hold the one-launch grid
+        self._two_launches(x, out, stream)
         return out
 
     def bind(self, x, out, stream=None):
         """A zero-argument launcher over fixed buffers (arguments resolved once)."""
+        self(x, out, stream)                   # settles one_launch
+        if not self.one_launch:
+            return lambda: self._two_launches(x, out, stream)
         fn, args = lib().mcv_w4a16_mlp, self._args(x, out, stream)
 
         def launch():

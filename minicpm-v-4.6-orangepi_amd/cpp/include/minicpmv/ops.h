@@ -41,6 +41,22 @@ void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, h
 void mlp_gate_up_silu_w4a16(const Tensor& x, const W4A16QuantizedWeight& gate, const W4A16QuantizedWeight& up,
                             Tensor& act, hipStream_t stream);
 
+// The whole decode MLP block, M = 1: out [1, H] = (silu(x . gate) * (x . up)) . down
+// (decoder_layer.cpp:1029-1046), bit-identical to mlp_gate_up_silu_w4a16 +
+// matmul_w4a16.  One launch (mcv_w4a16_mlp) where the shape allows, else those
+// two launches.  The weights stay owned by the caller and must outlive it.
+struct DecodeMlpW4A16 {
+    const W4A16QuantizedWeight* gate{nullptr};   // [H, I]
+    const W4A16QuantizedWeight* up{nullptr};     // [H, I]
+    const W4A16QuantizedWeight* down{nullptr};   // [I, H]
+    Tensor workspace;                            // zero-filled once; one stream at a time
+    Tensor act;                                  // fp16 [1, I], for the two-launch path
+    bool one_launch{true};
+};
+DecodeMlpW4A16 make_decode_mlp_w4a16(const W4A16QuantizedWeight& gate, const W4A16QuantizedWeight& up,
+                                     const W4A16QuantizedWeight& down);
+void mlp_w4a16(const Tensor& x, DecodeMlpW4A16& mlp, Tensor& out, hipStream_t stream);
+
 // int32 out [M, N] = int8 x [M, K] . int8 w [K, N], exact.
 void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream);
 // The same over a quantized weight object, in whatever layout it holds

@@ -85,6 +85,45 @@ void mlp_gate_up_silu_w4a16(const Tensor& x, const W4A16QuantizedWeight& gate, c
               "mlp_gate_up_silu");
 }
 
+DecodeMlpW4A16 make_decode_mlp_w4a16(const W4A16QuantizedWeight& gate, const W4A16QuantizedWeight& up,
+                                     const W4A16QuantizedWeight& down) {
+    require(up.K == gate.K && up.N == gate.N, "decode MLP gate and up must have the same shape");
+    require(down.K == gate.N && down.N == gate.K, "decode MLP down must be [I, H] for gate [H, I]");
+    DecodeMlpW4A16 mlp;
+    mlp.gate = &gate;
+    mlp.up = &up;
+    mlp.down = &down;
+    const int64_t ws = mcv_w4a16_mlp_workspace_bytes(gate.K, gate.N);
+    mlp.one_launch = ws > 0;
+    if (mlp.one_launch) {
+        mlp.workspace = Tensor({ws}, DType::UInt8);
+        mlp.workspace.zero();
+    }
+    mlp.act = Tensor({1, gate.N}, DType::Float16);
+    mlp.act.allocate();
+    return mlp;
+}
+
+void mlp_w4a16(const Tensor& x, DecodeMlpW4A16& mlp, Tensor& out, hipStream_t stream) {
+    const W4A16QuantizedWeight &g = *mlp.gate, &u = *mlp.up, &d = *mlp.down;
+    require(x.dtype() == DType::Float16 && x.shape() == std::vector<int64_t>{1, g.K}, "decode MLP x must be fp16 [1, H]");
+    require(out.dtype() == DType::Float16 && out.shape() == std::vector<int64_t>{1, g.K},
+            "decode MLP out must be fp16 [1, H]");
+    if (mlp.one_launch) {
+        const int rc = mcv_w4a16_mlp(x.data(), g.K, g.N, g.w_int8.data(), g.scales.data(), g.zeros.data(), g.zero_bias,
+                                     u.w_int8.data(), u.scales.data(), u.zeros.data(), u.zero_bias, d.w_int8.data(),
+                                     d.scales.data(), d.zeros.data(), d.zero_bias, out.data(), mlp.workspace.data(),
+                                     stream);
+        if (rc != MCV_ERR_SHAPE) {
+            check_mcv(rc, "mlp_w4a16");
+            return;
+        }
+        mlp.one_launch = false;          // this shape or device cannot hold the one-launch grid
+    }
+    mlp_gate_up_silu_w4a16(x, g, u, mlp.act, stream);
+    matmul_w4a16(mlp.act, d, out, stream);
+}
+
 void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream) {
     require(x.dtype() == DType::Int8, "matmul_w8a8_i32 x must be int8");
     require(w_int8.dtype() == DType::Int8, "matmul_w8a8_i32 w must be int8");

@@ -103,7 +103,39 @@ int main() {
     matmul_w4a16(x, q4, out, ctx.stream());
     if (!check("slab64-nibbles")) return 1;
 
-    // 3) shape validation mirrors the reference's host wrapper
+    // 3) the decode MLP block over the same gate/up weight and a [N, K] down
+    // projection: one launch == gate+up+silu*mul then the down GEMV, bit for bit
+    {
+        std::vector<int32_t> dq(static_cast<size_t>(N) * K / 8), dz(static_cast<size_t>(N / G) * K / 8);
+        std::vector<uint16_t> ds(static_cast<size_t>(N / G) * K);
+        std::uniform_int_distribution<int> qd(0, 15);
+        for (auto& v : dq) {
+            uint32_t word = 0;
+            for (int sl = 0; sl < 8; ++sl) word |= static_cast<uint32_t>(qd(rng)) << (4 * sl);
+            v = static_cast<int32_t>(word);
+        }
+        for (auto& v : dz) v = static_cast<int32_t>(0x77777777u);
+        for (auto& v : ds) v = t::f2h(sd(rng));
+        W4A16QuantizedWeight down = pack_w4a16_awq(dq.data(), dz.data(), ds.data(), N, K);
+        DecodeMlpW4A16 mlp = make_decode_mlp_w4a16(q4, q4, down);
+        Tensor y1({1, K}, DType::Float16), y2({1, K}, DType::Float16), act({1, N}, DType::Float16);
+        y1.allocate();
+        y2.allocate();
+        act.allocate();
+        for (int rep = 0; rep < 3; ++rep) mlp_w4a16(x, mlp, y1, ctx.stream());
+        mlp_gate_up_silu_w4a16(x, q4, q4, act, ctx.stream());
+        matmul_w4a16(act, down, y2, ctx.stream());
+        std::vector<uint16_t> h1(K), h2(K);
+        y1.copy_to_host(h1.data(), h1.size() * 2);
+        y2.copy_to_host(h2.data(), h2.size() * 2);
+        uint32_t err = 1;
+        mlp.workspace.copy_to_host(&err, 4);
+        std::printf("decode MLP one_launch=%d bit-identical=%d give-up flag=%u\n", mlp.one_launch ? 1 : 0,
+                    h1 == h2 ? 1 : 0, err);
+        if (!mlp.one_launch || h1 != h2 || err != 0) return 1;
+    }
+
+    // 4) shape validation mirrors the reference's host wrapper
     try {
         Tensor bad({2, K}, DType::Float16);
         bad.allocate();

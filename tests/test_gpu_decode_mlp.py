@@ -41,6 +41,7 @@ def test_decode_mlp_matches_two_launches_and_oracle(mcv, oracle, cuda, H, I, zb_
     mlp = mcv.DecodeMlpW4A16(wg, wu, wd)
     out = torch.empty((1, H), dtype=torch.float16, device="cuda")
     for trial in range(3):                       # the call counters advance call after call
+        assert mlp.one_launch
         x = f16_normal(rng, (1, H), 1.0 + trial)
         xd = _to_dev(x)
         out.fill_(0)
@@ -118,9 +119,30 @@ def test_decode_mlp_rejects_bad_shapes(mcv, oracle, cuda):
     wd, _ = _weights(mcv, oracle, rng, 384, 256)
     with pytest.raises(mcv.McvError):
         mcv.DecodeMlpW4A16(wg, wu, wg)           # down must be [I, H]
-    big = [_weights(mcv, oracle, rng, K, N)[0] for K, N in ((256, 6144), (256, 6144), (6144, 256))]
-    with pytest.raises(mcv.McvError, match="two groups"):
-        mcv.DecodeMlpW4A16(*big)(torch.zeros((1, 256), dtype=torch.float16, device="cuda"))
+
+
+
+def test_decode_mlp_falls_back_to_two_launches(mcv, oracle, cuda):
+    """I = 6144 puts three down-projection groups on a wave slot: the
+    one-launch kernel refuses it and the object runs the two launches."""
+    torch = _torch()
+    rng = np.random.default_rng(9)
+    H, I = 256, 6144
+    wg, rg = _weights(mcv, oracle, rng, H, I)
+    wu, ru = _weights(mcv, oracle, rng, H, I)
+    wd, rd = _weights(mcv, oracle, rng, I, H)
+    mlp = mcv.DecodeMlpW4A16(wg, wu, wd)
+    x = f16_normal(rng, (1, H), 1.0)
+    xd = _to_dev(x)
+    out = mlp(xd)
+    assert not mlp.one_launch
+    two = mcv.matmul_w4a16(mcv.mlp_gate_up_silu_w4a16(xd, wg, wu), wd)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), two.view(torch.int16))
+    a_o = oracle.silu_mul(oracle.f2h_rne(oracle.w4a16_matmul(x, *rg)), oracle.f2h_rne(oracle.w4a16_matmul(x, *ru)))
+    ref = oracle.w4a16_matmul(a_o.reshape(1, I), *rd)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - ref).max() <= MAX_ABS and rel_l2(got, ref) <= REL_L2
     mlp = mcv.DecodeMlpW4A16(wg, wu, wd)
     with pytest.raises(mcv.McvError):
         mlp(torch.zeros((1, 128), dtype=torch.float16, device="cuda"))
