@@ -210,10 +210,13 @@ typedef struct mcv_w4a16_part {
 int mcv_w4a16_gemv_multi(const void* x_dev, int64_t M, int64_t K, const mcv_w4a16_part* parts, int n_parts,
                          mcv_stream_t stream);
 
-/* Workspace for mcv_w4a16_lm_head_argmax over V columns: device memory of
- * this many bytes, 128-byte aligned, zero-filled once before its first use
- * (it holds the slot tree of the fused argmax; every call leaves it
- * zero-filled again).  Calls sharing one workspace must not overlap. */
+/* Workspace for mcv_w4a16_lm_head_argmax over V columns (0 < V < 2^24):
+ * device memory of this many bytes, 128-byte aligned, zero-filled once before
+ * its first use.  It holds per-workgroup call counters and the call-tagged key
+ * words of the fused argmax, which every call keeps consistent; one workspace
+ * serves one V, and calls sharing it must not overlap.  The u32 at byte 0
+ * turns non-zero if the wait for the keys ever gave up (~40 ms; that call's
+ * token is then undefined).  Returns 0 for an unsupported V. */
 int64_t mcv_lm_head_workspace_bytes(int64_t V);
 
 /* Greedy lm_head over a W4A16 weight: logits[v] = x . W[:, v] (fp16 RNE of the
@@ -223,10 +226,10 @@ int64_t mcv_lm_head_workspace_bytes(int64_t V);
  * V on are ignored, like the reference's clipped chunk tails, :472).
  * logits_dev may be NULL.  token_dev receives an int64 on the device.
  * Replaces the 16 chunk matmuls + 16 D2H copies + host scan of lm_head_greedy
- * (src/csrc/lib/language_model.cpp:412-482) with one kernel: the GEMV's
- * workgroups fold their best (value, index) into 64 (max, arrival count)
- * slots of the workspace; the arrivals completing a slot bump a global count,
- * and the last of those reads the 64 slot maxima and writes the token. */
+ * (src/csrc/lib/language_model.cpp:412-482) with one kernel: each workgroup
+ * of the GEMV publishes its best (value, index) as one call-tagged word in the
+ * workspace, and the grid's last workgroup waits until all carry this call's
+ * tag, takes the maximum and writes the token. */
 int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
                              const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                              int zero_bias, void* logits_dev, int64_t* token_dev,

@@ -483,7 +483,7 @@ class LmHeadW4A16:
     src/csrc/lib/language_model.cpp:412-482).  Owns its workspaces.
 
     Three routes to the same token: launch() writes it on the device (the
-    in-kernel arrival tree); launch_slots() + read_slots_token() -- what
+    call-tagged key words the last workgroup reads); launch_slots() + read_slots_token() -- what
     __call__ uses, since it returns the token to the host anyway -- leave
     call-tagged slot maxima that the host folds after its copy;
     launch_partials() + reduce_partials() use a second kernel."""
@@ -497,7 +497,7 @@ class LmHeadW4A16:
             raise McvError(f"vocab {vocab} exceeds weight width {w.N}")
         self.w, self.vocab = w, vocab
         dev = w.qweight.device
-        # zero-filled once; every fused call leaves the combining tree zeroed again
+        # zero-filled once; the fused calls keep its call counters and tagged keys consistent
         self.workspace = torch.zeros(lib().mcv_lm_head_workspace_bytes(vocab), dtype=torch.uint8, device=dev)
         self.slots = torch.zeros(lib().mcv_lm_head_slots_bytes() // 8, dtype=torch.int64, device=dev)
         self.tag = 0

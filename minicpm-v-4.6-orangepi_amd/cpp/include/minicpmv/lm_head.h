@@ -18,7 +18,7 @@ namespace minicpmv {
 struct LmHeadW4A16 {
     W4A16QuantizedWeight weight;   // [hidden, >= vocab]
     int64_t vocab{0};
-    Tensor workspace;              // zero-filled once; every call leaves it zeroed
+    Tensor workspace;              // zero-filled once; calls keep its counters and tagged keys consistent
     Tensor token;                  // Int64 [1]
     Tensor slots;                  // tagged slot maxima of the host-finished argmax
     uint32_t tag{0};               // tag of the last slots call

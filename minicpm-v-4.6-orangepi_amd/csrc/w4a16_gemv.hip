@@ -22,50 +22,74 @@
 namespace mcv {
 namespace {
 
-// Cross-workgroup argmax without fences.  64 slots (128 B apart, slot j taken
-// by the slabs s with s % 64 == j) each hold a 64-bit key maximum and a 32-bit
-// arrival count; one more 128-byte line holds a global count.  A workgroup
-// folds its key into its slot with atomicMax and waits for that atomic to
-// return -- it has then been performed at the device-coherent point -- before
-// it bumps the slot's count.  The arrival that completes a slot bumps the
-// global count (only 64 such arrivals, so it never serialises); the arrival
-// that completes the global count knows every slot count completed after all
-// of that slot's maxima were performed, so one wave reads the 64 slot maxima
-// in a single parallel round of atomic reads, writes the token and clears the
-// workspace.  The last workgroup's tail is four device round trips.  Every
-// call leaves the workspace all zero.  Measured on MI355X with the lm_head's
-// 3877 workgroups: 3877 atomics on one address serialise to 45 us (spread over
-// 64 addresses they are free), a __threadfence per workgroup adds ~30 us,
-// CAS-combined (key, count) words 22-39 us (retry storms when the last
-// arrivals bunch).
-constexpr int kTreeStride = 16;                               // u64 words per slot: 128 B
-constexpr int kTreeWords = 64;
-constexpr int64_t kTreeBytes = (kTreeWords + 1) * kTreeStride * 8;
+// Cross-workgroup argmax without fences or counters (the L2s of the eight
+// XCDs are not coherent with each other).  Every workgroup publishes its best
+// key as one call-tagged 64-bit word (bits 63..40 tag, 39..24 the fp16 key,
+// 23..0 the complement of the column index) with a device-scope store, which
+// goes through to the coherent point; the grid's last workgroup polls all the
+// words with device-scope loads until each carries this call's tag, takes
+// the maximum and writes the token -- one store's visibility plus one poll
+// after the last workgroup.  The tag comes from a per-workgroup call counter:
+// each workgroup reads its own counter once and bumps it, so a call's
+// workgroups agree on the tag without talking to each other, and a graph
+// replay reads the counters afresh.  Workspace (zero-filled once, kept
+// consistent by every call): u32 give-up flag at word 0, u32 call counters at
+// words 64.., then the u64 keys, both sized for one workgroup per slab.
+// Measured on MI355X with the lm_head's workgroups: 3877 atomics on one
+// address serialise to 45 us, a __threadfence per workgroup adds ~30 us,
+// CAS-combined (key, count) words 22-39 us, and the fence-free 64-slot
+// arrival tree this replaces (atomicMax, then slot and global counts, then a
+// read of the slot maxima) ~1.8 us: four device round trips.
+constexpr int kTreeWords = 64;                                // slots of the host-finished route
+constexpr int kLmEpoch = 64;                                  // u32 index of the first call counter
+constexpr int kLmPollVec = 8;                                 // key words per lane per poll
+constexpr int kLmSpinLimit = 1 << 18;
+
+__host__ __device__ inline int64_t lm_keys_index(int64_t nslab) { return (kLmEpoch + nslab + 1) / 2; }
 
 // Run by one full wave of each workgroup after its columns are final; `key`
-// is the workgroup's best key (wave-uniform).
-__device__ __forceinline__ void argmax_arrive(unsigned long long* __restrict__ ws, unsigned long long key, int slab,
-                                              int nblk, int lane, int64_t* __restrict__ token) {
-    const int j = slab & (kTreeWords - 1);
-    const unsigned expected = static_cast<unsigned>((nblk - j + kTreeWords - 1) / kTreeWords);
-    const unsigned nslots = static_cast<unsigned>(nblk < kTreeWords ? nblk : kTreeWords);
-    unsigned* gcount = reinterpret_cast<unsigned*>(ws + kTreeWords * kTreeStride + 8);
-    int last = 0;
+// is the workgroup's best argmax_key64 (wave-uniform), `epoch` its call
+// counter as read at the start of the kernel.
+__device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ ws, unsigned long long key,
+                                               unsigned epoch, int b, int nblk, int nslab, int lane,
+                                               int64_t* __restrict__ token) {
+    unsigned* ws32 = reinterpret_cast<unsigned*>(ws);
+    unsigned long long* keys = ws + lm_keys_index(nslab);
+    const unsigned long long tag = (epoch + 1u) & 0xffffffu;
     if (lane == 0) {
-        unsigned long long* slot = ws + j * kTreeStride;
-        const unsigned long long before = atomicMax(slot, key);
-        asm volatile("s_waitcnt vmcnt(0)" : : "v"(before) : "memory");   // the max has returned, i.e. is performed
-        if (atomicAdd(reinterpret_cast<unsigned*>(slot + 8), 1u) + 1u == expected)
-            last = atomicAdd(gcount, 1u) + 1u == nslots;
+        __hip_atomic_store(ws32 + kLmEpoch + b, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long k16 = key >> 32, idx = key & 0xffffffull;
+        __hip_atomic_store(keys + b, (tag << 40) | (k16 << 24) | (k16 ? idx : 0ull), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (!__shfl(last, 0, 64)) return;
-    unsigned long long* slot = ws + lane * kTreeStride;
-    // atomic reads of the final slot maxima (atomicMax with 0 changes nothing)
-    const unsigned long long m = wave_max_u64(static_cast<unsigned>(lane) < nslots ? atomicMax(slot, 0ull) : 0ull);
-    if (lane == 0) *token = argmax_index(m);
-    atomicExch(slot, 0ull);
-    atomicExch(reinterpret_cast<unsigned*>(slot + 8), 0u);
-    if (lane == 0) atomicExch(gcount, 0u);
+    if (b != nblk - 1) return;
+    unsigned long long best = 0ull;
+    for (int base = 0; base < nblk; base += 64 * kLmPollVec) {
+        unsigned long long v[kLmPollVec];
+        for (int spins = 0;; ++spins) {
+#pragma unroll
+            for (int i = 0; i < kLmPollVec; ++i) {
+                const int j = base + lane + 64 * i;
+                v[i] = __hip_atomic_load(keys + (j < nblk ? j : b), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            unsigned long long bad = 0;
+#pragma unroll
+            for (int i = 0; i < kLmPollVec; ++i) bad |= (v[i] >> 40) ^ tag;
+            if (__all(bad == 0)) break;
+            if (spins > kLmSpinLimit) {
+                if (lane == 0) __hip_atomic_fetch_or(ws32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int i = 0; i < kLmPollVec; ++i) {
+            const unsigned long long k = v[i] & 0xffffffffffull;
+            best = k > best ? k : best;
+        }
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) *token = (best >> 24) ? static_cast<int64_t>(0xffffffu - static_cast<uint32_t>(best & 0xffffffu)) : 0;
 }
 
 // ARGMAX modes of the GEMV epilogue (M == 1 only).
@@ -150,9 +174,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
 // waves contribute -0.0, the exact additive identity, so the sums equal the
 // GEMV's whenever that also gives each wave one group).  The best key then
 // leaves through one of two routes:
-//   kLmTree  -- the fence-free 64-slot arrival tree above; the last arrival
-//               writes the token (four device round trips after the last
-//               workgroup);
+//   kLmTree  -- the call-tagged key words above; the grid's last workgroup
+//               polls them and writes the token on the device;
 //   kLmSlots -- one fire-and-forget atomicMax of a call-tagged key into one
 //               of 64 slots; whoever reads the token takes the maximum of the
 //               slots that carry this call's tag (the host, after the copy it
@@ -183,6 +206,13 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
     asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
     const int s0 = static_cast<int>(blockIdx.x) * SPW;
+    // this workgroup's call counter (device-token route), issued before the
+    // weight loads and needed only at the end
+    unsigned epoch = 0;
+    if constexpr (MODE == kLmTree)
+        if (wave == 0)
+            epoch = __hip_atomic_load(reinterpret_cast<unsigned*>(ws) + kLmEpoch + blockIdx.x, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
     const int ns = nslab - s0 < SPW ? nslab - s0 : SPW;                  // workgroup-uniform
     const uint32_t zshift = (lane & 7) * 4;                              // slab bases are multiples of 8 columns
     const uint4* __restrict__ wbase = qw + lane;
@@ -250,7 +280,7 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     if (wave != 0) return;
     best = wave_max_u64(lane < kLmWaves ? wbest[lane] : 0ull);
     if constexpr (MODE == kLmTree) {
-        argmax_arrive(ws, best, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token);
+        argmax_publish(ws, best, epoch, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), nslab, lane, token);
     } else {
         if (lane == 0) {
             // argmax_key64 -> slot key: the fp16 key moves to bits 39..24, the
@@ -587,8 +617,9 @@ int mcv_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* q
 }
 
 int64_t mcv_lm_head_workspace_bytes(int64_t V) {
-    (void)V;
-    return kTreeBytes;
+    if (V <= 0 || V >= (int64_t(1) << 24)) return 0;
+    const int64_t nslab = ceil_div(V, kSlab);
+    return (lm_keys_index(nslab) + nslab) * 8;
 }
 
 int mcv_w4a16_gemv_argmax_partials(const void* x, int64_t K, int64_t N, int64_t V, const void* qw,
@@ -634,8 +665,8 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
     if (!x || !token || !workspace) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: null x/token/workspace");
     if (V <= 0 || V > N) return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax: need 0 < V <= N (V=%lld N=%lld)",
                                      (long long)V, (long long)N);
-    if (ceil_div(V, kSlab) > int64_t(kTreeWords) * 0xffff)
-        return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax: V too large for the combining tree");
+    if (V >= (int64_t(1) << 24))
+        return fail(MCV_ERR_SHAPE, "mcv_w4a16_lm_head_argmax: V must be below 2^24 (V=%lld)", (long long)V);
     if (reinterpret_cast<uintptr_t>(workspace) % 128 != 0)
         return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: workspace must be 128-byte aligned");
     if ((rc = require_device()) != MCV_OK) return rc;

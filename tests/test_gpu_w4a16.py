@@ -205,11 +205,11 @@ def test_lm_head_full_vocab(mcv, oracle, cuda):
     top2 = np.sort(ref)[-2:]
     assert top2[1] - top2[0] > 1e-2
     assert tok == int(np.argmax(ref))
-    # the device-token route: same token, same logits, workspace left zeroed
+    # the device-token route: same token, same logits, no wait gave up
     lt = torch.empty(V, dtype=torch.float16, device="cuda")
     assert int(head.launch(_to_dev(x), lt).item()) == tok
     assert torch.equal(lt.view(torch.int16), logits.view(torch.int16))
-    assert int(head.workspace.count_nonzero()) == 0
+    assert int(head.workspace[:4].view(torch.int32).item()) == 0
     # repeated calls (slots and workspace reused) give the same answer
     assert head(_to_dev(x)) == tok
     assert head(_to_dev(x), logits) == tok
@@ -260,9 +260,9 @@ def test_lm_head_shapes(mcv, oracle, cuda, K, V, zb):
 
 @pytest.mark.parametrize("V", [4097, 8320, 100000])
 def test_lm_head_routes_agree(mcv, oracle, cuda, V):
-    """The in-kernel arrival tree (64 level-1 slots, uneven arrival counts),
+    """The call-tagged key words read by the grid's last workgroup,
     the host-finished tagged slots and the two-kernel keys + reduction give
-    the same token and logits; the tree leaves its workspace zeroed."""
+    the same token and logits, call after call with no wait giving up."""
     torch = _torch()
     K, NW = 512, -(-V // 8) * 8
     rng = np.random.default_rng(V + 11)
@@ -276,7 +276,7 @@ def test_lm_head_routes_agree(mcv, oracle, cuda, V):
         lb = torch.empty(V, dtype=torch.float16, device="cuda")
         lc = torch.empty(V, dtype=torch.float16, device="cuda")
         tree = int(head.launch(x, la).item())
-        assert int(head.workspace.count_nonzero()) == 0
+        assert int(head.workspace[:4].view(torch.int32).item()) == 0
         head.launch_partials(x, lb)
         two = int(head.reduce_partials().item())
         slots = head(x, lc)
@@ -372,7 +372,7 @@ def test_lm_head_bound_launchers(mcv, oracle, cuda):
         lb.fill_(0)
         assert int(tree().item()) == want
         assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
-    assert int(head.workspace.count_nonzero()) == 0
+    assert int(head.workspace[:4].view(torch.int32).item()) == 0
     slots = head.bind(x, lb, route="slots")
     t0 = head.tag
     for i in range(3):
