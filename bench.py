@@ -358,11 +358,12 @@ def wl_qkvz(pkg, args, fused=True):
                 kernel="w4a16_gemv_multi_kernel" if fused else "w4a16_gemv_kernel x2")
 
 
-def wl_mlp_w8a8(pkg, args, fused=True):
+def wl_mlp_w8a8(pkg, args, mode="block"):
     """The decode MLP block over W8A8 weights (gate/up 1024->3584, down
     3584->1024), 32 layer sets (352 MB, past the MALL), from the normed fp16
-    row: fused = quantise x, one gate+up+silu*mul launch, quantise act, down;
-    unfused = the reference's quantise, gate, up, silu_mul, quantise, down."""
+    row: block = the whole block in one launch (DecodeMlpW8A8); fused =
+    quantise x, one gate+up+silu*mul launch, quantise act, down; unfused = the
+    reference's quantise, gate, up, silu_mul, quantise, down."""
     import torch
     H, I = 1024, 3584
     nsets = args.copies or 32
@@ -380,9 +381,14 @@ def wl_mlp_w8a8(pkg, args, fused=True):
     aq = torch.empty((1, I), dtype=torch.int8, device="cuda")
     asc = torch.empty(1, dtype=torch.float32, device="cuda")
     y = torch.empty((1, H), dtype=torch.float16, device="cuda")
+    fused = mode == "fused"
+    mlps = [pkg.DecodeMlpW8A8(*L) for L in sets] if mode == "block" else None
 
     def block(i):
         L = sets[i]
+        if mlps is not None:
+            mlps[i](x, y)
+            return
         pkg.w8a8_quantize(x, xq, xs)
         if fused:
             pkg.mlp_gate_up_silu_w8a8(xq, xs, L[0], L[1], a)
@@ -395,11 +401,15 @@ def wl_mlp_w8a8(pkg, args, fused=True):
 
     nbytes = 3 * H * I + 2 * (2 * I + I) * 4 + (2 * H + H) + (2 * I + I) * 2 + 2 * H
     total_ms, _ = time_steps(block, len(sets), args.steps, args.warmup)
+    if mlps is not None and (any(m.wait_gave_up() for m in mlps) or not all(m.one_launch for m in mlps)):
+        raise RuntimeError("W8A8 decode MLP: the one-launch kernel did not run cleanly")
+    suffix = {"block": "", "fused": "_4launch", "unfused": "_unfused"}[mode]
+    kernel = {"block": "w8a8_mlp_kernel (whole block, one launch)", "fused": "w8a8 mlp block (4 launches)",
+              "unfused": "w8a8 mlp block (6 launches)"}[mode]
     return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=[total_ms / args.steps], unit="GB/s", bound="hbm",
-                config={"workload": "w8a8_mlp_block_decode" + ("" if fused else "_unfused"), "M": 1, "hidden": H,
+                config={"workload": "w8a8_mlp_block_decode" + suffix, "M": 1, "hidden": H,
                         "intermediate": I, "weight_sets_rotated": len(sets)},
-                dtype="int8 (i32 accumulate, fused f16 epilogue)",
-                kernel="w8a8 mlp block (" + ("4 launches)" if fused else "6 launches)"))
+                dtype="int8 (i32 accumulate, fused f16 epilogue)", kernel=kernel)
 
 
 def wl_prefill(pkg, args):
@@ -508,7 +518,8 @@ WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
              "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, mode="unfused"), "prefill": wl_prefill, "w8a8": wl_w8a8,
              "copy": wl_copy, "norm_quant": wl_norm_quant, "mlp_w8a8": wl_mlp_w8a8, "qkvz": wl_qkvz,
              "qkvz_unfused": lambda pkg, args: wl_qkvz(pkg, args, fused=False),
-             "mlp_w8a8_unfused": lambda pkg, args: wl_mlp_w8a8(pkg, args, fused=False),
+             "mlp_w8a8_4launch": lambda pkg, args: wl_mlp_w8a8(pkg, args, mode="fused"),
+             "mlp_w8a8_unfused": lambda pkg, args: wl_mlp_w8a8(pkg, args, mode="unfused"),
              "norm_quant_unfused": lambda pkg, args: wl_norm_quant(pkg, args, fused=False), "vendor_f16": wl_vendor, "vendor_int8": lambda pkg, args: wl_vendor(pkg, args, int8=True)}
 
 

@@ -315,6 +315,24 @@ int mcv_w8a8_gemm_f16(const int8_t* xq_dev, const void* x_scale_dev, int x_scale
                       const void* w_scale_dev, int w_scale_dtype, void* out_dev,
                       mcv_stream_t stream);
 
+/* The whole W8A8 decode MLP block, M = 1, in one launch, from the normed fp16
+ * row x [1][H]: quantise x, gate and up int8 GEMVs with the fused epilogue,
+ * silu * mul, quantise the act row, the down int8 GEMV with its epilogue ->
+ * out fp16 [1][H].  Bit-identical to mcv_w8a8_quantize_act,
+ * mcv_w8a8_gate_up_silu, mcv_w8a8_quantize_act, mcv_w8a8_gemm_f16 with fp32
+ * scales (the decoder layers' W8A8 MLP sequence,
+ * src/csrc/lib/decoder_layer.cpp:1022-1046).  Weights are MCV_W8_TILED
+ * (gate/up H x I, down I x H) with fp32 per-channel scales; H <= 8192, I <= 16384, H and
+ * I multiples of 128.  Values pass between workgroups through `workspace_dev`
+ * (mcv_w8a8_mlp_workspace_bytes(H, I) bytes, 256-byte aligned, zero-filled
+ * once; one shape per workspace; calls sharing it must not overlap; the u32
+ * at byte 0 turns non-zero if a wait ever gave up).  MCV_ERR_SHAPE when the
+ * launch would not fit on the device at once. */
+int64_t mcv_w8a8_mlp_workspace_bytes(int64_t H, int64_t I);
+int mcv_w8a8_mlp(const void* x_dev, int64_t H, int64_t I, const int8_t* w_gate_dev, const float* ws_gate_dev,
+                 const int8_t* w_up_dev, const float* ws_up_dev, const int8_t* w_down_dev, const float* ws_down_dev,
+                 void* out_dev, void* workspace_dev, mcv_stream_t stream);
+
 /* Decode MLP front half over W8A8 weights: act[M][N] fp16 = silu(gate) * up,
  * gate and up each the fused epilogue of mcv_w8a8_gemm_f16 over the same
  * quantised x (one activation quantisation shared by both, as

@@ -85,6 +85,8 @@ _SIGS = {
     "mcv_w8a8_gate_up_silu": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp,
                                        _vp]),
     "mcv_w8a8_pack_tiled_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
+    "mcv_w8a8_mlp_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "mcv_w8a8_mlp": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mcv_w8a8_quantize_weight_nk_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_pack_tiled_nk_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
@@ -676,6 +678,62 @@ def matmul_w8a8(x_int8, x_scale, w: W8A8QuantizedWeight, out=None, use_f32_scale
     _check(lib().mcv_w8a8_gemm_f16(_dev(x_int8), _dev(x_scale), _scale_dtype(x_scale), M, K, w.N, _dev(w.w_int8),
                                    w.layout, _dev(ws), _scale_dtype(ws), _dev(out), _stream(stream)), "matmul_w8a8")
     return out
+
+
+class DecodeMlpW8A8:
+    """The whole W8A8 decode MLP block, M = 1, in one launch from the normed
+    fp16 row: out[H] = deq(quant(silu(deq(quant(x) . gate)) * deq(quant(x) . up)) . down),
+    bit-identical to w8a8_quantize, mlp_gate_up_silu_w8a8, w8a8_quantize and
+    matmul_w8a8 with fp32 scales (decoder_layer.cpp:1022-1046); those four
+    launches where the one-launch grid does not fit (one_launch turns False).
+    Weights must be MCV_W8_TILED.  Calls on one object must not overlap."""
+
+    ERROR_WORD = 0
+    _ERR_SHAPE = 2
+
+    def __init__(self, gate: "W8A8QuantizedWeight", up: "W8A8QuantizedWeight", down: "W8A8QuantizedWeight"):
+        torch = _torch()
+        if (up.K, up.N) != (gate.K, gate.N) or (down.K, down.N) != (gate.N, gate.K):
+            raise McvError("decode MLP (W8A8): gate/up must be [H, I] and down [I, H]")
+        if any(w.layout != W8_TILED for w in (gate, up, down)):
+            raise McvError("decode MLP (W8A8): weights must be in the tiled layout")
+        self.gate, self.up, self.down = gate, up, down
+        self.H, self.I = gate.K, gate.N
+        dev = gate.w_int8.device
+        nbytes = lib().mcv_w8a8_mlp_workspace_bytes(self.H, self.I)
+        self.one_launch = nbytes > 0
+        self.workspace = torch.zeros(max(nbytes, 4) // 4, dtype=torch.int32, device=dev)
+
+    def _four_launches(self, x, out, stream):
+        xq, xs, _ = w8a8_quantize(x.view(1, self.H), stream=stream)
+        act = mlp_gate_up_silu_w8a8(xq, xs, self.gate, self.up, stream=stream)
+        aq, asc, _ = w8a8_quantize(act, stream=stream)
+        matmul_w8a8(aq, asc, self.down, out.view(1, self.H), stream=stream)
+
+    def __call__(self, x, out=None, stream=None):
+        torch = _torch()
+        if x.dtype != torch.float16 or x.numel() != self.H or not x.is_contiguous():
+            raise McvError(f"decode MLP (W8A8): x must be contiguous fp16 [1, {self.H}]")
+        if out is None:
+            out = torch.empty((1, self.H), dtype=torch.float16, device=x.device)
+        if out.dtype != torch.float16 or out.numel() != self.H or not out.is_contiguous():
+            raise McvError(f"decode MLP (W8A8): out must be contiguous fp16 [1, {self.H}]")
+        if self.one_launch:
+            g, u, d = self.gate, self.up, self.down
+            rc = lib().mcv_w8a8_mlp(_dev(x), self.H, self.I, _dev(g.w_int8), _dev(g.w_scale_f32), _dev(u.w_int8),
+                                    _dev(u.w_scale_f32), _dev(d.w_int8), _dev(d.w_scale_f32), _dev(out),
+                                    _dev(self.workspace), _stream(stream))
+            if rc != self._ERR_SHAPE:
+                _check(rc, "mcv_w8a8_mlp")
+                return out
+            self.one_launch = False
+        self._four_launches(x, out, stream)
+        return out
+
+    def wait_gave_up(self) -> bool:
+        """True if a wait for another workgroup's words in any earlier call
+        timed out (synchronises)."""
+        return bool(int(self.workspace[self.ERROR_WORD].item()))
 
 
 def mlp_gate_up_silu_w8a8(x_int8, x_scale, w_gate: W8A8QuantizedWeight, w_up: W8A8QuantizedWeight, out=None,

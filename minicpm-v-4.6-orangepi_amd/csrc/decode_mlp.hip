@@ -242,19 +242,305 @@ __global__ __launch_bounds__(64 * kMaxWaves) void w4a16_mlp_kernel(const uint16_
     if (col < H) out[col] = f2h(acc);
 }
 
-// Workgroups of this kernel that the current device holds at once
-// (occupancy per CU x CUs), cached per device and block size.
-int resident_blocks(int threads) {
+// ---------------------------------------------------------------- W8A8 --
+// The W8A8 decode MLP block from the normed fp16 row, in one launch:
+//   xq, xs = quantize(x); act = silu(deq(xq . gate)) * deq(xq . up);
+//   aq, as = quantize(act); out = deq(aq . down)
+// with every step as the separate kernels do it (mcv_w8a8_quantize_act,
+// mcv_w8a8_gate_up_silu, mcv_w8a8_gemm_f16 with fp32 scales) -- bit-identical,
+// since the int32 sums are exact in any order and a row maximum is a maximum.
+// Phase 1: one workgroup per 32-column half of an act slab quantises x itself
+// (H values, into LDS), runs the dual int8 GEMV over the tiled weights and
+// publishes its act values (tag << 16 | fp16) and the maximum of their
+// magnitudes (tag << 32 | fp32).  Phase 2: workgroup (half of an output slab,
+// k-part) loads its down-projection operand lines at the start, polls the
+// half maxima and its k-range of act words, quantises that range with the row
+// scale into LDS, forms its int32 partial sums and publishes them; the
+// k-part-0 workgroup adds the parts and applies the epilogue.
+constexpr int kW8Line = 1024;                 // bytes of one 32-column x 32-k operand line
+constexpr int kW8Waves = 8;
+constexpr int kW8U = 4;                       // k-blocks per wave per trip (phase 1) / per part (phase 2)
+constexpr int kW8PartBlocks = kW8Waves * kW8U;  // k-blocks of one phase-2 part
+constexpr int kW8MaxH = 8192;                 // the quantised x row staged in LDS
+constexpr int kW8XWords = kW8MaxH / 2 / (64 * kW8Waves);   // fp16 pairs of x per thread
+constexpr int kW8MaxParts = 16;               // phase-2 k-parts per output half: I <= 16384
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t w8_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// Maximum over the workgroup's eight waves (values are magnitudes, >= 0).
+__device__ __forceinline__ float block_max8(float m, float* __restrict__ scratch8) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) scratch8[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = scratch8[0];
+#pragma unroll
+    for (int w = 1; w < kW8Waves; ++w) m = scratch8[w] > m ? scratch8[w] : m;
+    return m;
+}
+
+struct W8Layout {                             // word offsets into the workspace
+    int act;                                  // u32 [I]
+    int amax;                                 // u64 [2 nslab1]
+    int part;                                 // u64 [2 nslab2][nparts][32]
+};
+
+__host__ __device__ inline W8Layout w8_layout(int H, int I, int nparts) {
+    const int nslab1 = (I + 63) / 64;
+    W8Layout l;
+    l.act = static_cast<int>(kWsHeader / 4);
+    l.amax = (l.act + nslab1 * 64 + 1) / 2;                             // u64 index
+    l.part = l.amax + 2 * nslab1;
+    (void)H;
+    (void)nparts;
+    return l;
+}
+
+// grid = 2 nslab2 nparts (phase 2, first) + 2 nslab1 (phase 1), block = 512.
+__global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ wg, const float* __restrict__ sg,
+    const int8_t* __restrict__ wu, const float* __restrict__ su, const int8_t* __restrict__ wd,
+    const float* __restrict__ sd, uint16_t* __restrict__ out, int H, int I, int nparts, unsigned* __restrict__ ws) {
+    __shared__ __attribute__((aligned(16))) int8_t xq_lds[kW8MaxH];
+    __shared__ int red[kW8Waves][2][64];
+    __shared__ float scratch8[kW8Waves];
+    __shared__ unsigned s_epoch;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5;
+    const int b = blockIdx.x;
+    const int nslab1 = (I + 63) / 64, nslab2 = (H + 63) / 64;
+    const int KB1 = (H + 127) / 128 * 4, KB2 = (I + 127) / 128 * 4;
+    const W8Layout L = w8_layout(H, I, nparts);
+    uint32_t* __restrict__ act = reinterpret_cast<uint32_t*>(ws) + L.act;
+    uint64_t* __restrict__ amax = reinterpret_cast<uint64_t*>(ws) + L.amax;
+    uint64_t* __restrict__ part = reinterpret_cast<uint64_t*>(ws) + L.part;
+    constexpr uint32_t kNowhere = 0xFFFFFF00u;
+    const unsigned epoch =
+        wave == 0 ? __hip_atomic_load(ws + kWsEpoch + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+    const int n2 = 2 * nslab2 * nparts;
+
+    if (b >= n2) {
+        // ---- phase 1: half j of act slab `slab`
+        const int u1 = b - n2, slab = u1 >> 1, j = u1 & 1;
+        const uint32_t wbytes = static_cast<uint32_t>(nslab1) * KB1 * 2 * kW8Line;
+        const __amdgpu_buffer_rsrc_t rg = w8_rsrc(wg, wbytes), ru = w8_rsrc(wu, wbytes);
+        // the weight lines of the first trip are in flight while x is quantised
+        int4_t wgv[kW8U], wuv[kW8U];
+        auto load_w = [&](int kb0) {
+#pragma unroll
+            for (int u = 0; u < kW8U; ++u) {
+                const int kb = kb0 + u * kW8Waves;
+                const uint32_t off =
+                    kb < KB1 ? ((static_cast<uint32_t>(slab) * KB1 + kb) * 2 + j) * kW8Line + lane * 16u : kNowhere;
+                wgv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
+                wuv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0));
+            }
+        };
+        // x as fp16 pairs, all loads issued at once and ahead of the weights
+        const uint32_t* __restrict__ x32 = reinterpret_cast<const uint32_t*>(x);
+        uint32_t xw[kW8XWords];
+#pragma unroll
+        for (int i = 0; i < kW8XWords; ++i) {
+            const int k2 = static_cast<int>(threadIdx.x) + i * 64 * kW8Waves;
+            xw[i] = k2 < H / 2 ? x32[k2] : 0u;
+        }
+        load_w(wave);
+        const int n = slab * 64 + 32 * j + (lane & 31);
+        const float sgv = n < I ? sg[n] : 0.f, suv = n < I ? su[n] : 0.f;
+        // x -> xq with the activation quantiser's arithmetic (H is a multiple
+        // of 128, so the k-blocks cover x exactly)
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < kW8XWords; ++i) {
+            const float v0 = fabsf(h2f(static_cast<uint16_t>(xw[i]))), v1 = fabsf(h2f(static_cast<uint16_t>(xw[i] >> 16)));
+            m = v0 > m ? v0 : m;
+            m = v1 > m ? v1 : m;
+        }
+        const float xs = act_scale(block_max8(m, scratch8));
+        const float inv = __fdiv_rn(1.0f, xs);
+#pragma unroll
+        for (int i = 0; i < kW8XWords; ++i) {
+            const int k2 = static_cast<int>(threadIdx.x) + i * 64 * kW8Waves;
+            if (k2 < H / 2) {
+                const uint32_t lo = static_cast<uint8_t>(act_quant(static_cast<uint16_t>(xw[i]), inv));
+                const uint32_t hi = static_cast<uint8_t>(act_quant(static_cast<uint16_t>(xw[i] >> 16), inv));
+                reinterpret_cast<uint16_t*>(xq_lds)[k2] = static_cast<uint16_t>(lo | (hi << 8));
+            }
+        }
+        __syncthreads();
+        int accg = 0, accu = 0;
+        for (int kb0 = wave;;) {
+#pragma unroll
+            for (int u = 0; u < kW8U; ++u) {
+                const int kb = kb0 + u * kW8Waves;
+                if (kb < KB1) {
+                    const int4_t xv = *reinterpret_cast<const int4_t*>(xq_lds + kb * 32 + h * 16);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        accg = __builtin_amdgcn_sdot4(wgv[u][q], xv[q], accg, false);
+                        accu = __builtin_amdgcn_sdot4(wuv[u][q], xv[q], accu, false);
+                    }
+                }
+            }
+            kb0 += kW8Waves * kW8U;
+            if (kb0 >= KB1) break;
+            load_w(kb0);
+        }
+        red[wave][0][lane] = accg;
+        red[wave][1][lane] = accu;
+        __syncthreads();
+        if (wave != 0) return;
+        const uint32_t tag = (epoch + 1u) & 0xffffu;
+        if (lane == 0)
+            __hip_atomic_store(ws + kWsEpoch + b, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // lanes 0-31: columns of the half; both k-halves of every wave
+        const int l = lane & 31;
+        int g = 0, uu = 0;
+        for (int w = 0; w < kW8Waves; ++w) {
+            g += red[w][0][l] + red[w][0][l + 32];
+            uu += red[w][1][l] + red[w][1][l + 32];
+        }
+        float a = 0.f;
+        if (lane < 32 && n < I) {
+            const uint16_t g16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(g), sgv), xs));
+            const uint16_t u16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(uu), suv), xs));
+            const uint16_t a16 = silu_mul_f16(g16, u16);
+            a = fabsf(h2f(a16));
+            __hip_atomic_store(act + n, (tag << 16) | a16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float o = __shfl_xor(a, off, 64);
+            a = o > a ? o : a;
+        }
+        if (lane == 0)
+            __hip_atomic_store(amax + u1, (static_cast<uint64_t>(tag) << 32) | __float_as_uint(a), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+
+    // ---- phase 2: half j of output slab `slab`, k-part p
+    const int p = b % nparts, u2 = b / nparts, slab = u2 >> 1, j = u2 & 1;
+    const int kbp = (KB2 + nparts - 1) / nparts;
+    const int kb_beg = p * kbp, kb_end = kb_beg + kbp < KB2 ? kb_beg + kbp : KB2;
+    const uint32_t wbytes = static_cast<uint32_t>(nslab2) * KB2 * 2 * kW8Line;
+    const __amdgpu_buffer_rsrc_t rd = w8_rsrc(wd, wbytes);
+    int4_t wdv[kW8U];
+#pragma unroll
+    for (int u = 0; u < kW8U; ++u) {
+        const int kb = kb_beg + wave + u * kW8Waves;
+        const uint32_t off =
+            kb < kb_end ? ((static_cast<uint32_t>(slab) * KB2 + kb) * 2 + j) * kW8Line + lane * 16u : kNowhere;
+        wdv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, 0));
+    }
+    const int ncol = slab * 64 + 32 * j + (lane & 31);
+    const float sdv = p == 0 && wave == 0 && ncol < H ? sd[ncol] : 0.f;
+    if (wave == 0 && lane == 0) {
+        s_epoch = epoch;
+        __hip_atomic_store(ws + kWsEpoch + b, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const uint32_t tag = (s_epoch + 1u) & 0xffffu;
+    // poll: thread t reads half maximum t (if any) and act words k0 + t, k0 + t + 512 of the k-range
+    const int k0 = kb_beg * 32, klen = (kb_end - kb_beg) * 32;
+    const int nmax = 2 * nslab1;
+    float am = 0.f;
+    uint32_t av[2] = {0u, 0u};
+    for (int spins = 0;; ++spins) {
+        bool ok = true;
+        am = 0.f;
+        if (static_cast<int>(threadIdx.x) < nmax) {
+            const uint64_t v = __hip_atomic_load(amax + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = static_cast<uint32_t>(v >> 32) == tag;
+            am = __uint_as_float(static_cast<uint32_t>(v));
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int k = static_cast<int>(threadIdx.x) + i * 64 * kW8Waves;
+            if (k < klen && k0 + k < I) {
+                av[i] = __hip_atomic_load(act + k0 + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = ok && (av[i] >> 16) == tag;
+            }
+        }
+        if (!__syncthreads_or(ok ? 0 : 1)) break;
+        if (spins > kSpinLimit) {
+            if (threadIdx.x == 0) __hip_atomic_fetch_or(ws + kWsError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    // the act row's scale (maximum of the half maxima), its k-range quantised into LDS
+    const float as = act_scale(block_max8(am, scratch8));
+    const float inv = __fdiv_rn(1.0f, as);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int k = static_cast<int>(threadIdx.x) + i * 64 * kW8Waves;
+        if (k < klen) xq_lds[k] = k0 + k < I ? act_quant(static_cast<uint16_t>(av[i] & 0xffffu), inv) : int8_t(0);
+    }
+    __syncthreads();
+    int acc = 0;
+#pragma unroll
+    for (int u = 0; u < kW8U; ++u) {
+        const int kb = kb_beg + wave + u * kW8Waves;
+        if (kb < kb_end) {
+            const int4_t xv = *reinterpret_cast<const int4_t*>(xq_lds + (kb - kb_beg) * 32 + h * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_sdot4(wdv[u][q], xv[q], acc, false);
+        }
+    }
+    red[wave][0][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    const int l = lane & 31;
+    int sum = 0;
+    for (int w = 0; w < kW8Waves; ++w) sum += red[w][0][l] + red[w][0][l + 32];
+    uint64_t* __restrict__ mypart = part + (static_cast<size_t>(u2) * nparts) * 32 + l;
+    if (p != 0) {
+        if (lane < 32)
+            __hip_atomic_store(mypart + p * 32, (static_cast<uint64_t>(tag) << 32) | static_cast<uint32_t>(sum),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // k-part 0: add the other parts (exact int32; read together, parts past
+    // nparts re-read part 1) and apply the epilogue
+    if (nparts > 1) {
+        uint64_t v[kW8MaxParts - 1];
+        poll_words<kW8MaxParts - 1>(
+            v,
+            [&](uint64_t (&w)[kW8MaxParts - 1]) {
+#pragma unroll
+                for (int q = 0; q < kW8MaxParts - 1; ++q)
+                    w[q] = __hip_atomic_load(mypart + (q + 1 < nparts ? q + 1 : 1) * 32, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+            },
+            [](uint64_t w) { return static_cast<uint32_t>(w >> 32); }, tag, ws, lane);
+#pragma unroll
+        for (int q = 0; q < kW8MaxParts - 1; ++q)
+            if (q + 1 < nparts) sum += static_cast<int>(static_cast<uint32_t>(v[q]));
+    }
+    if (lane < 32 && ncol < H) out[ncol] = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum), sdv), as));
+}
+
+// Workgroups of `kernel` that the current device holds at once (occupancy
+// per CU x CUs), cached per device, kernel and block size.
+template <typename Kernel>
+int resident_blocks(Kernel kernel, int which, int threads) {
     static std::mutex mu;
     static std::unordered_map<int64_t, int> cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    const int64_t key = (static_cast<int64_t>(dev) << 16) | threads;
+    const int64_t key = (static_cast<int64_t>(dev) << 20) | (static_cast<int64_t>(which) << 16) | threads;
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, w4a16_mlp_kernel, threads, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
     const int n = per_cu * cus;
@@ -304,7 +590,7 @@ int mcv_w4a16_mlp(const void* x, int64_t H, int64_t I, const void* qw_gate, cons
                     (long long)H, (long long)I);
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    const int resident = resident_blocks(threads);
+    const int resident = resident_blocks(w4a16_mlp_kernel, 0, threads);
     if (grid > resident)
         return fail(MCV_ERR_SHAPE, "%s: %lld workgroups of %d threads exceed the %d the device holds at once", who,
                     (long long)grid, threads, resident);
@@ -319,6 +605,47 @@ int mcv_w4a16_mlp(const void* x, int64_t H, int64_t I, const void* qw_gate, cons
                        static_cast<uint16_t*>(out), static_cast<int>(H), static_cast<int>(I), ks1, ks2,
                        static_cast<unsigned*>(workspace));
     return check_launch("w4a16_mlp_kernel");
+}
+
+static int w8_parts(int64_t I) { return static_cast<int>(ceil_div(ceil_div(I, 128) * 4, kW8PartBlocks)); }
+
+int64_t mcv_w8a8_mlp_workspace_bytes(int64_t H, int64_t I) {
+    if (H <= 0 || I <= 0 || H > kW8MaxH || w8_parts(I) > kW8MaxParts) return 0;
+    const W8Layout l = w8_layout(static_cast<int>(H), static_cast<int>(I), w8_parts(I));
+    return (static_cast<int64_t>(l.part) + 2 * ceil_div(H, kSlab) * w8_parts(I) * 32) * 8;
+}
+
+int mcv_w8a8_mlp(const void* x, int64_t H, int64_t I, const int8_t* w_gate, const float* ws_gate, const int8_t* w_up,
+                 const float* ws_up, const int8_t* w_down, const float* ws_down, void* out, void* workspace,
+                 mcv_stream_t stream) {
+    const char* who = "mcv_w8a8_mlp";
+    if (!x || !out || !workspace) return fail(MCV_ERR_INVALID_ARG, "%s: null x/out/workspace", who);
+    if (!w_gate || !ws_gate || !w_up || !ws_up || !w_down || !ws_down)
+        return fail(MCV_ERR_INVALID_ARG, "%s: null weight or scale pointer", who);
+    if ((reinterpret_cast<uintptr_t>(w_gate) | reinterpret_cast<uintptr_t>(w_up) | reinterpret_cast<uintptr_t>(w_down)) % 16)
+        return fail(MCV_ERR_INVALID_ARG, "%s: weights must be 16-byte aligned", who);
+    if (H <= 0 || H % kGroup != 0 || I <= 0 || I % kGroup != 0 || H > kW8MaxH || I > 16384)
+        return fail(MCV_ERR_SHAPE, "%s: H, I must be positive multiples of 128, H <= %d, I <= 16384 (H=%lld I=%lld)",
+                    who, kW8MaxH, (long long)H, (long long)I);
+    if (reinterpret_cast<uintptr_t>(x) % 4 != 0) return fail(MCV_ERR_INVALID_ARG, "%s: x must be 4-byte aligned", who);
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "%s: workspace must be 256-byte aligned", who);
+    const int nparts = w8_parts(I);
+    const int64_t grid = 2 * ceil_div(H, kSlab) * nparts + 2 * ceil_div(I, kSlab);
+    if (grid > kMaxBlocks)
+        return fail(MCV_ERR_SHAPE, "%s: %lld workgroups exceed %d (H=%lld I=%lld)", who, (long long)grid, kMaxBlocks,
+                    (long long)H, (long long)I);
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    const int resident = resident_blocks(w8a8_mlp_kernel, 1, 64 * kW8Waves);
+    if (grid > resident)
+        return fail(MCV_ERR_SHAPE, "%s: %lld workgroups exceed the %d the device holds at once", who, (long long)grid,
+                    resident);
+    hipLaunchKernelGGL(w8a8_mlp_kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * kW8Waves), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), w_gate, ws_gate, w_up, ws_up,
+                       w_down, ws_down, static_cast<uint16_t*>(out), static_cast<int>(H), static_cast<int>(I), nparts,
+                       static_cast<unsigned*>(workspace));
+    return check_launch("w8a8_mlp_kernel");
 }
 
 }  // extern "C"

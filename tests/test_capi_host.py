@@ -190,6 +190,15 @@ def test_validation_errors_without_device(mcv):
     assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, None, 0, fake, fake, None) == 1
     assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, fake, 2, fake, fake, None) == 1
     assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, *w3, fake, ctypes.c_void_p(0x1080), None) == 1
+    # the one-launch W8A8 MLP block
+    assert L.mcv_w8a8_mlp_workspace_bytes(1024, 3584) > 3584 * 4
+    assert L.mcv_w8a8_mlp_workspace_bytes(8192 + 128, 3584) == 0
+    w2 = (fake, fake)
+    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, *w2, fake, None, None) == 1
+    assert L.mcv_w8a8_mlp(fake, 1000, 3584, *w2, *w2, *w2, fake, fake, None) == 2
+    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, fake, None, fake, fake, None) == 1
+    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, ctypes.c_void_p(0x1008), fake, fake, fake, None) == 1
+    assert b"16-byte" in L.mcv_last_error()
     assert b"aligned" in L.mcv_last_error()
 
 

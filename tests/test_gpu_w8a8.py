@@ -4,7 +4,7 @@ against the oracle's epilogue).  Benchmark shapes: M in {1, 256, 1024}, K=1024, 
 import numpy as np
 import pytest
 
-from helpers import f16_normal
+from helpers import f16_normal, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -234,3 +234,41 @@ def _tiled_to_kn(mcv, w):
     l = n % 32 + 32 * ((k % 32) // 16)
     off = ((((n // 64) * kb + k // 32) * 2 + (n % 64) // 32) * 64 + l) * 16 + k % 16
     return t[off]
+
+
+@pytest.mark.parametrize("H,I", [(1024, 3584), (3584, 1024), (256, 384), (128, 128), (2048, 6144)],
+                         ids=lambda v: str(v))
+def test_decode_mlp_block_one_launch(mcv, oracle, cuda, H, I):
+    """The whole W8A8 MLP block in one launch == quantise x, gate+up+silu*mul,
+    quantise act, down GEMV, bit for bit, call after call; and the oracle's
+    composition of the same stages."""
+    torch = _torch()
+    rng = np.random.default_rng(H * 5 + I)
+    wg = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
+    wu = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
+    wd = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (I, H), 0.02)))
+    mlp = mcv.DecodeMlpW8A8(wg, wu, wd)
+    out = torch.empty((1, H), dtype=torch.float16, device="cuda")
+    want = torch.empty_like(out)
+    for trial in range(3):
+        x = f16_normal(rng, (1, H), 1.0 + trial)
+        xd = _f16_dev(x)
+        mlp(xd, out)
+        assert mlp.one_launch
+        mlp._four_launches(xd, want, None)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"trial {trial}"
+    assert not mlp.wait_gave_up()
+    # oracle: quantise, int32 products, reference epilogues, silu*mul, quantise, down
+    q_o, s_o, _ = oracle.w8a8_quantize_act(x)
+    g_o = oracle.w8a8_dequant(oracle.gemm_i32(q_o, _tiled_to_kn(mcv, wg)), s_o, wg.w_scale_f32.cpu().numpy())
+    u_o = oracle.w8a8_dequant(oracle.gemm_i32(q_o, _tiled_to_kn(mcv, wu)), s_o, wu.w_scale_f32.cpu().numpy())
+    a_o = oracle.silu_mul(g_o, u_o)
+    aq_o, as_o, _ = oracle.w8a8_quantize_act(a_o.reshape(1, I))
+    y_o = oracle.w8a8_dequant(oracle.gemm_i32(aq_o, _tiled_to_kn(mcv, wd)), as_o, wd.w_scale_f32.cpu().numpy())
+    got = _u16(out).view(np.float16).astype(np.float32)
+    ref = y_o.view(np.float16).astype(np.float32)
+    # silu's exp may differ by an fp32 ulp between libms, which can move an act
+    # value by one fp16 ulp and so a quantised act by one step
+    assert np.abs(got - ref).max() <= 2e-2 and rel_l2(got, ref) <= 1e-3
+    assert (_u16(out) == y_o).mean() > 0.9
