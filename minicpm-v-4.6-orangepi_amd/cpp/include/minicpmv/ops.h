@@ -83,6 +83,22 @@ void matmul_w4a16_multi(const Tensor& x, const std::vector<const W4A16QuantizedW
 void mlp_gate_up_silu_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8A8QuantizedWeight& gate,
                            const W8A8QuantizedWeight& up, Tensor& act, hipStream_t stream);
 
+// The whole W8A8 decode MLP block, M = 1, from the normed fp16 row:
+// w8a8_quantize, mlp_gate_up_silu_w8a8, w8a8_quantize, matmul_w8a8 with fp32
+// scales (decoder_layer.cpp:1022-1046), bit-identical; one launch
+// (mcv_w8a8_mlp) for tiled weights where the grid fits, else those four.
+struct DecodeMlpW8A8 {
+    const W8A8QuantizedWeight* gate{nullptr};    // [H, I]
+    const W8A8QuantizedWeight* up{nullptr};      // [H, I]
+    const W8A8QuantizedWeight* down{nullptr};    // [I, H]
+    Tensor workspace;                            // zero-filled once; one stream at a time
+    Tensor xq, xs, act, aq, as;                  // buffers of the four-launch path
+    bool one_launch{true};
+};
+DecodeMlpW8A8 make_decode_mlp_w8a8(const W8A8QuantizedWeight& gate, const W8A8QuantizedWeight& up,
+                                   const W8A8QuantizedWeight& down);
+void mlp_w8a8(const Tensor& x, DecodeMlpW8A8& mlp, Tensor& out, hipStream_t stream);
+
 // out fp16 [M, N] = RNE((acc * w_scale[n]) * x_scale[m]); scales fp16 or fp32.
 void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream);
 

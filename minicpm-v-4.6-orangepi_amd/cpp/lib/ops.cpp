@@ -182,6 +182,56 @@ void rms_norm_w8a8_quantize(const Tensor& x, const Tensor& gamma, double epsilon
               "rms_norm_w8a8_quantize");
 }
 
+DecodeMlpW8A8 make_decode_mlp_w8a8(const W8A8QuantizedWeight& gate, const W8A8QuantizedWeight& up,
+                                   const W8A8QuantizedWeight& down) {
+    require(up.K == gate.K && up.N == gate.N, "decode MLP (W8A8) gate and up must have the same shape");
+    require(down.K == gate.N && down.N == gate.K, "decode MLP (W8A8) down must be [I, H] for gate [H, I]");
+    DecodeMlpW8A8 mlp;
+    mlp.gate = &gate;
+    mlp.up = &up;
+    mlp.down = &down;
+    const bool tiled = gate.layout == MCV_W8_TILED && up.layout == MCV_W8_TILED && down.layout == MCV_W8_TILED;
+    const int64_t ws = tiled ? mcv_w8a8_mlp_workspace_bytes(gate.K, gate.N) : 0;
+    mlp.one_launch = ws > 0;
+    if (mlp.one_launch) {
+        mlp.workspace = Tensor({ws}, DType::UInt8);
+        mlp.workspace.zero();
+    }
+    mlp.xq = Tensor({1, gate.K}, DType::Int8);
+    mlp.xs = Tensor({1}, DType::Float32);
+    mlp.act = Tensor({1, gate.N}, DType::Float16);
+    mlp.aq = Tensor({1, gate.N}, DType::Int8);
+    mlp.as = Tensor({1}, DType::Float32);
+    for (Tensor* t : {&mlp.xq, &mlp.xs, &mlp.act, &mlp.aq, &mlp.as}) t->allocate();
+    return mlp;
+}
+
+void mlp_w8a8(const Tensor& x, DecodeMlpW8A8& mlp, Tensor& out, hipStream_t stream) {
+    const W8A8QuantizedWeight &g = *mlp.gate, &u = *mlp.up, &d = *mlp.down;
+    require(x.dtype() == DType::Float16 && x.shape() == std::vector<int64_t>{1, g.K},
+            "decode MLP (W8A8) x must be fp16 [1, H]");
+    require(out.dtype() == DType::Float16 && out.shape() == std::vector<int64_t>{1, g.K},
+            "decode MLP (W8A8) out must be fp16 [1, H]");
+    if (mlp.one_launch) {
+        const int rc = mcv_w8a8_mlp(x.data(), g.K, g.N, static_cast<const int8_t*>(g.w_int8.data()),
+                                    static_cast<const float*>(g.w_scale_f32.data()),
+                                    static_cast<const int8_t*>(u.w_int8.data()),
+                                    static_cast<const float*>(u.w_scale_f32.data()),
+                                    static_cast<const int8_t*>(d.w_int8.data()),
+                                    static_cast<const float*>(d.w_scale_f32.data()), out.data(), mlp.workspace.data(),
+                                    stream);
+        if (rc != MCV_ERR_SHAPE) {
+            check_mcv(rc, "mlp_w8a8");
+            return;
+        }
+        mlp.one_launch = false;          // this shape or device cannot hold the one-launch grid
+    }
+    w8a8_quantize(x, mlp.xq, mlp.xs, stream);
+    mlp_gate_up_silu_w8a8(mlp.xq, mlp.xs, g, u, mlp.act, stream);
+    w8a8_quantize(mlp.act, mlp.aq, mlp.as, stream);
+    matmul_w8a8(mlp.aq, mlp.as, d, out, stream);
+}
+
 void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream) {
     require(acc.dtype() == DType::Int32 && out.dtype() == DType::Float16, "w8a8_dequant requires int32 acc and fp16 out");
     require(acc.shape().size() == 2, "w8a8_dequant acc must be [M, N]");

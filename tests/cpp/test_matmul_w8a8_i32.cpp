@@ -36,9 +36,43 @@ static int run(HipContext& ctx, int M, int K, int N, int lo, int hi, bool extrem
     return bad != 0;
 }
 
+// The W8A8 decode MLP block: one launch (tiled weights) == the four-launch
+// sequence over [K, N] weights, bit for bit (same int8 values and scales).
+static int run_mlp(HipContext& ctx, int H, int I) {
+    std::mt19937 rng(H + I);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    auto dense = [&](int K, int N, float sd) {
+        std::vector<uint16_t> h(static_cast<size_t>(K) * N);
+        for (auto& v : h) v = t::f2h(nd(rng) * sd);
+        Tensor w({K, N}, DType::Float16);
+        w.copy_from_host(h.data(), h.size() * 2);
+        return w;
+    };
+    Tensor gd = dense(H, I, 0.02f), ud = dense(H, I, 0.02f), dd = dense(I, H, 0.02f), xt = dense(1, H, 1.0f);
+    W8A8QuantizedWeight g = quantize_dense_weight_w8a8(gd), u = quantize_dense_weight_w8a8(ud),
+                        d = quantize_dense_weight_w8a8(dd);
+    DecodeMlpW8A8 one = make_decode_mlp_w8a8(g, u, d);
+    Tensor y1({1, H}, DType::Float16), y2({1, H}, DType::Float16);
+    y1.allocate();
+    y2.allocate();
+    for (int rep = 0; rep < 3; ++rep) mlp_w8a8(xt, one, y1, ctx.stream());
+    DecodeMlpW8A8 four = make_decode_mlp_w8a8(g, u, d);
+    four.one_launch = false;
+    mlp_w8a8(xt, four, y2, ctx.stream());
+    std::vector<uint16_t> h1(H), h2(H);
+    y1.copy_to_host(h1.data(), h1.size() * 2);
+    y2.copy_to_host(h2.data(), h2.size() * 2);
+    uint32_t err = 1;
+    one.workspace.copy_to_host(&err, 4);
+    std::printf("W8A8 decode MLP H=%d I=%d one_launch=%d bit-identical=%d give-up flag=%u\n", H, I,
+                one.one_launch ? 1 : 0, h1 == h2 ? 1 : 0, err);
+    return !(one.one_launch && h1 == h2 && err == 0);
+}
+
 int main() {
     HipContext ctx(0);
-    int rc = run(ctx, 1, 1024, 3584, -8, 7, false);
+    int rc = run_mlp(ctx, 1024, 3584);
+    rc |= run(ctx, 1, 1024, 3584, -8, 7, false);
     rc |= run(ctx, 256, 1024, 512, -128, 127, false);
     rc |= run(ctx, 4, 1024, 64, -128, 127, true);
     return rc;
