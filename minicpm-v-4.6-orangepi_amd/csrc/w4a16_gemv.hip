@@ -40,7 +40,7 @@ namespace {
 // CAS-combined (key, count) words 22-39 us, and the fence-free 64-slot
 // arrival tree this replaces (atomicMax, then slot and global counts, then a
 // read of the slot maxima) ~1.8 us: four device round trips.
-constexpr int kTreeWords = 64;                                // slots of the host-finished route
+constexpr int kSlotWords = 64;                                // slots of the host-finished route
 constexpr int kLmEpoch = 64;                                  // u32 index of the first call counter
 constexpr int kLmPollVec = 8;                                 // key words per lane per poll
 constexpr int kLmSpinLimit = 1 << 18;
@@ -185,6 +185,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
 // replayed): SPW 16 (243 workgroups) with the tree 26.9-27.2 us, with slots
 // 25.7-26.0 us; SPW 8 27.1-27.3 / 26.4-27.0 us; SPW 1-4 28-30 us; the former
 // one-slab, four-wave kernel ~27.9 us.  Direct launches run ~1 us faster.
+// 256 workgroups with 15 or 16 slabs each (no idle CU) measured the same as
+// 243 with 16 (28.7 against 28.6 us on one box).
 constexpr int kLmWaves = 8;
 constexpr int kLmTree = 0;
 constexpr int kLmSlots = 1;
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
             // index complement keeps its low 24 bits (V < 2^24)
             const unsigned long long k16 = best >> 32;
             const unsigned long long idx = best & 0xffffffull;
-            atomicMax(ws + (blockIdx.x & (kTreeWords - 1)) * kSlotStride,
+            atomicMax(ws + (blockIdx.x & (kSlotWords - 1)) * kSlotStride,
                       (static_cast<unsigned long long>(tag) << 40) | (k16 << 24) | (k16 ? idx : 0ull));
         }
     }
@@ -674,7 +676,7 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
                           static_cast<hipStream_t>(stream));
 }
 
-int64_t mcv_lm_head_slots_bytes(void) { return int64_t(kTreeWords) * kSlotStride * 8; }
+int64_t mcv_lm_head_slots_bytes(void) { return int64_t(kSlotWords) * kSlotStride * 8; }
 
 int mcv_w4a16_lm_head_argmax_slots(const void* x, int64_t K, int64_t N, int64_t V, const void* qw,
                                    const void* scales, const void* zeros, int zero_bias, void* logits, void* slots,
@@ -698,7 +700,7 @@ int mcv_w4a16_lm_head_argmax_slots(const void* x, int64_t K, int64_t N, int64_t 
 int64_t mcv_lm_head_slots_token(const uint64_t* slots_host, uint32_t tag) {
     if (!slots_host) return fail(MCV_ERR_INVALID_ARG, "mcv_lm_head_slots_token: null slots");
     uint64_t best = 0;
-    for (int j = 0; j < kTreeWords; ++j) {
+    for (int j = 0; j < kSlotWords; ++j) {
         const uint64_t k = slots_host[static_cast<size_t>(j) * kSlotStride];
         if ((k >> 40) != tag) continue;                                  // no workgroup of this call used slot j
         const uint64_t v = k & 0xffffffffffull;
