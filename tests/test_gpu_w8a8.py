@@ -272,3 +272,23 @@ def test_decode_mlp_block_one_launch(mcv, oracle, cuda, H, I):
     # value by one fp16 ulp and so a quantised act by one step
     assert np.abs(got - ref).max() <= 2e-2 and rel_l2(got, ref) <= 1e-3
     assert (_u16(out) == y_o).mean() > 0.9
+
+
+def test_decode_mlp_block_falls_back(mcv, oracle, cuda):
+    """H = 8320 does not fit the one-launch kernel's LDS x row: the object
+    runs the four launches and returns their result."""
+    torch = _torch()
+    rng = np.random.default_rng(77)
+    H, I = 8320, 128
+    wg = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
+    wu = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
+    wd = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (I, H), 0.02)))
+    mlp = mcv.DecodeMlpW8A8(wg, wu, wd)
+    assert not mlp.one_launch
+    xd = _f16_dev(f16_normal(rng, (1, H), 1.0))
+    out = mlp(xd)
+    xq, xs, _ = mcv.w8a8_quantize(xd)
+    aq, asc, _ = mcv.w8a8_quantize(mcv.mlp_gate_up_silu_w8a8(xq, xs, wg, wu))
+    want = mcv.matmul_w8a8(aq, asc, wd)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
