@@ -146,24 +146,43 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
     // lane's 32 columns' weight scales (zero past N) and its rows' x scales.
     // Transposed blocks: register r of lane l holds row 32 i + l%32 and column
     // 32 j + 8 (r/4) + 4 (l/32) + r%4.
+    // Buffer loads, so columns past N and rows past M read as zero with no
+    // branch, and all of them are issued before any is used (a branch per
+    // scale put a wait behind every fp16 load: 32 serial round trips).
     const int h = lane >> 5;
     float wsv[2][4][4];
     float xsv_all[C::MB];
     if constexpr (OUT_F16) {
+        const __amdgpu_buffer_rsrc_t wsr = rsrc(ws, static_cast<uint32_t>(N) * (ws16 ? 2u : 4u));
+        const __amdgpu_buffer_rsrc_t xsr = rsrc(xs, static_cast<uint32_t>(M) * (xs16 ? 2u : 4u));
+        uint32_t wraw[2][4][4], xraw[C::MB];
+        const uint32_t wsz = ws16 ? 2u : 4u, xsz = xs16 ? 2u : 4u;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int col = slab * kSlab + 32 * j + 8 * g + 4 * h + e;
-                    wsv[j][g][e] = col < N ? scale_at(ws, ws16, col) : 0.f;
+                    const uint32_t off = static_cast<uint32_t>(slab * kSlab + 32 * j + 8 * g + 4 * h + e) * wsz;
+                    wraw[j][g][e] = ws16 ? __builtin_amdgcn_raw_buffer_load_b16(wsr, off, 0, 0)
+                                         : __builtin_amdgcn_raw_buffer_load_b32(wsr, off, 0, 0);
                 }
 #pragma unroll
         for (int i = 0; i < C::MB; ++i) {
-            const int row = m0 + 32 * i + (lane & 31);
-            xsv_all[i] = row < M ? scale_at(xs, xs16, row) : 0.f;
+            const uint32_t off = static_cast<uint32_t>(m0 + 32 * i + (lane & 31)) * xsz;
+            xraw[i] = xs16 ? __builtin_amdgcn_raw_buffer_load_b16(xsr, off, 0, 0)
+                           : __builtin_amdgcn_raw_buffer_load_b32(xsr, off, 0, 0);
         }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    wsv[j][g][e] = ws16 ? h2f(static_cast<uint16_t>(wraw[j][g][e])) : __uint_as_float(wraw[j][g][e]);
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i)
+            xsv_all[i] = xs16 ? h2f(static_cast<uint16_t>(xraw[i])) : __uint_as_float(xraw[i]);
     }
 
     // Stage kt: weights from `cur`, x from LDS buffer kt&1.  During its k32
@@ -342,6 +361,23 @@ __global__ __launch_bounds__(64 * NW) void w8a8_tiled_gemv_kernel(
         for (int t = 0; t < NWT; ++t)
 #pragma unroll
             for (int jj = 0; jj < HALVES; ++jj) acc[m][t][jj] = 0;
+    // the epilogue's scales, loaded now so the tail does not wait for them:
+    // thread -> (row em, half ejj, column el of the half)
+    const int etid = threadIdx.x;
+    const int em = etid / (32 * HALVES), ejj = (etid >> 5) % HALVES, el = etid & 31;
+    const int en = slab * kSlab + 32 * (j0 + ejj) + el;
+    const bool eok = etid < 32 * HALVES * MR && em < M && en < N;
+    // raw bits now, converted in the epilogue (a conversion here would wait)
+    uint32_t r_xs = 0, r_ws = 0, r_ws2 = 0;
+    if constexpr (OUT_F16) {
+        if (eok) {
+            r_xs = xs16 ? static_cast<const uint16_t*>(xs)[em] : static_cast<const uint32_t*>(xs)[em];
+            r_ws = ws16 ? static_cast<const uint16_t*>(ws)[en] : static_cast<const uint32_t*>(ws)[en];
+            if constexpr (DUAL)
+                r_ws2 = ws16 ? static_cast<const uint16_t*>(ws2)[en] : static_cast<const uint32_t*>(ws2)[en];
+        }
+    }
+    auto bits_to_f = [](uint32_t r, int is16) { return is16 ? h2f(static_cast<uint16_t>(r)) : __uint_as_float(r); };
     for (int kb0 = wave; kb0 < KB; kb0 += NW * U) {
         int4_t wv[U][NWT][HALVES];
         int4_t xv[U][MR];
@@ -397,13 +433,14 @@ __global__ __launch_bounds__(64 * NW) void w8a8_tiled_gemv_kernel(
     const int n = slab * kSlab + 32 * (j0 + jj) + l;
     if (m >= M || n >= N) return;
     const size_t o = static_cast<size_t>(m) * N + n;
+    const float e_xs = bits_to_f(r_xs, xs16), e_ws = bits_to_f(r_ws, ws16);
     if constexpr (DUAL) {
-        const float xsv = scale_at(xs, xs16, m);
-        const uint16_t g16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[0]), scale_at(ws, ws16, n)), xsv));
-        const uint16_t u16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[1]), scale_at(ws2, ws16, n)), xsv));
+        const float e_ws2 = bits_to_f(r_ws2, ws16);
+        const uint16_t g16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[0]), e_ws), e_xs));
+        const uint16_t u16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[1]), e_ws2), e_xs));
         static_cast<uint16_t*>(out)[o] = silu_mul_f16(g16, u16);
     } else if constexpr (OUT_F16) {
-        const float v = __fmul_rn(__fmul_rn(static_cast<float>(sum[0]), scale_at(ws, ws16, n)), scale_at(xs, xs16, m));
+        const float v = __fmul_rn(__fmul_rn(static_cast<float>(sum[0]), e_ws), e_xs);
         static_cast<uint16_t*>(out)[o] = f2h(v);
     } else {
         static_cast<int32_t*>(out)[o] = sum[0];
