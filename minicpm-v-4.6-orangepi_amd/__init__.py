@@ -503,6 +503,7 @@ class LmHeadW4A16:
         self.workspace = torch.zeros(lib().mcv_lm_head_workspace_bytes(vocab), dtype=torch.uint8, device=dev)
         self.slots = torch.zeros(lib().mcv_lm_head_slots_bytes() // 8, dtype=torch.int64, device=dev)
         self.tag = 0
+        self._slots_stream = None                     # stream of the last slots launch (None: current)
         self.keys = torch.empty(-(-vocab // SLAB), dtype=torch.int64, device=dev)
         self.token = torch.zeros(1, dtype=torch.int64, device=dev)
 
@@ -522,13 +523,22 @@ class LmHeadW4A16:
                                               _dev(self.workspace), _stream(stream)), "mcv_w4a16_lm_head_argmax")
         return self.token
 
+    def _next_tag(self, stream) -> int:
+        """Tags must grow call by call; at the wrap the slots are zero-filled
+        again, on the launch stream so the fill is ordered with the calls."""
+        if self.tag >= self.TAG_MAX:
+            torch = _torch()
+            with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+                self.slots.zero_()
+            self.tag = 0
+        self.tag += 1
+        self._slots_stream = stream
+        return self.tag
+
     def launch_slots(self, x, logits=None, stream=None) -> int:
         """Stream-ordered: leaves this call's tagged maxima in self.slots; returns the tag."""
         self._check_io(x, logits)
-        if self.tag >= self.TAG_MAX:                  # tags must grow: start over from zero-filled slots
-            self.slots.zero_()
-            self.tag = 0
-        self.tag += 1
+        self._next_tag(stream)
         q, s, z = self.w.ptrs()
         _check(lib().mcv_w4a16_lm_head_argmax_slots(_dev(x), self.w.K, self.w.N, self.vocab, q, s, z,
                                                     self.w.zero_bias, _dev(logits) if logits is not None else 0,
@@ -558,15 +568,16 @@ class LmHeadW4A16:
         fn, slots = lib().mcv_w4a16_lm_head_argmax_slots, _dev(self.slots)
 
         def launch_slots():
-            if self.tag >= self.TAG_MAX:
-                self.slots.zero_()
-                self.tag = 0
-            self.tag += 1
-            _check(fn(*head, slots, self.tag, st), "mcv_w4a16_lm_head_argmax_slots")
-            return self.tag
+            tag = self._next_tag(stream)
+            _check(fn(*head, slots, tag, st), "mcv_w4a16_lm_head_argmax_slots")
+            return tag
         return launch_slots
 
     def read_slots_token(self, tag: int) -> int:
+        """The token of call `tag` from the slots (waits for the stream the
+        slots were last launched on, then copies them to the host)."""
+        if self._slots_stream is not None:
+            self._slots_stream.synchronize()
         host = np.ascontiguousarray(self.slots.cpu().numpy())      # synchronising copy
         return int(lib().mcv_lm_head_slots_token(_np_ptr(host), tag))
 

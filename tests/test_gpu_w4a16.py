@@ -384,3 +384,23 @@ def test_lm_head_bound_launchers(mcv, oracle, cuda):
         head.bind(x, lb, route="both")
     with pytest.raises(mcv.McvError):
         head.bind(x, torch.empty(V - 1, dtype=torch.float16, device="cuda"))
+
+
+def test_lm_head_slots_on_side_stream(mcv, oracle, cuda):
+    """Slot launches on a non-current stream, including the zero-fill at the
+    tag wrap: read_slots_token waits for that stream before it copies."""
+    torch = _torch()
+    K, V = 512, 5000
+    rng = np.random.default_rng(17)
+    qweight, qzeros, scales = mcv.quantize_int4(f16_normal(rng, (K, V), 0.02))
+    head = mcv.LmHeadW4A16(_dev_weight(mcv, qweight, qzeros, scales), V)
+    xs = [_to_dev(f16_normal(rng, (1, K), 1.0)) for _ in range(2)]
+    want = [int(head.launch(x).item()) for x in xs]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    head.tag = head.TAG_MAX - 2
+    for i in range(4):                                # crosses the wrap at the third call
+        tag = head.launch_slots(xs[i % 2], stream=side)
+        assert head.read_slots_token(tag) == want[i % 2]
+    bound = head.bind(xs[1], stream=side, route="slots")
+    assert head.read_slots_token(bound()) == want[1]
