@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void w4a16_mlp_kernel(const uint16_
     uint32_t zv = 0;
     if (present) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) wv[c] = dc.q[static_cast<size_t>(g * 4 + c) * kSlab];
+        for (int c = 0; c < 4; ++c) wv[c] = load_weights(dc.q + static_cast<size_t>(g * 4 + c) * kSlab);
         sv = dc.s[static_cast<size_t>(g) * dc.npad];
         zv = dc.z[static_cast<size_t>(g) * (dc.npad >> 3)];
     }

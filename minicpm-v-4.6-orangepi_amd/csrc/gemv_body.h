@@ -17,6 +17,17 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t smask, uint32_t 
     return r;
 }
 
+// One 16-byte chunk of packed weights.  Every weight byte is read once per
+// call, so the loads are non-temporal: on MI355X this took the streaming
+// lm_head from 26.7 to 24.8 us per step (A/B, one box) -- the weight stream
+// no longer displaces the scales, zeros and activations it shares the caches
+// with.
+__device__ __forceinline__ uint4 load_weights(const uint4* p) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 // The group's 128 activation values as 64 half2 words.  The index is
 // wave-uniform, so these become scalar loads into SGPRs.
 __device__ __forceinline__ void load_x_group(const uint32_t* __restrict__ xw, int g, uint32_t (&xs)[64]) {
@@ -94,9 +105,9 @@ __device__ __forceinline__ void gate_up_partials(const uint32_t* __restrict__ xw
     for (int g = g0; g < G; g += step) {
         uint4 wgv[4], wuv[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) wgv[c] = gc.q[static_cast<size_t>(g * 4 + c) * kSlab];
+        for (int c = 0; c < 4; ++c) wgv[c] = load_weights(gc.q + static_cast<size_t>(g * 4 + c) * kSlab);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) wuv[c] = uc.q[static_cast<size_t>(g * 4 + c) * kSlab];
+        for (int c = 0; c < 4; ++c) wuv[c] = load_weights(uc.q + static_cast<size_t>(g * 4 + c) * kSlab);
         const uint16_t sgv = gc.s[static_cast<size_t>(g) * gc.npad], suv = uc.s[static_cast<size_t>(g) * uc.npad];
         const uint32_t zgv = gc.z[static_cast<size_t>(g) * (gc.npad >> 3)];
         const uint32_t zuv = uc.z[static_cast<size_t>(g) * (uc.npad >> 3)];

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
             const int g = gb + i;
             if (g < G) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) wv[i][c] = wp[static_cast<size_t>(g * 4 + c) * kSlab];
+                for (int c = 0; c < 4; ++c) wv[i][c] = load_weights(wp + static_cast<size_t>(g * 4 + c) * kSlab);
                 sv[i] = sp[static_cast<size_t>(g) * Npad];
                 zv[i] = zp[static_cast<size_t>(g) * zstride];
             }
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     auto issue = [&](uint4 (&wv)[4], uint16_t& sv, uint32_t& zv, int slab, int g) {
         const uint4* __restrict__ p = wbase + (static_cast<size_t>(slab) * C + g * 4) * kSlab;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) wv[c] = p[c * kSlab];
+        for (int c = 0; c < 4; ++c) wv[c] = load_weights(p + c * kSlab);
         sv = sbase[static_cast<size_t>(g) * Npad + slab * kSlab];
         zv = zbase[static_cast<size_t>(g) * zstride + slab * (kSlab / 8)];
     };
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_multi_kernel(const uin
     for (int g = wave; g < G; g += KSPLIT) {
         uint4 wv[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) wv[c] = wp[static_cast<size_t>(g * 4 + c) * kSlab];
+        for (int c = 0; c < 4; ++c) wv[c] = load_weights(wp + static_cast<size_t>(g * 4 + c) * kSlab);
         const uint16_t sv = P.scales[static_cast<size_t>(g) * P.Npad + n];
         const uint32_t zv = P.zeros[static_cast<size_t>(g) * zstride + (n >> 3)];
         uint32_t xs[64];
