@@ -338,8 +338,8 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
                 const int kb = kb0 + u * kW8Waves;
                 const uint32_t off =
                     kb < KB1 ? ((static_cast<uint32_t>(slab) * KB1 + kb) * 2 + j) * kW8Line + lane * 16u : kNowhere;
-                wgv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
-                wuv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0));
+                wgv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 2));
+                wuv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 2));
             }
         };
         // x as fp16 pairs, all loads issued at once and ahead of the weights
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
         const int kb = kb_beg + wave + u * kW8Waves;
         const uint32_t off =
             kb < kb_end ? ((static_cast<uint32_t>(slab) * KB2 + kb) * 2 + j) * kW8Line + lane * 16u : kNowhere;
-        wdv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, 0));
+        wdv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, 2));
     }
     const int ncol = slab * 64 + 32 * j + (lane & 31);
     const float sdv = p == 0 && wave == 0 && ncol < H ? sd[ncol] : 0.f;

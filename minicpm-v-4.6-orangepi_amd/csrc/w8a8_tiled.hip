@@ -391,7 +391,7 @@ __global__ __launch_bounds__(64 * NW) void w8a8_tiled_gemv_kernel(
                 for (int jj = 0; jj < HALVES; ++jj) {
                     const uint32_t off =
                         live ? ((static_cast<uint32_t>(slab) * KB + kb) * 2 + j0 + jj) * kW8Block + lane * 16u : kNowhere;
-                    wv[u][t][jj] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(wr[t], off, 0, 0));
+                    wv[u][t][jj] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(wr[t], off, 0, 2));
                 }
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
