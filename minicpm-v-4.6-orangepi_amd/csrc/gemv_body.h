@@ -18,10 +18,11 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t smask, uint32_t 
 }
 
 // One 16-byte chunk of packed weights.  Every weight byte is read once per
-// call, so the loads are non-temporal: on MI355X this took the streaming
-// lm_head from 26.7 to 24.8 us per step (A/B, one box) -- the weight stream
-// no longer displaces the scales, zeros and activations it shares the caches
-// with.
+// call, so the loads are non-temporal.  Measured on MI355X (same-box A/B):
+// with the weights streamed from HBM, as in a decode step whose layers and
+// lm_head together exceed the 256 MB MALL, the lm_head step went from 26.7 to
+// 24.8 us and the K=N=1024 GEMV from 3.20 to 2.99 us; with a working set that
+// fits the MALL the GEMVs are 0.2-0.4 us slower than with ordinary loads.
 __device__ __forceinline__ uint4 load_weights(const uint4* p) {
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
