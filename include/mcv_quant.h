@@ -167,15 +167,21 @@ int mcv_w4a16_gate_up_silu(const void* x_dev, int64_t M, int64_t K, int64_t N,
  * kernel through `workspace_dev` (per-workgroup call counters and call-tagged
  * words): mcv_w4a16_mlp_workspace_bytes(H, I) bytes, 256-byte aligned,
  * zero-filled once before the first call; one workspace serves one (H, I)
- * shape, and calls sharing it must not overlap.  The u32 at byte 0 of the
- * workspace becomes non-zero if a wait for another workgroup's words ever gave
- * up (after ~0.3 s; the output of that call is then undefined). */
+ * shape, and calls sharing it must not overlap.  Every wait is bounded: if a
+ * wait for another workgroup's words gives up (after ~0.3 s -- e.g. another
+ * stream's kernels kept part of the grid from being resident), the u32 at
+ * byte 0 of the workspace becomes non-zero, and so does `*status` when status
+ * is not NULL, and the output of that call is undefined.  status may point to
+ * host-mapped pinned memory (hipHostMalloc + hipHostGetDevicePointer), where
+ * the host sees a give-up without synchronising.  After a give-up the
+ * workspace must be zero-filled again before the next call. */
 int64_t mcv_w4a16_mlp_workspace_bytes(int64_t H, int64_t I);
 int mcv_w4a16_mlp(const void* x_dev, int64_t H, int64_t I,
                   const void* qw_gate_dev, const void* scales_gate_dev, const void* zeros_gate_dev, int zero_bias_gate,
                   const void* qw_up_dev, const void* scales_up_dev, const void* zeros_up_dev, int zero_bias_up,
                   const void* qw_down_dev, const void* scales_down_dev, const void* zeros_down_dev,
-                  int zero_bias_down, void* out_dev, void* workspace_dev, mcv_stream_t stream);
+                  int zero_bias_down, void* out_dev, void* workspace_dev, uint32_t* status,
+                  mcv_stream_t stream);
 
 /* Materialise dequantised weights: w_f16_kn [K][N] = fp16 RNE((q - z) * s)
  * and/or w8_kn [K][N] = q - z (int8), either may be NULL.  The int8 form is
@@ -215,8 +221,9 @@ int mcv_w4a16_gemv_multi(const void* x_dev, int64_t M, int64_t K, const mcv_w4a1
  * its first use.  It holds per-workgroup call counters and the call-tagged key
  * words of the fused argmax, which every call keeps consistent; one workspace
  * serves one V, and calls sharing it must not overlap.  The u32 at byte 0
- * turns non-zero if the wait for the keys ever gave up (~40 ms; that call's
- * token is then undefined).  Returns 0 for an unsupported V. */
+ * turns non-zero if the wait for the keys ever gave up (~40 ms); that call's
+ * token is then -1, and the workspace must be zero-filled again before the
+ * next call.  Returns 0 for an unsupported V. */
 int64_t mcv_lm_head_workspace_bytes(int64_t V);
 
 /* Greedy lm_head over a W4A16 weight: logits[v] = x . W[:, v] (fp16 RNE of the
@@ -229,11 +236,13 @@ int64_t mcv_lm_head_workspace_bytes(int64_t V);
  * (src/csrc/lib/language_model.cpp:412-482) with one kernel: each workgroup
  * of the GEMV publishes its best (value, index) as one call-tagged word in the
  * workspace, and the grid's last workgroup waits until all carry this call's
- * tag, takes the maximum and writes the token. */
+ * tag, takes the maximum and writes the token.  If that bounded wait gives up
+ * the token is -1, the workspace's give-up word is set and so is `*status`
+ * (may be NULL; host-mapped pinned memory works, as for mcv_w4a16_mlp). */
 int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
                              const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                              int zero_bias, void* logits_dev, int64_t* token_dev,
-                             void* workspace_dev, mcv_stream_t stream);
+                             void* workspace_dev, uint32_t* status, mcv_stream_t stream);
 
 /* The greedy lm_head with the last step of the argmax left to the reader of
  * the token, for callers that copy the token to the host anyway (the
@@ -318,20 +327,25 @@ int mcv_w8a8_gemm_f16(const int8_t* xq_dev, const void* x_scale_dev, int x_scale
 /* The whole W8A8 decode MLP block, M = 1, in one launch, from the normed fp16
  * row x [1][H]: quantise x, gate and up int8 GEMVs with the fused epilogue,
  * silu * mul, quantise the act row, the down int8 GEMV with its epilogue ->
- * out fp16 [1][H].  Bit-identical to mcv_w8a8_quantize_act,
- * mcv_w8a8_gate_up_silu, mcv_w8a8_quantize_act, mcv_w8a8_gemm_f16 with fp32
- * scales (the decoder layers' W8A8 MLP sequence,
+ * out fp16 [1][H] (the decoder layers' W8A8 MLP sequence,
  * src/csrc/lib/decoder_layer.cpp:1022-1046).  Weights are MCV_W8_TILED
- * (gate/up H x I, down I x H) with fp32 per-channel scales; H <= 8192, I <= 16384, H and
- * I multiples of 128.  Values pass between workgroups through `workspace_dev`
+ * (gate/up H x I, down I x H); H <= 8192, I <= 16384, H and I multiples of 128.
+ * scale_dtype MCV_F16: the weight scales are the reference's fp16 w_scale
+ * (truncating encode) and every epilogue uses the activation scale rounded to
+ * fp16, as the reference's w8a8_quantize stores it -- bit-identical to
+ * mcv_w8a8_quantize_act, mcv_w8a8_gate_up_silu, mcv_w8a8_quantize_act,
+ * mcv_w8a8_gemm_f16 with fp16 scales, i.e. the reference's precision.
+ * MCV_F32: fp32 weight and activation scales throughout (the same sequence
+ * with fp32 scales).  Values pass between workgroups through `workspace_dev`
  * (mcv_w8a8_mlp_workspace_bytes(H, I) bytes, 256-byte aligned, zero-filled
- * once; one shape per workspace; calls sharing it must not overlap; the u32
- * at byte 0 turns non-zero if a wait ever gave up).  MCV_ERR_SHAPE when the
- * launch would not fit on the device at once. */
+ * once; one shape per workspace; calls sharing it must not overlap); waits
+ * give up as in mcv_w4a16_mlp, flagging the workspace's u32 at byte 0 and
+ * `*status` (may be NULL).  MCV_ERR_SHAPE when the launch would not fit on
+ * the device at once. */
 int64_t mcv_w8a8_mlp_workspace_bytes(int64_t H, int64_t I);
-int mcv_w8a8_mlp(const void* x_dev, int64_t H, int64_t I, const int8_t* w_gate_dev, const float* ws_gate_dev,
-                 const int8_t* w_up_dev, const float* ws_up_dev, const int8_t* w_down_dev, const float* ws_down_dev,
-                 void* out_dev, void* workspace_dev, mcv_stream_t stream);
+int mcv_w8a8_mlp(const void* x_dev, int64_t H, int64_t I, const int8_t* w_gate_dev, const void* ws_gate_dev,
+                 const int8_t* w_up_dev, const void* ws_up_dev, const int8_t* w_down_dev, const void* ws_down_dev,
+                 int scale_dtype, void* out_dev, void* workspace_dev, uint32_t* status, mcv_stream_t stream);
 
 /* Decode MLP front half over W8A8 weights: act[M][N] fp16 = silu(gate) * up,
  * gate and up each the fused epilogue of mcv_w8a8_gemm_f16 over the same

@@ -66,10 +66,11 @@ _SIGS = {
     "mcv_w4a16_gemv_multi": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp]),
     "mcv_w4a16_mlp_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "mcv_w4a16_mlp": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int,
-                               _vp, _vp, _vp]),
+                               _vp, _vp, _vp, _vp]),
     "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "mcv_lm_head_workspace_bytes": (_c_i64, [_c_i64]),
-    "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
+    "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp,
+                                          _vp]),
     "mcv_lm_head_slots_bytes": (_c_i64, []),
     "mcv_w4a16_lm_head_argmax_slots": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp,
                                                 ctypes.c_uint32, _vp]),
@@ -86,7 +87,7 @@ _SIGS = {
                                        _vp]),
     "mcv_w8a8_pack_tiled_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "mcv_w8a8_mlp_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
-    "mcv_w8a8_mlp": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mcv_w8a8_mlp": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
     "mcv_w8a8_quantize_weight_nk_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_pack_tiled_nk_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
@@ -416,7 +417,7 @@ class DecodeMlpW4A16:
             raise McvError(f"decode MLP: out must be contiguous fp16 [1, {self.H}]")
         g, u, d = self.gate, self.up, self.down
         return ((_dev(x), self.H, self.I) + g.ptrs() + (g.zero_bias,) + u.ptrs() + (u.zero_bias,) + d.ptrs()
-                + (d.zero_bias, _dev(out), _dev(self.workspace), _stream(stream)))
+                + (d.zero_bias, _dev(out), _dev(self.workspace), None, _stream(stream)))
 
     def _two_launches(self, x, out, stream):
         mlp_gate_up_silu_w4a16(x.view(1, self.H), self.gate, self.up, self.act, stream)
@@ -520,7 +521,7 @@ class LmHeadW4A16:
         q, s, z = self.w.ptrs()
         _check(lib().mcv_w4a16_lm_head_argmax(_dev(x), self.w.K, self.w.N, self.vocab, q, s, z, self.w.zero_bias,
                                               _dev(logits) if logits is not None else 0, _dev(self.token),
-                                              _dev(self.workspace), _stream(stream)), "mcv_w4a16_lm_head_argmax")
+                                              _dev(self.workspace), None, _stream(stream)), "mcv_w4a16_lm_head_argmax")
         return self.token
 
     def _next_tag(self, stream) -> int:
@@ -557,7 +558,7 @@ class LmHeadW4A16:
                 _dev(logits) if logits is not None else 0)
         st = _stream(stream)
         if route == "tree":
-            fn, args = lib().mcv_w4a16_lm_head_argmax, head + (_dev(self.token), _dev(self.workspace), st)
+            fn, args = lib().mcv_w4a16_lm_head_argmax, head + (_dev(self.token), _dev(self.workspace), None, st)
 
             def launch():
                 _check(fn(*args), "mcv_w4a16_lm_head_argmax")
@@ -623,18 +624,27 @@ def quantize_dense_weight_w8a8(weight_kn, layout: int = W8_TILED) -> W8A8Quantiz
                                torch.from_numpy(s32).to(dev), K, N, layout)
 
 
+_NO_F32 = object()     # w8a8_quantize(x_scale=_NO_F32): write only the fp16 scale
+
+
 def w8a8_quantize(x, x_int8=None, x_scale=None, x_scale_f16=None, stream=None):
     """Per-row activation quant (ops.cpp:1135-1171 generalised to M rows).
-    Returns (x_int8 [M, K], x_scale fp32 [M], x_scale_f16 [M] or None)."""
+    Returns (x_int8 [M, K], x_scale fp32 [M] or None, x_scale_f16 [M] or None);
+    the fp16 scale is the RNE encoding of the fp32 one, the reference's stored
+    form.  x_scale=_NO_F32 skips the fp32 scale (x_scale_f16 is then required)."""
     torch = _torch()
     if x.dtype != torch.float16 or x.dim() != 2 or not x.is_contiguous():
         raise McvError("w8a8_quantize x must be contiguous fp16 [M, K]")
     M, K = x.shape
     if x_int8 is None:
         x_int8 = torch.empty((M, K), dtype=torch.int8, device=x.device)
-    if x_scale is None:
+    if x_scale is _NO_F32:
+        x_scale = None
+        if x_scale_f16 is None:
+            raise McvError("w8a8_quantize: needs an fp32 or an fp16 scale output")
+    elif x_scale is None:
         x_scale = torch.empty(M, dtype=torch.float32, device=x.device)
-    _check(lib().mcv_w8a8_quantize_act(_dev(x), M, K, _dev(x_int8), _dev(x_scale),
+    _check(lib().mcv_w8a8_quantize_act(_dev(x), M, K, _dev(x_int8), _dev(x_scale) if x_scale is not None else 0,
                                        _dev(x_scale_f16) if x_scale_f16 is not None else 0, _stream(stream)),
            "w8a8_quantize")
     return x_int8, x_scale, x_scale_f16
@@ -693,33 +703,53 @@ def matmul_w8a8(x_int8, x_scale, w: W8A8QuantizedWeight, out=None, use_f32_scale
 
 class DecodeMlpW8A8:
     """The whole W8A8 decode MLP block, M = 1, in one launch from the normed
-    fp16 row: out[H] = deq(quant(silu(deq(quant(x) . gate)) * deq(quant(x) . up)) . down),
-    bit-identical to w8a8_quantize, mlp_gate_up_silu_w8a8, w8a8_quantize and
-    matmul_w8a8 with fp32 scales (decoder_layer.cpp:1022-1046); those four
-    launches where the one-launch grid does not fit (one_launch turns False).
-    Weights must be MCV_W8_TILED.  Calls on one object must not overlap."""
+    fp16 row: out[H] = deq(quant(silu(deq(quant(x) . gate)) * deq(quant(x) . up)) . down)
+    (decoder_layer.cpp:1022-1046), bit-identical to w8a8_quantize,
+    mlp_gate_up_silu_w8a8, w8a8_quantize and matmul_w8a8 with the same
+    scales; those four launches where the one-launch grid does not fit
+    (one_launch turns False).  precision "reference" (default): the fp16
+    activation scale and the truncated fp16 weight scale in every epilogue, as
+    the reference's dispatcher stores and reads them (decoder_layer.cpp:216-237);
+    "f32": fp32 scales throughout (BASELINE config 5's precision).  Weights
+    must be MCV_W8_TILED.  Calls on one object must not overlap."""
 
     ERROR_WORD = 0
     _ERR_SHAPE = 2
 
-    def __init__(self, gate: "W8A8QuantizedWeight", up: "W8A8QuantizedWeight", down: "W8A8QuantizedWeight"):
+    def __init__(self, gate: "W8A8QuantizedWeight", up: "W8A8QuantizedWeight", down: "W8A8QuantizedWeight",
+                 precision: str = "reference"):
         torch = _torch()
         if (up.K, up.N) != (gate.K, gate.N) or (down.K, down.N) != (gate.N, gate.K):
             raise McvError("decode MLP (W8A8): gate/up must be [H, I] and down [I, H]")
         if any(w.layout != W8_TILED for w in (gate, up, down)):
             raise McvError("decode MLP (W8A8): weights must be in the tiled layout")
+        if precision not in ("reference", "f32"):
+            raise McvError(f"decode MLP (W8A8): precision must be 'reference' or 'f32', got {precision!r}")
         self.gate, self.up, self.down = gate, up, down
         self.H, self.I = gate.K, gate.N
+        self.f32 = precision == "f32"
         dev = gate.w_int8.device
         nbytes = lib().mcv_w8a8_mlp_workspace_bytes(self.H, self.I)
         self.one_launch = nbytes > 0
         self.workspace = torch.zeros(max(nbytes, 4) // 4, dtype=torch.int32, device=dev)
 
+    def _scales(self, w):
+        return w.w_scale_f32 if self.f32 else w.w_scale
+
+    def _quant(self, x, stream):
+        torch = _torch()
+        if self.f32:
+            xq, xs, _ = w8a8_quantize(x, stream=stream)
+            return xq, xs
+        s16 = torch.empty(x.shape[0], dtype=torch.float16, device=x.device)
+        xq, _, s16 = w8a8_quantize(x, x_scale=_NO_F32, x_scale_f16=s16, stream=stream)
+        return xq, s16
+
     def _four_launches(self, x, out, stream):
-        xq, xs, _ = w8a8_quantize(x.view(1, self.H), stream=stream)
-        act = mlp_gate_up_silu_w8a8(xq, xs, self.gate, self.up, stream=stream)
-        aq, asc, _ = w8a8_quantize(act, stream=stream)
-        matmul_w8a8(aq, asc, self.down, out.view(1, self.H), stream=stream)
+        xq, xs = self._quant(x.view(1, self.H), stream)
+        act = mlp_gate_up_silu_w8a8(xq, xs, self.gate, self.up, use_f32_scale=self.f32, stream=stream)
+        aq, asc = self._quant(act, stream)
+        matmul_w8a8(aq, asc, self.down, out.view(1, self.H), use_f32_scale=self.f32, stream=stream)
 
     def __call__(self, x, out=None, stream=None):
         torch = _torch()
@@ -731,9 +761,10 @@ class DecodeMlpW8A8:
             raise McvError(f"decode MLP (W8A8): out must be contiguous fp16 [1, {self.H}]")
         if self.one_launch:
             g, u, d = self.gate, self.up, self.down
-            rc = lib().mcv_w8a8_mlp(_dev(x), self.H, self.I, _dev(g.w_int8), _dev(g.w_scale_f32), _dev(u.w_int8),
-                                    _dev(u.w_scale_f32), _dev(d.w_int8), _dev(d.w_scale_f32), _dev(out),
-                                    _dev(self.workspace), _stream(stream))
+            rc = lib().mcv_w8a8_mlp(_dev(x), self.H, self.I, _dev(g.w_int8), _dev(self._scales(g)), _dev(u.w_int8),
+                                    _dev(self._scales(u)), _dev(d.w_int8), _dev(self._scales(d)),
+                                    MCV_F32 if self.f32 else MCV_F16, _dev(out), _dev(self.workspace), None,
+                                    _stream(stream))
             if rc != self._ERR_SHAPE:
                 _check(rc, "mcv_w8a8_mlp")
                 return out

@@ -99,16 +99,23 @@ def build_cpp_layer(jobs: int | None = None) -> Path:
 
 
 def build_cpp_tests(jobs: int | None = None) -> list[Path]:
-    """Compile tests/cpp/*.cpp into tests/cpp/bin/ against the C++ layer."""
+    """Compile tests/cpp/*.cpp into tests/cpp/bin/ against the C++ layer.  The
+    test programs also link the CPU oracle (oracle/build/libmcv_oracle.so, test
+    infrastructure) as their checker; the product libraries never do."""
     tdir = ROOT / "tests" / "cpp"
     srcs = sorted(tdir.glob("test_*.cpp"))
     bindir = tdir / "bin"
     bindir.mkdir(parents=True, exist_ok=True)
+    oracle = ROOT / "oracle"
+    if not (oracle / "build" / "libmcv_oracle.so").exists():
+        _run(["make", "-C", str(oracle)])
 
     def one(src: Path) -> Path:
         exe = bindir / src.stem
-        _run(["g++", *CXX_FLAGS, str(src), "-o", str(exe), f"-L{LIB}", "-lminicpmv_ops", "-lmcv_quant",
-              "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../../minicpm-v-4.6-orangepi_amd/lib", "-Wl,-rpath,/opt/rocm/lib"])
+        _run(["g++", *CXX_FLAGS, f"-I{oracle}", str(src), "-o", str(exe), f"-L{LIB}", "-lminicpmv_ops", "-lmcv_quant",
+              f"-L{oracle / 'build'}", "-lmcv_oracle", "-L/opt/rocm/lib", "-lamdhip64",
+              "-Wl,-rpath,$ORIGIN/../../../minicpm-v-4.6-orangepi_amd/lib", "-Wl,-rpath,$ORIGIN/../../../oracle/build",
+              "-Wl,-rpath,/opt/rocm/lib"])
         return exe
 
     if not srcs:

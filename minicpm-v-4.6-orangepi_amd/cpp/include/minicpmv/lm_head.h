@@ -3,9 +3,11 @@
 // Replaces lm_head_greedy (src/csrc/lib/language_model.cpp:412-482): final
 // RMSNorm, then -- instead of 16 chunk matmuls, 16 blocking D2H copies and a
 // host scan -- one GEMV with the argmax folded into it.  Same tie rule: the
-// first maximum wins, fp16 subnormals compare as zero, NaN never wins.
+// first maximum wins, fp16 subnormals compare as zero, NaN never wins.  The
+// head objects own every buffer a call needs, so calls allocate nothing.
 #pragma once
 
+#include "minicpmv/hip_context.h"
 #include "minicpmv/quantized_weight.h"
 #include "minicpmv/tensor.h"
 
@@ -21,13 +23,20 @@ struct LmHeadW4A16 {
     Tensor workspace;              // zero-filled once; calls keep its counters and tagged keys consistent
     Tensor token;                  // Int64 [1]
     Tensor slots;                  // tagged slot maxima of the host-finished argmax
+    Tensor normed;                 // Float16 [1, hidden]: the final RMSNorm's output
+    WaitStatus status;             // set by the device-token route if its bounded wait gave up
     uint32_t tag{0};               // tag of the last slots call
 };
 
 LmHeadW4A16 make_lm_head_w4a16(W4A16QuantizedWeight weight, int64_t vocab);
 
 // Stream-ordered: token and (optional, fp16 [1, vocab]) logits on the device.
+// Throws (after re-zeroing the workspace, which synchronises `stream`) if an
+// earlier call's wait for the workgroups' keys gave up.
 void lm_head_argmax_w4a16(const Tensor& hidden_1xH, LmHeadW4A16& head, Tensor* logits, hipStream_t stream);
+// Copies the device token to the host (synchronises `stream`); throws if the
+// call that wrote it gave up waiting (token -1).
+int64_t lm_head_read_token(LmHeadW4A16& head, hipStream_t stream);
 
 // Stream-ordered, host-finished argmax: the GEMV leaves call-tagged maxima in
 // head.slots (no device round trip at the end of the kernel); returns the tag
@@ -42,9 +51,21 @@ int64_t lm_head_read_slots_token(const LmHeadW4A16& head, uint32_t tag, hipStrea
 int64_t lm_head_greedy_w4a16(const Tensor& last_hidden_1xH, const Tensor* final_norm, double rms_epsilon,
                              LmHeadW4A16& head, hipStream_t stream);
 
-// W8A8 variant (language_model.cpp:434-467): one activation quantisation, the
-// fused int8 GEMM over [hidden, vocab], argmax on the device.
+// The W8A8 lm_head (language_model.cpp:434-467) with the reference's
+// precision: one activation quantisation with its fp16 scale, the fused int8
+// GEMV with the truncated fp16 weight scale, the first-maximum argmax on the
+// device.  The weight stays owned by the caller.
+struct LmHeadW8A8 {
+    const W8A8QuantizedWeight* weight{nullptr};   // [hidden, >= vocab]
+    int64_t vocab{0};
+    Tensor normed;                 // Float16 [1, hidden]
+    Tensor xq;                     // Int8 [1, hidden]
+    Tensor xs;                     // Float16 [1]
+    Tensor logits;                 // Float16 [1, weight N]
+    Tensor token;                  // Int64 [1]
+};
+LmHeadW8A8 make_lm_head_w8a8(const W8A8QuantizedWeight& weight, int64_t vocab);
 int64_t lm_head_greedy_w8a8(const Tensor& last_hidden_1xH, const Tensor* final_norm, double rms_epsilon,
-                            const W8A8QuantizedWeight& head, int64_t vocab, hipStream_t stream);
+                            LmHeadW8A8& head, hipStream_t stream);
 
 }  // namespace minicpmv

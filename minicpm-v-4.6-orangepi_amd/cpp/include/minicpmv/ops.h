@@ -12,6 +12,7 @@
 // M; scales may be fp16 or fp32.
 #pragma once
 
+#include "minicpmv/hip_context.h"
 #include "minicpmv/quantized_weight.h"
 #include "minicpmv/tensor.h"
 
@@ -45,17 +46,25 @@ void mlp_gate_up_silu_w4a16(const Tensor& x, const W4A16QuantizedWeight& gate, c
 // (decoder_layer.cpp:1029-1046), bit-identical to mlp_gate_up_silu_w4a16 +
 // matmul_w4a16.  One launch (mcv_w4a16_mlp) where the shape allows, else those
 // two launches.  The weights stay owned by the caller and must outlive it.
+// The one-launch kernel's waits are bounded; a give-up sets `status`, which
+// mlp_w4a16 checks at every call (a plain host read, no synchronisation) and
+// check_wait_status at the caller's own synchronisation points: both throw.
 struct DecodeMlpW4A16 {
     const W4A16QuantizedWeight* gate{nullptr};   // [H, I]
     const W4A16QuantizedWeight* up{nullptr};     // [H, I]
     const W4A16QuantizedWeight* down{nullptr};   // [I, H]
     Tensor workspace;                            // zero-filled once; one stream at a time
     Tensor act;                                  // fp16 [1, I], for the two-launch path
+    WaitStatus status;                           // host-mapped give-up word of the one-launch kernel
     bool one_launch{true};
 };
 DecodeMlpW4A16 make_decode_mlp_w4a16(const W4A16QuantizedWeight& gate, const W4A16QuantizedWeight& up,
                                      const W4A16QuantizedWeight& down);
 void mlp_w4a16(const Tensor& x, DecodeMlpW4A16& mlp, Tensor& out, hipStream_t stream);
+// Throws if a wait of an earlier one-launch call gave up (that call's output
+// is undefined).  Before throwing it drains `stream` and re-zeroes the
+// workspace, so the object works again afterwards.
+void check_wait_status(DecodeMlpW4A16& mlp, hipStream_t stream);
 
 // int32 out [M, N] = int8 x [M, K] . int8 w [K, N], exact.
 void matmul_w8a8_i32(const Tensor& x, const Tensor& w_int8, Tensor& out, hipStream_t stream);
@@ -84,20 +93,26 @@ void mlp_gate_up_silu_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8
                            const W8A8QuantizedWeight& up, Tensor& act, hipStream_t stream);
 
 // The whole W8A8 decode MLP block, M = 1, from the normed fp16 row:
-// w8a8_quantize, mlp_gate_up_silu_w8a8, w8a8_quantize, matmul_w8a8 with fp32
-// scales (decoder_layer.cpp:1022-1046), bit-identical; one launch
-// (mcv_w8a8_mlp) for tiled weights where the grid fits, else those four.
+// w8a8_quantize, mlp_gate_up_silu_w8a8, w8a8_quantize, matmul_w8a8
+// (decoder_layer.cpp:1022-1046), bit-identical; one launch (mcv_w8a8_mlp)
+// for tiled weights where the grid fits, else those four.  By default every
+// epilogue uses the fp16 activation scale and the truncated fp16 weight
+// scale, the reference's precision (decoder_layer.cpp:216-237); f32_scales
+// selects fp32 scales throughout.  Give-ups are reported as for DecodeMlpW4A16.
 struct DecodeMlpW8A8 {
     const W8A8QuantizedWeight* gate{nullptr};    // [H, I]
     const W8A8QuantizedWeight* up{nullptr};      // [H, I]
     const W8A8QuantizedWeight* down{nullptr};    // [I, H]
     Tensor workspace;                            // zero-filled once; one stream at a time
-    Tensor xq, xs, act, aq, as;                  // buffers of the four-launch path
+    Tensor xq, xs, act, aq, as;                  // buffers of the four-launch path (scales fp16 or fp32)
+    WaitStatus status;                           // host-mapped give-up word of the one-launch kernel
+    bool f32_scales{false};
     bool one_launch{true};
 };
 DecodeMlpW8A8 make_decode_mlp_w8a8(const W8A8QuantizedWeight& gate, const W8A8QuantizedWeight& up,
-                                   const W8A8QuantizedWeight& down);
+                                   const W8A8QuantizedWeight& down, bool f32_scales = false);
 void mlp_w8a8(const Tensor& x, DecodeMlpW8A8& mlp, Tensor& out, hipStream_t stream);
+void check_wait_status(DecodeMlpW8A8& mlp, hipStream_t stream);
 
 // out fp16 [M, N] = RNE((acc * w_scale[n]) * x_scale[m]); scales fp16 or fp32.
 void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream);

@@ -1,10 +1,12 @@
 // decode_dispatch.cpp -- W8A8 / W4A16 / dense choice per projection.
 #include "minicpmv/decode_dispatch.h"
 
+#include "minicpmv/hip_context.h"
 #include "minicpmv/ops.h"
 
 #include <cstdlib>
 #include <stdexcept>
+#include <unordered_map>
 
 namespace minicpmv {
 
@@ -47,24 +49,68 @@ void matmul_decode_w8a8_prequant(const Tensor& x_int8, const Tensor& x_scale, co
     matmul_w8a8(x_int8, x_scale, w8_weight, out, stream);
 }
 
-void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W4A16QuantizedWeight* quant_weight,
-                            const W8A8QuantizedWeight* w8_weight, Tensor& out, hipStream_t stream) {
-    if (w8a8_weight_ready(w8_weight) && x.shape().size() == 2) {
-        Tensor x_int8(x.shape(), DType::Int8);
+void DecodeScratch::reserve(int64_t M, int64_t K) {
+    if (static_cast<int64_t>(x_int8.numel()) < M * K) {
+        x_int8 = Tensor({M * K}, DType::Int8);
         x_int8.allocate();
-        Tensor x_scale({x.shape()[0]}, DType::Float32);
+    }
+    if (static_cast<int64_t>(x_scale.numel()) < M) {
+        x_scale = Tensor({M}, DType::Float16);
         x_scale.allocate();
-        w8a8_quantize(x, x_int8, x_scale, stream);
-        matmul_decode_w8a8_prequant(x_int8, x_scale, *w8_weight, out, stream);
-        // The temporaries are freed on return; hipFree waits for the kernels.
+    }
+}
+
+namespace {
+
+bool rank2(const Tensor& x) { return x.shape().size() == 2; }
+
+void w8a8_branch(const Tensor& x, const W8A8QuantizedWeight& w8, Tensor& out, hipStream_t stream,
+                 DecodeScratch& scratch) {
+    const int64_t M = x.shape()[0], K = x.shape()[1];
+    scratch.reserve(M, K);
+    // Non-owning tensors of the operators' shapes over the scratch bytes.
+    Tensor xq = Tensor::view(scratch.x_int8, {M, K}, DType::Int8);
+    Tensor xs = Tensor::view(scratch.x_scale, {M}, DType::Float16);
+    w8a8_quantize(x, xq, xs, stream);
+    matmul_decode_w8a8_prequant(xq, xs, w8, out, stream);
+}
+
+}  // namespace
+
+void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W4A16QuantizedWeight* quant_weight,
+                            const W8A8QuantizedWeight* w8_weight, Tensor& out, hipStream_t stream,
+                            DecodeScratch& scratch) {
+    const bool one_row = rank2(x) && x.shape()[0] == 1;
+    const bool q4_ready = quant_weight != nullptr && quant_weight->w_int8.data() != nullptr;
+    if (w8a8_weight_ready(w8_weight) && one_row) {
+        w8a8_branch(x, *w8_weight, out, stream, scratch);
         return;
     }
-    if (quant_weight != nullptr && quant_weight->w_int8.data() != nullptr && x.shape().size() == 2) {
+    if (q4_ready && one_row) {
         matmul_w4a16(x, *quant_weight, out, stream);
         return;
     }
-    if (dense_weight == nullptr) throw std::runtime_error("matmul_decode_dispatch: no weight for this projection");
-    matmul_b_transposed(x, *dense_weight, out, stream);
+    if (dense_weight != nullptr) {
+        matmul_b_transposed(x, *dense_weight, out, stream);
+        return;
+    }
+    if (q4_ready && rank2(x)) {
+        matmul_w4a16(x, *quant_weight, out, stream);
+        return;
+    }
+    if (w8a8_weight_ready(w8_weight) && rank2(x)) {
+        w8a8_branch(x, *w8_weight, out, stream, scratch);
+        return;
+    }
+    throw std::runtime_error("matmul_decode_dispatch: no weight for this projection");
+}
+
+void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W4A16QuantizedWeight* quant_weight,
+                            const W8A8QuantizedWeight* w8_weight, Tensor& out, hipStream_t stream) {
+    thread_local std::unordered_map<int, DecodeScratch> per_device;
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    matmul_decode_dispatch(x, dense_weight, quant_weight, w8_weight, out, stream, per_device[dev]);
 }
 
 }  // namespace minicpmv

@@ -104,16 +104,36 @@ DecodeMlpW4A16 make_decode_mlp_w4a16(const W4A16QuantizedWeight& gate, const W4A
     return mlp;
 }
 
+namespace {
+
+// A give-up leaves the per-workgroup call counters out of step: drain the
+// stream, zero the workspace and the status word, then report.
+[[noreturn]] void raise_mlp_gave_up(Tensor& workspace, WaitStatus& status, hipStream_t stream, const char* who) {
+    check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    workspace.zero();
+    status.clear();
+    throw std::runtime_error(std::string(who) +
+                             ": a wait for another workgroup's words gave up in an earlier call (its output is "
+                             "undefined); the workspace was reset");
+}
+
+}  // namespace
+
+void check_wait_status(DecodeMlpW4A16& mlp, hipStream_t stream) {
+    if (mlp.status.gave_up()) raise_mlp_gave_up(mlp.workspace, mlp.status, stream, "mlp_w4a16");
+}
+
 void mlp_w4a16(const Tensor& x, DecodeMlpW4A16& mlp, Tensor& out, hipStream_t stream) {
     const W4A16QuantizedWeight &g = *mlp.gate, &u = *mlp.up, &d = *mlp.down;
     require(x.dtype() == DType::Float16 && x.shape() == std::vector<int64_t>{1, g.K}, "decode MLP x must be fp16 [1, H]");
     require(out.dtype() == DType::Float16 && out.shape() == std::vector<int64_t>{1, g.K},
             "decode MLP out must be fp16 [1, H]");
     if (mlp.one_launch) {
+        check_wait_status(mlp, stream);
         const int rc = mcv_w4a16_mlp(x.data(), g.K, g.N, g.w_int8.data(), g.scales.data(), g.zeros.data(), g.zero_bias,
                                      u.w_int8.data(), u.scales.data(), u.zeros.data(), u.zero_bias, d.w_int8.data(),
                                      d.scales.data(), d.zeros.data(), d.zero_bias, out.data(), mlp.workspace.data(),
-                                     stream);
+                                     mlp.status.device_word(), stream);
         if (rc != MCV_ERR_SHAPE) {
             check_mcv(rc, "mlp_w4a16");
             return;
@@ -183,13 +203,17 @@ void rms_norm_w8a8_quantize(const Tensor& x, const Tensor& gamma, double epsilon
 }
 
 DecodeMlpW8A8 make_decode_mlp_w8a8(const W8A8QuantizedWeight& gate, const W8A8QuantizedWeight& up,
-                                   const W8A8QuantizedWeight& down) {
+                                   const W8A8QuantizedWeight& down, bool f32_scales) {
     require(up.K == gate.K && up.N == gate.N, "decode MLP (W8A8) gate and up must have the same shape");
     require(down.K == gate.N && down.N == gate.K, "decode MLP (W8A8) down must be [I, H] for gate [H, I]");
+    for (const W8A8QuantizedWeight* w : {&gate, &up, &down})
+        require((f32_scales ? w->w_scale_f32 : w->w_scale).data() != nullptr,
+                f32_scales ? "decode MLP (W8A8) needs fp32 weight scales" : "decode MLP (W8A8) needs fp16 weight scales");
     DecodeMlpW8A8 mlp;
     mlp.gate = &gate;
     mlp.up = &up;
     mlp.down = &down;
+    mlp.f32_scales = f32_scales;
     const bool tiled = gate.layout == MCV_W8_TILED && up.layout == MCV_W8_TILED && down.layout == MCV_W8_TILED;
     const int64_t ws = tiled ? mcv_w8a8_mlp_workspace_bytes(gate.K, gate.N) : 0;
     mlp.one_launch = ws > 0;
@@ -197,11 +221,12 @@ DecodeMlpW8A8 make_decode_mlp_w8a8(const W8A8QuantizedWeight& gate, const W8A8Qu
         mlp.workspace = Tensor({ws}, DType::UInt8);
         mlp.workspace.zero();
     }
+    const DType sd = f32_scales ? DType::Float32 : DType::Float16;
     mlp.xq = Tensor({1, gate.K}, DType::Int8);
-    mlp.xs = Tensor({1}, DType::Float32);
+    mlp.xs = Tensor({1}, sd);
     mlp.act = Tensor({1, gate.N}, DType::Float16);
     mlp.aq = Tensor({1, gate.N}, DType::Int8);
-    mlp.as = Tensor({1}, DType::Float32);
+    mlp.as = Tensor({1}, sd);
     for (Tensor* t : {&mlp.xq, &mlp.xs, &mlp.act, &mlp.aq, &mlp.as}) t->allocate();
     return mlp;
 }
@@ -213,13 +238,13 @@ void mlp_w8a8(const Tensor& x, DecodeMlpW8A8& mlp, Tensor& out, hipStream_t stre
     require(out.dtype() == DType::Float16 && out.shape() == std::vector<int64_t>{1, g.K},
             "decode MLP (W8A8) out must be fp16 [1, H]");
     if (mlp.one_launch) {
-        const int rc = mcv_w8a8_mlp(x.data(), g.K, g.N, static_cast<const int8_t*>(g.w_int8.data()),
-                                    static_cast<const float*>(g.w_scale_f32.data()),
-                                    static_cast<const int8_t*>(u.w_int8.data()),
-                                    static_cast<const float*>(u.w_scale_f32.data()),
-                                    static_cast<const int8_t*>(d.w_int8.data()),
-                                    static_cast<const float*>(d.w_scale_f32.data()), out.data(), mlp.workspace.data(),
-                                    stream);
+        check_wait_status(mlp, stream);
+        auto scales = [&](const W8A8QuantizedWeight& w) { return (mlp.f32_scales ? w.w_scale_f32 : w.w_scale).data(); };
+        const int rc = mcv_w8a8_mlp(x.data(), g.K, g.N, static_cast<const int8_t*>(g.w_int8.data()), scales(g),
+                                    static_cast<const int8_t*>(u.w_int8.data()), scales(u),
+                                    static_cast<const int8_t*>(d.w_int8.data()), scales(d),
+                                    mlp.f32_scales ? MCV_F32 : MCV_F16, out.data(), mlp.workspace.data(),
+                                    mlp.status.device_word(), stream);
         if (rc != MCV_ERR_SHAPE) {
             check_mcv(rc, "mlp_w8a8");
             return;
@@ -230,6 +255,10 @@ void mlp_w8a8(const Tensor& x, DecodeMlpW8A8& mlp, Tensor& out, hipStream_t stre
     mlp_gate_up_silu_w8a8(mlp.xq, mlp.xs, g, u, mlp.act, stream);
     w8a8_quantize(mlp.act, mlp.aq, mlp.as, stream);
     matmul_w8a8(mlp.aq, mlp.as, d, out, stream);
+}
+
+void check_wait_status(DecodeMlpW8A8& mlp, hipStream_t stream) {
+    if (mlp.status.gave_up()) raise_mlp_gave_up(mlp.workspace, mlp.status, stream, "mlp_w8a8");
 }
 
 void w8a8_dequant(const Tensor& acc, const Tensor& x_scale, const Tensor& w_scale, Tensor& out, hipStream_t stream) {

@@ -1,57 +1,79 @@
-// tensor.cpp -- hipMalloc-backed device buffers and tensors.
+// tensor.cpp -- device memory ownership for the operator surface.
+//
+// DeviceBuffer owns one hipMalloc allocation through a unique_ptr whose
+// deleter calls hipFree, so moves, resets and destruction are the smart
+// pointer's; Tensor adds a validated shape and dtype and allocates lazily.
+// Element counts are checked for overflow when a shape is set, so every later
+// size computation is exact.
 #include "minicpmv/tensor.h"
 
 #include "minicpmv/hip_context.h"
 
 #include <hip/hip_runtime_api.h>
 
-#include <numeric>
+#include <limits>
 #include <stdexcept>
+#include <string>
+#include <utility>
 
 namespace minicpmv {
+namespace {
 
-size_t dtype_size(DType dtype) {
-    switch (dtype) {
-        case DType::Float16:
-        case DType::BFloat16: return 2;
-        case DType::Float32:
-        case DType::Int32: return 4;
-        case DType::Int64: return 8;
-        case DType::UInt8:
-        case DType::Int8: return 1;
-    }
-    throw std::runtime_error("unknown dtype");
+struct DTypeInfo {
+    size_t bytes;
+    const char* name;
+};
+
+// Indexed by the DType enumerators in declaration order.
+constexpr DTypeInfo kDTypes[] = {
+    {2, "F16"},  // Float16
+    {2, "BF16"}, // BFloat16
+    {4, "F32"},  // Float32
+    {4, "I32"},  // Int32
+    {8, "I64"},  // Int64
+    {1, "U8"},   // UInt8
+    {1, "I8"},   // Int8
+};
+
+const DTypeInfo& info(DType dtype) {
+    const auto i = static_cast<size_t>(dtype);
+    if (i >= sizeof(kDTypes) / sizeof(kDTypes[0])) throw std::runtime_error("unknown dtype");
+    return kDTypes[i];
 }
 
-const char* dtype_name(DType dtype) {
-    switch (dtype) {
-        case DType::Float16: return "F16";
-        case DType::BFloat16: return "BF16";
-        case DType::Float32: return "F32";
-        case DType::Int32: return "I32";
-        case DType::Int64: return "I64";
-        case DType::UInt8: return "U8";
-        case DType::Int8: return "I8";
+// Product of the dimensions; 0 for an empty shape (the reference's convention
+// for a default-constructed tensor); throws on a negative dimension or a
+// product that does not fit in size_t.
+size_t checked_numel(const std::vector<int64_t>& shape) {
+    if (shape.empty()) return 0;
+    size_t n = 1;
+    for (int64_t d : shape) {
+        if (d < 0) throw std::runtime_error("Tensor: negative dimension " + std::to_string(d));
+        const auto u = static_cast<size_t>(d);
+        if (u != 0 && n > std::numeric_limits<size_t>::max() / u)
+            throw std::runtime_error("Tensor: element count overflows");
+        n *= u;
     }
-    return "?";
+    return n;
 }
+
+}  // namespace
+
+size_t dtype_size(DType dtype) { return info(dtype).bytes; }
+
+const char* dtype_name(DType dtype) { return info(dtype).name; }
+
+void DeviceBuffer::HipFree::operator()(void* p) const noexcept { (void)hipFree(p); }
 
 DeviceBuffer::DeviceBuffer(size_t bytes) { allocate(bytes); }
 
-DeviceBuffer::~DeviceBuffer() { reset(); }
-
-DeviceBuffer::DeviceBuffer(DeviceBuffer&& other) noexcept : data_(other.data_), size_bytes_(other.size_bytes_) {
-    other.data_ = nullptr;
-    other.size_bytes_ = 0;
-}
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& other) noexcept
+    : mem_(std::move(other.mem_)), size_bytes_(std::exchange(other.size_bytes_, 0)) {}
 
 DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& other) noexcept {
     if (this != &other) {
-        reset();
-        data_ = other.data_;
-        size_bytes_ = other.size_bytes_;
-        other.data_ = nullptr;
-        other.size_bytes_ = 0;
+        mem_ = std::move(other.mem_);               // frees what this buffer held
+        size_bytes_ = std::exchange(other.size_bytes_, 0);
     }
     return *this;
 }
@@ -59,47 +81,61 @@ DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& other) noexcept {
 void DeviceBuffer::allocate(size_t bytes) {
     reset();
     if (bytes == 0) return;
-    check_hip(hipMalloc(&data_, bytes), "hipMalloc");
+    void* p = nullptr;
+    check_hip(hipMalloc(&p, bytes), "hipMalloc");
+    mem_.reset(p);
     size_bytes_ = bytes;
 }
 
 void DeviceBuffer::reset() {
-    if (data_ != nullptr) {
-        (void)hipFree(data_);
-        data_ = nullptr;
-        size_bytes_ = 0;
-    }
+    mem_.reset();
+    size_bytes_ = 0;
 }
 
-Tensor::Tensor(std::vector<int64_t> shape, DType dtype) : shape_(std::move(shape)), dtype_(dtype) {
-    for (int64_t d : shape_)
-        if (d < 0) throw std::runtime_error("Tensor: negative dimension");
+Tensor::Tensor(std::vector<int64_t> shape, DType dtype)
+    : shape_(std::move(shape)), dtype_(dtype), numel_(checked_numel(shape_)) {
+    if (numel_ > std::numeric_limits<size_t>::max() / dtype_size(dtype_))
+        throw std::runtime_error("Tensor: byte size overflows");
 }
 
-void Tensor::allocate() { buffer_.allocate(size_bytes()); }
+Tensor Tensor::view(const Tensor& storage, std::vector<int64_t> shape, DType dtype) {
+    Tensor t(std::move(shape), dtype);
+    if (storage.data() == nullptr) throw std::runtime_error("Tensor::view: storage is not allocated");
+    if (t.size_bytes() > storage.size_bytes())
+        throw std::runtime_error("Tensor::view: " + std::to_string(t.size_bytes()) + " bytes over a tensor of " +
+                                 std::to_string(storage.size_bytes()));
+    t.borrowed_ = storage.data();
+    return t;
+}
+
+void Tensor::allocate() {
+    if (borrowed_ != nullptr) throw std::runtime_error("Tensor::allocate: a view owns no memory");
+    buffer_.allocate(size_bytes());
+}
 
 void Tensor::copy_from_host(const void* src, size_t bytes) {
-    if (bytes > size_bytes()) throw std::runtime_error("Tensor::copy_from_host: more bytes than the tensor holds");
-    if (buffer_.data() == nullptr) allocate();
-    check_hip(hipMemcpy(buffer_.data(), src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    if (bytes > size_bytes())
+        throw std::runtime_error("Tensor::copy_from_host: " + std::to_string(bytes) + " bytes into a tensor of " +
+                                 std::to_string(size_bytes()));
+    if (data() == nullptr) allocate();
+    if (bytes != 0) check_hip(hipMemcpy(data(), src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
 }
 
 void Tensor::copy_to_host(void* dst, size_t bytes) const {
-    if (bytes > buffer_.size_bytes()) throw std::runtime_error("Tensor::copy_to_host: more bytes than allocated");
-    check_hip(hipMemcpy(dst, buffer_.data(), bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    const size_t have = borrowed_ != nullptr ? size_bytes() : buffer_.size_bytes();
+    if (bytes > have)
+        throw std::runtime_error("Tensor::copy_to_host: " + std::to_string(bytes) + " bytes from an allocation of " +
+                                 std::to_string(have));
+    if (bytes != 0) check_hip(hipMemcpy(dst, data(), bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
 }
 
 void Tensor::zero() {
-    if (buffer_.data() == nullptr) allocate();
-    if (size_bytes() != 0) check_hip(hipMemset(buffer_.data(), 0, size_bytes()), "hipMemset");
+    if (data() == nullptr) allocate();
+    if (size_bytes() != 0) check_hip(hipMemset(data(), 0, size_bytes()), "hipMemset");
 }
 
-size_t Tensor::numel() const {
-    if (shape_.empty()) return 0;
-    return std::accumulate(shape_.begin(), shape_.end(), size_t{1},
-                           [](size_t a, int64_t b) { return a * static_cast<size_t>(b); });
-}
+size_t Tensor::numel() const { return numel_; }
 
-size_t Tensor::size_bytes() const { return numel() * dtype_size(dtype_); }
+size_t Tensor::size_bytes() const { return numel_ * dtype_size(dtype_); }
 
 }  // namespace minicpmv

@@ -94,6 +94,17 @@ __device__ __forceinline__ uint16_t silu_mul_f16(uint16_t g, uint16_t u) {
     return f2h(t);
 }
 
+// A bounded wait for another workgroup's words gave up: sets the u32 give-up
+// word of the workspace (device scope) and, when the caller passed one, the
+// status word -- a plain system-scope store of 1, so a word in host-mapped
+// pinned memory turns non-zero where the host can read it without
+// synchronising, and no PCIe atomic is needed.  Vector memory operations
+// only; reached only on the give-up path.
+__device__ __forceinline__ void flag_gave_up(unsigned* ws_word, unsigned* status) {
+    __hip_atomic_fetch_or(ws_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (status != nullptr) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

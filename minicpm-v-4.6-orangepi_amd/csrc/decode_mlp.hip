@@ -74,7 +74,7 @@ __host__ __device__ inline int64_t act_bytes(int64_t I) { return (I + kSlab - 1)
 // workspace.  All loads of one read are issued before any is compared.
 template <int N, typename Load, typename TagOf>
 __device__ __forceinline__ void poll_words(uint64_t (&v)[N], Load load_all, TagOf tag_of, uint32_t tag,
-                                           unsigned* __restrict__ ws, int lane) {
+                                           unsigned* __restrict__ ws, unsigned* status, int lane) {
     for (int spins = 0;; ++spins) {
         load_all(v);
         uint32_t bad = 0;
@@ -82,7 +82,7 @@ __device__ __forceinline__ void poll_words(uint64_t (&v)[N], Load load_all, TagO
         for (int i = 0; i < N; ++i) bad |= tag_of(v[i]) ^ tag;
         if (__all(bad == 0)) return;
         if (spins > kSpinLimit) {
-            if (lane == 0) __hip_atomic_fetch_or(ws + kWsError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) flag_gave_up(ws + kWsError, status);
             return;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -97,7 +97,7 @@ __device__ __forceinline__ void poll_words(uint64_t (&v)[N], Load load_all, TagO
 __global__ __launch_bounds__(64 * kMaxWaves) void w4a16_mlp_kernel(const uint16_t* __restrict__ x, W4Ptrs gate,
                                                                    W4Ptrs up, W4Ptrs down, uint16_t* __restrict__ out,
                                                                    int H, int I, int ks1, int ks2,
-                                                                   unsigned* __restrict__ ws) {
+                                                                   unsigned* __restrict__ ws, unsigned* status) {
     __shared__ float red[2][kMaxWaves][kSlab];
     __shared__ uint32_t xg[kP2Waves][kSlab];                             // one act group per wave, half2 words
     __shared__ unsigned s_epoch;
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void w4a16_mlp_kernel(const uint16_
                 const uint32_t t0 = static_cast<uint32_t>(v) >> 16, t1 = static_cast<uint32_t>(v >> 48);
                 return t0 == t1 ? t0 : ~t0;
             },
-            tag, ws, lane);
+            tag, ws, status, lane);
         xg[wave][lane] = (static_cast<uint32_t>(av[0]) & 0xffffu) | (static_cast<uint32_t>(av[0] >> 32) << 16);
         uint32_t xs[64];
 #pragma unroll
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void w4a16_mlp_kernel(const uint16_
                     v[i] = __hip_atomic_load(slab_part + (2 + i < ks2 ? 2 + i : 2) * kSlab, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
             },
-            [](uint64_t v) { return static_cast<uint32_t>(v >> 32); }, tag, ws, lane);
+            [](uint64_t v) { return static_cast<uint32_t>(v >> 32); }, tag, ws, status, lane);
 #pragma unroll
         for (int i = 0; i < kMaxWaves - 2; ++i)
             if (2 + i < ks2) acc += __uint_as_float(static_cast<uint32_t>(pv[i]));
@@ -301,11 +301,33 @@ __host__ __device__ inline W8Layout w8_layout(int H, int I, int nparts) {
     return l;
 }
 
+// Per-channel weight scale n as fp32: fp32 storage, or (REF16) the
+// reference's truncated fp16 copy widened exactly.
+template <bool REF16>
+__device__ __forceinline__ float w8_scale(const void* __restrict__ s, int n) {
+    if constexpr (REF16) return h2f(static_cast<const uint16_t*>(s)[n]);
+    else return static_cast<const float*>(s)[n];
+}
+
+// The scale a row's epilogue multiplies by: the quantiser's fp32 scale, or
+// (REF16) its fp16 RNE encoding widened back, the value the reference stores
+// in w8a8_quantize's fp16 x_scale and its dequant reads
+// (op_kernel/w8a8_quantize_custom.cpp:41, w8a8_dequant_custom.cpp:43-44).
+template <bool REF16>
+__device__ __forceinline__ float epilogue_scale(float xs) {
+    if constexpr (REF16) return h2f(f2h(xs));
+    else return xs;
+}
+
 // grid = 2 nslab2 nparts (phase 2, first) + 2 nslab1 (phase 1), block = 512.
+// REF16: fp16 weight scales and fp16-rounded activation scales in every
+// epilogue, the reference's precision; otherwise fp32 throughout.
+template <bool REF16>
 __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
-    const uint16_t* __restrict__ x, const int8_t* __restrict__ wg, const float* __restrict__ sg,
-    const int8_t* __restrict__ wu, const float* __restrict__ su, const int8_t* __restrict__ wd,
-    const float* __restrict__ sd, uint16_t* __restrict__ out, int H, int I, int nparts, unsigned* __restrict__ ws) {
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ wg, const void* __restrict__ sg,
+    const int8_t* __restrict__ wu, const void* __restrict__ su, const int8_t* __restrict__ wd,
+    const void* __restrict__ sd, uint16_t* __restrict__ out, int H, int I, int nparts, unsigned* __restrict__ ws,
+    unsigned* status) {
     __shared__ __attribute__((aligned(16))) int8_t xq_lds[kW8MaxH];
     __shared__ int red[kW8Waves][2][64];
     __shared__ float scratch8[kW8Waves];
@@ -352,7 +374,7 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
         }
         load_w(wave);
         const int n = slab * 64 + 32 * j + (lane & 31);
-        const float sgv = n < I ? sg[n] : 0.f, suv = n < I ? su[n] : 0.f;
+        const float sgv = n < I ? w8_scale<REF16>(sg, n) : 0.f, suv = n < I ? w8_scale<REF16>(su, n) : 0.f;
         // x -> xq with the activation quantiser's arithmetic (H is a multiple
         // of 128, so the k-blocks cover x exactly)
         float m = 0.f;
@@ -364,6 +386,7 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
         }
         const float xs = act_scale(block_max8(m, scratch8));
         const float inv = __fdiv_rn(1.0f, xs);
+        const float xse = epilogue_scale<REF16>(xs);
 #pragma unroll
         for (int i = 0; i < kW8XWords; ++i) {
             const int k2 = static_cast<int>(threadIdx.x) + i * 64 * kW8Waves;
@@ -408,8 +431,8 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
         }
         float a = 0.f;
         if (lane < 32 && n < I) {
-            const uint16_t g16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(g), sgv), xs));
-            const uint16_t u16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(uu), suv), xs));
+            const uint16_t g16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(g), sgv), xse));
+            const uint16_t u16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(uu), suv), xse));
             const uint16_t a16 = silu_mul_f16(g16, u16);
             a = fabsf(h2f(a16));
             __hip_atomic_store(act + n, (tag << 16) | a16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -440,7 +463,7 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
         wdv[u] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, 2));
     }
     const int ncol = slab * 64 + 32 * j + (lane & 31);
-    const float sdv = p == 0 && wave == 0 && ncol < H ? sd[ncol] : 0.f;
+    const float sdv = p == 0 && wave == 0 && ncol < H ? w8_scale<REF16>(sd, ncol) : 0.f;
     if (wave == 0 && lane == 0) {
         s_epoch = epoch;
         __hip_atomic_store(ws + kWsEpoch + b, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -470,7 +493,7 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
         }
         if (!__syncthreads_or(ok ? 0 : 1)) break;
         if (spins > kSpinLimit) {
-            if (threadIdx.x == 0) __hip_atomic_fetch_or(ws + kWsError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (threadIdx.x == 0) flag_gave_up(ws + kWsError, status);
             break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -519,12 +542,13 @@ __global__ __launch_bounds__(64 * kW8Waves) void w8a8_mlp_kernel(
                     w[q] = __hip_atomic_load(mypart + (q + 1 < nparts ? q + 1 : 1) * 32, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
             },
-            [](uint64_t w) { return static_cast<uint32_t>(w >> 32); }, tag, ws, lane);
+            [](uint64_t w) { return static_cast<uint32_t>(w >> 32); }, tag, ws, status, lane);
 #pragma unroll
         for (int q = 0; q < kW8MaxParts - 1; ++q)
             if (q + 1 < nparts) sum += static_cast<int>(static_cast<uint32_t>(v[q]));
     }
-    if (lane < 32 && ncol < H) out[ncol] = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum), sdv), as));
+    if (lane < 32 && ncol < H)
+        out[ncol] = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum), sdv), epilogue_scale<REF16>(as)));
 }
 
 // Workgroups of `kernel` that the current device holds at once (occupancy
@@ -563,7 +587,8 @@ int64_t mcv_w4a16_mlp_workspace_bytes(int64_t H, int64_t I) {
 int mcv_w4a16_mlp(const void* x, int64_t H, int64_t I, const void* qw_gate, const void* scales_gate,
                   const void* zeros_gate, int zero_bias_gate, const void* qw_up, const void* scales_up,
                   const void* zeros_up, int zero_bias_up, const void* qw_down, const void* scales_down,
-                  const void* zeros_down, int zero_bias_down, void* out, void* workspace, mcv_stream_t stream) {
+                  const void* zeros_down, int zero_bias_down, void* out, void* workspace, uint32_t* status,
+                  mcv_stream_t stream) {
     const char* who = "mcv_w4a16_mlp";
     if (!x || !out || !workspace) return fail(MCV_ERR_INVALID_ARG, "%s: null x/out/workspace", who);
     if (!qw_gate || !scales_gate || !zeros_gate || !qw_up || !scales_up || !zeros_up || !qw_down || !scales_down ||
@@ -603,7 +628,7 @@ int mcv_w4a16_mlp(const void* x, int64_t H, int64_t I, const void* qw_gate, cons
                        W4Ptrs{static_cast<const uint4*>(qw_down), static_cast<const uint16_t*>(scales_down),
                               static_cast<const uint32_t*>(zeros_down), static_cast<uint32_t>(zero_bias_down)},
                        static_cast<uint16_t*>(out), static_cast<int>(H), static_cast<int>(I), ks1, ks2,
-                       static_cast<unsigned*>(workspace));
+                       static_cast<unsigned*>(workspace), static_cast<unsigned*>(status));
     return check_launch("w4a16_mlp_kernel");
 }
 
@@ -615,13 +640,15 @@ int64_t mcv_w8a8_mlp_workspace_bytes(int64_t H, int64_t I) {
     return (static_cast<int64_t>(l.part) + 2 * ceil_div(H, kSlab) * w8_parts(I) * 32) * 8;
 }
 
-int mcv_w8a8_mlp(const void* x, int64_t H, int64_t I, const int8_t* w_gate, const float* ws_gate, const int8_t* w_up,
-                 const float* ws_up, const int8_t* w_down, const float* ws_down, void* out, void* workspace,
-                 mcv_stream_t stream) {
+int mcv_w8a8_mlp(const void* x, int64_t H, int64_t I, const int8_t* w_gate, const void* ws_gate, const int8_t* w_up,
+                 const void* ws_up, const int8_t* w_down, const void* ws_down, int scale_dtype, void* out,
+                 void* workspace, uint32_t* status, mcv_stream_t stream) {
     const char* who = "mcv_w8a8_mlp";
     if (!x || !out || !workspace) return fail(MCV_ERR_INVALID_ARG, "%s: null x/out/workspace", who);
     if (!w_gate || !ws_gate || !w_up || !ws_up || !w_down || !ws_down)
         return fail(MCV_ERR_INVALID_ARG, "%s: null weight or scale pointer", who);
+    if (scale_dtype != MCV_F32 && scale_dtype != MCV_F16)
+        return fail(MCV_ERR_INVALID_ARG, "%s: scale_dtype must be MCV_F32 or MCV_F16", who);
     if ((reinterpret_cast<uintptr_t>(w_gate) | reinterpret_cast<uintptr_t>(w_up) | reinterpret_cast<uintptr_t>(w_down)) % 16)
         return fail(MCV_ERR_INVALID_ARG, "%s: weights must be 16-byte aligned", who);
     if (H <= 0 || H % kGroup != 0 || I <= 0 || I % kGroup != 0 || H > kW8MaxH || I > 16384)
@@ -637,14 +664,15 @@ int mcv_w8a8_mlp(const void* x, int64_t H, int64_t I, const int8_t* w_gate, cons
                     (long long)H, (long long)I);
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    const int resident = resident_blocks(w8a8_mlp_kernel, 1, 64 * kW8Waves);
+    auto kernel = scale_dtype == MCV_F16 ? w8a8_mlp_kernel<true> : w8a8_mlp_kernel<false>;
+    const int resident = resident_blocks(kernel, scale_dtype == MCV_F16 ? 2 : 1, 64 * kW8Waves);
     if (grid > resident)
         return fail(MCV_ERR_SHAPE, "%s: %lld workgroups exceed the %d the device holds at once", who, (long long)grid,
                     resident);
-    hipLaunchKernelGGL(w8a8_mlp_kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * kW8Waves), 0,
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(64 * kW8Waves), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), w_gate, ws_gate, w_up, ws_up,
                        w_down, ws_down, static_cast<uint16_t*>(out), static_cast<int>(H), static_cast<int>(I), nparts,
-                       static_cast<unsigned*>(workspace));
+                       static_cast<unsigned*>(workspace), static_cast<unsigned*>(status));
     return check_launch("w8a8_mlp_kernel");
 }
 

@@ -461,7 +461,8 @@ int64_t tiles_of(const Shape& s, int64_t M, int64_t nslab) {
 // 256 CUs; failing that, the shape with the most workgroups.
 // MCV_W4GEMM_SHAPE="TM,WN,KS,BK,DEPTH" overrides it for tuning sweeps.
 Shape choose_shape(int64_t M, int64_t K, int64_t nslab) {
-    if (const char* e = std::getenv("MCV_W4GEMM_SHAPE")) {
+    static const char* const e = std::getenv("MCV_W4GEMM_SHAPE");      // read once per process
+    if (e != nullptr) {
         Shape s{0, 0, 0, 0, 0};
         if (std::sscanf(e, "%d,%d,%d,%d,%d", &s.tm, &s.wn, &s.ks, &s.bk, &s.depth) == 5 && pick(s) &&
             K % (int64_t(s.bk) * s.ks) == 0)
@@ -499,7 +500,8 @@ int launch_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const
     // the rows for M=2048, K=3584, N=1024 (25.8 against 28.5); even at M=128
     // and 512.  So: column-major when M < N.  MCV_W4GEMM_ORDER=0/1 overrides.
     int col_major = M < N ? 1 : 0;
-    if (const char* e = std::getenv("MCV_W4GEMM_ORDER")) col_major = std::atoi(e) ? 1 : 0;
+    static const char* const order = std::getenv("MCV_W4GEMM_ORDER");  // read once per process
+    if (order != nullptr) col_major = std::atoi(order) ? 1 : 0;
     const int64_t n_tiles = ceil_div(nslab, s.wn);
     const int64_t total = ceil_div(M, s.tm) * n_tiles;
     // Buffer offsets are 32-bit: x inside one row tile (TM * K * 2 bytes) and

@@ -52,7 +52,7 @@ __host__ __device__ inline int64_t lm_keys_index(int64_t nslab) { return (kLmEpo
 // counter as read at the start of the kernel.
 __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ ws, unsigned long long key,
                                                unsigned epoch, int b, int nblk, int nslab, int lane,
-                                               int64_t* __restrict__ token) {
+                                               int64_t* __restrict__ token, unsigned* status) {
     unsigned* ws32 = reinterpret_cast<unsigned*>(ws);
     unsigned long long* keys = ws + lm_keys_index(nslab);
     const unsigned long long tag = (epoch + 1u) & 0xffffffu;
@@ -64,6 +64,7 @@ __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ 
     }
     if (b != nblk - 1) return;
     unsigned long long best = 0ull;
+    bool gave_up = false;
     for (int base = 0; base < nblk; base += 64 * kLmPollVec) {
         unsigned long long v[kLmPollVec];
         for (int spins = 0;; ++spins) {
@@ -77,7 +78,8 @@ __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ 
             for (int i = 0; i < kLmPollVec; ++i) bad |= (v[i] >> 40) ^ tag;
             if (__all(bad == 0)) break;
             if (spins > kLmSpinLimit) {
-                if (lane == 0) __hip_atomic_fetch_or(ws32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) flag_gave_up(ws32, status);
+                gave_up = true;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -89,7 +91,10 @@ __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ 
         }
     }
     best = wave_max_u64(best);
-    if (lane == 0) *token = (best >> 24) ? static_cast<int64_t>(0xffffffu - static_cast<uint32_t>(best & 0xffffffu)) : 0;
+    // -1: the keys of this call never all arrived, so no token is known
+    if (lane == 0)
+        *token = gave_up ? int64_t(-1)
+                 : (best >> 24) ? static_cast<int64_t>(0xffffffu - static_cast<uint32_t>(best & 0xffffffu)) : 0;
 }
 
 // ARGMAX modes of the GEMV epilogue (M == 1 only).
@@ -196,7 +201,7 @@ template <int SPW, int MODE>
 __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ logits, int K, int V, int Npad,
-    int nslab, unsigned long long* __restrict__ ws, int64_t* __restrict__ token, uint32_t tag) {
+    int nslab, unsigned long long* __restrict__ ws, int64_t* __restrict__ token, uint32_t tag, unsigned* status) {
     __shared__ float part[SPW][kLmWaves][kSlab];
     __shared__ unsigned long long wbest[kLmWaves];
     const int lane = threadIdx.x & 63;
@@ -282,7 +287,8 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     if (wave != 0) return;
     best = wave_max_u64(lane < kLmWaves ? wbest[lane] : 0ull);
     if constexpr (MODE == kLmTree) {
-        argmax_publish(ws, best, epoch, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), nslab, lane, token);
+        argmax_publish(ws, best, epoch, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), nslab, lane, token,
+                       status);
     } else {
         if (lane == 0) {
             // argmax_key64 -> slot key: the fp16 key moves to bits 39..24, the
@@ -461,6 +467,21 @@ int env_int(const char* name, int fallback) {
     return std::atoi(v);
 }
 
+// Sweep overrides of the GEMV k-split and the lm_head's slabs per workgroup,
+// read once per process: the tagged-word kernels index per-workgroup call
+// counters by blockIdx, so the grid of one shape must not change while its
+// workspace is in use.
+struct GemvOverrides {
+    int ksplit;
+    int gpw;
+    int lm_spw;
+};
+const GemvOverrides& gemv_overrides() {
+    static const GemvOverrides o{env_int("MCV_GEMV_KSPLIT", 0), env_int("MCV_GEMV_GPW", 0),
+                                 env_int("MCV_LMHEAD_SPW", 0)};
+    return o;
+}
+
 // One quantisation group (four 16-byte loads per lane) per wave per trip,
 // and enough waves per workgroup (up to 16, at most one per group) that the
 // grid holds >= 8K waves, 32 per CU.  Measured on the lm_head shape (K=1024,
@@ -474,7 +495,8 @@ GemvCfg choose_gemv(int64_t G, int64_t blocks) {
     int ks = 1;
     while (ks < 16 && blocks * ks < 8192 && ks * 2 <= G) ks *= 2;
     const int gpw = 1;
-    GemvCfg c{env_int("MCV_GEMV_KSPLIT", ks), env_int("MCV_GEMV_GPW", gpw)};
+    const GemvOverrides& o = gemv_overrides();
+    GemvCfg c{o.ksplit ? o.ksplit : ks, o.gpw ? o.gpw : gpw};
     if (c.ksplit != 1 && c.ksplit != 2 && c.ksplit != 4 && c.ksplit != 8 && c.ksplit != 16) c.ksplit = ks;
     if (c.gpw != 1 && c.gpw != 2 && c.gpw != 4 && c.gpw != 8) c.gpw = gpw;
     return c;
@@ -583,13 +605,13 @@ int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void
 // lm_head shape; MCV_LMHEAD_SPW (1, 2, 4, 8, 16) overrides it for sweeps.
 int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* qw, const void* scales,
                    const void* zeros, int zero_bias, void* logits, int64_t* token, void* ws, uint32_t tag, int mode,
-                   hipStream_t stream) {
+                   unsigned* status, hipStream_t stream) {
     const int64_t nslab = ceil_div(V, kSlab);
     const int64_t npad = ceil_div(N, kSlab) * kSlab;
-    int spw = env_int("MCV_LMHEAD_SPW", 16);
+    int spw = gemv_overrides().lm_spw ? gemv_overrides().lm_spw : 16;
     if (spw != 1 && spw != 2 && spw != 4 && spw != 8 && spw != 16) spw = 16;
     using LmFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int,
-                          int, int, unsigned long long*, int64_t*, uint32_t);
+                          int, int, unsigned long long*, int64_t*, uint32_t, unsigned*);
     LmFn fn = nullptr;
 #define MCV_LM(SPW_)                                                                                  \
     if (spw == SPW_)                                                                                  \
@@ -602,7 +624,7 @@ int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* q
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
                        static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(logits), static_cast<int>(K),
                        static_cast<int>(V), static_cast<int>(npad), static_cast<int>(nslab),
-                       static_cast<unsigned long long*>(ws), token, tag);
+                       static_cast<unsigned long long*>(ws), token, tag, status);
     return check_launch("w4a16_lm_head_kernel");
 }
 
@@ -661,7 +683,7 @@ int mcv_argmax_reduce_keys(const void* keys, int64_t n_keys, int64_t* token, mcv
 
 int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, const void* qw, const void* scales,
                              const void* zeros, int zero_bias, void* logits, int64_t* token, void* workspace,
-                             mcv_stream_t stream) {
+                             uint32_t* status, mcv_stream_t stream) {
     int rc = MCV_OK;
     if (!w4_args_ok(qw, scales, zeros, zero_bias, K, N, "mcv_w4a16_lm_head_argmax", &rc)) return rc;
     if (!x || !token || !workspace) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: null x/token/workspace");
@@ -673,7 +695,7 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
         return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax: workspace must be 128-byte aligned");
     if ((rc = require_device()) != MCV_OK) return rc;
     return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, token, workspace, 0u, kLmTree,
-                          static_cast<hipStream_t>(stream));
+                          static_cast<unsigned*>(status), static_cast<hipStream_t>(stream));
 }
 
 int64_t mcv_lm_head_slots_bytes(void) { return int64_t(kSlotWords) * kSlotStride * 8; }
@@ -693,7 +715,7 @@ int mcv_w4a16_lm_head_argmax_slots(const void* x, int64_t K, int64_t N, int64_t 
     if (reinterpret_cast<uintptr_t>(slots) % 128 != 0)
         return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_lm_head_argmax_slots: slots must be 128-byte aligned");
     if ((rc = require_device()) != MCV_OK) return rc;
-    return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, nullptr, slots, tag, kLmSlots,
+    return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, nullptr, slots, tag, kLmSlots, nullptr,
                           static_cast<hipStream_t>(stream));
 }
 

@@ -463,7 +463,8 @@ int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const in
         return fail(MCV_ERR_SHAPE, "w8a8 tiled GEMV: weight or activation exceeds 4 GiB");
     const bool narrow = nslab < 128;
     int nw = narrow && KB <= 64 ? 8 : 16, halves = narrow ? 1 : 2, u = narrow && KB <= 64 ? 4 : 2;
-    if (const char* e = std::getenv("MCV_W8GEMV")) {
+    static const char* const e = std::getenv("MCV_W8GEMV");            // read once per process
+    if (e != nullptr) {
         int a = 0, b = 0, c = 0;
         if (std::sscanf(e, "%d,%d,%d", &a, &b, &c) == 3) { nw = a; halves = b; u = c; }
     }
@@ -522,7 +523,8 @@ constexpr Shape8 kShapes8[] = {{128, 4, 1, 2}, {64, 4, 1, 2}, {64, 2, 2, 2}, {32
 // The first listed shape whose grid covers most of the 256 CUs, else the one
 // with the most workgroups; MCV_W8GEMM_SHAPE="TM,WN,KS" overrides it.
 Shape8 choose8(int64_t M, int64_t KT, int64_t nslab) {
-    if (const char* e = std::getenv("MCV_W8GEMM_SHAPE")) {
+    static const char* const e = std::getenv("MCV_W8GEMM_SHAPE");      // read once per process
+    if (e != nullptr) {
         Shape8 s{0, 0, 0, 2};
         if (std::sscanf(e, "%d,%d,%d,%d", &s.tm, &s.wn, &s.ks, &s.depth) >= 3 && pick8<true>(s) && KT % s.ks == 0)
             return s;
@@ -571,7 +573,8 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
     // Down the tile columns when x is the smaller operand (M < N); along the
     // tile rows otherwise.  MCV_W8GEMM_ORDER=0/1 overrides (tuning sweeps).
     int col_major = M < N ? 1 : 0;
-    if (const char* e = std::getenv("MCV_W8GEMM_ORDER")) col_major = std::atoi(e) ? 1 : 0;
+    static const char* const order = std::getenv("MCV_W8GEMM_ORDER");  // read once per process
+    if (order != nullptr) col_major = std::atoi(order) ? 1 : 0;
     if (f16)
         hipLaunchKernelGGL(pick8<true>(s), dim3(static_cast<unsigned>(total)), dim3(256), 0, stream, xq, w,
                            static_cast<int>(M), static_cast<int>(K), static_cast<int>(N), KBs, out, xs, xs16, ws, ws16,

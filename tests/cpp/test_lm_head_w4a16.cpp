@@ -2,7 +2,13 @@
 // (lm_head_greedy semantics, src/csrc/lib/language_model.cpp:412-482), against
 // a CPU reference: RMSNorm in fp32 -> fp16, the group formula over the
 // unpacked (q - z), fp16 logits, first-maximum scan.  Plus: exact ties pick
-// the first index, the workspace is reusable, and the W8A8 variant agrees.
+// the first index, the workspace is reusable, the W8A8 variant's logits are
+// bit-exact against the oracle's composition of the reference's steps
+// (language_model.cpp:434-467: fp16 x_scale, truncated fp16 w_scale), and a
+// give-up of the device-token route's bounded wait -- forced from the host by
+// putting one workgroup's call counter out of step -- yields token -1, the
+// status word and a thrown error, after which the head works again.
+#include "mcv_oracle.h"
 #include "mcv_quant.h"
 #include "minicpmv/hip_context.h"
 #include "minicpmv/lm_head.h"
@@ -96,9 +102,66 @@ int main() {
     if (tok2 != scan || hl[777] != hl[4321] || tok2 != 777) rc = 1;
 
     // W8A8 head on the same fp16 weights: per-channel int8 + per-token int8
-    W8A8QuantizedWeight h8 = quantize_w8a8_host(w.data(), K, N);
-    const int64_t t8 = lm_head_greedy_w8a8(x, &gamma, eps, h8, V, ctx.stream());
-    std::printf("W8A8 lm_head token=%lld\n", (long long)t8);
-    if (bv - second > 5e-2f && t8 != best) rc = 1;
+    W8A8QuantizedWeight wq8 = quantize_w8a8_host(w.data(), K, N);
+    LmHeadW8A8 h8 = make_lm_head_w8a8(wq8, V);
+    const int64_t t8 = lm_head_greedy_w8a8(x, &gamma, eps, h8, ctx.stream());
+    {
+        // the oracle's composition over the kernel's own normed row
+        std::vector<uint16_t> normed(K), got(V);
+        h8.normed.copy_to_host(normed.data(), K * 2);
+        h8.logits.copy_to_host(got.data(), V * 2);
+        std::vector<int8_t> xq(K), wq(static_cast<size_t>(K * N));
+        float xs32 = 0.f;
+        uint16_t xs16 = 0;
+        std::vector<float> ws32(N), ws(N);
+        std::vector<uint16_t> ws16(N), want(N);
+        std::vector<int32_t> acc(N);
+        or_w8a8_quantize_act(normed.data(), 1, K, xq.data(), &xs32, &xs16);
+        or_w8a8_quantize_weight(w.data(), K, N, wq.data(), ws32.data(), ws16.data());
+        or_gemm_i32(xq.data(), wq.data(), 1, K, N, acc.data(), 0);
+        for (int64_t n = 0; n < N; ++n) ws[n] = or_h2f(ws16[n]);
+        const float xs = or_h2f(xs16);
+        or_w8a8_dequant(acc.data(), &xs, ws.data(), 1, N, want.data());
+        int bad = 0;
+        for (int64_t n = 0; n < V; ++n) bad += got[n] != want[n];
+        const int64_t want_tok = or_argmax_f16(want.data(), V);
+        std::printf("W8A8 lm_head token=%lld oracle=%lld logit mismatches=%d\n", (long long)t8, (long long)want_tok, bad);
+        if (bad != 0 || t8 != want_tok) rc = 1;
+        if (bv - second > 5e-2f && t8 != best) rc = 1;
+    }
+
+    // Give-up of the device-token route: workgroup 0's call counter (u32 word
+    // 64 of the workspace) five ahead of the others, so its key never carries
+    // the tag the last workgroup polls for.  The kernel still ends (bounded
+    // wait), writes token -1 and sets the status word; the next call throws
+    // and resets the workspace, after which the head works again.
+    {
+        lm_head_argmax_w4a16(x2, head, nullptr, ctx.stream());
+        const int64_t before = lm_head_read_token(head, ctx.stream());
+        uint32_t counters[2] = {0, 0};
+        check_hip(hipMemcpy(counters, static_cast<uint8_t*>(head.workspace.data()) + 64 * 4, 8, hipMemcpyDeviceToHost),
+                  "hipMemcpy");
+        const uint32_t ahead = counters[0] + 5;
+        check_hip(hipMemcpy(static_cast<uint8_t*>(head.workspace.data()) + 64 * 4, &ahead, 4, hipMemcpyHostToDevice),
+                  "hipMemcpy");
+        lm_head_argmax_w4a16(x2, head, nullptr, ctx.stream());
+        int64_t sentinel = 0;
+        check_hip(hipMemcpy(&sentinel, head.token.data(), 8, hipMemcpyDeviceToHost), "hipMemcpy");
+        uint32_t ws_flag = 0;
+        check_hip(hipMemcpy(&ws_flag, head.workspace.data(), 4, hipMemcpyDeviceToHost), "hipMemcpy");
+        const bool status = head.status.gave_up();
+        bool threw = false;
+        try {
+            lm_head_argmax_w4a16(x2, head, nullptr, ctx.stream());
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()).find("gave up") != std::string::npos;
+        }
+        lm_head_argmax_w4a16(x2, head, nullptr, ctx.stream());      // the workspace was reset: works again
+        const int64_t after = lm_head_read_token(head, ctx.stream());
+        std::printf("give-up: counters %u %u, token %lld, workspace flag %u, status %d, threw %d, recovered %d\n",
+                    counters[0], counters[1], (long long)sentinel, ws_flag, int(status), int(threw),
+                    int(after == before));
+        if (sentinel != -1 || ws_flag == 0 || !status || !threw || after != before || before != 777) rc = 1;
+    }
     return rc;
 }

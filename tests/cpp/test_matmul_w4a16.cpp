@@ -133,6 +133,34 @@ int main() {
         std::printf("decode MLP one_launch=%d bit-identical=%d give-up flag=%u\n", mlp.one_launch ? 1 : 0,
                     h1 == h2 ? 1 : 0, err);
         if (!mlp.one_launch || h1 != h2 || err != 0) return 1;
+
+        // A give-up of the one-launch kernel's bounded waits, forced from the
+        // host: every call counter but workgroup 0's (u32 words 65..1087 of
+        // the workspace) set ahead, so workgroup 0 -- a phase-2 workgroup --
+        // never sees the tag it polls for.  The kernel still ends; the status
+        // word turns non-zero without a synchronisation; the next call
+        // throws, resets the workspace, and the call after that is exact again.
+        std::vector<uint32_t> ahead(1023, 77u);
+        check_hip(hipMemcpy(static_cast<uint8_t*>(mlp.workspace.data()) + 65 * 4, ahead.data(), ahead.size() * 4,
+                            hipMemcpyHostToDevice),
+                  "hipMemcpy");
+        mlp_w4a16(x, mlp, y1, ctx.stream());
+        ctx.synchronize();
+        uint32_t ws_flag = 0;
+        mlp.workspace.copy_to_host(&ws_flag, 4);
+        const bool status = mlp.status.gave_up();
+        bool threw = false;
+        try {
+            mlp_w4a16(x, mlp, y1, ctx.stream());
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()).find("gave up") != std::string::npos;
+        }
+        mlp_w4a16(x, mlp, y1, ctx.stream());
+        y1.copy_to_host(h1.data(), h1.size() * 2);
+        check_wait_status(mlp, ctx.stream());              // no give-up since the reset: no throw
+        std::printf("decode MLP give-up: workspace flag %u, status %d, threw %d, exact after reset %d\n", ws_flag,
+                    int(status), int(threw), int(h1 == h2));
+        if (ws_flag == 0 || !status || !threw || h1 != h2) return 1;
     }
 
     // 4) shape validation mirrors the reference's host wrapper

@@ -182,22 +182,24 @@ def test_validation_errors_without_device(mcv):
     assert L.mcv_w4a16_mlp_workspace_bytes(1024, 3584) == 4 * (64 + 1024) + 3584 * 4 + 16 * 16 * 64 * 8
     assert L.mcv_w4a16_mlp_workspace_bytes(0, 3584) == 0
     w3 = (fake, fake, fake, 0)
-    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, *w3, fake, None, None) == 1
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, *w3, fake, None, None, None) == 1
     assert b"workspace" in L.mcv_last_error()
-    assert L.mcv_w4a16_mlp(fake, 1000, 3584, *w3, *w3, *w3, fake, fake, None) == 2
-    assert L.mcv_w4a16_mlp(fake, 1024, 6144, *w3, *w3, *w3, fake, fake, None) == 2      # 48 groups over 16 slots
+    assert L.mcv_w4a16_mlp(fake, 1000, 3584, *w3, *w3, *w3, fake, fake, None, None) == 2
+    assert L.mcv_w4a16_mlp(fake, 1024, 6144, *w3, *w3, *w3, fake, fake, None, None) == 2   # 48 groups over 16 slots
     assert b"two groups" in L.mcv_last_error()
-    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, None, 0, fake, fake, None) == 1
-    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, fake, 2, fake, fake, None) == 1
-    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, *w3, fake, ctypes.c_void_p(0x1080), None) == 1
-    # the one-launch W8A8 MLP block
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, None, 0, fake, fake, None, None) == 1
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, fake, fake, fake, 2, fake, fake, None, None) == 1
+    assert L.mcv_w4a16_mlp(fake, 1024, 3584, *w3, *w3, *w3, fake, ctypes.c_void_p(0x1080), None, None) == 1
+    # the one-launch W8A8 MLP block (scale dtype 1 = the reference's fp16 scales, 0 = fp32)
     assert L.mcv_w8a8_mlp_workspace_bytes(1024, 3584) > 3584 * 4
     assert L.mcv_w8a8_mlp_workspace_bytes(8192 + 128, 3584) == 0
     w2 = (fake, fake)
-    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, *w2, fake, None, None) == 1
-    assert L.mcv_w8a8_mlp(fake, 1000, 3584, *w2, *w2, *w2, fake, fake, None) == 2
-    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, fake, None, fake, fake, None) == 1
-    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, ctypes.c_void_p(0x1008), fake, fake, fake, None) == 1
+    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, *w2, 1, fake, None, None, None) == 1
+    assert L.mcv_w8a8_mlp(fake, 1000, 3584, *w2, *w2, *w2, 1, fake, fake, None, None) == 2
+    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, fake, None, 0, fake, fake, None, None) == 1
+    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, *w2, 7, fake, fake, None, None) == 1
+    assert b"scale_dtype" in L.mcv_last_error()
+    assert L.mcv_w8a8_mlp(fake, 1024, 3584, *w2, *w2, ctypes.c_void_p(0x1008), fake, 1, fake, fake, None, None) == 1
     assert b"16-byte" in L.mcv_last_error()
     assert b"aligned" in L.mcv_last_error()
 

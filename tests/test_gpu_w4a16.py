@@ -106,7 +106,8 @@ def test_gemm_mfma_vs_oracle(mcv, oracle, cuda, M, K, N):
     _check(_host_f32(out), ref, f"mfma M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("M,K,N", [(512, 1024, 3584), (2048, 1024, 3584), (2048, 3584, 1024)], ids=lambda v: str(v))
+@pytest.mark.parametrize("M,K,N", [(512, 1024, 3584), (512, 3584, 1024), (2048, 1024, 3584), (2048, 3584, 1024)],
+                         ids=lambda v: str(v))
 def test_gemm_mfma_full_size(mcv, oracle, cuda, M, K, N):
     # prefill benchmark sizes: fp64 product of the oracle-exact dequantised weights
     torch = _torch()

@@ -236,18 +236,66 @@ def _tiled_to_kn(mcv, w):
     return t[off]
 
 
+def _oracle_w8a8_proj(oracle, mcv, x_u16, w, f32):
+    """The reference's W8A8 projection of one row by the oracle: per-tensor
+    quantisation, exact int32 products, dequant with the activation and weight
+    scales -- fp16 (the reference's stored forms, decoder_layer.cpp:216-237)
+    or fp32."""
+    q_o, s_o, s16_o = oracle.w8a8_quantize_act(x_u16)
+    ws = w.w_scale_f32.cpu().numpy() if f32 else oracle.h2f(_u16(w.w_scale))
+    xs = s_o if f32 else oracle.h2f(s16_o)
+    return oracle.w8a8_dequant(oracle.gemm_i32(q_o, _tiled_to_kn(mcv, w)), xs, ws)
+
+
+@pytest.mark.parametrize("H,I", [(1024, 3584), (3584, 1024), (256, 384), (2048, 6144)], ids=lambda v: str(v))
+def test_decode_mlp_reference_precision_vs_oracle(mcv, oracle, cuda, H, I):
+    """DecodeMlpW8A8's default (reference) precision, one launch, bit-exact
+    against the oracle's composition of the reference's steps: quantise the
+    row (fp16 scale), gate and up through gemm_i32 + dequant with the fp16
+    x_scale and the truncated fp16 w_scale, silu_mul, the same for down.  exp
+    inside silu is the one step host and device libms may round differently,
+    so that step uses the device's silu_mul (within one fp16 ulp of the
+    oracle's, checked here too)."""
+    torch = _torch()
+    rng = np.random.default_rng(H * 7 + I)
+    wg = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
+    wu = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
+    wd = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (I, H), 0.02)))
+    mlp = mcv.DecodeMlpW8A8(wg, wu, wd)                  # precision="reference"
+    out = torch.empty((1, H), dtype=torch.float16, device="cuda")
+    for trial in range(2):
+        x = f16_normal(rng, (1, H), 1.0 + trial)
+        mlp(_f16_dev(x), out)
+        assert mlp.one_launch
+        g_o = _oracle_w8a8_proj(oracle, mcv, x, wg, False)
+        u_o = _oracle_w8a8_proj(oracle, mcv, x, wu, False)
+        act = _u16(mcv.silu_mul(_f16_dev(g_o), _f16_dev(u_o)))
+        act_o = oracle.silu_mul(g_o, u_o)
+        assert (np.abs(act.astype(np.int32) - act_o.astype(np.int32)) <= 1).all()
+        want = _oracle_w8a8_proj(oracle, mcv, act.reshape(1, I), wd, False)
+        got = _u16(out)
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"trial {trial}: {bad.size} mismatches, first at {bad[:4].tolist()}"
+    assert not mlp.wait_gave_up()
+    # the same block through the separate operators, reference precision
+    want4 = torch.empty_like(out)
+    mlp._four_launches(_f16_dev(x), want4, None)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want4.view(torch.int16))
+
+
 @pytest.mark.parametrize("H,I", [(1024, 3584), (3584, 1024), (256, 384), (128, 128), (2048, 6144)],
                          ids=lambda v: str(v))
 def test_decode_mlp_block_one_launch(mcv, oracle, cuda, H, I):
-    """The whole W8A8 MLP block in one launch == quantise x, gate+up+silu*mul,
-    quantise act, down GEMV, bit for bit, call after call; and the oracle's
-    composition of the same stages."""
+    """The whole W8A8 MLP block in one launch with fp32 scales == quantise x,
+    gate+up+silu*mul, quantise act, down GEMV, bit for bit, call after call;
+    and the oracle's composition of the same stages."""
     torch = _torch()
     rng = np.random.default_rng(H * 5 + I)
     wg = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
     wu = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
     wd = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (I, H), 0.02)))
-    mlp = mcv.DecodeMlpW8A8(wg, wu, wd)
+    mlp = mcv.DecodeMlpW8A8(wg, wu, wd, precision="f32")
     out = torch.empty((1, H), dtype=torch.float16, device="cuda")
     want = torch.empty_like(out)
     for trial in range(3):
@@ -283,7 +331,7 @@ def test_decode_mlp_block_falls_back(mcv, oracle, cuda):
     wg = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
     wu = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (H, I), 0.02)))
     wd = mcv.quantize_dense_weight_w8a8(_f16_dev(f16_normal(rng, (I, H), 0.02)))
-    mlp = mcv.DecodeMlpW8A8(wg, wu, wd)
+    mlp = mcv.DecodeMlpW8A8(wg, wu, wd, precision="f32")
     assert not mlp.one_launch
     xd = _f16_dev(f16_normal(rng, (1, H), 1.0))
     out = mlp(xd)
