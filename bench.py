@@ -1,17 +1,32 @@
-"""Benchmark of the MI355X quantized-matmul hot path.
+"""Benchmark of the MI355X quantized-matmul hot path (BASELINE.json's five configurations).
 
-Default workload (one JSON line on stdout): the headline configuration, the W4A16
-lm_head -- M=1, K=1024, V=248094 -- as one GEMV launch per step with the
-argmax folded into it, with 8 distinct weight copies (1.06 GB) rotated so no
-step hits the 256 MB MALL.  Its steps are launched directly from bound
-launchers (the host issues one in ~4 us, far inside the ~27 us step); the
-short-kernel workloads replay captured HIP graphs, so back-to-back kernels are
-not gated by the host's launch rate.  `value` is whole-job HBM throughput in GB/s of algorithmic bytes
-(132,484,244 B per step, inputs resident in HBM).  `--workload` selects the
-other benchmark configurations (gemv1, mlp, lm_head, prefill, w8a8) and the vendor library's dense
-GEMM at the same shapes (vendor_f16, vendor_int8) as a yardstick.
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all]
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload lm_head]
+Default (`--workload all`): one JSON line whose headline is configuration 3,
+the W4A16 lm_head (M=1, K=1024, V=248094, one GEMV launch per step with the
+argmax folded in, 8 weight copies = 1.06 GB rotated so no step reads the
+256 MB MALL): W untimed steps, then exactly K steps between one HIP event pair
+on the launch stream.  `value` is HBM throughput of algorithmic bytes
+(132,484,244 B per step, inputs resident in HBM).  The line's `configs` object
+carries every configuration of the north star, each measured in the same run:
+
+  1  W4A16 GEMV K=N=1024                      (1024 rotated weight sets, 562 MB)
+  2  W4A16 decode MLP block, one launch        (96 rotated layer sets, 549 MB)
+  3  the lm_head (the headline, repeated)
+  4  W4A16 prefill GEMM, M in {128,512,2048} x (K,N) in {(1024,3584),(3584,1024)}
+  5  W8A8 GEMM M in {1,256,1024}, K=1024, N=3584 (fused fp16 epilogue)
+
+For each: `us_per_call` = mean duration of back-to-back launches (HIP graphs of
+100 launches, so the host's launch rate does not gate short kernels), from
+which `value` and `roofline.achieved` follow; `kernel_us_median` /
+`kernel_us_mean` = per-launch HIP event pairs around each of >= 100 launches
+(the queue is kept full by a sleep kernel, so each pair brackets one kernel);
+`cpu_baseline` = the oracle's restatement of the reference's CPU path on this
+host, one thread and all threads (bounded samples, stated in `sample`).
+
+`--workload` also runs any single configuration or one of the comparison
+workloads (two-launch / unfused MLPs, W8A8 MLP, projections, vendor GEMMs,
+the copy calibration) for profiling.
 """
 from __future__ import annotations
 
@@ -29,6 +44,8 @@ METRIC = "W4A16 M=1 GEMV HBM GB/s (% peak) + µs/call; prefill GEMM TFLOPS (% MF
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 INT8_MFMA_PEAK_TOPS = 5000.0
+GRAPH_CHUNK = 100          # launches per captured graph
+PER_LAUNCH = 200           # event-bracketed launches per configuration
 
 
 def log(*a):
@@ -41,6 +58,14 @@ def load_pkg():
     return ge.load_package()
 
 
+def load_oracle():
+    """The CPU oracle -- loaded only for the cpu_baseline legs, as the timed
+    restatement of the reference's CPU path."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import load_oracle as lo
+    return lo()
+
+
 def f16_normal(rng, shape, std):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16).view(np.uint16)
 
@@ -50,13 +75,17 @@ def to_dev_f16(a_u16):
     return torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16)).cuda().view(torch.float16)
 
 
-GRAPH_CHUNK = 100     # launches per captured graph
+def w4a16_bytes(K, N):
+    G = K // 128
+    return K * N // 2 + G * N * 2 + G * N // 2
 
 
+# --------------------------------------------------------------------------- #
+# GPU timing                                                                   #
+# --------------------------------------------------------------------------- #
 def _capture(launch, first, count, n_sets):
-    """A HIP graph holding `count` launches (weight sets rotating from
-    `first`), captured on a side stream; replayed, the kernels run back to back
-    with no host launch cost between them."""
+    """A HIP graph of `count` launches (weight sets rotating from `first`),
+    captured on a side stream."""
     import torch
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
@@ -70,68 +99,128 @@ def _capture(launch, first, count, n_sets):
     return g
 
 
-def time_steps(launch, n_sets, steps, warmup):
-    """`steps` back-to-back steps replayed from HIP graphs on torch's current
-    stream, bracketed by one event pair (and a synchronize on both sides).
-    The warmup steps run eagerly first, then once more as a graph replay.
-    Returns (total ms over `steps`, per-step ms of every graph chunk)."""
+def time_graph(launch, n_sets, steps, warmup=3):
+    """Mean ms per launch over `steps` back-to-back launches replayed from HIP
+    graphs on torch's current stream, between one event pair."""
     import torch
     for i in range(warmup):
         launch(i % n_sets)
     torch.cuda.synchronize()
-    chunks = []
-    done = 0
+    chunks, done = [], 0
     while done < steps:
         n = min(GRAPH_CHUNK, steps - done)
-        chunks.append((n, _capture(launch, warmup + done, n, n_sets)))
+        chunks.append(_capture(launch, warmup + done, n, n_sets))
         done += n
-    chunks[0][1].replay()                      # graph warmup
+    chunks[0].replay()
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chunks]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
-    for (n, g), (a, b) in zip(chunks, ev):
-        a.record()
+    for g in chunks:
         g.replay()
-        b.record()
     t1.record()
     torch.cuda.synchronize()
-    per_chunk = [a.elapsed_time(b) / n for (n, _), (a, b) in zip(chunks, ev)]
-    return t0.elapsed_time(t1), per_chunk
+    return t0.elapsed_time(t1) / steps
 
 
 def time_direct(launch, n_sets, steps, warmup):
-    """`steps` back-to-back direct launches from the host between one event
-    pair on torch's current stream (a synchronize on both sides), for steps
-    long enough that the host (~4 us per bound launch) stays ahead of the GPU.
-    Returns (total ms over `steps`, [per-step ms])."""
+    """`warmup` untimed launches, then exactly `steps` back-to-back host
+    launches between one event pair on torch's current stream (the stream the
+    bound launchers use), synchronised on both sides.  A spin kernel enqueued
+    before the first event keeps the GPU busy while the host enqueues the
+    first launches, so the timed region holds the `steps` kernels and not the
+    host's latency to issue the first of them.  Returns total ms."""
     import torch
     for i in range(warmup):
         launch(i % n_sets)
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _sleep_ms(min(steps * 0.006, 2.0) + 0.3)
     t0.record()
     for i in range(steps):
         launch(i % n_sets)
     t1.record()
     torch.cuda.synchronize()
-    total = t0.elapsed_time(t1)
-    return total, [total / steps]
+    return t0.elapsed_time(t1)
 
 
-def time_each_launch(launch, n_sets, steps):
-    """Average duration of the dominant kernel: `steps` launches of it alone,
-    replayed back to back from HIP graphs between HIP events recorded on the
-    stream they run on (torch's current stream).  Returns per-launch ms, one
-    value per graph chunk."""
-    _, per = time_steps(launch, n_sets, steps, 2)
-    return per
+_SLEEP_CYCLES_PER_MS = None
+
+
+def _sleep_ms(ms):
+    """Occupy the stream for about `ms` (torch's spin kernel, calibrated once)."""
+    import torch
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1_000_000)
+        a.record()
+        torch.cuda._sleep(10_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = 10_000_000 / max(a.elapsed_time(b), 1e-3)
+    torch.cuda._sleep(int(ms * _SLEEP_CYCLES_PER_MS))
+
+
+_HIP = None
+
+
+def _hip():
+    """The HIP runtime, for timing events torch does not create: events
+    without the system-scope release fence (hipEventDisableSystemFence), whose
+    markers do not write back the L2 around every kernel they bracket."""
+    global _HIP
+    if _HIP is None:
+        import ctypes
+        h = ctypes.CDLL("libamdhip64.so")
+        h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        _HIP = h
+    return _HIP
+
+
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+
+
+def time_per_launch(launch, n_sets, n=PER_LAUNCH, host_us=25.0):
+    """Per-launch durations (ms): a HIP event pair (no system fence) around
+    each of `n` launches on torch's current stream.  A spin kernel first keeps
+    the stream busy while the host enqueues them, so the GPU runs marker,
+    kernel, marker back to back; each pair still includes its markers'
+    processing (measured on MI355X: +1.5 us on a 3 us kernel, +0.3 us on a
+    25 us one, against rocprofv3's kernel durations)."""
+    import ctypes
+    import torch
+    h = _hip()
+    launch(0)
+    torch.cuda.synchronize()
+    ev = []
+    for _ in range(2 * n):
+        e = ctypes.c_void_p()
+        if h.hipEventCreateWithFlags(ctypes.byref(e), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+        ev.append(e)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _sleep_ms(n * host_us / 1000.0 + 2.0)
+    for i in range(n):
+        h.hipEventRecord(ev[2 * i], stream)
+        launch(i % n_sets)
+        h.hipEventRecord(ev[2 * i + 1], stream)
+    torch.cuda.synchronize()
+    out = []
+    for i in range(n):
+        f = ctypes.c_float()
+        if h.hipEventElapsedTime(ctypes.byref(f), ev[2 * i], ev[2 * i + 1]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        out.append(f.value)
+    for e in ev:
+        h.hipEventDestroy(e)
+    return out
 
 
 def traffic_from_profiles(workload: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    """HBM bytes per launch from rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each
     scaled by the copy-kernel calibration), committed in profiles/traffic.json."""
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
@@ -142,326 +231,509 @@ def traffic_from_profiles(workload: str):
         return None
 
 
-# --------------------------------------------------------------------------- #
-# CPU baseline: the oracle's restatement of the reference CPU path            #
-# --------------------------------------------------------------------------- #
-def cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes, budget_s=12.0):
-    sys.path.insert(0, str(ROOT / "tests"))
-    from helpers import load_oracle       # cpu_baseline leg only: the oracle is timed, not shipped
-    o = load_oracle()
-    w8 = o.unpack_awq(qweight, qzeros)
-    cores = min(16, os.cpu_count() or 1)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 20):
-        t = time.perf_counter()
-        logits = o.w4a16_matmul(x, w8, scales, nthreads=cores)[0, :V]
-        tok = int(np.argmax(logits))  # first maximum, as the reference's scan
-        times.append(time.perf_counter() - t)
-    med = float(np.median(times))
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"full lm_head K=1024 V={V}: oracle fp32 group formula over unpacked int8 (q-z) "
-                      f"+ argmax, {len(times)} calls, median {med * 1e3:.1f} ms/call",
-            "us_per_call": round(med * 1e6, 1), "token": tok}
-
-
-def cpu_baseline_generic(fn, nbytes_or_flops, unit, sample, budget_s=10.0):
-    cores = min(16, os.cpu_count() or 1)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 20):
-        t = time.perf_counter()
-        fn(cores)
-        times.append(time.perf_counter() - t)
-    med = float(np.median(times))
+def gpu_result(name, kernel, amount, unit, bound, launch, n_sets, steps, extra=None):
+    """Times one configuration: back-to-back mean (value, roofline) and the
+    per-launch median."""
+    per = time_graph(launch, n_sets, steps)
+    pl = np.array(time_per_launch(launch, n_sets))
     scale = 1e9 if unit == "GB/s" else 1e12
-    return {"value": round(nbytes_or_flops / med / scale, 4), "unit": unit, "cores": cores, "kind": "port",
-            "sample": f"{sample}, {len(times)} calls, median {med * 1e3:.2f} ms/call", "us_per_call": round(med * 1e6, 1)}
+    value = amount / (per / 1e3) / scale
+    peak = HBM_PEAK_GBS if bound == "hbm" else (INT8_MFMA_PEAK_TOPS if unit == "TOP/s" else FP16_MFMA_PEAK_TFLOPS)
+    r = {"kernel": kernel, "us_per_call": round(per * 1e3, 3), "value": round(value, 2), "unit": unit,
+         "kernel_us_median": round(float(np.median(pl)) * 1e3, 3), "kernel_us_mean": round(float(pl.mean()) * 1e3, 3),
+         "per_launch_samples": int(pl.size), "back_to_back_launches": steps,
+         "roofline": {"bound": bound, "achieved": round(value, 2), "peak": peak, "unit": unit,
+                      "frac": round(value / peak, 4), "traffic": traffic_from_profiles(name),
+                      "algorithmic_per_launch": amount}}
+    if extra:
+        r.update(extra)
+    log(f"[{name}] {r['us_per_call']} us/call back to back, median {r['kernel_us_median']} us per launch, "
+        f"{r['value']} {unit} ({100 * r['roofline']['frac']:.1f}% of peak)")
+    return r
 
 
 # --------------------------------------------------------------------------- #
-# workloads                                                                    #
+# CPU baseline: the oracle's restatement of the reference's CPU path           #
 # --------------------------------------------------------------------------- #
-def w4a16_bytes(K, N):
-    G = K // 128
-    return K * N // 2 + G * N * 2 + G * N // 2
+def cpu_info():
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except AttributeError:
+        threads = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    # the GPU box grants 16 host threads per GPU
+    return {"nproc": os.cpu_count(), "affinity": threads, "threads_used": min(16, threads), "model": model}
 
 
-def wl_lm_head(pkg, args):
-    import torch
-    K, V, NW = 1024, 248094, 248096
-    copies = args.copies or 8
-    rng = np.random.default_rng(1)
-    t = time.perf_counter()
-    w = f16_normal(rng, (K, NW), 0.02)
-    x = f16_normal(rng, (1, K), 1.0)
-    qweight, qzeros, scales = pkg.quantize_int4(w)
-    del w
-    qw, sc, zr = pkg.pack_awq(qweight, qzeros, scales)
-    log(f"[lm_head] synthetic weights quantised + packed in {time.perf_counter() - t:.1f} s")
-    base = pkg.W4A16QuantizedWeight.from_packed(qw, sc, zr, K, NW, 0)
-    heads = [pkg.LmHeadW4A16(base, V)]
-    for _ in range(copies - 1):
-        wc = pkg.W4A16QuantizedWeight(base.qweight.clone(), base.scales.clone(), base.zeros.clone(), K, NW, 0)
-        heads.append(pkg.LmHeadW4A16(wc, V))
-    xd = to_dev_f16(x)
-    logits = torch.empty(V, dtype=torch.float16, device="cuda")
-    nbytes = K * V // 2 + (K // 128) * V * 2 + (K // 128) * V // 2 + 2 * V + 2 * K
-    # one step = one launch of the fused GEMV + argmax kernel, so the step
-    # timing is also the dominant kernel's average launch duration
-    # Launched directly from bound launchers (arguments resolved once): the
-    # ~27 us step keeps the GPU ahead of the host, and graph replay was
-    # measured to lengthen this kernel by 0.5-1.4 us.
-    tree_fns = [h.bind(xd, logits) for h in heads]
-    tree = lambda i: tree_fns[i]()
-    # host-finished route (what lm_head_greedy_w4a16 runs): the step is the GEMV
-    # leaving tagged slot maxima; the 64-way fold happens on the host after the
-    # copy it makes anyway
-    slot_fns = [h.bind(xd, logits, route="slots") for h in heads]
-    slots = lambda i: slot_fns[i]()
-    main, other = (slots, tree) if args.argmax == "slots" else (tree, slots)
-    timer = time_steps if args.graph else time_direct
-    total_ms, kms = timer(main, copies, args.steps, args.warmup)
-    alt_ms, _ = timer(other, copies, args.steps, args.warmup)
-    token = heads[0](xd) if args.argmax == "slots" else int(heads[0].launch(xd, logits).item())
-    alt_name = "tree" if args.argmax == "slots" else "slots"
-    res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
-               config={"workload": "w4a16_lm_head_gemv_argmax", "M": 1, "K": K, "V": V, "argmax": args.argmax,
-                       "launch": "graph" if args.graph else "direct",
-                       "weight_copies_rotated": copies, "rotated_bytes": copies * (qw.nbytes + sc.nbytes + zr.nbytes),
-                       "algorithmic_bytes_per_step": nbytes, "token": token},
-               alt={alt_name: {"us_per_call": round(alt_ms / args.steps * 1e3, 2),
-                               "value": round(nbytes / (alt_ms / args.steps / 1e3) / 1e9, 2)}},
-               dtype="w4a16 (f16 x int4, f32 accumulate)",
-               kernel=f"w4a16_lm_head_kernel<16,{'kLmSlots' if args.argmax == 'slots' else 'kLmTree'}> (GEMV + fused argmax)")
-    if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline_lm_head(x, qweight, qzeros, scales, V, nbytes)
-    return res
+def _median_time(fn, budget_s, max_reps=31):
+    fn()                                           # warmup
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < max_reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return float(np.median(times)), len(times)
 
 
-def wl_gemv1(pkg, args):
-    import torch
-    K = N = 1024
-    sets = args.copies or 1024          # 1024 x 0.55 MB = 562 MB rotated
-    rng = np.random.default_rng(1)
-    w = f16_normal(rng, (K, N), 0.02)
-    x = f16_normal(rng, (1, K), 1.0)
-    qweight, qzeros, scales = pkg.quantize_int4(w)
-    base = pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales)
-    ws = [base] + [pkg.W4A16QuantizedWeight(base.qweight.clone(), base.scales.clone(), base.zeros.clone(), K, N, 0)
-                   for _ in range(sets - 1)]
-    xd = to_dev_f16(x)
-    out = torch.empty((1, N), dtype=torch.float16, device="cuda")
-    nbytes = w4a16_bytes(K, N) + 2 * K + 2 * N
-    total_ms, _ = time_steps(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps, args.warmup)
-    kms = time_each_launch(lambda i: pkg.matmul_w4a16(xd, ws[i], out), sets, args.steps)
-    res = dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
-               config={"workload": "w4a16_gemv_1024x1024", "M": 1, "K": K, "N": N, "weight_sets_rotated": sets},
-               dtype="w4a16 (f16 x int4, f32 accumulate)", kernel="w4a16_gemv_kernel")
-    if not args.no_cpu:
-        sys.path.insert(0, str(ROOT / "tests"))
-        from helpers import load_oracle
+def cpu_baseline(fn, amount_1, amount_all, unit, sample_1, sample_all, info, budget_s=1.0):
+    """fn(nthreads) runs the sample; amount_* its bytes (or FLOPs) for one
+    thread and for all threads.  `value` is the all-threads rate."""
+    scale = 1e9 if unit == "GB/s" else 1e12
+    t1, n1 = _median_time(lambda: fn(1, False), budget_s)
+    ta, na = _median_time(lambda: fn(info["threads_used"], True), budget_s)
+    digits = 3 if unit == "GB/s" else 7
+    return {"value": round(amount_all / ta / scale, digits), "unit": unit, "cores": info["threads_used"],
+            "kind": "port",
+            "sample": f"all threads: {sample_all}, median of {na} calls, {ta * 1e3:.2f} ms/call; "
+                      f"one thread: {sample_1}, median of {n1} calls, {t1 * 1e3:.2f} ms/call",
+            "one_thread": {"value": round(amount_1 / t1 / scale, digits), "ms_per_call": round(t1 * 1e3, 3)},
+            "all_threads": {"value": round(amount_all / ta / scale, digits), "ms_per_call": round(ta * 1e3, 3)},
+            "nproc": info["nproc"], "cpu_model": info["model"]}
+
+
+# --------------------------------------------------------------------------- #
+# configurations                                                               #
+# --------------------------------------------------------------------------- #
+class Cfg:
+    """One configuration: set up, time on the GPU, time the CPU baseline."""
+
+    def __init__(self, pkg, args, info):
+        self.pkg, self.args, self.info = pkg, args, info
+
+
+def _clone_w4(pkg, base, n):
+    return [base] + [pkg.W4A16QuantizedWeight(base.qweight.clone(), base.scales.clone(), base.zeros.clone(), base.K,
+                                              base.N, base.zero_bias) for _ in range(n - 1)]
+
+
+class Gemv1(Cfg):
+    name = "w4a16_gemv_1024x1024"
+
+    def setup(self):
+        import torch
+        pkg = self.pkg
+        K = N = 1024
+        self.K, self.N = K, N
+        rng = np.random.default_rng(1)
+        self.x = f16_normal(rng, (1, K), 1.0)
+        self.qweight, self.qzeros, self.scales = pkg.quantize_int4(f16_normal(rng, (K, N), 0.02))
+        base = pkg.W4A16QuantizedWeight.from_awq(self.qweight, self.qzeros, self.scales)
+        self.ws = _clone_w4(pkg, base, self.args.copies or 1024)          # 1024 x 0.55 MB = 562 MB
+        self.xd = to_dev_f16(self.x)
+        self.out = torch.empty((1, N), dtype=torch.float16, device="cuda")
+        self.bytes = w4a16_bytes(K, N) + 2 * K + 2 * N
+
+    def gpu(self):
+        pkg, ws, xd, out = self.pkg, self.ws, self.xd, self.out
+        return gpu_result(self.name, "w4a16_gemv_kernel<8,1,none>", self.bytes, "GB/s", "hbm",
+                          lambda i: pkg.matmul_w4a16(xd, ws[i], out), len(ws), 200,
+                          {"config": {"M": 1, "K": self.K, "N": self.N, "weight_sets_rotated": len(ws),
+                                      "algorithmic_bytes": self.bytes}})
+
+    def cpu(self):
         o = load_oracle()
-        w8 = o.unpack_awq(qweight, qzeros)
-        res["cpu_baseline"] = cpu_baseline_generic(lambda c: o.w4a16_matmul(x, w8, scales, nthreads=1), nbytes, "GB/s",
-                                                   "K=N=1024 GEMV, oracle fp32 group formula, 1 thread", 5.0)
-        res["cpu_baseline"]["cores"] = 1
-    return res
+        w8 = o.unpack_awq(self.qweight, self.qzeros)
+        fn = lambda c, _: o.w4a16_matmul(self.x, w8, self.scales, nthreads=c)
+        s = "K=N=1024 GEMV (fp32 group formula over unpacked int8 q-z)"
+        return cpu_baseline(fn, self.bytes, self.bytes, "GB/s", s, s, self.info)
 
 
-def wl_mlp(pkg, args, mode="block"):
-    """The decode MLP block: gate/up 1024->3584, silu*mul, down 3584->1024, 24 layer sets x 4 copies.
-    block (default): the whole block in one launch (DecodeMlpW4A16); two: one
-    gate+up+silu*mul launch and the down GEMV; unfused: the reference's four
-    launches (gate, up, silu_mul, down)."""
+class Mlp(Cfg):
+    name = "w4a16_mlp_block_decode"
+
+    def setup(self):
+        import torch
+        pkg = self.pkg
+        H, I = 1024, 3584
+        self.H, self.I = H, I
+        layers, self.host = [], []
+        for s in range(24):
+            rng = np.random.default_rng(100 + s)
+            mats, hm = [], []
+            for (K, N) in ((H, I), (H, I), (I, H)):
+                q = pkg.quantize_int4(f16_normal(rng, (K, N), 0.02))
+                hm.append(q)
+                mats.append(pkg.W4A16QuantizedWeight.from_awq(*q))
+            layers.append(mats)
+            if s == 0:
+                self.host = hm
+        sets = list(layers)
+        for _ in range((self.args.copies or 4) - 1):
+            sets += [[pkg.W4A16QuantizedWeight(m.qweight.clone(), m.scales.clone(), m.zeros.clone(), m.K, m.N, 0)
+                      for m in L] for L in layers]
+        self.sets = sets
+        self.mlps = [pkg.DecodeMlpW4A16(*L) for L in sets]
+        self.x = f16_normal(np.random.default_rng(1), (1, H), 1.0)
+        self.xd = to_dev_f16(self.x)
+        self.y = torch.empty((1, H), dtype=torch.float16, device="cuda")
+        self.bytes = 2 * w4a16_bytes(H, I) + w4a16_bytes(I, H) + 2 * H + 2 * H
+
+    def gpu(self):
+        mlps, xd, y = self.mlps, self.xd, self.y
+        r = gpu_result(self.name, "w4a16_mlp_kernel (gate, up, silu*mul, down in one launch)", self.bytes, "GB/s",
+                       "hbm", lambda i: mlps[i](xd, y), len(mlps), 200,
+                       {"config": {"M": 1, "hidden": self.H, "intermediate": self.I,
+                                   "layer_sets_rotated": len(mlps), "algorithmic_bytes": self.bytes}})
+        if any(m.act_wait_gave_up() for m in mlps) or not all(m.one_launch for m in mlps):
+            raise RuntimeError("decode MLP: the one-launch kernel did not run cleanly")
+        return r
+
+    def cpu(self):
+        o = load_oracle()
+        (gq, gz, gs), (uq, uz, us), (dq, dz, ds) = self.host
+        wg, wu, wd = o.unpack_awq(gq, gz), o.unpack_awq(uq, uz), o.unpack_awq(dq, dz)
+
+        def block(c, _):
+            g = o.f2h_rne(o.w4a16_matmul(self.x, wg, gs, nthreads=c))
+            u = o.f2h_rne(o.w4a16_matmul(self.x, wu, us, nthreads=c))
+            a = o.silu_mul(g, u)
+            return o.w4a16_matmul(a, wd, ds, nthreads=c)
+        s = "one decode MLP block H=1024 I=3584 (gate, up, silu*mul, down)"
+        return cpu_baseline(block, self.bytes, self.bytes, "GB/s", s, s, self.info)
+
+
+class Prefill(Cfg):
+    def __init__(self, pkg, args, info, M, K, N):
+        super().__init__(pkg, args, info)
+        self.M, self.K, self.N = M, K, N
+        self.name = f"w4a16_prefill_gemm_M{M}_K{K}_N{N}"
+
+    def setup(self, weights=None):
+        import torch
+        pkg, M, K, N = self.pkg, self.M, self.K, self.N
+        if weights is None:
+            rng = np.random.default_rng(K * 7 + N)
+            q = pkg.quantize_int4(f16_normal(rng, (K, N), 0.02))
+            base = pkg.W4A16QuantizedWeight.from_awq(*q)
+            weights = (q, _clone_w4(pkg, base, self.args.copies or 300))     # 300 x 1.9 MB = 572 MB
+        self.host, self.ws = weights
+        self.x = f16_normal(np.random.default_rng(M + K), (M, K), 1.0)
+        self.xd = to_dev_f16(self.x)
+        self.out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        self.flops = 2.0 * M * K * N
+        return weights
+
+    def gpu(self):
+        pkg, ws, xd, out = self.pkg, self.ws, self.xd, self.out
+        return gpu_result(self.name, "w4a16_gemm_kernel", self.flops, "TFLOP/s", "mfma",
+                          lambda i: pkg.matmul_w4a16(xd, ws[i], out), len(ws), 200,
+                          {"config": {"M": self.M, "K": self.K, "N": self.N, "weight_sets_rotated": len(ws),
+                                      "flops": self.flops}})
+
+    def cpu(self):
+        o = load_oracle()
+        qw, qz, sc = self.host
+        w8 = o.unpack_awq(qw, qz)
+        m1, ma = 4, 32
+        fn = lambda c, full: o.w4a16_matmul(self.x[: (ma if full else m1)], w8, sc, nthreads=c)
+        per_row = 2.0 * self.K * self.N
+        return cpu_baseline(fn, m1 * per_row, ma * per_row, "TFLOP/s",
+                            f"{m1} of the {self.M} rows, K={self.K} N={self.N}",
+                            f"{ma} of the {self.M} rows, K={self.K} N={self.N}", self.info)
+
+
+class W8a8(Cfg):
+    def __init__(self, pkg, args, info, M, shared=None):
+        super().__init__(pkg, args, info)
+        self.M, self.K, self.N = M, 1024, 3584
+        self.name = f"w8a8_gemm_M{M}_K1024_N3584"
+        self.shared = shared
+
+    def setup(self):
+        import torch
+        pkg, M, K, N = self.pkg, self.M, self.K, self.N
+        if self.shared is None:
+            rng = np.random.default_rng(11)
+            wf = f16_normal(rng, (K, N), 0.02)
+            base = pkg.quantize_dense_weight_w8a8(to_dev_f16(wf))
+            sets = [base] + [pkg.W8A8QuantizedWeight(base.w_int8.clone(), base.w_scale.clone(),
+                                                     base.w_scale_f32.clone(), K, N, base.layout)
+                             for _ in range((self.args.copies or 160) - 1)]          # 160 x 3.7 MB = 590 MB
+            self.shared = (wf, sets)
+        self.wf, self.ws = self.shared
+        self.x = f16_normal(np.random.default_rng(500 + M), (M, K), 1.0)
+        self.xq, self.xs, _ = pkg.w8a8_quantize(to_dev_f16(self.x))
+        self.out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        self.flops = 2.0 * M * K * N
+        self.bytes = K * N + 4 * N + M * K + 4 * M + 2 * M * N
+        return self.shared
+
+    def gpu(self):
+        pkg, ws, xq, xs, out = self.pkg, self.ws, self.xq, self.xs, self.out
+        M = self.M
+        if M <= 4:
+            kernel, amount, unit, bound = "w8a8_tiled_gemv_kernel (v_dot4, fused fp16 epilogue)", self.bytes, "GB/s", "hbm"
+        else:
+            kernel, amount, unit, bound = "w8a8_tiled_gemm_kernel (int8 MFMA, fused fp16 epilogue)", self.flops, "TOP/s", "mfma"
+        r = gpu_result(self.name, kernel, amount, unit, bound, lambda i: pkg.matmul_w8a8(xq, xs, ws[i], out), len(ws),
+                       200, {"config": {"M": M, "K": self.K, "N": self.N, "weight_sets_rotated": len(ws),
+                                        "scales": "fp32 per-token and per-channel", "flops": self.flops,
+                                        "algorithmic_bytes": self.bytes}})
+        # the MFMA-side figure for every M, the HBM-side one for M = 1
+        r["tops"] = round(self.flops / (r["us_per_call"] / 1e6) / 1e12, 3)
+        return r
+
+    def cpu(self):
+        o = load_oracle()
+        q_o, s_o, _ = o.w8a8_quantize_act(self.x)
+        wq_o, ws_o, _ = o.w8a8_quantize_weight(self.wf)
+        m1 = min(self.M, 8)
+        ma = min(self.M, 64)
+
+        def fn(c, full):
+            m = ma if full else m1
+            return o.w8a8_dequant(o.gemm_i32(q_o[:m], wq_o, nthreads=c), s_o[:m], ws_o)
+        per_row = 2.0 * self.K * self.N
+        unit = "GB/s" if self.M <= 4 else "TOP/s"
+        if unit == "GB/s":
+            a1 = aa = self.bytes
+        else:
+            a1, aa = m1 * per_row, ma * per_row
+        return cpu_baseline(fn, a1, aa, unit, f"{m1} of the {self.M} rows (int32 GEMM + epilogue)",
+                            f"{ma} of the {self.M} rows (int32 GEMM + epilogue)", self.info)
+
+
+class LmHead(Cfg):
+    name = "w4a16_lm_head_gemv_argmax"
+
+    def setup(self):
+        import torch
+        pkg = self.pkg
+        K, V, NW = 1024, 248094, 248096
+        self.K, self.V = K, V
+        rng = np.random.default_rng(1)
+        t = time.perf_counter()
+        w = f16_normal(rng, (K, NW), 0.02)
+        self.x = f16_normal(rng, (1, K), 1.0)
+        self.qweight, self.qzeros, self.scales = pkg.quantize_int4(w)
+        del w
+        qw, sc, zr = pkg.pack_awq(self.qweight, self.qzeros, self.scales)
+        log(f"[lm_head] synthetic weights quantised + packed in {time.perf_counter() - t:.1f} s")
+        base = pkg.W4A16QuantizedWeight.from_packed(qw, sc, zr, K, NW, 0)
+        copies = self.args.copies or 8
+        self.heads = [pkg.LmHeadW4A16(w_, V) for w_ in _clone_w4(pkg, base, copies)]
+        self.rotated = copies * (qw.nbytes + sc.nbytes + zr.nbytes)
+        self.xd = to_dev_f16(self.x)
+        self.logits = torch.empty(V, dtype=torch.float16, device="cuda")
+        self.bytes = K * V // 2 + (K // 128) * V * 2 + (K // 128) * V // 2 + 2 * V + 2 * K
+        # bound launchers: arguments resolved once, ~4 us of host time per launch
+        self.tree = [h.bind(self.xd, self.logits) for h in self.heads]
+        self.slots = [h.bind(self.xd, self.logits, route="slots") for h in self.heads]
+
+    def gpu_steps(self, steps, warmup, route):
+        fns = self.tree if route == "tree" else self.slots
+        return time_direct(lambda i: fns[i](), len(fns), steps, warmup)
+
+    def per_launch(self, route):
+        fns = self.tree if route == "tree" else self.slots
+        return np.array(time_per_launch(lambda i: fns[i](), len(fns), 200, host_us=15.0))
+
+    def token(self):
+        return int(self.heads[0].launch(self.xd, self.logits).item())
+
+    def cpu(self):
+        o = load_oracle()
+        w8 = o.unpack_awq(self.qweight, self.qzeros)
+        V = self.V
+
+        def fn(c, _):
+            logits = o.f2h_rne(o.w4a16_matmul(self.x, w8, self.scales, nthreads=c)[0, :V])
+            return o.argmax_f16(logits)
+        s = f"full lm_head K=1024 V={V}: fp32 group formula over unpacked int8 (q-z) + first-max argmax"
+        return cpu_baseline(fn, self.bytes, self.bytes, "GB/s", s, s, self.info, budget_s=4.0)
+
+
+# --------------------------------------------------------------------------- #
+# the default run                                                              #
+# --------------------------------------------------------------------------- #
+PREFILL_SHAPES = [(M, K, N) for M in (128, 512, 2048) for (K, N) in ((1024, 3584), (3584, 1024))]
+
+
+def run_all(pkg, args, info):
     import torch
-    H, I = 1024, 3584
-    nsets, reps = 24, args.copies or 4
-    layers = []
-    for s in range(nsets):
-        rng = np.random.default_rng(100 + s)
-        mats = []
-        for (K, N) in ((H, I), (H, I), (I, H)):
-            qweight, qzeros, scales = pkg.quantize_int4(f16_normal(rng, (K, N), 0.02))
-            mats.append(pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales))
-        layers.append(mats)
-    sets = list(layers)
-    for _ in range(reps - 1):
-        sets += [[pkg.W4A16QuantizedWeight(m.qweight.clone(), m.scales.clone(), m.zeros.clone(), m.K, m.N, 0)
-                  for m in L] for L in layers]
-    x = to_dev_f16(f16_normal(np.random.default_rng(1), (1, H), 1.0))
-    g = torch.empty((1, I), dtype=torch.float16, device="cuda")
-    u = torch.empty_like(g)
-    a = torch.empty_like(g)
-    y = torch.empty((1, H), dtype=torch.float16, device="cuda")
-    mlps = [pkg.DecodeMlpW4A16(*L) for L in sets] if mode == "block" else None
+    t0 = time.perf_counter()
+    gemv, mlp, lm = Gemv1(pkg, args, info), Mlp(pkg, args, info), LmHead(pkg, args, info)
+    pre = [Prefill(pkg, args, info, *s) for s in PREFILL_SHAPES]
+    w8 = [W8a8(pkg, args, info, M) for M in (1, 256, 1024)]
+    gemv.setup()
+    mlp.setup()
+    shared = {}
+    for p in pre:
+        shared[(p.K, p.N)] = p.setup(shared.get((p.K, p.N)))
+    sh8 = None
+    for c in w8:
+        c.shared = sh8
+        sh8 = c.setup()
+    lm.setup()
+    log(f"[setup] {time.perf_counter() - t0:.1f} s")
+
+    cpu = {}
+    if not args.no_cpu:
+        t = time.perf_counter()
+        for c in [gemv, mlp, lm, *pre, *w8]:
+            cpu[c.name] = c.cpu()
+        log(f"[cpu baselines] {time.perf_counter() - t:.1f} s on {info['threads_used']} threads ({info['model']})")
+
+    configs = {}
+    configs["1_gemv_K1024_N1024"] = gemv.gpu()
+    configs["2_mlp_block_H1024_I3584"] = mlp.gpu()
+    configs["4_prefill_gemm"] = {p.name: p.gpu() for p in pre}
+    configs["5_w8a8_gemm_K1024_N3584"] = {c.name: c.gpu() for c in w8}
+    for key, c in (("1_gemv_K1024_N1024", gemv), ("2_mlp_block_H1024_I3584", mlp)):
+        configs[key]["cpu_baseline"] = cpu.get(c.name)
+    for p in pre:
+        configs["4_prefill_gemm"][p.name]["cpu_baseline"] = cpu.get(p.name)
+    for c in w8:
+        configs["5_w8a8_gemm_K1024_N3584"][c.name]["cpu_baseline"] = cpu.get(c.name)
+
+    # headline: the lm_head, W untimed steps then exactly K timed steps
+    route, other = (args.argmax, "slots" if args.argmax == "tree" else "tree")
+    lm.gpu_steps(200, 20, route)                 # the other configurations ran on other shapes: settle clocks
+    total_ms = lm.gpu_steps(args.steps, args.warmup, route)
+    alt_ms = lm.gpu_steps(max(args.steps, 200), args.warmup, other)
+    pl = lm.per_launch(route)
+    token = lm.token()
+    torch.cuda.synchronize()
+    ms = total_ms / args.steps
+    value = lm.bytes / (ms / 1e3) / 1e9
+    kernel = f"w4a16_lm_head_kernel<16,{'kLmTree' if route == 'tree' else 'kLmSlots'}> (GEMV + fused argmax)"
+    lm_entry = {"kernel": kernel, "us_per_call": round(ms * 1e3, 3), "value": round(value, 2), "unit": "GB/s",
+                "kernel_us_median": round(float(np.median(pl)) * 1e3, 3),
+                "kernel_us_mean": round(float(pl.mean()) * 1e3, 3), "per_launch_samples": int(pl.size),
+                "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(lm.name),
+                             "algorithmic_per_launch": lm.bytes},
+                "alt_route": {other: {"us_per_call": round(alt_ms / max(args.steps, 200) * 1e3, 3),
+                                      "value": round(lm.bytes / (alt_ms / max(args.steps, 200) / 1e3) / 1e9, 2)}},
+                "config": {"M": 1, "K": lm.K, "V": lm.V, "argmax": route, "launch": "direct",
+                           "weight_copies_rotated": len(lm.heads), "rotated_bytes": lm.rotated,
+                           "algorithmic_bytes": lm.bytes, "token": token},
+                "cpu_baseline": cpu.get(lm.name)}
+    configs["3_lm_head_K1024_V248094"] = lm_entry
+    log(f"[lm_head] {lm_entry['us_per_call']} us/step over {args.steps} steps, median {lm_entry['kernel_us_median']} "
+        f"us per launch, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak)")
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16 (f16 x int4, f32 accumulate)",
+        "data": "synthetic (seeded N(0,1) fp16 activations, N(0,0.02) fp16 weights quantised in-build)",
+        "config": {"workload": lm.name, **lm_entry["config"]},
+        "roofline": {k: v for k, v in lm_entry["roofline"].items() if k != "algorithmic_per_launch"} | {
+            "kernel": kernel, "kernel_us_mean": lm_entry["kernel_us_mean"],
+            "kernel_us_median": lm_entry["kernel_us_median"]},
+        "cpu_baseline": lm_entry["cpu_baseline"],
+        "configs": configs,
+        "host": info,
+    }
+
+
+# --------------------------------------------------------------------------- #
+# single workloads (profiling runs)                                            #
+# --------------------------------------------------------------------------- #
+def single(pkg, args, info, which):
+    """One configuration (or comparison workload) as its own JSON line."""
+    import torch
+    if which == "lm_head":
+        lm = LmHead(pkg, args, info)
+        lm.setup()
+        total = lm.gpu_steps(args.steps, args.warmup, args.argmax)
+        ms = total / args.steps
+        return {"workload": lm.name, "us_per_call": round(ms * 1e3, 3),
+                "value": round(lm.bytes / (ms / 1e3) / 1e9, 2), "unit": "GB/s"}
+    if which == "gemv1":
+        c = Gemv1(pkg, args, info)
+    elif which == "mlp":
+        c = Mlp(pkg, args, info)
+    elif which == "prefill":
+        c = Prefill(pkg, args, info, args.M or 2048, args.K or 1024, args.N or 3584)
+    elif which == "w8a8":
+        c = W8a8(pkg, args, info, args.M or 1024)
+    else:
+        return EXTRA[which](pkg, args)
+    c.setup()
+    r = c.gpu()
+    if not args.no_cpu:
+        r["cpu_baseline"] = c.cpu()
+    torch.cuda.synchronize()
+    return {"workload": c.name, **r}
+
+
+def _mlp_variant(pkg, args, mode):
+    """Comparison decode-MLP launch sequences over 96 rotated W4A16 layer sets:
+    two launches (gate+up+silu*mul, down) or the reference's four."""
+    import torch
+    m = Mlp(pkg, args, None)
+    m.setup()
+    H, I = m.H, m.I
+    a = torch.empty((1, I), dtype=torch.float16, device="cuda")
+    g, u = torch.empty_like(a), torch.empty_like(a)
 
     def block(i):
-        L = sets[i]
-        if mode == "block":
-            mlps[i](x, y)
-            return
+        L = m.sets[i]
         if mode == "two":
-            pkg.mlp_gate_up_silu_w4a16(x, L[0], L[1], a)
+            pkg.mlp_gate_up_silu_w4a16(m.xd, L[0], L[1], a)
         else:
-            pkg.matmul_w4a16(x, L[0], g)
-            pkg.matmul_w4a16(x, L[1], u)
+            pkg.matmul_w4a16(m.xd, L[0], g)
+            pkg.matmul_w4a16(m.xd, L[1], u)
             pkg.silu_mul(g, u, a)
-        pkg.matmul_w4a16(a, L[2], y)
-
-    nbytes = 2 * w4a16_bytes(H, I) + w4a16_bytes(I, H) + 2 * H * 2 + 2 * I * 2 * 3 + 2 * H
-    total_ms, _ = time_steps(block, len(sets), args.steps, args.warmup)
-    kms = time_each_launch(block, len(sets), args.steps)
-    if mlps is not None and any(m.act_wait_gave_up() for m in mlps):
-        raise RuntimeError("decode MLP: a wait for act words gave up")
-    suffix = {"block": "", "two": "_2launch", "unfused": "_unfused"}[mode]
-    kernel = {"block": "w4a16_mlp_kernel (whole block, one launch)",
-              "two": "mlp block (gate+up+silu launch, down GEMV)", "unfused": "mlp block (4 launches)"}[mode]
-    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
-                config={"workload": "w4a16_mlp_block_decode" + suffix, "M": 1, "hidden": H,
-                        "intermediate": I, "weight_sets_rotated": len(sets)},
-                dtype="w4a16 (f16 x int4, f32 accumulate)", kernel=kernel)
+        pkg.matmul_w4a16(a, L[2], m.y)
+    return {"workload": f"w4a16_mlp_block_decode_{mode}", **gpu_result(
+        f"mlp_{mode}", f"mlp block ({mode})", m.bytes, "GB/s", "hbm", block, len(m.sets), 200)}
 
 
-def wl_qkvz(pkg, args, fused=True):
-    """The linear-attention layer's input projections at decode (qkv
-    1024->6144 and z 1024->2048 from the same normed row), 64 rotated layer
-    sets: one multi-projection launch, or two GEMVs."""
-    import torch
-    H = 1024
-    nsets = args.copies or 64
-    sets = []
-    for s in range(nsets):
-        rng = np.random.default_rng(300 + s)
-        mats = []
-        for N in (6144, 2048):
-            qweight, qzeros, scales = pkg.quantize_int4(f16_normal(rng, (H, N), 0.02))
-            mats.append(pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales))
-        sets.append(mats)
-    x = to_dev_f16(f16_normal(np.random.default_rng(1), (1, H), 1.0))
-    outs = [torch.empty((1, 6144), dtype=torch.float16, device="cuda"),
-            torch.empty((1, 2048), dtype=torch.float16, device="cuda")]
-
-    def step(i):
-        if fused:
-            pkg.matmul_w4a16_multi(x, sets[i], outs)
-        else:
-            pkg.matmul_w4a16(x, sets[i][0], outs[0])
-            pkg.matmul_w4a16(x, sets[i][1], outs[1])
-
-    nbytes = w4a16_bytes(H, 6144) + w4a16_bytes(H, 2048) + 2 * H + 2 * (6144 + 2048)
-    total_ms, _ = time_steps(step, len(sets), args.steps, args.warmup)
-    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=[total_ms / args.steps], unit="GB/s", bound="hbm",
-                config={"workload": "w4a16_qkv_z_decode" + ("" if fused else "_unfused"), "M": 1, "K": H,
-                        "N": [6144, 2048], "weight_sets_rotated": len(sets)},
-                dtype="w4a16 (f16 x int4, f32 accumulate)",
-                kernel="w4a16_gemv_multi_kernel" if fused else "w4a16_gemv_kernel x2")
-
-
-def wl_mlp_w8a8(pkg, args, mode="block"):
-    """The decode MLP block over W8A8 weights (gate/up 1024->3584, down
-    3584->1024), 32 layer sets (352 MB, past the MALL), from the normed fp16
-    row: block = the whole block in one launch (DecodeMlpW8A8); fused =
-    quantise x, one gate+up+silu*mul launch, quantise act, down; unfused = the
-    reference's quantise, gate, up, silu_mul, quantise, down."""
+def _mlp_w8a8(pkg, args, mode):
+    """The W8A8 decode MLP block over 32 rotated layer sets (352 MB): one launch
+    (reference or fp32 scales) or the reference's six launches."""
     import torch
     H, I = 1024, 3584
-    nsets = args.copies or 32
     sets = []
-    for s in range(nsets):
+    for s in range(args.copies or 32):
         rng = np.random.default_rng(200 + s)
         sets.append([pkg.quantize_dense_weight_w8a8(to_dev_f16(f16_normal(rng, (K, N), 0.02)))
                      for (K, N) in ((H, I), (H, I), (I, H))])
     x = to_dev_f16(f16_normal(np.random.default_rng(1), (1, H), 1.0))
-    xq = torch.empty((1, H), dtype=torch.int8, device="cuda")
-    xs = torch.empty(1, dtype=torch.float32, device="cuda")
-    g = torch.empty((1, I), dtype=torch.float16, device="cuda")
-    u = torch.empty_like(g)
-    a = torch.empty_like(g)
-    aq = torch.empty((1, I), dtype=torch.int8, device="cuda")
-    asc = torch.empty(1, dtype=torch.float32, device="cuda")
     y = torch.empty((1, H), dtype=torch.float16, device="cuda")
-    fused = mode == "fused"
-    mlps = [pkg.DecodeMlpW8A8(*L) for L in sets] if mode == "block" else None
-
-    def block(i):
-        L = sets[i]
-        if mlps is not None:
-            mlps[i](x, y)
-            return
-        pkg.w8a8_quantize(x, xq, xs)
-        if fused:
-            pkg.mlp_gate_up_silu_w8a8(xq, xs, L[0], L[1], a)
-        else:
-            pkg.matmul_w8a8(xq, xs, L[0], g)
-            pkg.matmul_w8a8(xq, xs, L[1], u)
-            pkg.silu_mul(g, u, a)
-        pkg.w8a8_quantize(a, aq, asc)
-        pkg.matmul_w8a8(aq, asc, L[2], y)
-
-    nbytes = 3 * H * I + 2 * (2 * I + I) * 4 + (2 * H + H) + (2 * I + I) * 2 + 2 * H
-    total_ms, _ = time_steps(block, len(sets), args.steps, args.warmup)
-    if mlps is not None and (any(m.wait_gave_up() for m in mlps) or not all(m.one_launch for m in mlps)):
-        raise RuntimeError("W8A8 decode MLP: the one-launch kernel did not run cleanly")
-    suffix = {"block": "", "fused": "_4launch", "unfused": "_unfused"}[mode]
-    kernel = {"block": "w8a8_mlp_kernel (whole block, one launch)", "fused": "w8a8 mlp block (4 launches)",
-              "unfused": "w8a8 mlp block (6 launches)"}[mode]
-    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=[total_ms / args.steps], unit="GB/s", bound="hbm",
-                config={"workload": "w8a8_mlp_block_decode" + suffix, "M": 1, "hidden": H,
-                        "intermediate": I, "weight_sets_rotated": len(sets)},
-                dtype="int8 (i32 accumulate, fused f16 epilogue)", kernel=kernel)
-
-
-def wl_prefill(pkg, args):
-    import torch
-    M, K, N = args.M or 2048, args.K or 1024, args.N or 3584
-    rng = np.random.default_rng(1)
-    qweight, qzeros, scales = pkg.quantize_int4(f16_normal(rng, (K, N), 0.02))
-    w = pkg.W4A16QuantizedWeight.from_awq(qweight, qzeros, scales)
-    x = to_dev_f16(f16_normal(rng, (M, K), 1.0))
-    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
-    flops = 2.0 * M * K * N
-    total_ms, _ = time_steps(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps, args.warmup)
-    kms = time_each_launch(lambda i: pkg.matmul_w4a16(x, w, out), 1, args.steps)
-    return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TFLOP/s", bound="mfma",
-                config={"workload": "w4a16_prefill_gemm", "M": M, "K": K, "N": N},
-                dtype="w4a16 (f16 MFMA, f32 accumulate)", kernel="w4a16_gemm_kernel")
-
-
-def wl_norm_quant(pkg, args, fused=True):
-    """Decode-time RMSNorm + W8A8 activation quantisation (M=1, H=1024 by
-    default): one fused launch, or rms_norm then w8a8_quantize."""
-    import torch
-    M, H = args.M or 1, args.K or 1024
-    rng = np.random.default_rng(1)
-    sets = 64
-    xs = [to_dev_f16(f16_normal(rng, (M, H), 1.0)) for _ in range(sets)]
-    g = to_dev_f16(f16_normal(rng, H, 1.0))
-    normed = torch.empty((M, H), dtype=torch.float16, device="cuda")
-    xq = torch.empty((M, H), dtype=torch.int8, device="cuda")
-    sc = torch.empty(M, dtype=torch.float32, device="cuda")
-    L = pkg.lib()
-    if fused:
-        fn = lambda i: L.mcv_rms_norm_w8a8_quantize(xs[i].data_ptr(), g.data_ptr(), M, H, 1e-6, normed.data_ptr(),
-                                                    xq.data_ptr(), sc.data_ptr(), None,
-                                                    torch.cuda.current_stream().cuda_stream)
+    if mode in ("block", "block_f32"):
+        mlps = [pkg.DecodeMlpW8A8(*L, precision="f32" if mode == "block_f32" else "reference") for L in sets]
+        fn = lambda i: mlps[i](x, y)
     else:
+        xq = torch.empty((1, H), dtype=torch.int8, device="cuda")
+        aq = torch.empty((1, I), dtype=torch.int8, device="cuda")
+        xs, as_ = (torch.empty(1, dtype=torch.float16, device="cuda") for _ in range(2))
+        g, u, a = (torch.empty((1, I), dtype=torch.float16, device="cuda") for _ in range(3))
+
         def fn(i):
-            L.mcv_rms_norm(xs[i].data_ptr(), g.data_ptr(), M, H, 1e-6, normed.data_ptr(),
-                           torch.cuda.current_stream().cuda_stream)
-            L.mcv_w8a8_quantize_act(normed.data_ptr(), M, H, xq.data_ptr(), sc.data_ptr(), None,
-                                    torch.cuda.current_stream().cuda_stream)
-    nbytes = M * (7 * H + 4) + 2 * H
-    total_ms, _ = time_steps(fn, sets, args.steps, args.warmup)
-    return dict(bytes=nbytes, total_ms=total_ms, kernel_ms=[total_ms / args.steps], unit="GB/s", bound="hbm",
-                config={"workload": "rms_norm_w8a8_quant" + ("" if fused else "_unfused"), "M": M, "H": H},
-                dtype="f16 -> int8", kernel="rms_norm_quant_kernel" if fused else "rms_norm_kernel + w8a8_quant_act_kernel")
+            L = sets[i]
+            pkg.w8a8_quantize(x, xq, pkg._NO_F32, xs)
+            pkg.matmul_w8a8(xq, xs, L[0], g, use_f32_scale=False)
+            pkg.matmul_w8a8(xq, xs, L[1], u, use_f32_scale=False)
+            pkg.silu_mul(g, u, a)
+            pkg.w8a8_quantize(a, aq, pkg._NO_F32, as_)
+            pkg.matmul_w8a8(aq, as_, L[2], y, use_f32_scale=False)
+    nbytes = 3 * H * I + 2 * (2 * I + I) + 2 * H + 2 * H
+    return {"workload": f"w8a8_mlp_block_decode_{mode}", **gpu_result(
+        f"mlp_w8a8_{mode}", f"w8a8 mlp ({mode})", nbytes, "GB/s", "hbm", fn, len(sets), 200)}
 
 
-def wl_vendor(pkg, args, int8=False):
-    """The vendor library's dense GEMM at the same shape (torch.matmul -> hipBLASLt
-    for fp16, torch._int_mm for int8): the yardstick for the quantised GEMMs,
-    which do strictly more work (dequant, epilogue) per output."""
+def _vendor(pkg, args, int8):
+    """The vendor library's dense GEMM at a prefill / W8A8 shape (torch.matmul
+    -> hipBLASLt, torch._int_mm), as a yardstick."""
     import torch
     M, K, N = args.M or (1024 if int8 else 2048), args.K or 1024, args.N or 3584
     g = torch.Generator(device="cuda")
@@ -472,124 +744,68 @@ def wl_vendor(pkg, args, int8=False):
         fn = lambda i: torch._int_mm(a, b)
     else:
         a = torch.randn(M, K, dtype=torch.float16, device="cuda", generator=g)
-        b = torch.randn(N, K, dtype=torch.float16, device="cuda", generator=g).t()   # column-major B
+        b = torch.randn(N, K, dtype=torch.float16, device="cuda", generator=g).t()
         c = torch.empty(M, N, dtype=torch.float16, device="cuda")
         fn = lambda i: torch.matmul(a, b, out=c)
-    flops = 2.0 * M * K * N
-    total_ms, _ = time_steps(fn, 1, args.steps, args.warmup)
-    kms = time_each_launch(fn, 1, args.steps)
-    return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TOP/s" if int8 else "TFLOP/s", bound="mfma",
-                config={"workload": "vendor_int8_gemm" if int8 else "vendor_f16_gemm", "M": M, "K": K, "N": N},
-                dtype="int8 (i32 accumulate)" if int8 else "f16 (f32 accumulate)",
-                kernel="torch._int_mm" if int8 else "torch.matmul (hipBLASLt)")
+    unit = "TOP/s" if int8 else "TFLOP/s"
+    return {"workload": f"vendor_{'int8' if int8 else 'f16'}_M{M}_K{K}_N{N}",
+            **gpu_result("vendor", "vendor GEMM", 2.0 * M * K * N, unit, "mfma", fn, 1, 200)}
 
 
-def wl_w8a8(pkg, args):
-    import torch
-    M, K, N = args.M or 1024, args.K or 1024, args.N or 3584
-    rng = np.random.default_rng(1)
-    wq = pkg.quantize_dense_weight_w8a8(to_dev_f16(f16_normal(rng, (K, N), 0.02)))
-    xq, xs, _ = pkg.w8a8_quantize(to_dev_f16(f16_normal(rng, (M, K), 1.0)))
-    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
-    flops = 2.0 * M * K * N
-    total_ms, _ = time_steps(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps, args.warmup)
-    kms = time_each_launch(lambda i: pkg.matmul_w8a8(xq, xs, wq, out), 1, args.steps)
-    return dict(bytes=flops, total_ms=total_ms, kernel_ms=kms, unit="TOP/s", bound="mfma",
-                config={"workload": "w8a8_gemm_fused", "M": M, "K": K, "N": N},
-                dtype="int8 (i32 accumulate, fused f16 epilogue)", kernel="w8a8_gemm_kernel<kn,f16>")
-
-
-def wl_copy(pkg, args):
-    """Calibration for the HBM counters: a plain 128 MiB device-to-device copy
-    (torch's copy kernel) reads and writes exactly 134,217,728 bytes."""
+def _copy(pkg, args):
+    """Calibration of the HBM counters: a 128 MiB device copy reads and writes
+    exactly 134,217,728 bytes each."""
     import torch
     n = 128 * 2**20
     src = [torch.ones(n, dtype=torch.uint8, device="cuda") for _ in range(4)]
     dst = torch.empty(n, dtype=torch.uint8, device="cuda")
-    total_ms, _ = time_steps(lambda i: dst.copy_(src[i]), 4, args.steps, args.warmup)
-    kms = time_each_launch(lambda i: dst.copy_(src[i]), 4, args.steps)
-    return dict(bytes=2 * n, total_ms=total_ms, kernel_ms=kms, unit="GB/s", bound="hbm",
-                config={"workload": "copy_128MiB_calibration", "bytes_read": n, "bytes_written": n},
-                dtype="u8", kernel="torch copy kernel")
+    return {"workload": "copy_128MiB_calibration",
+            **gpu_result("copy", "torch copy kernel", 2 * n, "GB/s", "hbm", lambda i: dst.copy_(src[i]), 4, 100)}
 
 
-WORKLOADS = {"lm_head": wl_lm_head, "gemv1": wl_gemv1, "mlp": wl_mlp,
-             "mlp_2launch": lambda pkg, args: wl_mlp(pkg, args, mode="two"),
-             "mlp_unfused": lambda pkg, args: wl_mlp(pkg, args, mode="unfused"), "prefill": wl_prefill, "w8a8": wl_w8a8,
-             "copy": wl_copy, "norm_quant": wl_norm_quant, "mlp_w8a8": wl_mlp_w8a8, "qkvz": wl_qkvz,
-             "qkvz_unfused": lambda pkg, args: wl_qkvz(pkg, args, fused=False),
-             "mlp_w8a8_4launch": lambda pkg, args: wl_mlp_w8a8(pkg, args, mode="fused"),
-             "mlp_w8a8_unfused": lambda pkg, args: wl_mlp_w8a8(pkg, args, mode="unfused"),
-             "norm_quant_unfused": lambda pkg, args: wl_norm_quant(pkg, args, fused=False), "vendor_f16": wl_vendor, "vendor_int8": lambda pkg, args: wl_vendor(pkg, args, int8=True)}
+EXTRA = {
+    "mlp_2launch": lambda p, a: _mlp_variant(p, a, "two"),
+    "mlp_unfused": lambda p, a: _mlp_variant(p, a, "unfused"),
+    "mlp_w8a8": lambda p, a: _mlp_w8a8(p, a, "block"),
+    "mlp_w8a8_f32": lambda p, a: _mlp_w8a8(p, a, "block_f32"),
+    "mlp_w8a8_unfused": lambda p, a: _mlp_w8a8(p, a, "unfused"),
+    "vendor_f16": lambda p, a: _vendor(p, a, False),
+    "vendor_int8": lambda p, a: _vendor(p, a, True),
+    "copy": _copy,
+}
+WORKLOADS = ["all", "lm_head", "gemv1", "mlp", "prefill", "w8a8", *EXTRA]
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # 1000 lm_head steps (~27 ms): the kernel's duration drifts by 1.5-3 us over
-    # the first ~5 ms of sustained streaming (clock management), so a short
-    # window reports the transient rather than the sustained rate
-    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--steps", type=int, default=1000, help="timed lm_head steps (the headline)")
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="lm_head", choices=sorted(WORKLOADS))
-    ap.add_argument("--copies", type=int, default=0, help="distinct weight sets rotated (0: workload default)")
+    ap.add_argument("--workload", default="all", choices=WORKLOADS)
+    ap.add_argument("--copies", type=int, default=0, help="distinct weight sets rotated (0: per-config default)")
     ap.add_argument("--M", type=int, default=0)
     ap.add_argument("--K", type=int, default=0)
     ap.add_argument("--N", type=int, default=0)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--argmax", default="tree", choices=["tree", "slots"],
                     help="lm_head: token on the device (tree) or host-finished tagged slots")
-    ap.add_argument("--graph", action="store_true", help="lm_head: replay HIP graphs instead of direct launches")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: every box in this build has a single MI355X and the hot path "
-              "has no multi-GPU leg (it would shard the weights by output column). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: every box in this build has a single MI355X, and this run has no "
+              "multi-GPU leg (the path would shard the weights by output column; see the design notes). "
+              "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (the HIP kernels have no CPU fallback)", file=sys.stderr)
         sys.exit(3)
     pkg = load_pkg()
-    r = WORKLOADS[args.workload](pkg, args)
-    steps = args.steps
-    ms_per_step = r["total_ms"] / steps
-    kms = np.array(r["kernel_ms"])
-    kmean = float(kms.mean())
-    scale = 1e9 if r["unit"] == "GB/s" else 1e12
-    value = r["bytes"] / (ms_per_step / 1e3) / scale
-    achieved = r["bytes"] / (kmean / 1e3) / scale
-    peak = HBM_PEAK_GBS if r["bound"] == "hbm" else (INT8_MFMA_PEAK_TOPS if r["unit"] == "TOP/s" else FP16_MFMA_PEAK_TFLOPS)
-    line = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": r["unit"],
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "us_per_call": round(ms_per_step * 1e3, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": r["dtype"],
-        "data": "synthetic (seeded N(0,1) fp16 activations, N(0,0.02) fp16 weights quantised in-build)",
-        "config": r["config"],
-        "roofline": {
-            "bound": r["bound"],
-            "achieved": round(achieved, 2),
-            "peak": peak,
-            "unit": "GB/s" if r["bound"] == "hbm" else ("TOP/s" if r["unit"] == "TOP/s" else "TFLOP/s"),
-            "frac": round(achieved / peak, 4),
-            "traffic": traffic_from_profiles(r["config"]["workload"]),
-            "kernel": r["kernel"],
-            "kernel_us_mean": round(kmean * 1e3, 3),
-            "kernel_us_median": round(float(np.median(kms)) * 1e3, 3),
-        },
-        "cpu_baseline": r.get("cpu_baseline"),
-    }
-    if "alt" in r:
-        line["alt_argmax_routes"] = r["alt"]
+    info = cpu_info()
+    if args.workload == "all":
+        line = run_all(pkg, args, info)
+    else:
+        line = single(pkg, args, info, args.workload)
     print(json.dumps(line), flush=True)
 
 
