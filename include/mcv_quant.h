@@ -244,6 +244,23 @@ int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
                              int zero_bias, void* logits_dev, int64_t* token_dev,
                              void* workspace_dev, uint32_t* status, mcv_stream_t stream);
 
+/* The device-token lm_head above for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Identical arguments
+ * and results to mcv_w4a16_lm_head_argmax, minus the workspace: the
+ * workspace lives in a library-owned array in device memory, one per GPU,
+ * held until the process ends, for V <= mcv_lm_head_noalloc_max_vocab()
+ * (2^20; larger V is MCV_ERR_SHAPE).  The call allocates nothing.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race and give undefined tokens.  The first
+ * call on a GPU, and every call whose V differs from the previous call's,
+ * zero-fills the array first with a fill kernel on `stream`. */
+int64_t mcv_lm_head_noalloc_max_vocab(void);
+int mcv_w4a16_lm_head_argmax_noalloc(const void* x_dev, int64_t K, int64_t N, int64_t V,
+                                     const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                                     int zero_bias, void* logits_dev, int64_t* token_dev,
+                                     uint32_t* status, mcv_stream_t stream);
+
 /* The greedy lm_head with the last step of the argmax left to the reader of
  * the token, for callers that copy the token to the host anyway (the
  * reference's lm_head_greedy returns it to the host, language_model.cpp:

@@ -15,6 +15,7 @@
 // src/csrc/lib/ops.cpp:1030-1095.
 #include <cstdint>
 #include <cstdlib>
+#include <mutex>
 
 #include "common.h"
 #include "gemv_body.h"
@@ -576,6 +577,24 @@ __global__ __launch_bounds__(256) void w4a16_tiled_i8_kernel(const uint16_t* __r
     out[n] = f2h(acc);
 }
 
+// ---- the lm_head's workspace in library memory, for callers that cannot
+// allocate (mcv_w4a16_lm_head_argmax_noalloc).  Every GPU the library runs on
+// holds its own copy of this array until the process ends; host code never
+// passes the array's name to a kernel (on the host it is only a stand-in):
+// it uses the device address hipGetSymbolAddress returns for the current GPU.
+constexpr int64_t kNoallocMaxV = int64_t(1) << 20;
+constexpr int64_t kNoallocWords = (kLmEpoch + (kNoallocMaxV + kSlab - 1) / kSlab + 1) / 2 +
+                                  (kNoallocMaxV + kSlab - 1) / kSlab;   // u64 words for V = kNoallocMaxV
+static __device__ __align__(256) unsigned long long scratch[kNoallocWords];
+
+// Zero-fills n u64 words (a kernel, not hipMemsetAsync, so a caller may
+// capture it in a graph).
+__global__ __launch_bounds__(256) void zero_words_kernel(unsigned long long* __restrict__ p, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        p[i] = 0ull;
+}
+
 }  // namespace
 
 // The GEMV launchers' k-split, for kernels that must add in the same order
@@ -628,6 +647,23 @@ int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* q
     return check_launch("w4a16_lm_head_kernel");
 }
 
+
+namespace {
+
+// Per-GPU state of the no-allocation route: the scratch array's device
+// address on that GPU and the vocabulary size of its last call (the
+// per-workgroup call counters and key words are laid out for one grid, so a
+// call with another V first zero-fills the array).  Fixed-size, so looking a
+// device up allocates nothing.
+constexpr int kNoallocMaxDevices = 64;
+struct NoallocSlot {
+    unsigned long long* ptr;
+    int64_t last_v;
+};
+NoallocSlot g_noalloc[kNoallocMaxDevices];
+std::mutex g_noalloc_mu;
+
+}  // namespace
 
 }  // namespace mcv
 
@@ -696,6 +732,47 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
     if ((rc = require_device()) != MCV_OK) return rc;
     return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, token, workspace, 0u, kLmTree,
                           static_cast<unsigned*>(status), static_cast<hipStream_t>(stream));
+}
+
+int64_t mcv_lm_head_noalloc_max_vocab(void) { return kNoallocMaxV; }
+
+int mcv_w4a16_lm_head_argmax_noalloc(const void* x, int64_t K, int64_t N, int64_t V, const void* qw,
+                                     const void* scales, const void* zeros, int zero_bias, void* logits,
+                                     int64_t* token, uint32_t* status, mcv_stream_t stream) {
+    const char* who = "mcv_w4a16_lm_head_argmax_noalloc";
+    int rc = MCV_OK;
+    if (!w4_args_ok(qw, scales, zeros, zero_bias, K, N, who, &rc)) return rc;
+    if (!x || !token) return fail(MCV_ERR_INVALID_ARG, "%s: null x/token", who);
+    if (V <= 0 || V > N) return fail(MCV_ERR_SHAPE, "%s: need 0 < V <= N (V=%lld N=%lld)", who, (long long)V, (long long)N);
+    if (V > kNoallocMaxV)
+        return fail(MCV_ERR_SHAPE, "%s: V=%lld exceeds the library scratch, which holds V <= %lld", who, (long long)V,
+                    (long long)kNoallocMaxV);
+    if ((rc = require_device()) != MCV_OK) return rc;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoallocMaxDevices)
+        return fail(MCV_ERR_HIP, "%s: no usable current device (%d)", who, dev);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    NoallocSlot& slot = g_noalloc[dev];
+    if (slot.ptr == nullptr) {
+        // once per GPU, with that GPU current: the array's address on it
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(MCV_ERR_HIP, "%s: hipGetSymbolAddress failed (%s)", who, hipGetErrorString(e));
+        slot.ptr = static_cast<unsigned long long*>(p);
+        slot.last_v = 0;
+    }
+    if (slot.last_v != V) {
+        // first call on this GPU, or a new grid: every counter and key word from zero
+        const int64_t words = mcv_lm_head_workspace_bytes(V) / 8;
+        hipLaunchKernelGGL(zero_words_kernel, dim3(static_cast<unsigned>(ceil_div(words, 256) < 64 ? ceil_div(words, 256) : 64)),
+                           dim3(256), 0, st, slot.ptr, words);
+        if ((rc = check_launch("zero_words_kernel")) != MCV_OK) return rc;
+        slot.last_v = V;
+    }
+    return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, token, slot.ptr, 0u, kLmTree,
+                          static_cast<unsigned*>(status), st);
 }
 
 int64_t mcv_lm_head_slots_bytes(void) { return int64_t(kSlotWords) * kSlotStride * 8; }
