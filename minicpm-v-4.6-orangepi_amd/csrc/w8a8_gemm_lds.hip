@@ -1,0 +1,395 @@
+// w8a8_gemm_lds.hip -- int8 x int8 -> int32 GEMM over the MFMA-tiled weight
+// layout (MCV_W8_TILED), both operands staged through LDS by gfx950's
+// direct-to-LDS loads, with the fused fp16 epilogue.  gfx950.
+//
+// acc[m][n] = sum_k xq[m][k] * w[k][n] (exact int32), optionally
+// out = fp16 RNE((float(acc) * ws[n]) * xs[m]).
+//
+// Workgroup: 4 waves in a 2 x 2 arrangement over a BM x BN output tile, each
+// wave BM/2 x BN/2 as 32 x 32 blocks of v_mfma_i32_32x32x32_i8.  K advances in
+// stages of 128; a stage's x rows (BM x 128 bytes) and weight lines (BN/32
+// column halves x 4 k32 blocks, 1 KiB each) are copied global -> LDS with
+// buffer_load_dwordx4 ... lds (no VGPR staging: a wave-wide instruction moves
+// 1 KiB into 1 KiB of LDS), NS stages in flight, one barrier per stage.
+//   - x: row-major in LDS, 128 bytes per row, the 16-byte chunk index XORed
+//     with the row's low 3 bits, so the operand reads of 32 rows at one k
+//     offset fall in distinct bank groups.  The XOR is applied by choosing
+//     which global chunk each lane fetches (the LDS side of the copy is always
+//     lane-linear).
+//   - weights: the tiled layout already stores each 32-column x 32-k block
+//     in operand order (lane l: column l%32, k-half l/32), so a line is
+//     copied verbatim and read back with one ds_read_b128 at lane*16.
+// Both operands of a k32 step come from LDS with conflict-free 16-byte reads;
+// each is used by two MFMAs of the wave.  The MFMA computes the transposed
+// tile (weights as the row operand), so a lane holds one output row and
+// 4 consecutive columns per register quad: int32 results leave as 16-byte
+// stores, fp16 ones as 16-byte stores after one v_permlane32_swap per pair.
+//
+// Each stage lives in its own __shared__ array, indexed by a compile-time
+// constant after the stage loop is unrolled NS ways, so the waitcnt pass sees
+// that the operand reads of stage s do not alias the copies in flight into
+// the other stages and keeps them in flight.  The explicit s_waitcnt vmcnt
+// before each barrier is the only wait on the copies; the barrier is a bare
+// s_barrier (a __syncthreads fence would wait for every copy in flight).
+//
+// Replaces matmul_w8a8_i32_custom + w8a8_dequant_custom
+// (src/csrc/custom_ops/op_kernel/matmul_w8a8_i32_custom.cpp:15-48,
+// w8a8_dequant_custom.cpp:33-69) for weights packed by
+// quantize_dense_weight_w8a8 (src/csrc/lib/quantized_weight.cpp:231-268).
+#include <cstdlib>
+
+#include "common.h"
+
+namespace mcv {
+namespace {
+
+constexpr int kLine = 1024;                 // one 32-column x 32-k operand line
+constexpr uint32_t kNowhere = 0xFFFFFF00u;  // a buffer offset past every range: the load returns zeros
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_l(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// 16 bytes per lane, global (buffer `r` at byte `voff`) -> LDS at lds + 16 * lane.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ int xcd_tile_l(int b, int total) {
+    const int per = total >> 3, rem = total & 7, x = b & 7, i = b >> 3;
+    return x * per + (x < rem ? x : rem) + i;
+}
+
+template <int BM, int BN, int NS>
+struct CfgL {
+    static constexpr int BK = 128;                     // k bytes per stage
+    static constexpr int A_BYTES = BM * BK;
+    static constexpr int B_BYTES = BN * BK;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int A_COPIES = A_BYTES / kLine;   // wave-wide 1 KiB copies per stage
+    static constexpr int B_COPIES = B_BYTES / kLine;
+    static_assert(A_COPIES % 4 == 0 && B_COPIES % 4 == 0, "copies split over four waves");
+    static constexpr int PA = A_COPIES / 4;            // x copies per wave per stage
+    static constexpr int PB = B_COPIES / 4;            // weight copies per wave per stage
+    static constexpr int P = PA + PB;
+    static constexpr int IB = BM / 64;                 // 32-row blocks per wave
+    static constexpr int JB = BN / 64;                 // 32-column blocks per wave
+    static_assert(IB >= 1 && JB >= 1 && NS >= 2 && NS <= 4, "tile shape");
+    static_assert(P * (NS - 2) < 64, "vmcnt");
+};
+
+// EPI: 0 int32 out; 4 | x-scale fp16 (1) | weight-scale fp16 (2): fp16 out
+// through the fused epilogue with fp16 or fp32 scales.
+template <int BM, int BN, int NS, int EPI>
+__global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
+    const int8_t* __restrict__ xq, const int8_t* __restrict__ w, int M, int K, int N, int KB, void* __restrict__ out,
+    const void* __restrict__ xs, const void* __restrict__ ws, int nslab, int n_tiles, int total_tiles, int KT) {
+    constexpr bool OUT_F16 = (EPI & 4) != 0;
+    constexpr bool XS16 = (EPI & 1) != 0, WS16 = (EPI & 2) != 0;
+    using C = CfgL<BM, BN, NS>;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds2[NS > 2 ? C::STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds3[NS > 3 ? C::STAGE : 16];
+    uint8_t* const bufs[4] = {lds0, lds1, lds2, lds3};
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int h = lane >> 5;
+
+    // Tiles of one XCD form a contiguous run, ordered down the tile columns so
+    // the XCD's L2 keeps few weight columns.
+    const int tile = xcd_tile_l(static_cast<int>(blockIdx.x), total_tiles);
+    const int m_tiles = total_tiles / n_tiles;
+    const int tm = tile % m_tiles, tn = tile / m_tiles;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int slab0 = n0 / kSlab;
+
+    // x rows m0..: rows past M read as zero; k past K within a row reads the
+    // next row, which meets zero (padded) weights.
+    const int rows_here = M - m0 < BM ? M - m0 : BM;
+    const __amdgpu_buffer_rsrc_t xr = rsrc_l(xq + static_cast<size_t>(m0) * K, static_cast<uint32_t>(rows_here) * K);
+    // weights: slabs past the last read as zero
+    const __amdgpu_buffer_rsrc_t wr = rsrc_l(w, static_cast<uint32_t>(nslab) * KB * 2 * kLine);
+
+    // This wave's copies of stage kt into `dst`: x copies wave*PA .. +PA (8
+    // rows of 128 bytes each), weight lines wave*PB .. +PB.  Stages past the
+    // last read from kNowhere: zeros land in a free buffer, and every stage
+    // issues the same number of copies, so the vmcnt waits stay exact.
+    auto issue = [&](int kt, uint8_t* dst) {
+        const bool live = kt < KT;
+#pragma unroll
+        for (int j = 0; j < C::PA; ++j) {
+            const int i = wave * C::PA + j;
+            const int row = i * 8 + (lane >> 3);
+            const int chunk = (lane & 7) ^ (row & 7);
+            const uint32_t off = live ? static_cast<uint32_t>(row * K + kt * C::BK + chunk * 16) : kNowhere;
+            dma16(xr, dst + i * kLine, off);
+        }
+#pragma unroll
+        for (int j = 0; j < C::PB; ++j) {
+            const int bi = wave * C::PB + j;                           // (slab sl, k32 block, half)
+            const int sl = bi >> 3;
+            const uint32_t off =
+                live ? (static_cast<uint32_t>(slab0 + sl) * KB * 2 + kt * 8 + (bi & 7)) * kLine + lane * 16u
+                     : kNowhere;
+            dma16(wr, dst + C::A_BYTES + bi * kLine, off);
+        }
+    };
+
+    // The fused epilogue's scales, as raw bits, issued before the first copy:
+    // loads complete in issue order, so the first stage's wait covers them.
+    // Register r of block (ib, jb) holds row wm*BM/2 + 32 ib + l%32 and column
+    // wn*BN/2 + 32 jb + 8 (r/4) + 4 h + r%4.
+    // Buffer loads: columns past N and rows past M read as zero with no branch,
+    // so all of them issue back to back.
+    uint32_t wraw[C::JB][4][4], xraw[C::IB];
+    if constexpr (OUT_F16) {
+        const __amdgpu_buffer_rsrc_t wsr = rsrc_l(ws, static_cast<uint32_t>(N) * (WS16 ? 2u : 4u));
+        const __amdgpu_buffer_rsrc_t xsr = rsrc_l(xs, static_cast<uint32_t>(M) * (XS16 ? 2u : 4u));
+#pragma unroll
+        for (int jb = 0; jb < C::JB; ++jb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t n = static_cast<uint32_t>(n0 + wn * (BN / 2) + 32 * jb + 8 * g + 4 * h + e);
+                    if constexpr (WS16) wraw[jb][g][e] = __builtin_amdgcn_raw_buffer_load_b16(wsr, n * 2u, 0, 0);
+                    else wraw[jb][g][e] = __builtin_amdgcn_raw_buffer_load_b32(wsr, n * 4u, 0, 0);
+                }
+#pragma unroll
+        for (int ib = 0; ib < C::IB; ++ib) {
+            const uint32_t m = static_cast<uint32_t>(m0 + wm * (BM / 2) + 32 * ib + (lane & 31));
+            if constexpr (XS16) xraw[ib] = __builtin_amdgcn_raw_buffer_load_b16(xsr, m * 2u, 0, 0);
+            else xraw[ib] = __builtin_amdgcn_raw_buffer_load_b32(xsr, m * 4u, 0, 0);
+        }
+    }
+
+    int16_t_v acc[C::IB][C::JB];
+#pragma unroll
+    for (int ib = 0; ib < C::IB; ++ib)
+#pragma unroll
+        for (int jb = 0; jb < C::JB; ++jb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[ib][jb][r] = 0;
+
+    // Operand addresses inside a stage (bytes), fixed per lane.
+    int a_off[C::IB][4];
+#pragma unroll
+    for (int ib = 0; ib < C::IB; ++ib) {
+        const int row = wm * (BM / 2) + 32 * ib + (lane & 31);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a_off[ib][s] = (row * 8 + ((2 * s + h) ^ (row & 7))) * 16;
+    }
+    int b_off[C::JB][4];
+#pragma unroll
+    for (int jb = 0; jb < C::JB; ++jb) {
+        const int col = wn * (BN / 2) + 32 * jb;
+        const int sl = col >> 6, jh = (col >> 5) & 1;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) b_off[jb][s] = C::A_BYTES + ((sl * 4 + s) * 2 + jh) * kLine + lane * 16;
+    }
+
+    auto compute = [&](const uint8_t* src) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            int4_t a[C::IB], b[C::JB];
+#pragma unroll
+            for (int ib = 0; ib < C::IB; ++ib) a[ib] = *reinterpret_cast<const int4_t*>(src + a_off[ib][s]);
+#pragma unroll
+            for (int jb = 0; jb < C::JB; ++jb) b[jb] = *reinterpret_cast<const int4_t*>(src + b_off[jb][s]);
+#pragma unroll
+            for (int ib = 0; ib < C::IB; ++ib)
+#pragma unroll
+                for (int jb = 0; jb < C::JB; ++jb)
+                    acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[jb], a[ib], acc[ib][jb], 0, 0, 0);
+        }
+    };
+
+    // Stage kt in buffer kt % NS.  Each step: this wave's copies of stage kt
+    // are done (vmcnt), every wave's are and every wave has finished stage
+    // kt - 1 (barrier); then the copies of stage kt + NS - 1 go into the
+    // buffer stage kt - 1 used, and stage kt is computed.
+#pragma unroll
+    for (int d = 0; d < NS - 1; ++d) issue(d, bufs[d]);
+    int kt = 0;
+    for (; kt + NS <= KT; kt += NS) {
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            wait_vmcnt<C::P * (NS - 2)>();
+            __builtin_amdgcn_s_barrier();
+            issue(kt + u + NS - 1, bufs[(u + NS - 1) % NS]);
+            compute(bufs[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NS - 1; ++u) {
+        if (kt + u < KT) {
+            wait_vmcnt<C::P * (NS - 2)>();
+            __builtin_amdgcn_s_barrier();
+            issue(kt + u + NS - 1, bufs[(u + NS - 1) % NS]);
+            compute(bufs[u]);
+        }
+    }
+
+    const int row_base = m0 + wm * (BM / 2);
+    const int col_base = n0 + wn * (BN / 2);
+    if constexpr (!OUT_F16) {
+        int32_t* o = static_cast<int32_t*>(out);
+        const bool vec_ok = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+        for (int ib = 0; ib < C::IB; ++ib) {
+            const int row = row_base + 32 * ib + (lane & 31);
+            if (row >= M) continue;
+#pragma unroll
+            for (int jb = 0; jb < C::JB; ++jb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int col = col_base + 32 * jb + 8 * g + 4 * h;
+                    if (col >= N) continue;
+                    int32_t* dst = o + static_cast<size_t>(row) * N + col;
+                    if (vec_ok) {
+                        *reinterpret_cast<int4_t*>(dst) = int4_t{acc[ib][jb][4 * g], acc[ib][jb][4 * g + 1],
+                                                                 acc[ib][jb][4 * g + 2], acc[ib][jb][4 * g + 3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (col + e < N) dst[e] = acc[ib][jb][4 * g + e];
+                    }
+                }
+        }
+    } else {
+        float wsv[C::JB][4][4], xsv[C::IB];
+#pragma unroll
+        for (int jb = 0; jb < C::JB; ++jb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    wsv[jb][g][e] = WS16 ? h2f(static_cast<uint16_t>(wraw[jb][g][e])) : __uint_as_float(wraw[jb][g][e]);
+#pragma unroll
+        for (int ib = 0; ib < C::IB; ++ib)
+            xsv[ib] = XS16 ? h2f(static_cast<uint16_t>(xraw[ib])) : __uint_as_float(xraw[ib]);
+        uint16_t* o = static_cast<uint16_t*>(out);
+        const bool vec_ok = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+        for (int ib = 0; ib < C::IB; ++ib) {
+            const int row = row_base + 32 * ib + (lane & 31);
+#pragma unroll
+            for (int jb = 0; jb < C::JB; ++jb)
+#pragma unroll
+                for (int g = 0; g < 4; g += 2) {
+                    uint32_t p[4];
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        auto deq = [&](int gg, int e) {
+                            return f2h(__fmul_rn(__fmul_rn(static_cast<float>(acc[ib][jb][4 * gg + e]), wsv[jb][gg][e]),
+                                                 xsv[ib]));
+                        };
+                        const uint32_t x0 = deq(g, 2 * d) | (uint32_t(deq(g, 2 * d + 1)) << 16);
+                        const uint32_t x1 = deq(g + 1, 2 * d) | (uint32_t(deq(g + 1, 2 * d + 1)) << 16);
+                        const auto sw = __builtin_amdgcn_permlane32_swap(x0, x1, false, false);
+                        p[d] = sw[0];
+                        p[2 + d] = sw[1];
+                    }
+                    const int col = col_base + 32 * jb + 8 * g + 8 * h;
+                    if (row >= M || col >= N) continue;
+                    uint16_t* dst = o + static_cast<size_t>(row) * N + col;
+                    if (vec_ok) {
+                        *reinterpret_cast<uint4*>(dst) = make_uint4(p[0], p[1], p[2], p[3]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (col + e < N) dst[e] = static_cast<uint16_t>(p[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
+        }
+    }
+}
+
+struct ShapeL {
+    int bm, bn, ns;
+};
+
+using GemmLFn = void (*)(const int8_t*, const int8_t*, int, int, int, int, void*, const void*, const void*, int, int,
+                         int, int);
+
+template <int EPI>
+GemmLFn pick_epi(const ShapeL& s) {
+#define MCV_L(BM_, BN_, NS_) \
+    if (s.bm == BM_ && s.bn == BN_ && s.ns == NS_) return w8a8_gemm_lds_kernel<BM_, BN_, NS_, EPI>;
+    MCV_L(128, 128, 3) MCV_L(128, 128, 4) MCV_L(64, 128, 4) MCV_L(128, 64, 4) MCV_L(64, 64, 4)
+#undef MCV_L
+    return nullptr;
+}
+
+GemmLFn pick_l(const ShapeL& s, int epi) {
+    switch (epi) {
+        case 4: return pick_epi<4>(s);
+        case 5: return pick_epi<5>(s);
+        case 6: return pick_epi<6>(s);
+        case 7: return pick_epi<7>(s);
+        default: return pick_epi<0>(s);
+    }
+}
+
+// Largest tiles first; the first shape whose grid covers most of the 256
+// CUs, else the one with the most workgroups.  Measured on MI355X (K=1024,
+// N=3584, graph-replayed, rotated weights): M=1024 128x128 with 3 stages
+// 9.5 us (4 stages 9.8, 64x128 12.2, 64x64 13.1); M=256 64x64 5.3 us
+// (64x128 6.6, 128x128 8.4).  The K loop there runs at ~0.58 us per
+// 32 KiB stage: a plain L2 -> LDS stream sustains ~104 GB/s per CU
+// (0.32 us per stage) and the stage's MFMAs take ~0.21 us, so the copies and
+// the operand reads contend for the LDS.  MCV_W8LDS_SHAPE="BM,BN,NS"
+// overrides the choice (read once per process; tuning sweeps).
+ShapeL choose_l(int64_t M, int64_t N) {
+    static const char* const e = std::getenv("MCV_W8LDS_SHAPE");
+    if (e != nullptr) {
+        ShapeL s{0, 0, 0};
+        if (std::sscanf(e, "%d,%d,%d", &s.bm, &s.bn, &s.ns) == 3 && pick_l(s, 0)) return s;
+    }
+    constexpr ShapeL kOrder[] = {{128, 128, 3}, {64, 128, 4}, {64, 64, 4}};
+    ShapeL best = kOrder[0];
+    int64_t best_t = -1;
+    for (const ShapeL& s : kOrder) {
+        const int64_t t = ceil_div(M, s.bm) * ceil_div(N, s.bn);
+        if (t >= 200) return s;
+        if (t > best_t) {
+            best_t = t;
+            best = s;
+        }
+    }
+    return best;
+}
+
+}  // namespace
+
+// xq [M][K] int8 (K % 16 == 0), w tiled; out int32 or fp16 [M][N].  Shapes
+// were validated by the caller.
+int launch_w8a8_gemm_lds(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
+                         const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream) {
+    const int64_t nslab = ceil_div(N, kSlab);
+    const int64_t KB = ceil_div(K, 128) * 4;
+    if (nslab * KB * 2 * kLine >= (int64_t(1) << 32) || M * K >= (int64_t(1) << 32))
+        return fail(MCV_ERR_SHAPE, "w8a8 GEMM: weight or activation exceeds 4 GiB");
+    const ShapeL s = choose_l(M, N);
+    const int64_t n_tiles = ceil_div(N, s.bn);
+    const int64_t total = ceil_div(M, s.bm) * n_tiles;
+    if (total > 0x7fffffff) return fail(MCV_ERR_SHAPE, "w8a8 GEMM: too many tiles");
+    const int KT = static_cast<int>(KB / 4);
+    const int epi = f16 ? 4 | (xs16 ? 1 : 0) | (ws16 ? 2 : 0) : 0;
+    hipLaunchKernelGGL(pick_l(s, epi), dim3(static_cast<unsigned>(total)),
+                       dim3(256), 0, stream, xq, w, static_cast<int>(M), static_cast<int>(K), static_cast<int>(N),
+                       static_cast<int>(KB), out, xs, ws, static_cast<int>(nslab), static_cast<int>(n_tiles),
+                       static_cast<int>(total), KT);
+    return check_launch("w8a8_gemm_lds_kernel");
+}
+
+}  // namespace mcv

@@ -27,6 +27,7 @@
 // wrappers (src/csrc/lib/ops.cpp:1097-1133, 1173-1210) for weights packed by
 // quantize_dense_weight_w8a8 (src/csrc/lib/quantized_weight.cpp:231-268).
 #include <cstdlib>
+#include <cstring>
 
 #include "common.h"
 
@@ -551,6 +552,9 @@ int64_t w8a8_tiled_bytes(int64_t K, int64_t N) {
     return ceil_div(N, kSlab) * kSlab * ceil_div(K, 128) * 128;
 }
 
+int launch_w8a8_gemm_lds(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
+                         const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
+
 // xq [M][K] int8 (16-byte aligned rows not required), w tiled; out int32 or
 // fp16 [M][N].  Shapes were validated by the caller.
 int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
@@ -563,6 +567,11 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
         return f16 ? launch_w8a8_gemv<true, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream)
                    : launch_w8a8_gemv<false, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream);
     }
+    // M > 4: the LDS-staged GEMM (w8a8_gemm_lds.hip); MCV_W8GEMM_KERNEL=regs
+    // keeps the register-operand kernel below (read once; comparisons).
+    static const char* const which = std::getenv("MCV_W8GEMM_KERNEL");
+    if (which == nullptr || std::strcmp(which, "regs") != 0)
+        return launch_w8a8_gemm_lds(xq, M, K, N, w, out, f16, xs, xs16, ws, ws16, stream);
     const int64_t KT_all = KB / 4;                      // 128-k stages over the padded K
     const Shape8 s = choose8(M, KT_all, nslab);
     const int64_t n_tiles = ceil_div(nslab, s.wn);
