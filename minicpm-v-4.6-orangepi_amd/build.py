@@ -78,7 +78,9 @@ def build_capi(jobs: int | None = None) -> Path:
         objs = list(ex.map(_compile_hip, srcs))
     out = LIB / "libmcv_quant.so"
     tmp = LIB / "libmcv_quant.so.tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    # --no-undefined: a kernel whose host stub was not emitted fails here,
+    # not at dlopen on the GPU box
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, out)
     return out
 

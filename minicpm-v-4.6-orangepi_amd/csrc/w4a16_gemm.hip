@@ -43,6 +43,9 @@ namespace mcv {
 
 int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                       const void* zeros, int zero_bias, void* out, hipStream_t stream);
+int choose_w4a16_lds(int64_t M, int64_t N, int* tm, int* ns);
+int launch_w4a16_gemm_lds(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
+                          const void* zeros, int zero_bias, void* out, int tm, int ns, hipStream_t stream);
 
 namespace {
 
@@ -493,6 +496,15 @@ int launch_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const
     if (N <= 0 || N > (int64_t(1) << 30) || M <= 0 || M > (int64_t(1) << 30))
         return fail(MCV_ERR_SHAPE, "mcv_w4a16_gemm_mfma: bad M/N (M=%lld N=%lld)", (long long)M, (long long)N);
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_mfma: x must be 16-byte aligned");
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    // The LDS-staged kernel (w4a16_gemm_lds.hip) where its tall tiles fill
+    // the chip, the register-staged one below otherwise;
+    // MCV_W4GEMM_KERNEL=regs forces the latter (read once per process).
+    static const char* const which = std::getenv("MCV_W4GEMM_KERNEL");
+    int tm = 0, ns = 0;
+    if ((which == nullptr || std::strcmp(which, "regs") != 0) && choose_w4a16_lds(M, N, &tm, &ns) == 0)
+        return launch_w4a16_gemm_lds(x, M, K, N, qw, scales, zeros, zero_bias, out, tm, ns, stream);
     const int64_t nslab = ceil_div(N, kSlab);
     const Shape s = choose_shape(M, K, nslab);
     // Tile order, measured (MI355X, graph-replayed): down the tile columns
@@ -508,8 +520,6 @@ int launch_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const
     // the packed weight (K * Npad / 2 bytes).
     if (total > 0x7fffffff || K > (int64_t(1) << 22) || K * nslab * kSlab / 2 >= (int64_t(1) << 32))
         return fail(MCV_ERR_SHAPE, "mcv_w4a16_gemm_mfma: problem too large (M=%lld N=%lld)", (long long)M, (long long)N);
-    int rc = require_device();
-    if (rc != MCV_OK) return rc;
     hipLaunchKernelGGL(pick(s), dim3(static_cast<unsigned>(total)), dim3(64 * s.waves()), 0, stream,
                        static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),

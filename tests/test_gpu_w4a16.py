@@ -96,6 +96,11 @@ def test_dequant_bit_exact(mcv, oracle, cuda):
 
 @pytest.mark.parametrize("M,K,N", [
     (8, 1024, 3584), (128, 1024, 3584), (130, 1024, 1000), (128, 3584, 1024), (256, 256, 264),
+    # LDS-staged kernel: 128-row tiles, ragged M and N (57 slabs, the last
+    # tile's fourth slab past the end), one k stage (fewer stages than buffers)
+    (2050, 128, 3592),
+    # 64-row tiles, ragged M and N
+    (1100, 256, 3000),
 ], ids=lambda v: str(v))
 def test_gemm_mfma_vs_oracle(mcv, oracle, cuda, M, K, N):
     x, qweight, qzeros, scales, _ = _case(3000 + M + K + N, M, K, N)
@@ -106,8 +111,8 @@ def test_gemm_mfma_vs_oracle(mcv, oracle, cuda, M, K, N):
     _check(_host_f32(out), ref, f"mfma M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("M,K,N", [(512, 1024, 3584), (512, 3584, 1024), (2048, 1024, 3584), (2048, 3584, 1024)],
-                         ids=lambda v: str(v))
+@pytest.mark.parametrize("M,K,N", [(512, 1024, 3584), (512, 3584, 1024), (1024, 1024, 3584), (2048, 1024, 3584),
+                                   (2048, 3584, 1024)], ids=lambda v: str(v))
 def test_gemm_mfma_full_size(mcv, oracle, cuda, M, K, N):
     # prefill benchmark sizes: fp64 product of the oracle-exact dequantised weights
     torch = _torch()
