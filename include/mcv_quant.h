@@ -99,8 +99,13 @@ int mcv_w4a16_pack_awq(const int32_t* qweight_host, const int32_t* qzeros_host,
 /* Replaces unpack_gptq_weight + pack_w4a16_weight
  * (src/csrc/lib/quantized_weight.cpp:75-120, 48-73): GPTQ v1 tensors (qweight
  * int32 [K/8][N], qzeros int32 [G][N/8], g_idx int32 [K] or NULL, scales fp16
- * [G][N]) to slab-64 with zero_bias = 1 (GPTQ stores zero - 1, :112).  g_idx
- * must be k/128 for every k (no act-order): MCV_ERR_UNSUPPORTED otherwise. */
+ * [G][N]) to slab-64 with zero_bias = 1 (GPTQ stores zero - 1, :112).  With
+ * an act-order g_idx (:98-117) row k's zero comes from group g_idx[k] while
+ * the scale stays that of group k/128, as in the reference; the int8 values
+ * q - zero are kept exact by re-basing each (k/128 group, column) on one
+ * common zero (unchanged nibbles when the rows' zeros agree, as in every
+ * sym=True checkpoint).  MCV_ERR_SHAPE for g_idx outside [0, G);
+ * MCV_ERR_UNSUPPORTED when one group's values span more than 16 levels. */
 int mcv_w4a16_pack_gptq(const int32_t* qweight_host, const int32_t* qzeros_host,
                         const int32_t* g_idx_host, const uint16_t* scales_host,
                         int64_t K, int64_t N, int64_t groups,

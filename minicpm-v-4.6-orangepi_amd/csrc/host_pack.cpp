@@ -147,23 +147,68 @@ int mcv_w4a16_pack_gptq(const int32_t* qweight, const int32_t* qzeros, const int
     if (!shape_ok(K, N) || N % 8 != 0 || groups * kGroup != K)
         return fail(MCV_ERR_SHAPE, "mcv_w4a16_pack_gptq: need K %% 128 == 0, N %% 8 == 0, groups*128 == K "
                     "(K=%lld N=%lld groups=%lld)", (long long)K, (long long)N, (long long)groups);
+    bool act_order = false;
     if (g_idx) {
-        for (int64_t k = 0; k < K; ++k)
-            if (g_idx[k] != k / kGroup)
-                return fail(MCV_ERR_UNSUPPORTED,
-                            "mcv_w4a16_pack_gptq: act-order g_idx (g_idx[%lld]=%d, expected %lld) is not supported",
-                            (long long)k, g_idx[k], (long long)(k / kGroup));
+        for (int64_t k = 0; k < K; ++k) {
+            if (g_idx[k] < 0 || g_idx[k] >= groups)
+                return fail(MCV_ERR_SHAPE, "mcv_w4a16_pack_gptq: g_idx out of range (g_idx[%lld]=%d, groups=%lld)",
+                            (long long)k, g_idx[k], (long long)groups);
+            act_order |= g_idx[k] != k / kGroup;
+        }
     }
     Slab64Writer wr(K, N, qw_out, scales_out, zeros_out);
-    for (int64_t k0 = 0; k0 < K / 8; ++k0)
-        for (int64_t n = 0; n < N; ++n) {
-            const uint32_t word = static_cast<uint32_t>(qweight[k0 * N + n]);
-            for (int i = 0; i < 8; ++i) wr.put_q(k0 * 8 + i, n, word >> (4 * i));
-        }
+    auto nib_q = [&](int64_t k, int64_t n) {
+        return static_cast<int>((static_cast<uint32_t>(qweight[(k / 8) * N + n]) >> (4 * (k % 8))) & 15u);
+    };
+    // zero of row k (stored zero - 1, :112); its group is g_idx[k] (:107)
+    auto zero_of = [&](int64_t gz, int64_t n) {
+        return static_cast<int>((static_cast<uint32_t>(qzeros[gz * (N / 8) + n / 8]) >> (4 * (n % 8))) & 15u) + 1;
+    };
+    if (!act_order) {
+        for (int64_t k0 = 0; k0 < K / 8; ++k0)
+            for (int64_t n = 0; n < N; ++n) {
+                const uint32_t word = static_cast<uint32_t>(qweight[k0 * N + n]);
+                for (int i = 0; i < 8; ++i) wr.put_q(k0 * 8 + i, n, word >> (4 * i));
+            }
+        for (int64_t g = 0; g < groups; ++g)
+            for (int64_t n = 0; n < N; ++n) {
+                const uint32_t word = static_cast<uint32_t>(qzeros[g * (N / 8) + n / 8]);
+                wr.put_z(g, n, word >> (4 * (n % 8)));
+                wr.put_s(g, n, scales[g * N + n]);
+            }
+        return MCV_OK;
+    }
+    // Act-order: the reference takes row k's zero from group g_idx[k] but
+    // keeps the scales by position, group k / 128 (:101-117 build
+    // w8 = q - zero[g_idx[k]]; pack_w4a16_weight and the kernel scale the
+    // 128-row group k / 128).  The slab layout has one zero per (k / 128,
+    // column); every w8 value is kept exact by storing, per (group, column),
+    // the common zero c and nibbles q - zero[g_idx[k]] + c:
+    //   - the rows' zeros agree (every sym=True checkpoint): c = that zero,
+    //     the nibbles unchanged;
+    //   - otherwise c = max(1, -min w8), which needs max w8 + c <= 15 (16
+    //     levels); a (group, column) whose w8 span more is refused.
     for (int64_t g = 0; g < groups; ++g)
         for (int64_t n = 0; n < N; ++n) {
-            const uint32_t word = static_cast<uint32_t>(qzeros[g * (N / 8) + n / 8]);
-            wr.put_z(g, n, word >> (4 * (n % 8)));
+            const int z0 = zero_of(g_idx[g * kGroup], n);
+            bool same = true;
+            int lo = 99, hi = -99;
+            for (int64_t k = g * kGroup; k < (g + 1) * kGroup; ++k) {
+                const int z = zero_of(g_idx[k], n);
+                same &= z == z0;
+                const int w8 = nib_q(k, n) - z;
+                lo = w8 < lo ? w8 : lo;
+                hi = w8 > hi ? w8 : hi;
+            }
+            const int c = same ? z0 : (-lo > 1 ? -lo : 1);
+            if (c + hi > 15 || c + lo < 0 || c > 16)
+                return fail(MCV_ERR_UNSUPPORTED,
+                            "mcv_w4a16_pack_gptq: act-order zero points of group %lld, column %lld put its int4 "
+                            "values on %d levels (w8 in [%d, %d]); at most 16 fit one zero per group",
+                            (long long)g, (long long)n, hi - lo + 1, lo, hi);
+            for (int64_t k = g * kGroup; k < (g + 1) * kGroup; ++k)
+                wr.put_q(k, n, static_cast<uint32_t>(nib_q(k, n) - zero_of(g_idx[k], n) + c));
+            wr.put_z(g, n, static_cast<uint32_t>(c - 1));
             wr.put_s(g, n, scales[g * N + n]);
         }
     return MCV_OK;

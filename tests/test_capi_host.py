@@ -85,10 +85,75 @@ def test_gptq_pack_roundtrip_vs_oracle(mcv, oracle):
     assert np.array_equal(qw, qw2)
 
 
-def test_gptq_act_order_rejected(mcv):
+def _gptq_words(rng, K, N, G, qmax, zlo, zhi):
+    """GPTQ v1 tensors with nibbles in [0, qmax] and stored zeros in [zlo, zhi]."""
+    qn = rng.integers(0, qmax + 1, (K, N)).astype(np.uint32)
+    qweight = np.zeros((K // 8, N), np.uint32)
+    for i in range(8):
+        qweight |= qn[i::8] << (4 * i)
+    zn = rng.integers(zlo, zhi + 1, (G, N)).astype(np.uint32)
+    qzeros = np.zeros((G, N // 8), np.uint32)
+    for s in range(8):
+        qzeros |= zn[:, s::8] << (4 * s)
+    return qweight.view(np.int32), qzeros.view(np.int32)
+
+
+def _slab_w8(mcv, qw, sc, zr, K, N):
+    q, zeff, s = mcv.unpack(qw, sc, zr, 1, K, N)
+    return (q.astype(np.int16) - np.repeat(zeff, 128, axis=0).astype(np.int16)).astype(np.int8), s
+
+
+def test_gptq_act_order_symmetric(mcv, oracle):
+    # sym=True checkpoints store zero 7 everywhere: act-order changes no value,
+    # and the packed nibbles equal those of the trivial g_idx
+    rng = np.random.default_rng(24)
+    K, N, G = 512, 72, 4
+    qweight, qzeros = _gptq_words(rng, K, N, G, 15, 7, 7)
+    scales = f16_normal(rng, (G, N), 0.01)
+    g_idx = rng.permutation(np.arange(K) // 128).astype(np.int32)
+    qw, sc, zr = mcv.pack_gptq(qweight, qzeros, g_idx, scales)
+    w8, s = _slab_w8(mcv, qw, sc, zr, K, N)
+    assert np.array_equal(w8, oracle.unpack_gptq(qweight, qzeros, g_idx, G))
+    assert np.array_equal(s, scales)          # scales stay with group k / 128, as in the reference
+    qw2, _, zr2 = mcv.pack_gptq(qweight, qzeros, None, scales)
+    assert np.array_equal(qw, qw2) and np.array_equal(zr, zr2)
+
+
+def test_gptq_act_order_rebased(mcv, oracle):
+    # zeros that differ between the groups a 128-row block draws from: every
+    # (block, column) is re-based on one common zero, the int8 values exact
+    rng = np.random.default_rng(25)
+    K, N, G = 1024, 136, 8
+    qweight, qzeros = _gptq_words(rng, K, N, G, 12, 5, 8)       # w8 = q - zero in [-9, 6]: 16 levels
+    scales = f16_normal(rng, (G, N), 0.01)
+    for g_idx in (rng.permutation(np.arange(K) // 128), np.arange(K) % G, (np.arange(K) * 7 // K) % G):
+        g_idx = g_idx.astype(np.int32)
+        qw, sc, zr = mcv.pack_gptq(qweight, qzeros, g_idx, scales)
+        w8, s = _slab_w8(mcv, qw, sc, zr, K, N)
+        assert np.array_equal(w8, oracle.unpack_gptq(qweight, qzeros, g_idx, G))
+        assert np.array_equal(s, scales)
+
+
+def test_gptq_act_order_too_wide_refused(mcv):
+    # one block draws rows from a zero-1 group and a zero-16 group: its values
+    # span 31 levels, more than one zero per block can express
+    K, N, G = 256, 8, 2
+    qn = np.zeros((K, N), np.uint32)
+    qn[0::2] = 15
+    qweight = np.zeros((K // 8, N), np.uint32)
+    for i in range(8):
+        qweight |= qn[i::8] << (4 * i)
+    qzeros = np.array([[0x00000000], [0xFFFFFFFF]], np.uint32)      # stored zeros 0 and 15
+    g_idx = (np.arange(K) % 2).astype(np.int32)
+    with pytest.raises(mcv.McvError, match="levels"):
+        mcv.pack_gptq(qweight.view(np.int32), qzeros.view(np.int32), g_idx, np.zeros((G, N), np.uint16))
+
+
+def test_gptq_g_idx_out_of_range(mcv):
     K, N = 256, 8
-    g_idx = (np.arange(K) // 128).astype(np.int32)[::-1].copy()
-    with pytest.raises(mcv.McvError, match="act-order"):
+    g_idx = (np.arange(K) // 128).astype(np.int32)
+    g_idx[7] = 2
+    with pytest.raises(mcv.McvError, match="out of range"):
         mcv.pack_gptq(np.zeros((K // 8, N), np.int32), np.zeros((2, 1), np.int32), g_idx,
                       np.zeros((2, N), np.uint16))
 

@@ -158,6 +158,33 @@ def test_gptq_zero_bias(mcv, oracle, cuda):
     assert np.array_equal(w8_dev.cpu().numpy(), w8)
 
 
+def test_gptq_act_order(mcv, oracle, cuda):
+    # act-order g_idx: row k's zero from group g_idx[k], the scale of group
+    # k / 128 (quantized_weight.cpp:98-117); zeros that differ between the
+    # groups a block draws from are re-based onto one zero per block
+    rng = np.random.default_rng(7)
+    K, N, G = 1024, 520, 8
+    qn = rng.integers(0, 13, (K, N)).astype(np.uint32)
+    qweight = np.zeros((K // 8, N), np.uint32)
+    for i in range(8):
+        qweight |= qn[i::8] << (4 * i)
+    zn = rng.integers(5, 9, (G, N)).astype(np.uint32)
+    qzeros = np.zeros((G, N // 8), np.uint32)
+    for s in range(8):
+        qzeros |= zn[:, s::8] << (4 * s)
+    qweight, qzeros = qweight.view(np.int32), qzeros.view(np.int32)
+    scales = f16_normal(rng, (G, N), 0.002)
+    g_idx = rng.permutation(np.arange(K) // 128).astype(np.int32)
+    w = mcv.W4A16QuantizedWeight.from_gptq(qweight, qzeros, g_idx, scales)
+    w8 = oracle.unpack_gptq(qweight, qzeros, g_idx, G)
+    _, w8_dev = mcv.w4a16_dequant(w, f16=False, i8=True)
+    assert np.array_equal(w8_dev.cpu().numpy(), w8)
+    for M in (1, 64):
+        x = f16_normal(rng, (M, K), 1.0)
+        out = _host_f32(mcv.matmul_w4a16(_to_dev(x), w))
+        _check(out, oracle.w4a16_matmul(x, w8, scales), f"gptq act-order M={M}")
+
+
 def _reference_tile_pack(w8, K, N):
     """The reference's pack_w4a16_weight + choose_w4a16_tile_len
     (src/csrc/lib/quantized_weight.cpp:41-73), restated to build its input format."""
