@@ -123,7 +123,7 @@ template <int TM, int NS>
 __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int M, int K, int N,
-    int nslab, int n_tiles, int total_tiles, int col_major) {
+    int nslab, int n_tiles, int total_tiles, int col_major, int xcd_m) {
     using C = CfgW<TM, NS>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
@@ -134,14 +134,23 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5;
-    // Each XCD gets a contiguous run of tiles.  col_major runs it down the
-    // tile columns (the XCD's L2 holds a few weight slabs; x rows cross
-    // XCDs), otherwise along the tile rows (each x row tile stays on one XCD;
-    // the weights cross).
-    const int tile = xcd_tile_w(static_cast<int>(blockIdx.x), total_tiles);
+    // Workgroup b runs on XCD b % 8.  With xcd_m > 0 the tile grid is cut
+    // into xcd_m x (8 / xcd_m) blocks, one per XCD, so each XCD's L2 sees
+    // only its block's x rows and weight slabs; otherwise each XCD gets a
+    // contiguous run of tiles, down the tile columns (col_major: an XCD holds
+    // a few weight slabs, x rows cross XCDs) or along the rows.
     const int m_tiles = total_tiles / n_tiles;
-    const int tm = col_major ? tile % m_tiles : tile / n_tiles;
-    const int tn = col_major ? tile / m_tiles : tile - tm * n_tiles;
+    int tm, tn;
+    if (xcd_m > 0) {
+        const int xb_n = 8 / xcd_m, mr = m_tiles / xcd_m, nr = n_tiles / xb_n;
+        const int xcd = static_cast<int>(blockIdx.x) & 7, i = static_cast<int>(blockIdx.x) >> 3;
+        tm = (xcd / xb_n) * mr + i % mr;
+        tn = (xcd % xb_n) * nr + i / mr;
+    } else {
+        const int tile = xcd_tile_w(static_cast<int>(blockIdx.x), total_tiles);
+        tm = col_major ? tile % m_tiles : tile / n_tiles;
+        tn = col_major ? tile / m_tiles : tile - tm * n_tiles;
+    }
     const int m0 = tm * TM;
     const int slab = tn * 4 + wave;
     const int Npad = nslab * kSlab;
@@ -368,7 +377,7 @@ struct ShapeW {
 };
 
 using GemmWFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int,
-                         int, int, int, int, int, int);
+                         int, int, int, int, int, int, int);
 
 GemmWFn pick_w(const ShapeW& s) {
 #define MCV_W(TM_, NS_) \
@@ -420,11 +429,26 @@ int launch_w4a16_gemm_lds(const void* x, int64_t M, int64_t K, int64_t N, const 
     const int64_t nslab = ceil_div(N, kSlab);
     const int64_t n_tiles = ceil_div(nslab, 4);
     const int64_t total = ceil_div(M, tm) * n_tiles;
-    // Down the tile columns when x is the smaller operand stream (M < N),
-    // along the rows otherwise; MCV_W4GEMM_ORDER=0/1 overrides (read once).
-    int col_major = M < N ? 1 : 0;
+    // Tile order: the XCD blocking with the fewest bytes of x and weights per
+    // XCD when the tile grid splits evenly, else a contiguous run per XCD,
+    // down the tile columns when M < N.  MCV_W4GEMM_ORDER=0/1 forces the
+    // run along the rows / columns (read once per process).
+    int col_major = M < N ? 1 : 0, xcd_m = 0;
     static const char* const order = std::getenv("MCV_W4GEMM_ORDER");
-    if (order != nullptr) col_major = std::atoi(order) ? 1 : 0;
+    if (order != nullptr) {
+        col_major = std::atoi(order) ? 1 : 0;
+    } else {
+        const int64_t m_tiles = ceil_div(M, tm);
+        int64_t best = -1;
+        for (int a = 1; a <= 8; a *= 2) {
+            if (m_tiles % a != 0 || n_tiles % (8 / a) != 0) continue;
+            const int64_t bytes = (m_tiles / a) * tm * K * 2 + (n_tiles / (8 / a)) * 4 * kSlab * K / 2;
+            if (best < 0 || bytes < best) {
+                best = bytes;
+                xcd_m = a;
+            }
+        }
+    }
     // Buffer offsets are 32-bit: x inside one row tile, the packed weight.
     if (total > 0x7fffffff || K > (int64_t(1) << 22) || K * nslab * kSlab / 2 >= (int64_t(1) << 31) ||
         int64_t(tm) * K * 2 >= (int64_t(1) << 31))
@@ -433,7 +457,7 @@ int launch_w4a16_gemm_lds(const void* x, int64_t M, int64_t K, int64_t N, const 
                        static_cast<const uint4*>(qw), static_cast<const uint16_t*>(scales),
                        static_cast<const uint32_t*>(zeros), static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(out),
                        static_cast<int>(M), static_cast<int>(K), static_cast<int>(N), static_cast<int>(nslab),
-                       static_cast<int>(n_tiles), static_cast<int>(total), col_major);
+                       static_cast<int>(n_tiles), static_cast<int>(total), col_major, xcd_m);
     return check_launch("w4a16_gemm_lds_kernel");
 }
 
