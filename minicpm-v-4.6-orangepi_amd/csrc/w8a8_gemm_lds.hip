@@ -12,8 +12,11 @@
 // buffer_load_dwordx4 ... lds (no VGPR staging: a wave-wide instruction moves
 // 1 KiB into 1 KiB of LDS), NS stages in flight, one barrier per stage.
 //   - x: row-major in LDS, 128 bytes per row, the 16-byte chunk index XORed
-//     with the row's low 3 bits, so the operand reads of 32 rows at one k
-//     offset fall in distinct bank groups.  The XOR is applied by choosing
+//     with bits 1..3 of the row: one ds_read_b128 pass serves 16 rows, two
+//     per 256-byte bank window, so the row's parity picks the half and bits
+//     1..3 must spread the 8 rows of each parity over the 8 chunks.  (XOR by
+//     the row's low 3 bits left rows r and r + 8 on the same banks: 229K
+//     bank-conflict cycles per M=1024 launch, a third of the LDS-active time.)  The XOR is applied by choosing
 //     which global chunk each lane fetches (the LDS side of the copy is always
 //     lane-linear).
 //   - weights: the tiled layout already stores each 32-column x 32-k block
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
         for (int j = 0; j < C::PA; ++j) {
             const int i = wave * C::PA + j;
             const int row = i * 8 + (lane >> 3);
-            const int chunk = (lane & 7) ^ (row & 7);
+            const int chunk = (lane & 7) ^ ((row >> 1) & 7);
             const uint32_t off = live ? static_cast<uint32_t>(row * K + kt * C::BK + chunk * 16) : kNowhere;
             dma16(xr, dst + i * kLine, off);
         }
@@ -186,7 +189,7 @@ __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
     for (int ib = 0; ib < C::IB; ++ib) {
         const int row = wm * (BM / 2) + 32 * ib + (lane & 31);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) a_off[ib][s] = (row * 8 + ((2 * s + h) ^ (row & 7))) * 16;
+        for (int s = 0; s < 4; ++s) a_off[ib][s] = (row * 8 + ((2 * s + h) ^ ((row >> 1) & 7))) * 16;
     }
     int b_off[C::JB][4];
 #pragma unroll
