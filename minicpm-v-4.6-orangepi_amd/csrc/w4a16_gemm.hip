@@ -43,9 +43,9 @@ namespace mcv {
 
 int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                       const void* zeros, int zero_bias, void* out, hipStream_t stream);
-int choose_w4a16_lds(int64_t M, int64_t N, int* tm, int* ns);
+int choose_w4a16_lds(int64_t M, int64_t K, int64_t N, int* tm, int* ns, int* kp);
 int launch_w4a16_gemm_lds(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
-                          const void* zeros, int zero_bias, void* out, int tm, int ns, hipStream_t stream);
+                          const void* zeros, int zero_bias, void* out, int tm, int ns, int kp, hipStream_t stream);
 
 namespace {
 
@@ -502,9 +502,9 @@ int launch_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const
     // the chip, the register-staged one below otherwise;
     // MCV_W4GEMM_KERNEL=regs forces the latter (read once per process).
     static const char* const which = std::getenv("MCV_W4GEMM_KERNEL");
-    int tm = 0, ns = 0;
-    if ((which == nullptr || std::strcmp(which, "regs") != 0) && choose_w4a16_lds(M, N, &tm, &ns) == 0)
-        return launch_w4a16_gemm_lds(x, M, K, N, qw, scales, zeros, zero_bias, out, tm, ns, stream);
+    int tm = 0, ns = 0, kp = 1;
+    if ((which == nullptr || std::strcmp(which, "regs") != 0) && choose_w4a16_lds(M, K, N, &tm, &ns, &kp) == 0)
+        return launch_w4a16_gemm_lds(x, M, K, N, qw, scales, zeros, zero_bias, out, tm, ns, kp, stream);
     const int64_t nslab = ceil_div(N, kSlab);
     const Shape s = choose_shape(M, K, nslab);
     // Tile order, measured (MI355X, graph-replayed): down the tile columns

@@ -7,7 +7,11 @@
 // Workgroup: 4 waves, tile TM rows x 4 slabs (256 columns); wave w owns slab
 // w of the tile over all TM rows: TM/32 x 2 blocks of
 // v_mfma_f32_32x32x16_f16.  K advances in stages of 128 (one quantisation
-// group, so a wave's scales and zeros are constant over a stage).  Per stage:
+// group, so a wave's scales and zeros are constant over a stage).  With
+// KP = 2 the waves are 2 k-parts x 2 slabs (128-column tiles, twice the
+// workgroups): a stage holds two groups, k-part p computes the p-th, and
+// k-part 1 hands its partial tile to k-part 0 through LDS at the end.  Per
+// stage:
 //   - x rows (TM x 256 bytes) are copied global -> LDS with
 //     buffer_load_dwordx4 ... lds, 4 rows per wave-wide 1 KiB copy; the
 //     16-byte chunk index is XORed with the row's low 4 bits (by choosing
@@ -99,12 +103,16 @@ __device__ __forceinline__ half8_t dequant_octet_w(uint32_t q, uint32_t zz, uint
     return r;
 }
 
-template <int TM, int NS>
+// TM rows per tile, NS stages in flight, KP k-parts: the four waves are KP
+// k-parts x WN = 4 / KP slabs, and a stage covers KP quantisation groups,
+// k-part p taking the p-th.
+template <int TM, int NS, int KP>
 struct CfgW {
-    static constexpr int BK = 128;                         // k per stage: one quantisation group
-    static constexpr int ROW = BK * 2;                     // bytes of one x row per stage
-    static constexpr int A_BYTES = TM * ROW;
-    static constexpr int B_BYTES = 4 * 4 * kLineW;         // 4 slabs x 4 packed chunks
+    static constexpr int WN = 4 / KP;                      // slabs per tile
+    static constexpr int BK = 128;                         // k per k-part per stage: one quantisation group
+    static constexpr int ROW = BK * 2;                     // bytes of one x row per k-part per stage
+    static constexpr int A_BYTES = KP * TM * ROW;          // x blocks of the KP k-parts
+    static constexpr int B_BYTES = 4 * 4 * kLineW;         // each wave's 4 packed chunks
     static constexpr int ZS_BYTES = 4 * 512;               // per wave: 64 zero dwords, 64 scale dwords
     static constexpr int STAGE = A_BYTES + B_BYTES + ZS_BYTES;
     static constexpr int A_COPIES = A_BYTES / kLineW;      // 4 rows per copy
@@ -115,16 +123,18 @@ struct CfgW {
     static constexpr int P = PA + PB + PS;                 // vector-memory ops per wave per stage
     static constexpr int MB = TM / 32;
     static_assert(TM == 32 || TM == 64 || TM == 128, "TM");
+    static_assert(KP == 1 || KP == 2, "KP");
     static_assert(NS >= 2 && NS <= 4 && P * (NS - 1) < 64, "stages");
     static_assert(NS * STAGE <= 160 * 1024, "LDS");
+    static_assert(KP == 1 || WN * MB * 2 * 16 * 64 * 4 <= STAGE, "k-part reduction buffer");
 };
 
-template <int TM, int NS>
+template <int TM, int NS, int KP>
 __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int M, int K, int N,
     int nslab, int n_tiles, int total_tiles, int col_major, int xcd_m) {
-    using C = CfgW<TM, NS>;
+    using C = CfgW<TM, NS, KP>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds2[NS > 2 ? C::STAGE : 16];
@@ -152,10 +162,11 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
         tn = col_major ? tile / m_tiles : tile - tm * n_tiles;
     }
     const int m0 = tm * TM;
-    const int slab = tn * 4 + wave;
+    const int kp = wave / C::WN;                           // k-part of this wave
+    const int slab = tn * C::WN + (wave - kp * C::WN);
     const int Npad = nslab * kSlab;
     const int CK = K / kChunkK;
-    const int KT = K / C::BK;
+    const int KT = K / (C::BK * KP);                       // stages
 
     const int rows_here = M - m0 < TM ? M - m0 : TM;
     const __amdgpu_buffer_rsrc_t xr =
@@ -179,8 +190,11 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     uint32_t xoff[C::PA];
 #pragma unroll
     for (int j = 0; j < C::PA; ++j) {
-        const int row = 4 * (wave * C::PA + j) + (lane >> 4);
-        xoff[j] = static_cast<uint32_t>(row * K) * 2u + static_cast<uint32_t>((lane & 15) ^ (row & 15)) * 16u;
+        const int i = wave * C::PA + j;                    // copy i: k-part block i / (TM/4), 4 rows
+        const int kb = i / (TM / 4);
+        const int row = 4 * (i - kb * (TM / 4)) + (lane >> 4);
+        xoff[j] = static_cast<uint32_t>(row * K + kb * C::BK) * 2u +
+                  static_cast<uint32_t>((lane & 15) ^ (row & 15)) * 16u;
     }
     const uint32_t zoff = (static_cast<uint32_t>(slab) * 32u + lane * 4u) | (lane < 8 ? 0u : 0x80000000u);
     const uint32_t soff = (static_cast<uint32_t>(slab) * 128u + lane * 4u) | (lane < 32 ? 0u : 0x80000000u);
@@ -188,15 +202,16 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     // stage kt into dst.
     auto issue_item = [&](int kt, uint8_t* dst, int it) {
         const int kc = kt < KT ? kt : KT - 1;
+        const int g = kc * KP + kp;                        // this wave's quantisation group
         if (it < C::PA) {
-            dma16_w(xr, dst + (wave * C::PA + it) * kLineW, xoff[it], kc * C::ROW);
+            dma16_w(xr, dst + (wave * C::PA + it) * kLineW, xoff[it], kc * KP * C::ROW);
         } else if (it < C::PA + C::PB) {
             const int c = it - C::PA;
-            dma16_w(qr, dst + C::A_BYTES + (wave * 4 + c) * kLineW, qoff, (kc * 4 + c) * kSlab * 16);
+            dma16_w(qr, dst + C::A_BYTES + (wave * 4 + c) * kLineW, qoff, (g * 4 + c) * kSlab * 16);
         } else if (it == C::PA + C::PB) {
-            dma4_w(zr, dst + C::A_BYTES + C::B_BYTES + wave * 512, zoff, kc * (Npad >> 3) * 4);
+            dma4_w(zr, dst + C::A_BYTES + C::B_BYTES + wave * 512, zoff, g * (Npad >> 3) * 4);
         } else {
-            dma4_w(sr, dst + C::A_BYTES + C::B_BYTES + wave * 512 + 256, soff, kc * Npad * 2);
+            dma4_w(sr, dst + C::A_BYTES + C::B_BYTES + wave * 512 + 256, soff, g * Npad * 2);
         }
     };
     auto issue = [&](int kt, uint8_t* dst) {
@@ -222,7 +237,8 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     // a constant 8 KiB further.
     int a_off[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) a_off[s] = (lane & 31) * C::ROW + (((2 * s + h) ^ (lane & 15)) << 4);
+    for (int s = 0; s < 8; ++s)
+        a_off[s] = kp * TM * C::ROW + (lane & 31) * C::ROW + (((2 * s + h) ^ (lane & 15)) << 4);
     const int b_off = C::A_BYTES + wave * 4 * kLineW + lane * 16;
     const int z_off = C::A_BYTES + C::B_BYTES + wave * 512 + ((lane & 31) >> 3) * 4;
     const int s_off = C::A_BYTES + C::B_BYTES + wave * 512 + 256 + (lane & 31) * 2;
@@ -336,6 +352,31 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+    // k-part 1 hands its partial tile to k-part 0 through LDS (the stage
+    // buffers are free once every wave is past the loop); fp32 adds, in the
+    // same order for every element.
+    if constexpr (KP == 2) {
+        float* red = reinterpret_cast<float*>(lds0) + lane;
+        const int wn = wave - kp * C::WN;
+        __syncthreads();
+        if (kp == 1) {
+#pragma unroll
+            for (int i = 0; i < C::MB; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) red[(((wn * C::MB + i) * 2 + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kp == 1) return;
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] += red[(((wn * C::MB + i) * 2 + j) * 16 + r) * 64];
+    }
+
     // Transposed 32x32 blocks: register r of lane l holds output row
     // 32 i + l%32 and column 32 j + 8 (r/4) + 4 (l/32) + r%4.  Swapping the
     // upper lanes of quad g with the lower lanes of quad g+1 leaves lane l with
@@ -373,48 +414,55 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
 }
 
 struct ShapeW {
-    int tm, ns;
+    int tm, ns, kp;
 };
 
 using GemmWFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int,
                          int, int, int, int, int, int, int);
 
 GemmWFn pick_w(const ShapeW& s) {
-#define MCV_W(TM_, NS_) \
-    if (s.tm == TM_ && s.ns == NS_) return w4a16_gemm_lds_kernel<TM_, NS_>;
-    MCV_W(128, 2) MCV_W(128, 3) MCV_W(64, 2) MCV_W(64, 3) MCV_W(32, 3)
+#define MCV_W(TM_, NS_, KP_) \
+    if (s.tm == TM_ && s.ns == NS_ && s.kp == KP_) return w4a16_gemm_lds_kernel<TM_, NS_, KP_>;
+    MCV_W(128, 2, 1) MCV_W(128, 3, 1) MCV_W(64, 2, 1) MCV_W(64, 3, 1) MCV_W(32, 3, 1) MCV_W(64, 2, 2) MCV_W(64, 3, 2)
+    MCV_W(32, 3, 2)
 #undef MCV_W
     return nullptr;
 }
 
 }  // namespace
 
-// The LDS kernel's shape for M x N, or -1 when the register-staged kernel
-// is the better choice.  Measured on MI355X (graph-replayed, 300 rotated
-// weight sets, microseconds per call; register-staged kernel in brackets):
-// M=2048 K=1024 N=3584 TM=128 NS=2 24.0 (26.6); M=1024 K=1024 N=3584 TM=64
-// NS=2 16.1 (17.9); M=512 K=1024 N=3584 TM=32 11.7 (12.0).  With 32-row
+// The LDS kernel's shape for M x K x N, or -1 when the register-staged
+// kernel is the better choice.  Measured on MI355X (graph-replayed, 300
+// rotated weight sets, microseconds per call; register-staged kernel in
+// brackets): M=2048 K=1024 N=3584 TM=128 24.0 (26.6); M=1024 K=1024 N=3584
+// TM=64 16.1 (17.9); M=512 K=1024 N=3584 TM=32 11.7 (12.0).  With 32-row
 // tiles each widened weight operand feeds only two MFMAs and the VALU work
-// (about 31 instructions per k16 step) dominates, and with N=1024 the grid
-// is too small for tall tiles: K=3584 N=1024 stays with the register-staged
-// kernel at every M (M=2048 30.3 against 32.3 at best; M=512 14.7 against
-// 26.7).  So: the tallest tile (128, then 64 rows) whose grid still covers
-// most of the 256 CUs, else -1.  MCV_W4LDS_SHAPE="TM,NS" forces a shape
-// (read once per process; tuning sweeps).
-int choose_w4a16_lds(int64_t M, int64_t N, int* tm, int* ns) {
+// (about 31 instructions per k16 step) dominates; with N=1024 the grid is
+// too small for tall single-k-part tiles, so 64-row tiles split K over two
+// k-parts of two waves (KP=2, 128-column tiles): M=2048 K=3584 N=1024 26.4
+// (30.7), M=512 K=1024 N=3584 10.2 (12.1); two stages in flight 0.2-0.5 us
+// slower.  Those tiles are VALU-bound (~7.8 widening instructions per MFMA).
+// So: the first of
+// 128-row, 64-row, 64-row-two-k-parts tiles whose grid still covers most of
+// the 256 CUs, else -1.  MCV_W4LDS_SHAPE="TM,NS,KP" forces a shape (read
+// once per process; tuning sweeps).
+int choose_w4a16_lds(int64_t M, int64_t K, int64_t N, int* tm, int* ns, int* kp) {
     static const char* const e = std::getenv("MCV_W4LDS_SHAPE");
-    ShapeW s{0, 0};
-    if (e != nullptr && std::sscanf(e, "%d,%d", &s.tm, &s.ns) == 2 && pick_w(s)) {
+    ShapeW s{0, 0, 1};
+    if (e != nullptr && std::sscanf(e, "%d,%d,%d", &s.tm, &s.ns, &s.kp) >= 2 && pick_w(s) &&
+        K % (int64_t(kGroup) * s.kp) == 0) {
         *tm = s.tm;
         *ns = s.ns;
+        *kp = s.kp;
         return 0;
     }
-    const int64_t n_tiles = ceil_div(ceil_div(N, kSlab), 4);
-    constexpr ShapeW kOrder[] = {{128, 2}, {64, 2}};
+    constexpr ShapeW kOrder[] = {{128, 2, 1}, {64, 2, 1}, {64, 3, 2}};
     for (const ShapeW& c : kOrder) {
-        if (ceil_div(M, c.tm) * n_tiles >= 200) {
+        if (K % (int64_t(kGroup) * c.kp) != 0) continue;
+        if (ceil_div(M, c.tm) * ceil_div(ceil_div(N, kSlab), 4 / c.kp) >= 200) {
             *tm = c.tm;
             *ns = c.ns;
+            *kp = c.kp;
             return 0;
         }
     }
@@ -422,12 +470,15 @@ int choose_w4a16_lds(int64_t M, int64_t N, int* tm, int* ns) {
 }
 
 int launch_w4a16_gemm_lds(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
-                          const void* zeros, int zero_bias, void* out, int tm, int ns, hipStream_t stream) {
-    const ShapeW s{tm, ns};
+                          const void* zeros, int zero_bias, void* out, int tm, int ns, int kp, hipStream_t stream) {
+    const ShapeW s{tm, ns, kp};
     GemmWFn fn = pick_w(s);
-    if (fn == nullptr) return fail(MCV_ERR_INVALID_ARG, "w4a16 GEMM: no LDS kernel for TM=%d NS=%d", tm, ns);
+    if (fn == nullptr || K % (int64_t(kGroup) * kp) != 0)
+        return fail(MCV_ERR_INVALID_ARG, "w4a16 GEMM: no LDS kernel for TM=%d NS=%d KP=%d, K=%lld", tm, ns, kp,
+                    (long long)K);
+    const int wn = 4 / kp;                                 // slabs per tile
     const int64_t nslab = ceil_div(N, kSlab);
-    const int64_t n_tiles = ceil_div(nslab, 4);
+    const int64_t n_tiles = ceil_div(nslab, wn);
     const int64_t total = ceil_div(M, tm) * n_tiles;
     // Tile order: the XCD blocking with the fewest bytes of x and weights per
     // XCD when the tile grid splits evenly, else a contiguous run per XCD,
@@ -442,7 +493,7 @@ int launch_w4a16_gemm_lds(const void* x, int64_t M, int64_t K, int64_t N, const 
         int64_t best = -1;
         for (int a = 1; a <= 8; a *= 2) {
             if (m_tiles % a != 0 || n_tiles % (8 / a) != 0) continue;
-            const int64_t bytes = (m_tiles / a) * tm * K * 2 + (n_tiles / (8 / a)) * 4 * kSlab * K / 2;
+            const int64_t bytes = (m_tiles / a) * tm * K * 2 + (n_tiles / (8 / a)) * wn * kSlab * K / 2;
             if (best < 0 || bytes < best) {
                 best = bytes;
                 xcd_m = a;

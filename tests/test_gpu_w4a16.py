@@ -101,6 +101,8 @@ def test_dequant_bit_exact(mcv, oracle, cuda):
     (2050, 128, 3592),
     # 64-row tiles, ragged M and N
     (1100, 256, 3000),
+    # 64-row tiles over two k-parts (128-column tiles), ragged M and N
+    (1700, 512, 1000),
 ], ids=lambda v: str(v))
 def test_gemm_mfma_vs_oracle(mcv, oracle, cuda, M, K, N):
     x, qweight, qzeros, scales, _ = _case(3000 + M + K + N, M, K, N)
