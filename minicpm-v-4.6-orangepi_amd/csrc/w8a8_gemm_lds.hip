@@ -34,6 +34,10 @@
 // the other stages and keeps them in flight.  The explicit s_waitcnt vmcnt
 // before each barrier is the only wait on the copies; the barrier is a bare
 // s_barrier (a __syncthreads fence would wait for every copy in flight).
+// The copies of a stage are spread over the k32 steps of the one three
+// stages earlier, step s+1's operands are read while step s's MFMAs run, and
+// the barrier sits between the MFMAs of a stage's last step, so the next
+// stage's first operands are read before the pipe drains.
 //
 // Replaces matmul_w8a8_i32_custom + w8a8_dequant_custom
 // (src/csrc/custom_ops/op_kernel/matmul_w8a8_i32_custom.cpp:15-48,
@@ -47,15 +51,15 @@ namespace mcv {
 namespace {
 
 constexpr int kLine = 1024;                 // one 32-column x 32-k operand line
-constexpr uint32_t kNowhere = 0xFFFFFF00u;  // a buffer offset past every range: the load returns zeros
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_l(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
-// 16 bytes per lane, global (buffer `r` at byte `voff`) -> LDS at lds + 16 * lane.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
+// 16 bytes per lane, global (buffer `r` at byte voff + soff) -> LDS at
+// lds + 16 * lane.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
 }
 
 template <int N>
@@ -84,7 +88,8 @@ struct CfgL {
     static constexpr int IB = BM / 64;                 // 32-row blocks per wave
     static constexpr int JB = BN / 64;                 // 32-column blocks per wave
     static_assert(IB >= 1 && JB >= 1 && NS >= 2 && NS <= 4, "tile shape");
-    static_assert(P * (NS - 2) < 64, "vmcnt");
+    static constexpr int PF = 2;                       // weight stages prefetched per tile
+    static_assert(P * (NS - 2) + PF * PB < 64, "vmcnt");
 };
 
 // EPI: 0 int32 out; 4 | x-scale fp16 (1) | weight-scale fp16 (2): fp16 out
@@ -92,7 +97,8 @@ struct CfgL {
 template <int BM, int BN, int NS, int EPI>
 __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
     const int8_t* __restrict__ xq, const int8_t* __restrict__ w, int M, int K, int N, int KB, void* __restrict__ out,
-    const void* __restrict__ xs, const void* __restrict__ ws, int nslab, int n_tiles, int total_tiles, int KT) {
+    const void* __restrict__ xs, const void* __restrict__ ws, int nslab, int n_tiles, int total_tiles, int KT,
+    int xcd_m) {
     constexpr bool OUT_F16 = (EPI & 4) != 0;
     constexpr bool XS16 = (EPI & 1) != 0, WS16 = (EPI & 2) != 0;
     using C = CfgL<BM, BN, NS>;
@@ -100,6 +106,7 @@ __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds2[NS > 2 ? C::STAGE : 16];
     __shared__ __attribute__((aligned(1024))) uint8_t lds3[NS > 3 ? C::STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) uint8_t sink[4 * kLine];   // prefetches land here, never read
     uint8_t* const bufs[4] = {lds0, lds1, lds2, lds3};
 
     const int lane = threadIdx.x & 63;
@@ -107,11 +114,27 @@ __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
     const int wm = wave & 1, wn = wave >> 1;
     const int h = lane >> 5;
 
-    // Tiles of one XCD form a contiguous run, ordered down the tile columns so
-    // the XCD's L2 keeps few weight columns.
-    const int tile = xcd_tile_l(static_cast<int>(blockIdx.x), total_tiles);
+    // Workgroup b runs on XCD b % 8.  With xcd_m > 0 the tile grid is cut
+    // into xcd_m x (8 / xcd_m) blocks, one per XCD, so each XCD's L2 sees
+    // only its block's x rows and weight columns; otherwise the tiles of one
+    // XCD form a contiguous run down the tile columns.  `rows` tiles of one
+    // tile column share an XCD, and this tile is the `ri`-th of them.
     const int m_tiles = total_tiles / n_tiles;
-    const int tm = tile % m_tiles, tn = tile / m_tiles;
+    int tm, tn, rows, ri;
+    if (xcd_m > 0) {
+        const int xb_n = 8 / xcd_m, mr = m_tiles / xcd_m, nr = n_tiles / xb_n;
+        const int xcd = static_cast<int>(blockIdx.x) & 7, i = static_cast<int>(blockIdx.x) >> 3;
+        ri = i % mr;
+        tm = (xcd / xb_n) * mr + ri;
+        tn = (xcd % xb_n) * nr + i / mr;
+        rows = mr;
+    } else {
+        const int tile = xcd_tile_l(static_cast<int>(blockIdx.x), total_tiles);
+        tm = tile % m_tiles;
+        tn = tile / m_tiles;
+        rows = m_tiles;
+        ri = tm;
+    }
     const int m0 = tm * BM, n0 = tn * BN;
     const int slab0 = n0 / kSlab;
 
@@ -122,29 +145,39 @@ __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
     // weights: slabs past the last read as zero
     const __amdgpu_buffer_rsrc_t wr = rsrc_l(w, static_cast<uint32_t>(nslab) * KB * 2 * kLine);
 
-    // This wave's copies of stage kt into `dst`: x copies wave*PA .. +PA (8
-    // rows of 128 bytes each), weight lines wave*PB .. +PB.  Stages past the
-    // last read from kNowhere: zeros land in a free buffer, and every stage
-    // issues the same number of copies, so the vmcnt waits stay exact.
+    // This wave's copies of a stage: x copies wave*PA .. +PA (8 rows of 128
+    // bytes each), weight lines wave*PB .. +PB.  Each lane's offset inside a
+    // stage is fixed (computed once here); the stage's advance is one scalar
+    // add for x and rides in the scalar offset for the weights, whose buffer
+    // is padded to whole stages.  Stages past the last re-read the last stage
+    // into a buffer that is never read again: every stage issues the same P
+    // copies with no branch, so the vmcnt waits stay exact (a select compiled
+    // into a branch makes the waitcnt pass wait for the next stage's copies
+    // before this stage's operand reads), and every access stays in range.
+    uint32_t xoff[C::PA], woff[C::PB];
+#pragma unroll
+    for (int j = 0; j < C::PA; ++j) {
+        const int row = (wave * C::PA + j) * 8 + (lane >> 3);
+        xoff[j] = static_cast<uint32_t>(row * K + (((lane & 7) ^ ((row >> 1) & 7)) << 4));
+    }
+#pragma unroll
+    for (int j = 0; j < C::PB; ++j) {
+        const int bi = wave * C::PB + j;                               // (slab bi / 8, k32 block, half)
+        woff[j] = (static_cast<uint32_t>(slab0 + (bi >> 3)) * KB * 2 + (bi & 7)) * kLine + lane * 16u;
+    }
+    auto issue_item = [&](int kt, uint8_t* dst, int it) {
+        const int kc = kt < KT ? kt : KT - 1;
+        if (it < C::PA) {
+            dma16(xr, dst + (wave * C::PA + it) * kLine, xoff[it] + static_cast<uint32_t>(kc * C::BK), 0);
+        } else {
+            const int j = it - C::PA;
+            dma16(wr, dst + C::A_BYTES + (wave * C::PB + j) * kLine, woff[j], kc * 8 * kLine);
+        }
+    };
+
     auto issue = [&](int kt, uint8_t* dst) {
-        const bool live = kt < KT;
 #pragma unroll
-        for (int j = 0; j < C::PA; ++j) {
-            const int i = wave * C::PA + j;
-            const int row = i * 8 + (lane >> 3);
-            const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-            const uint32_t off = live ? static_cast<uint32_t>(row * K + kt * C::BK + chunk * 16) : kNowhere;
-            dma16(xr, dst + i * kLine, off);
-        }
-#pragma unroll
-        for (int j = 0; j < C::PB; ++j) {
-            const int bi = wave * C::PB + j;                           // (slab sl, k32 block, half)
-            const int sl = bi >> 3;
-            const uint32_t off =
-                live ? (static_cast<uint32_t>(slab0 + sl) * KB * 2 + kt * 8 + (bi & 7)) * kLine + lane * 16u
-                     : kNowhere;
-            dma16(wr, dst + C::A_BYTES + bi * kLine, off);
-        }
+        for (int it = 0; it < C::P; ++it) issue_item(kt, dst, it);
     };
 
     // The fused epilogue's scales, as raw bits, issued before the first copy:
@@ -152,21 +185,48 @@ __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
     // Register r of block (ib, jb) holds row wm*BM/2 + 32 ib + l%32 and column
     // wn*BN/2 + 32 jb + 8 (r/4) + 4 h + r%4.
     // Buffer loads: columns past N and rows past M read as zero with no branch,
-    // so all of them issue back to back.
+    // so all of them issue back to back.  A lane's four consecutive weight
+    // scales come in one load when N % 4 == 0 and the scales are aligned
+    // (a quad is then wholly inside or wholly past N); otherwise one load per
+    // scale.  Each gather instruction holds the address unit for the whole
+    // wave, and these go ahead of the first stage's copies: 8 instead of 32
+    // per wave brings the first stage in ~0.25 us sooner.  They are older
+    // than every copy, so their number does not enter the vmcnt waits.
     uint32_t wraw[C::JB][4][4], xraw[C::IB];
     if constexpr (OUT_F16) {
         const __amdgpu_buffer_rsrc_t wsr = rsrc_l(ws, static_cast<uint32_t>(N) * (WS16 ? 2u : 4u));
         const __amdgpu_buffer_rsrc_t xsr = rsrc_l(xs, static_cast<uint32_t>(M) * (XS16 ? 2u : 4u));
+        const bool quads = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(ws) & (WS16 ? 7u : 15u)) == 0;
+        if (quads) {
 #pragma unroll
-        for (int jb = 0; jb < C::JB; ++jb)
+            for (int jb = 0; jb < C::JB; ++jb)
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
+                for (int g = 0; g < 4; ++g) {
+                    const uint32_t n = static_cast<uint32_t>(n0 + wn * (BN / 2) + 32 * jb + 8 * g + 4 * h);
+                    if constexpr (WS16) {
+                        const auto v = __builtin_amdgcn_raw_buffer_load_b64(wsr, n * 2u, 0, 0);
+                        wraw[jb][g][0] = v[0] & 0xFFFFu;
+                        wraw[jb][g][1] = v[0] >> 16;
+                        wraw[jb][g][2] = v[1] & 0xFFFFu;
+                        wraw[jb][g][3] = v[1] >> 16;
+                    } else {
+                        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wsr, n * 4u, 0, 0);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t n = static_cast<uint32_t>(n0 + wn * (BN / 2) + 32 * jb + 8 * g + 4 * h + e);
-                    if constexpr (WS16) wraw[jb][g][e] = __builtin_amdgcn_raw_buffer_load_b16(wsr, n * 2u, 0, 0);
-                    else wraw[jb][g][e] = __builtin_amdgcn_raw_buffer_load_b32(wsr, n * 4u, 0, 0);
+                        for (int e = 0; e < 4; ++e) wraw[jb][g][e] = v[e];
+                    }
                 }
+        } else {
+#pragma unroll
+            for (int jb = 0; jb < C::JB; ++jb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t n = static_cast<uint32_t>(n0 + wn * (BN / 2) + 32 * jb + 8 * g + 4 * h + e);
+                        if constexpr (WS16) wraw[jb][g][e] = __builtin_amdgcn_raw_buffer_load_b16(wsr, n * 2u, 0, 0);
+                        else wraw[jb][g][e] = __builtin_amdgcn_raw_buffer_load_b32(wsr, n * 4u, 0, 0);
+                    }
+        }
 #pragma unroll
         for (int ib = 0; ib < C::IB; ++ib) {
             const uint32_t m = static_cast<uint32_t>(m0 + wm * (BM / 2) + 32 * ib + (lane & 31));
@@ -200,47 +260,111 @@ __global__ __launch_bounds__(256) void w8a8_gemm_lds_kernel(
         for (int s = 0; s < 4; ++s) b_off[jb][s] = C::A_BYTES + ((sl * 4 + s) * 2 + jh) * kLine + lane * 16;
     }
 
-    auto compute = [&](const uint8_t* src) {
+    // Operands of k32 step s, double-buffered: step s uses set s & 1.
+    int4_t af[2][C::IB], bf[2][C::JB];
+    auto read_ops = [&](const uint8_t* src, int s, int set) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            int4_t a[C::IB], b[C::JB];
+        for (int ib = 0; ib < C::IB; ++ib) af[set][ib] = *reinterpret_cast<const int4_t*>(src + a_off[ib][s]);
 #pragma unroll
-            for (int ib = 0; ib < C::IB; ++ib) a[ib] = *reinterpret_cast<const int4_t*>(src + a_off[ib][s]);
+        for (int jb = 0; jb < C::JB; ++jb) bf[set][jb] = *reinterpret_cast<const int4_t*>(src + b_off[jb][s]);
+    };
+    constexpr int kNM = C::IB * C::JB;                 // MFMAs per k32 step
+    constexpr int kNR = C::IB + C::JB;                 // operand reads per k32 step
+    auto mfmas = [&](int set, int lo, int hi) {
 #pragma unroll
-            for (int jb = 0; jb < C::JB; ++jb) b[jb] = *reinterpret_cast<const int4_t*>(src + b_off[jb][s]);
-#pragma unroll
-            for (int ib = 0; ib < C::IB; ++ib)
-#pragma unroll
-                for (int jb = 0; jb < C::JB; ++jb)
-                    acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[jb], a[ib], acc[ib][jb], 0, 0, 0);
+        for (int m = lo; m < hi; ++m) {
+            const int ib = m / C::JB, jb = m % C::JB;
+            acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[set][jb], af[set][ib], acc[ib][jb], 0, 0, 0);
         }
     };
 
-    // Stage kt in buffer kt % NS.  Each step: this wave's copies of stage kt
-    // are done (vmcnt), every wave's are and every wave has finished stage
-    // kt - 1 (barrier); then the copies of stage kt + NS - 1 go into the
-    // buffer stage kt - 1 used, and stage kt is computed.
+    // One stage from `cur`.  Steps 0-2 read step s+1's operands while step
+    // s's MFMAs run and spread the copies of stage kt + NS - 1 into `prv`
+    // (free since the last barrier) over the steps: a burst of copies stalls
+    // the issuing wave, and with one wave per SIMD the MFMA pipe with it.
+    // Each step is its own scheduling region laid out as (DS read, copy,
+    // MFMA) groups.  Step 3 crosses into the next stage between its MFMAs:
+    // wait for the next stage's copies (this wave's by vmcnt, everyone's by
+    // the barrier, which also says every wave is done reading `cur`), then
+    // read the next stage's step-0 operands from `nxt` before the last MFMAs.
+    auto run_stage = [&](int kt, const uint8_t* cur, const uint8_t* nxt, uint8_t* prv) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const int c = s & 1, n = c ^ 1;
+            constexpr int kLo[4] = {0, C::P / 3, 2 * C::P / 3, C::P};
+#pragma unroll
+            for (int it = kLo[s]; it < kLo[s + 1]; ++it) issue_item(kt + NS - 1, prv, it);
+            read_ops(cur, s + 1, n);
+            mfmas(c, 0, kNM);
+            constexpr int kCp[3] = {kLo[1] - kLo[0], kLo[2] - kLo[1], kLo[3] - kLo[2]};
+#pragma unroll
+            for (int i = 0; i < kNM; ++i) {
+                const int nr = kNR / kNM + (i < kNR % kNM ? 1 : 0);
+                const int nc = kCp[s] / kNM + (i < kCp[s] % kNM ? 1 : 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (r < nr) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (r < nc) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // copy
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        mfmas(1, 0, (kNM + 1) / 2);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        wait_vmcnt<C::P * (NS - 2)>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        read_ops(nxt, 0, 0);
+        mfmas(1, (kNM + 1) / 2, kNM);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Stage kt lives in buffer kt % NS.  Prologue: stages 0 .. NS-2 (stage
+    // NS-1 goes out during stage 0), then the first crossing.
 #pragma unroll
     for (int d = 0; d < NS - 1; ++d) issue(d, bufs[d]);
+    // Weight prefetch.  The `rows` tiles of a tile column on one XCD read the
+    // same weight lines in step with each other, so without it each line is
+    // first asked for one ring depth ahead of its use and every stage waits
+    // out an HBM miss (0.5 us per stage instead of 0.3 at K=1024, N=3584).
+    // The ri-th of them asks now for stages NS - 1 + ri + f * rows (f < PF)
+    // of its columns, into a sink nobody reads (together they cover stages
+    // NS - 1 .. NS - 2 + PF * rows); when the loop gets there the lines are L2
+    // hits.  (Asking two stages ahead of the ring instead, one line per wave
+    // per stage, was too late: the misses take longer under this load.)  A
+    // stage past the last asks for an offset past the buffer, which moves
+    // nothing.  PF * PB copies per wave, always, so the vmcnt waits stay
+    // exact.
+#pragma unroll
+    for (int f = 0; f < C::PF; ++f) {
+        const int sp = NS - 1 + ri + f * rows;
+        const uint32_t dead = static_cast<uint32_t>(sp >= KT) << 31;
+        const int spc = sp < KT ? sp : KT - 1;
+#pragma unroll
+        for (int j = 0; j < C::PB; ++j) dma16(wr, sink + wave * kLine, woff[j] | dead, spc * 8 * kLine);
+    }
+    wait_vmcnt<C::P * (NS - 2) + C::PF * C::PB>();
+    __builtin_amdgcn_s_barrier();
+    read_ops(bufs[0], 0, 0);
+    // Every stage runs the same body; the last ones copy the last stage
+    // again and the last crossing reads operands that are never used.
     int kt = 0;
     for (; kt + NS <= KT; kt += NS) {
 #pragma unroll
-        for (int u = 0; u < NS; ++u) {
-            wait_vmcnt<C::P * (NS - 2)>();
-            __builtin_amdgcn_s_barrier();
-            issue(kt + u + NS - 1, bufs[(u + NS - 1) % NS]);
-            compute(bufs[u]);
-        }
+        for (int u = 0; u < NS; ++u) run_stage(kt + u, bufs[u], bufs[(u + 1) % NS], bufs[(u + NS - 1) % NS]);
     }
+    // (the tail leaves by `break`, so each tail stage is reached only from
+    // the one before and the copy accounting stays exact)
 #pragma unroll
     for (int u = 0; u < NS - 1; ++u) {
-        if (kt + u < KT) {
-            wait_vmcnt<C::P * (NS - 2)>();
-            __builtin_amdgcn_s_barrier();
-            issue(kt + u + NS - 1, bufs[(u + NS - 1) % NS]);
-            compute(bufs[u]);
-        }
+        if (kt + u >= KT) break;
+        run_stage(kt + u, bufs[u], bufs[(u + 1) % NS], bufs[(u + NS - 1) % NS]);
     }
+    // no copy may land in LDS after the workgroup has left
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     const int row_base = m0 + wm * (BM / 2);
     const int col_base = n0 + wn * (BN / 2);
@@ -322,7 +446,7 @@ struct ShapeL {
 };
 
 using GemmLFn = void (*)(const int8_t*, const int8_t*, int, int, int, int, void*, const void*, const void*, int, int,
-                         int, int);
+                         int, int, int);
 
 template <int EPI>
 GemmLFn pick_epi(const ShapeL& s) {
@@ -380,18 +504,31 @@ int launch_w8a8_gemm_lds(const int8_t* xq, int64_t M, int64_t K, int64_t N, cons
                          const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream) {
     const int64_t nslab = ceil_div(N, kSlab);
     const int64_t KB = ceil_div(K, 128) * 4;
-    if (nslab * KB * 2 * kLine >= (int64_t(1) << 32) || M * K >= (int64_t(1) << 32))
-        return fail(MCV_ERR_SHAPE, "w8a8 GEMM: weight or activation exceeds 4 GiB");
+    // (bit 31 of a weight offset marks a prefetch with nothing to fetch)
+    if (nslab * KB * 2 * kLine >= (int64_t(1) << 31) || M * K >= (int64_t(1) << 32))
+        return fail(MCV_ERR_SHAPE, "w8a8 GEMM: weight exceeds 2 GiB or activation 4 GiB");
     const ShapeL s = choose_l(M, N);
     const int64_t n_tiles = ceil_div(N, s.bn);
     const int64_t total = ceil_div(M, s.bm) * n_tiles;
     if (total > 0x7fffffff) return fail(MCV_ERR_SHAPE, "w8a8 GEMM: too many tiles");
     const int KT = static_cast<int>(KB / 4);
     const int epi = f16 ? 4 | (xs16 ? 1 : 0) | (ws16 ? 2 : 0) : 0;
+    // Tile order: a contiguous run of tiles per XCD, down the tile columns.
+    // Cutting the grid into one 2-D block per XCD halves the x bytes each L2
+    // sees but doubles the weight columns, which come from HBM: slower at
+    // M = 1024 (8.7 against 8.4 us).  MCV_W8LDS_XCDM=a forces the a x (8 / a)
+    // blocking (read once per process; tuning sweeps).
+    const int64_t m_tiles = ceil_div(M, s.bm);
+    int xcd_m = 0;
+    static const char* const xe = std::getenv("MCV_W8LDS_XCDM");
+    if (xe != nullptr) {
+        const int a = std::atoi(xe);
+        if ((a == 1 || a == 2 || a == 4 || a == 8) && m_tiles % a == 0 && n_tiles % (8 / a) == 0) xcd_m = a;
+    }
     hipLaunchKernelGGL(pick_l(s, epi), dim3(static_cast<unsigned>(total)),
                        dim3(256), 0, stream, xq, w, static_cast<int>(M), static_cast<int>(K), static_cast<int>(N),
                        static_cast<int>(KB), out, xs, ws, static_cast<int>(nslab), static_cast<int>(n_tiles),
-                       static_cast<int>(total), KT);
+                       static_cast<int>(total), KT, xcd_m);
     return check_launch("w8a8_gemm_lds_kernel");
 }
 
