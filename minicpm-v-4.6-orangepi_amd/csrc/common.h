@@ -44,6 +44,44 @@ typedef int int16_t_v __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
+// (a & smask) | vmagic in one v_and_or_b32, the mask in an SGPR.
+__device__ __forceinline__ uint32_t and_or_b32(uint32_t a, uint32_t smask, uint32_t vmagic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(smask), "v"(vmagic));
+    return r;
+}
+
+// The W4A16 GEMMs' weight operands: two packed words (k-octets: k 2p at bits
+// 4p..4p+3, k 2p+1 at bits 16+4p..19+4p) widened into the fp16 MFMA operands
+// k0..k7 = RNE((q - z) * s), the values mcv_w4a16_dequant materialises.  A
+// nibble pair becomes half2(1024 + q) through the fp16 exponent (mlo =
+// 0x000F000F, vmagic = 0x64006400), minus zz = half2(1024 + z) (exact), times
+// ss = half2(s) (one rounding).  The eight pairs of the two words go through
+// each step together, so each step's eight instructions are independent: a
+// VALU result read by the next instruction costs a wait state on gfx950, and
+// one word at a time as a single chain left a nop between most of them.
+__device__ __forceinline__ void dequant_pair(uint32_t qa, uint32_t qb, uint32_t zza, uint32_t ssa, uint32_t zzb,
+                                             uint32_t ssb, uint32_t mlo, uint32_t vmagic, half8_t& ra, half8_t& rb) {
+    uint32_t t[8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        t[2 * p] = and_or_b32(p ? qa >> (4 * p) : qa, mlo, vmagic);
+        t[2 * p + 1] = and_or_b32(p ? qb >> (4 * p) : qb, mlo, vmagic);
+    }
+    half2_t d[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = as_h2(t[i]) - as_h2((i & 1) ? zzb : zza);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = d[i] * as_h2((i & 1) ? ssb : ssa);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        ra[2 * p] = d[2 * p][0];
+        ra[2 * p + 1] = d[2 * p][1];
+        rb[2 * p] = d[2 * p + 1][0];
+        rb[2 * p + 1] = d[2 * p + 1][1];
+    }
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }

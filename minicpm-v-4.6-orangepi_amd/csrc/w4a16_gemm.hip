@@ -50,27 +50,6 @@ int launch_w4a16_gemm_lds(const void* x, int64_t M, int64_t K, int64_t N, const 
 namespace {
 
 
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t smask, uint32_t vmagic) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(smask), "v"(vmagic));
-    return r;
-}
-
-// Widens one packed word (k-octet: nibble s holds k = order[s]) into the
-// fp16 operand k0..k7 = (q - z) * s.  zz = half2(1024 + z), ss = half2(s).
-__device__ __forceinline__ half8_t dequant_octet(uint32_t q, uint32_t zz, uint32_t ss, uint32_t mlo,
-                                                 uint32_t vmagic) {
-    const half2_t z2 = as_h2(zz), s2 = as_h2(ss);
-    const half2_t p0 = (as_h2(and_or(q, mlo, vmagic)) - z2) * s2;          // k0, k1
-    const half2_t p1 = (as_h2(and_or(q >> 4, mlo, vmagic)) - z2) * s2;     // k2, k3
-    const half2_t p2 = (as_h2(and_or(q >> 8, mlo, vmagic)) - z2) * s2;     // k4, k5
-    const half2_t p3 = (as_h2(and_or(q >> 12, mlo, vmagic)) - z2) * s2;    // k6, k7
-    half8_t r;
-    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
-    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
-    return r;
-}
-
 // Workgroup b of `total` is dispatched to XCD b % 8; hand XCD x the
 // contiguous logical range [x * per + min(x, rem), ...).
 __device__ __forceinline__ int xcd_tile(int b, int total) {
@@ -272,8 +251,7 @@ __global__ __launch_bounds__(64 * WN * KS) void w4a16_gemm_kernel(
             const uint32_t words[4] = {q[c].x, q[c].y, q[c].z, q[c].w};
             // lanes 32-63 of octet 2t <-> lanes 0-31 of octet 2t+1
             const auto sw = __builtin_amdgcn_permlane32_swap(words[2 * t], words[2 * t + 1], false, false);
-            b0 = dequant_octet(sw[0], zs.x, zs.z, mlo, vmagic);
-            b1 = dequant_octet(sw[1], zs.y, zs.w, mlo, vmagic);
+            dequant_pair(sw[0], sw[1], zs.x, zs.z, zs.y, zs.w, mlo, vmagic, b0, b1);
         };
         half8_t af[2][C::MB], bf[2][2];
 #pragma unroll

@@ -82,27 +82,6 @@ __device__ __forceinline__ int xcd_tile_w(int b, int total) {
     return x * per + (x < rem ? x : rem) + i;
 }
 
-__device__ __forceinline__ uint32_t and_or_w(uint32_t a, uint32_t smask, uint32_t vmagic) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(smask), "v"(vmagic));
-    return r;
-}
-
-// One packed word (k-octet: nibble s holds k = order[s]) -> the fp16 operand
-// k0..k7 = (q - z) * s; zz = half2(1024 + z), ss = half2(s).
-__device__ __forceinline__ half8_t dequant_octet_w(uint32_t q, uint32_t zz, uint32_t ss, uint32_t mlo,
-                                                   uint32_t vmagic) {
-    const half2_t z2 = as_h2(zz), s2 = as_h2(ss);
-    const half2_t p0 = (as_h2(and_or_w(q, mlo, vmagic)) - z2) * s2;
-    const half2_t p1 = (as_h2(and_or_w(q >> 4, mlo, vmagic)) - z2) * s2;
-    const half2_t p2 = (as_h2(and_or_w(q >> 8, mlo, vmagic)) - z2) * s2;
-    const half2_t p3 = (as_h2(and_or_w(q >> 12, mlo, vmagic)) - z2) * s2;
-    half8_t r;
-    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
-    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
-    return r;
-}
-
 // TM rows per tile, NS stages in flight, KP k-parts: the four waves are KP
 // k-parts x WN = 4 / KP slabs, and a stage covers KP quantisation groups,
 // k-part p taking the p-th.
@@ -254,8 +233,7 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
         const uint32_t w0 = (s & 1) ? qc.z : qc.x, w1 = (s & 1) ? qc.w : qc.y;
         // lanes 32-63 of octet 2t <-> lanes 0-31 of octet 2t+1
         const auto sw = __builtin_amdgcn_permlane32_swap(w0, w1, false, false);
-        b0 = dequant_octet_w(sw[0], zz0, ss0, mlo, vmagic);
-        b1 = dequant_octet_w(sw[1], zz1, ss1, mlo, vmagic);
+        dequant_pair(sw[0], sw[1], zz0, ss0, zz1, ss1, mlo, vmagic, b0, b1);
     };
     auto read_a = [&](const uint8_t* src, int s, half8_t* dst) {
 #pragma unroll
@@ -433,19 +411,21 @@ GemmWFn pick_w(const ShapeW& s) {
 
 // The LDS kernel's shape for M x K x N, or -1 when the register-staged
 // kernel is the better choice.  Measured on MI355X (graph-replayed, 300
-// rotated weight sets, microseconds per call; register-staged kernel in
-// brackets): M=2048 K=1024 N=3584 TM=128 24.0 (26.6); M=1024 K=1024 N=3584
-// TM=64 16.1 (17.9); M=512 K=1024 N=3584 TM=32 11.7 (12.0).  With 32-row
-// tiles each widened weight operand feeds only two MFMAs and the VALU work
-// (about 31 instructions per k16 step) dominates; with N=1024 the grid is
-// too small for tall single-k-part tiles, so 64-row tiles split K over two
-// k-parts of two waves (KP=2, 128-column tiles): M=2048 K=3584 N=1024 26.4
-// (30.7), M=512 K=1024 N=3584 10.2 (12.1); two stages in flight 0.2-0.5 us
-// slower.  Those tiles are VALU-bound (~7.8 widening instructions per MFMA).
-// So: the first of
-// 128-row, 64-row, 64-row-two-k-parts tiles whose grid still covers most of
-// the 256 CUs, else -1.  MCV_W4LDS_SHAPE="TM,NS,KP" forces a shape (read
-// once per process; tuning sweeps).
+// rotated weight sets of random data, microseconds per call; register-staged
+// kernel in brackets): M=2048 K=1024 N=3584 TM=128 22.5 (26.6); M=1024
+// K=1024 N=3584 TM=64 14.7 (17.9); M=512 K=1024 N=3584 TM=32 11.7 (12.0).
+// With 32-row tiles each widened weight operand feeds only two MFMAs and the
+// VALU work (about 31 instructions per k16 step) dominates; with N=1024 the
+// grid is too small for tall single-k-part tiles, so 64-row tiles split K
+// over two k-parts of two waves (KP=2, 128-column tiles): M=2048 K=3584
+// N=1024 24.0 (30.7), M=512 K=1024 N=3584 9.8 (12.1).  Three stages in
+// flight: with two, the copies of stage kt + 1 go out during stage kt and the
+// last of them has a k16 step or two to land before the next barrier waits
+// for it (M=1024: 15.4 against 14.7 us; M=2048 K=1024: equal with random
+// data, 1 us slower with constant data).  So: the first of 128-row, 64-row,
+// 64-row-two-k-parts tiles whose grid still covers most of the 256 CUs, else
+// -1.  MCV_W4LDS_SHAPE="TM,NS,KP" forces a shape (read once per process;
+// tuning sweeps).
 int choose_w4a16_lds(int64_t M, int64_t K, int64_t N, int* tm, int* ns, int* kp) {
     static const char* const e = std::getenv("MCV_W4LDS_SHAPE");
     ShapeW s{0, 0, 1};
@@ -456,7 +436,7 @@ int choose_w4a16_lds(int64_t M, int64_t K, int64_t N, int* tm, int* ns, int* kp)
         *kp = s.kp;
         return 0;
     }
-    constexpr ShapeW kOrder[] = {{128, 2, 1}, {64, 2, 1}, {64, 3, 2}};
+    constexpr ShapeW kOrder[] = {{128, 3, 1}, {64, 3, 1}, {64, 3, 2}};
     for (const ShapeW& c : kOrder) {
         if (K % (int64_t(kGroup) * c.kp) != 0) continue;
         if (ceil_div(M, c.tm) * ceil_div(ceil_div(N, kSlab), 4 / c.kp) >= 200) {
