@@ -293,14 +293,17 @@ def test_lm_head_shapes(mcv, oracle, cuda, K, V, zb):
     assert int(head.launch(_to_dev(x)).item()) == tok
 
 
+# K = 1024 takes the lm_head's one-group-per-wave path, with 5, 9 and 98
+# workgroups; three calls in a row per shape.
+@pytest.mark.parametrize("K", [512, 1024])
 @pytest.mark.parametrize("V", [4097, 8320, 100000])
-def test_lm_head_routes_agree(mcv, oracle, cuda, V):
+def test_lm_head_routes_agree(mcv, oracle, cuda, V, K):
     """The call-tagged key words read by the grid's last workgroup,
     the host-finished tagged slots and the two-kernel keys + reduction give
     the same token and logits, call after call with no wait giving up."""
     torch = _torch()
-    K, NW = 512, -(-V // 8) * 8
-    rng = np.random.default_rng(V + 11)
+    NW = -(-V // 8) * 8
+    rng = np.random.default_rng(V + 11 + K)
     w_f16 = f16_normal(rng, (K, NW), 0.02)
     qweight, qzeros, scales = mcv.quantize_int4(w_f16)
     w = _dev_weight(mcv, qweight, qzeros, scales)
