@@ -507,7 +507,10 @@ class LmHead(Cfg):
     def setup(self):
         import torch
         pkg = self.pkg
-        K, V, NW = 1024, 248094, 248096
+        # V: the full vocabulary, or (--V, or `vocab`) one GPU's share of a
+        # column split
+        K, V = 1024, getattr(self, "vocab", 0) or self.args.V or 248094
+        NW = -(-V // 8) * 8
         self.K, self.V = K, V
         rng = np.random.default_rng(1)
         t = time.perf_counter()
@@ -518,7 +521,7 @@ class LmHead(Cfg):
         qw, sc, zr = pkg.pack_awq(self.qweight, self.qzeros, self.scales)
         log(f"[lm_head] synthetic weights quantised + packed in {time.perf_counter() - t:.1f} s")
         base = pkg.W4A16QuantizedWeight.from_packed(qw, sc, zr, K, NW, 0)
-        copies = self.args.copies or 8
+        copies = self.args.copies or max(8, -(-1_050_000_000 // (qw.nbytes + sc.nbytes + zr.nbytes)))
         self.heads = [pkg.LmHeadW4A16(w_, V) for w_ in _clone_w4(pkg, base, copies)]
         self.rotated = copies * (qw.nbytes + sc.nbytes + zr.nbytes)
         self.xd = to_dev_f16(self.x)
@@ -549,6 +552,42 @@ class LmHead(Cfg):
             return o.argmax_f16(logits)
         s = f"full lm_head K=1024 V={V}: fp32 group formula over unpacked int8 (q-z) + first-max argmax"
         return cpu_baseline(fn, self.bytes, self.bytes, "GB/s", s, s, self.info, budget_s=4.0)
+
+
+SHARD_V = -(-248094 // 8)          # one GPU's columns of an 8-way split of the vocabulary
+
+
+def lm_head_entry(lm, args, route, steps, cpu_entry):
+    """One lm_head line: `steps` timed back-to-back launches (after untimed
+    ones), the other argmax route, per-launch durations and the token."""
+    import torch
+    other = "slots" if route == "tree" else "tree"
+    lm.gpu_steps(200, 20, route)                 # the other configurations ran on other shapes: settle clocks
+    total_ms = lm.gpu_steps(steps, args.warmup, route)
+    alt_ms = lm.gpu_steps(max(steps, 200), args.warmup, other)
+    pl = lm.per_launch(route)
+    token = lm.token()
+    torch.cuda.synchronize()
+    ms = total_ms / steps
+    value = lm.bytes / (ms / 1e3) / 1e9
+    spw = lm.pkg.lm_head_slabs_per_workgroup(lm.V)
+    kernel = f"w4a16_lm_head_kernel<{spw},{'kLmTree' if route == 'tree' else 'kLmSlots'}> (GEMV + fused argmax)"
+    entry = {"kernel": kernel, "us_per_call": round(ms * 1e3, 3), "value": round(value, 2), "unit": "GB/s",
+             "kernel_us_median": round(float(np.median(pl)) * 1e3, 3),
+             "kernel_us_mean": round(float(pl.mean()) * 1e3, 3), "per_launch_samples": int(pl.size),
+             "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(value / HBM_PEAK_GBS, 4),
+                          "traffic": traffic_from_profiles(lm.name) if lm.V == 248094 else None,
+                          "algorithmic_per_launch": lm.bytes},
+             "alt_route": {other: {"us_per_call": round(alt_ms / max(steps, 200) * 1e3, 3),
+                                   "value": round(lm.bytes / (alt_ms / max(steps, 200) / 1e3) / 1e9, 2)}},
+             "config": {"M": 1, "K": lm.K, "V": lm.V, "argmax": route, "launch": "direct",
+                        "weight_copies_rotated": len(lm.heads), "rotated_bytes": lm.rotated,
+                        "algorithmic_bytes": lm.bytes, "token": token},
+             "cpu_baseline": cpu_entry}
+    log(f"[lm_head V={lm.V}] {entry['us_per_call']} us/step over {steps} steps, median {entry['kernel_us_median']} "
+        f"us per launch, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak)")
+    return entry
 
 
 # --------------------------------------------------------------------------- #
@@ -595,31 +634,19 @@ def run_all(pkg, args, info):
         configs["5_w8a8_gemm_K1024_N3584"][c.name]["cpu_baseline"] = cpu.get(c.name)
 
     # headline: the lm_head, W untimed steps then exactly K timed steps
-    route, other = (args.argmax, "slots" if args.argmax == "tree" else "tree")
-    lm.gpu_steps(200, 20, route)                 # the other configurations ran on other shapes: settle clocks
-    total_ms = lm.gpu_steps(args.steps, args.warmup, route)
-    alt_ms = lm.gpu_steps(max(args.steps, 200), args.warmup, other)
-    pl = lm.per_launch(route)
-    token = lm.token()
-    torch.cuda.synchronize()
-    ms = total_ms / args.steps
-    value = lm.bytes / (ms / 1e3) / 1e9
-    kernel = f"w4a16_lm_head_kernel<16,{'kLmTree' if route == 'tree' else 'kLmSlots'}> (GEMV + fused argmax)"
-    lm_entry = {"kernel": kernel, "us_per_call": round(ms * 1e3, 3), "value": round(value, 2), "unit": "GB/s",
-                "kernel_us_median": round(float(np.median(pl)) * 1e3, 3),
-                "kernel_us_mean": round(float(pl.mean()) * 1e3, 3), "per_launch_samples": int(pl.size),
-                "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(lm.name),
-                             "algorithmic_per_launch": lm.bytes},
-                "alt_route": {other: {"us_per_call": round(alt_ms / max(args.steps, 200) * 1e3, 3),
-                                      "value": round(lm.bytes / (alt_ms / max(args.steps, 200) / 1e3) / 1e9, 2)}},
-                "config": {"M": 1, "K": lm.K, "V": lm.V, "argmax": route, "launch": "direct",
-                           "weight_copies_rotated": len(lm.heads), "rotated_bytes": lm.rotated,
-                           "algorithmic_bytes": lm.bytes, "token": token},
-                "cpu_baseline": cpu.get(lm.name)}
+    route = args.argmax
+    lm_entry = lm_head_entry(lm, args, route, args.steps, cpu.get(lm.name))
+    value, ms, kernel = lm_entry["value"], lm_entry["us_per_call"] / 1e3, lm_entry["kernel"]
     configs["3_lm_head_K1024_V248094"] = lm_entry
-    log(f"[lm_head] {lm_entry['us_per_call']} us/step over {args.steps} steps, median {lm_entry['kernel_us_median']} "
-        f"us per launch, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak)")
+    # the same kernel on one GPU's share of an 8-way column split of the
+    # vocabulary (not a BASELINE configuration; how the lm_head would run sharded)
+    del lm.heads, lm.tree, lm.slots
+    shard = LmHead(pkg, args, info)
+    shard.vocab = SHARD_V
+    shard.setup()
+    sh_cpu = None if args.no_cpu else shard.cpu()
+    configs[f"3s_lm_head_shard_K1024_V{SHARD_V}"] = lm_head_entry(shard, args, route, args.steps, sh_cpu)
+    del shard
     return {
         "metric": METRIC,
         "value": round(value, 2),
@@ -790,6 +817,7 @@ def main():
     ap.add_argument("--M", type=int, default=0)
     ap.add_argument("--K", type=int, default=0)
     ap.add_argument("--N", type=int, default=0)
+    ap.add_argument("--V", type=int, default=0, help="lm_head vocabulary (default 248094)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--argmax", default="tree", choices=["tree", "slots"],
                     help="lm_head: token on the device (tree) or host-finished tagged slots")

@@ -231,6 +231,12 @@ int mcv_w4a16_gemv_multi(const void* x_dev, int64_t M, int64_t K, const mcv_w4a1
  * next call.  Returns 0 for an unsupported V. */
 int64_t mcv_lm_head_workspace_bytes(int64_t V);
 
+/* Slabs of 64 columns per workgroup that the lm_head entry points launch for
+ * V columns (1, 2, 4, 8 or 16; a function of V alone), or 0 for an
+ * unsupported V.  A query for labels and tuning reports; no reference
+ * counterpart (the reference's lm_head runs 16 chunk matmuls). */
+int64_t mcv_lm_head_slabs_per_workgroup(int64_t V);
+
 /* Greedy lm_head over a W4A16 weight: logits[v] = x . W[:, v] (fp16 RNE of the
  * fp32 sum) for v < V, and token = the first index of the maximum logit, with
  * fp16 subnormals compared as zero and NaN never winning (language_model.cpp:

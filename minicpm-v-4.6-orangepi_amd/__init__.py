@@ -69,6 +69,7 @@ _SIGS = {
                                _vp, _vp, _vp, _vp]),
     "mcv_w4a16_gemv_tiled_i8": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
     "mcv_lm_head_workspace_bytes": (_c_i64, [_c_i64]),
+    "mcv_lm_head_slabs_per_workgroup": (_c_i64, [_c_i64]),
     "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp,
                                           _vp]),
     "mcv_lm_head_noalloc_max_vocab": (_c_i64, []),
@@ -807,6 +808,11 @@ def silu_mul(gate, up, out=None, stream=None):
         out = torch.empty_like(gate)
     _check(lib().mcv_silu_mul(_dev(gate), _dev(up), _dev(out), gate.numel(), _stream(stream)), "silu_mul")
     return out
+
+
+def lm_head_slabs_per_workgroup(vocab: int) -> int:
+    """Slabs of 64 columns per workgroup the lm_head launches for `vocab` columns."""
+    return int(lib().mcv_lm_head_slabs_per_workgroup(int(vocab)))
 
 
 def argmax_last_dim(x, out=None, stream=None):

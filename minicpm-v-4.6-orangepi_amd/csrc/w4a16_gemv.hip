@@ -620,15 +620,34 @@ int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void
     return check_launch("w4a16_gemv_kernel");
 }
 
-// Shared launcher of both argmax routes.  SPW 16 measured best on the
-// lm_head shape; MCV_LMHEAD_SPW (1, 2, 4, 8, 16) overrides it for sweeps.
+// Slabs per workgroup: the most (up to 16) that still leave >= 240
+// workgroups, except that a grid of one slab per workgroup is used whenever
+// it fits two workgroups per CU.  Measured on MI355X (K=1024, rotated weight
+// copies past the MALL, 5000 direct launches, us per call, SPW 1/2/4/8/16):
+// the full vocabulary V=248094 (3877 slabs) -/-/-/24.7/24.1; a half,
+// V=124047: 18.6/16.0/15.4/14.8/19.1; a quarter, V=62024: 10.9/9.9/9.9/
+// 11.8/18.6; an eighth, V=31012 (485 slabs): 6.9/7.6/8.4/11.6/18.5 -- long
+// double-buffered runs of slabs pay while the grid still covers the CUs,
+// and at a few slabs per workgroup more workgroups hide more latency.  A
+// function of V alone, so a workspace (sized for one workgroup per slab)
+// always meets the same grid.  MCV_LMHEAD_SPW (1, 2, 4, 8, 16) overrides it
+// for sweeps.
+int lm_head_spw(int64_t nslab) {
+    const int o = gemv_overrides().lm_spw;
+    if (o == 1 || o == 2 || o == 4 || o == 8 || o == 16) return o;
+    int spw = 16;
+    while (spw > 1 && ceil_div(nslab, spw) < 240) spw /= 2;
+    if (spw == 2 && nslab <= 512) spw = 1;
+    return spw;
+}
+
+// Shared launcher of both argmax routes.
 int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* qw, const void* scales,
                    const void* zeros, int zero_bias, void* logits, int64_t* token, void* ws, uint32_t tag, int mode,
                    unsigned* status, hipStream_t stream) {
     const int64_t nslab = ceil_div(V, kSlab);
     const int64_t npad = ceil_div(N, kSlab) * kSlab;
-    int spw = gemv_overrides().lm_spw ? gemv_overrides().lm_spw : 16;
-    if (spw != 1 && spw != 2 && spw != 4 && spw != 8 && spw != 16) spw = 16;
+    const int spw = lm_head_spw(nslab);
     using LmFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int,
                           int, int, unsigned long long*, int64_t*, uint32_t, unsigned*);
     LmFn fn = nullptr;
@@ -680,6 +699,11 @@ int64_t mcv_lm_head_workspace_bytes(int64_t V) {
     if (V <= 0 || V >= (int64_t(1) << 24)) return 0;
     const int64_t nslab = ceil_div(V, kSlab);
     return (lm_keys_index(nslab) + nslab) * 8;
+}
+
+int64_t mcv_lm_head_slabs_per_workgroup(int64_t V) {
+    if (V <= 0 || V >= (int64_t(1) << 24)) return 0;
+    return lm_head_spw(ceil_div(V, kSlab));
 }
 
 int mcv_w4a16_gemv_argmax_partials(const void* x, int64_t K, int64_t N, int64_t V, const void* qw,

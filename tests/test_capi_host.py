@@ -308,6 +308,23 @@ def test_lm_head_slots_token_known_answer(mcv):
     assert L.mcv_w4a16_lm_head_argmax_slots(fake, 128, big, big, fake, fake, fake, 0, None, fake, 1, None) == 2
 
 
+def test_lm_head_grid_choice(mcv):
+    """Slabs per workgroup by vocabulary: 16 on the full vocabulary (243
+    workgroups), fewer on a GPU's share of a column split, one slab per
+    workgroup once that grid fits two workgroups per CU; the workspace always
+    covers one workgroup per slab."""
+    L = mcv.lib()
+    spw = L.mcv_lm_head_slabs_per_workgroup
+    cases = {248094: 16, 124047: 8, 100000: 4, 62024: 4, 40000: 2, 31012: 1, 8320: 1, 4097: 1, 1: 1}
+    for V, want in cases.items():
+        assert spw(V) == want, V
+        assert mcv.lm_head_slabs_per_workgroup(V) == want
+        nslab = -(-V // 64)
+        assert -(-nslab // want) >= min(nslab, 240) or want == 1
+        assert L.mcv_lm_head_workspace_bytes(V) >= nslab * 8
+    assert spw(0) == 0 and spw(1 << 24) == 0
+
+
 @pytest.mark.parametrize("K,N", [(1024, 3584), (200, 72), (2048, 1000)])
 def test_w8a8_checkpoint_quantiser(mcv, oracle, K, N):
     """[N, K] checkpoint bits -> int8 + scales in one host pass, bit-identical

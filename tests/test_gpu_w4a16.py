@@ -293,10 +293,11 @@ def test_lm_head_shapes(mcv, oracle, cuda, K, V, zb):
     assert int(head.launch(_to_dev(x)).item()) == tok
 
 
-# K = 1024 takes the lm_head's one-group-per-wave path, with 5, 9 and 98
-# workgroups; three calls in a row per shape.
-@pytest.mark.parametrize("K", [512, 1024])
-@pytest.mark.parametrize("V", [4097, 8320, 100000])
+# K = 1024 takes the lm_head's one-group-per-wave path.  Slabs per
+# workgroup follow V: 4097 and 8320 one (65, 130 workgroups), 40000 two
+# (313), 100000 four (391), 124047 eight (243); three calls in a row per shape.
+@pytest.mark.parametrize("K,V", [(K, V) for K in (512, 1024) for V in (4097, 8320, 100000)]
+                         + [(1024, 40000), (1024, 124047)])
 def test_lm_head_routes_agree(mcv, oracle, cuda, V, K):
     """The call-tagged key words read by the grid's last workgroup,
     the host-finished tagged slots and the two-kernel keys + reduction give
