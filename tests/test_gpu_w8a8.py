@@ -155,6 +155,27 @@ def test_w8a8_end_to_end(mcv, oracle, cuda, M):
                        mcv.w8a8_dequant(acc, xs16, wq.w_scale))
 
 
+# The M > 4 GEMM's fused epilogue on ragged shapes: a last tile past M and N,
+# K padded with zero weights, N % 4 != 0 (scales loaded one per column, not
+# four at once), with fp32 and with the reference's fp16 scales.
+@pytest.mark.parametrize("M,K,N", [(257, 1040, 1000), (70, 256, 1003), (1030, 384, 3590)], ids=lambda v: str(v))
+def test_w8a8_gemm_fused_ragged(mcv, oracle, cuda, M, K, N):
+    rng = np.random.default_rng(900 + M + N)
+    x = f16_normal(rng, (M, K), 1.0)
+    wf = f16_normal(rng, (K, N), 0.02)
+    wq = mcv.quantize_dense_weight_w8a8(_f16_dev(wf))
+    xq, xs, _ = mcv.w8a8_quantize(_f16_dev(x))
+    xs16 = xs.half()
+    q_o, s_o, s16_o = oracle.w8a8_quantize_act(x)
+    assert np.array_equal(_u16(xs16), s16_o)
+    wq_o, ws_o, ws16_o = oracle.w8a8_quantize_weight(wf)
+    acc_o = oracle.gemm_i32(q_o, wq_o)
+    got = _u16(mcv.matmul_w8a8(xq, xs, wq))
+    assert np.array_equal(got, oracle.w8a8_dequant(acc_o, s_o, ws_o))
+    got16 = _u16(mcv.matmul_w8a8(xq, xs16, wq, use_f32_scale=False))
+    assert np.array_equal(got16, oracle.w8a8_dequant(acc_o, oracle.h2f(s16_o), oracle.h2f(ws16_o)))
+
+
 def test_nk_layout_fused(mcv, cuda):
     torch = _torch()
     rng = np.random.default_rng(77)
