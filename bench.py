@@ -577,7 +577,7 @@ def lm_head_entry(lm, args, route, steps, cpu_entry):
              "kernel_us_mean": round(float(pl.mean()) * 1e3, 3), "per_launch_samples": int(pl.size),
              "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(value / HBM_PEAK_GBS, 4),
-                          "traffic": traffic_from_profiles(lm.name) if lm.V == 248094 else None,
+                          "traffic": traffic_from_profiles(lm.name if lm.V == 248094 else f"{lm.name}_V{lm.V}"),
                           "algorithmic_per_launch": lm.bytes},
              "alt_route": {other: {"us_per_call": round(alt_ms / max(steps, 200) * 1e3, 3),
                                    "value": round(lm.bytes / (alt_ms / max(steps, 200) / 1e3) / 1e9, 2)}},
