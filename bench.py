@@ -779,6 +779,45 @@ def _vendor(pkg, args, int8):
             **gpu_result("vendor", "vendor GEMM", 2.0 * M * K * N, unit, "mfma", fn, 1, 200)}
 
 
+def _lm_head_w8a8(pkg, args, part):
+    """The W8A8 lm_head step as lm_head_greedy_w8a8 runs it (language_model.cpp:
+    434-480 with the argmax on the device): activation quantisation with the
+    fp16 scale, then the W8A8 GEMV over V = 248094 columns with the fp16 weight
+    scale and the argmax folded in (one key per slab, then their reduction);
+    4 rotated weight copies (1.0 GB).  part = "step", "unfused" (the same
+    GEMV without the fold, then the separate argmax over the logits), "gemv"
+    (the GEMV alone) or "argmax" (the separate argmax alone)."""
+    import torch
+    K, V = 1024, args.V or 248094
+    rng = np.random.default_rng(1)
+    x = to_dev_f16(f16_normal(rng, (1, K), 1.0))
+    base = pkg.quantize_dense_weight_w8a8(f16_normal(rng, (K, V), 0.02))
+    ws = [base] + [pkg.W8A8QuantizedWeight(base.w_int8.clone(), base.w_scale.clone(), base.w_scale_f32.clone(), K, V,
+                                           base.layout) for _ in range((args.copies or 4) - 1)]
+    xq = torch.empty((1, K), dtype=torch.int8, device="cuda")
+    xs = torch.empty(1, dtype=torch.float16, device="cuda")
+    logits = torch.empty((1, V), dtype=torch.float16, device="cuda")
+    keys = torch.empty(-(-V // 64), dtype=torch.int64, device="cuda")
+    tok = torch.empty(1, dtype=torch.int64, device="cuda")
+    pkg.w8a8_quantize(x, xq, pkg._NO_F32, xs)
+
+    def step(i):
+        if part in ("step", "unfused"):
+            pkg.w8a8_quantize(x, xq, pkg._NO_F32, xs)
+        if part == "step":
+            pkg.lm_head_argmax_w8a8(xq, xs, ws[i], V, logits, keys, tok)
+            return
+        if part != "argmax":
+            pkg.matmul_w8a8(xq, xs, ws[i], logits, use_f32_scale=False)
+        if part != "gemv":
+            pkg.argmax_last_dim(logits, tok)
+    gemv_bytes = K * V + 2 * V + 2 * V + K                  # weights, fp16 scales, logits, int8 x
+    nbytes = {"gemv": gemv_bytes, "argmax": 2 * V, "step": gemv_bytes + 2 * K,
+              "unfused": gemv_bytes + 2 * V + 2 * K}[part]
+    return {"workload": f"w8a8_lm_head_{part}_V{V}", **gpu_result(
+        f"lm_head_w8a8_{part}", f"w8a8 lm_head ({part})", nbytes, "GB/s", "hbm", step, len(ws), 200)}
+
+
 def _copy(pkg, args):
     """Calibration of the HBM counters: a 128 MiB device copy reads and writes
     exactly 134,217,728 bytes each."""
@@ -799,6 +838,10 @@ EXTRA = {
     "vendor_f16": lambda p, a: _vendor(p, a, False),
     "vendor_int8": lambda p, a: _vendor(p, a, True),
     "copy": _copy,
+    "lm_head_w8a8": lambda p, a: _lm_head_w8a8(p, a, "step"),
+    "lm_head_w8a8_unfused": lambda p, a: _lm_head_w8a8(p, a, "unfused"),
+    "lm_head_w8a8_gemv": lambda p, a: _lm_head_w8a8(p, a, "gemv"),
+    "lm_head_w8a8_argmax": lambda p, a: _lm_head_w8a8(p, a, "argmax"),
 }
 WORKLOADS = ["all", "lm_head", "gemv1", "mlp", "prefill", "w8a8", *EXTRA]
 

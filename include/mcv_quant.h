@@ -386,6 +386,18 @@ int mcv_w8a8_gate_up_silu(const int8_t* xq_dev, const void* x_scale_dev, int x_s
                           const int8_t* w_up_dev, const void* w_scale_up_dev, int w_scale_dtype, void* act_dev,
                           mcv_stream_t stream);
 
+/* W8A8 lm_head, step one of two (M = 1): logits[v] = the fused epilogue of
+ * mcv_w8a8_gemm_f16 over the MCV_W8_TILED weight [K][N] for v < V (bit-
+ * identical to it; logits_dev may be NULL), and one first-maximum argmax key
+ * per 64-column slab into keys_dev (ceil(V / 64) u64, 8-byte aligned), as
+ * mcv_w4a16_gemv_argmax_partials writes them; mcv_argmax_reduce_keys(keys_dev,
+ * ceil(V / 64), token_dev) finishes.  Replaces the W8A8 branch of
+ * lm_head_greedy (src/csrc/lib/language_model.cpp:434-480: 16 chunk
+ * matmul_w8a8 + w8a8_dequant launches, their D2H copies and the host scan). */
+int mcv_w8a8_gemv_argmax_partials(const int8_t* xq_dev, const void* x_scale_dev, int x_scale_dtype, int64_t K,
+                                  int64_t N, int64_t V, const int8_t* w_dev, const void* w_scale_dev,
+                                  int w_scale_dtype, void* logits_dev, void* keys_dev, mcv_stream_t stream);
+
 /* Bytes of a K x N weight in MCV_W8_TILED (0 on bad shape). */
 int64_t mcv_w8a8_tiled_bytes(int64_t K, int64_t N);
 

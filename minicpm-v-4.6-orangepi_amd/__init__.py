@@ -85,6 +85,8 @@ _SIGS = {
     "mcv_w8a8_gemm_i32": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_dequant": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),
     "mcv_w8a8_gemm_f16": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _vp, _vp]),
+    "mcv_w8a8_gemv_argmax_partials": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_int, _vp, _vp,
+                                               _vp]),
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_tiled_bytes": (_c_i64, [_c_i64, _c_i64]),
     "mcv_w8a8_gate_up_silu": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp,
@@ -623,7 +625,9 @@ def quantize_dense_weight_w8a8(weight_kn, layout: int = W8_TILED) -> W8A8Quantiz
         if hasattr(weight_kn, "detach") else np.asarray(weight_kn).view(np.uint16)
     K, N = w_np.shape
     q, s32, s16 = quantize_w8a8_weight_host(w_np, layout)
-    dev = weight_kn.device if hasattr(weight_kn, "device") and weight_kn.device.type == "cuda" else "cuda"
+    # numpy arrays carry .device == "cpu" (a string) in numpy 2: only a torch
+    # CUDA tensor names its device
+    dev = weight_kn.device if getattr(getattr(weight_kn, "device", None), "type", None) == "cuda" else "cuda"
     return W8A8QuantizedWeight(torch.from_numpy(q).to(dev), torch.from_numpy(s16.view(np.int16)).to(dev).view(torch.float16),
                                torch.from_numpy(s32).to(dev), K, N, layout)
 
@@ -703,6 +707,34 @@ def matmul_w8a8(x_int8, x_scale, w: W8A8QuantizedWeight, out=None, use_f32_scale
     _check(lib().mcv_w8a8_gemm_f16(_dev(x_int8), _dev(x_scale), _scale_dtype(x_scale), M, K, w.N, _dev(w.w_int8),
                                    w.layout, _dev(ws), _scale_dtype(ws), _dev(out), _stream(stream)), "matmul_w8a8")
     return out
+
+
+def lm_head_argmax_w8a8(x_int8, x_scale, w: W8A8QuantizedWeight, vocab: int, logits=None, keys=None, token=None,
+                        use_f32_scale=False, stream=None):
+    """The W8A8 lm_head on the device (language_model.cpp:434-480): the fused
+    GEMV over the first `vocab` columns (logits bit-identical to matmul_w8a8,
+    written when `logits` is given) with one argmax key per 64-column slab,
+    then their reduction.  Returns the int64 [1] token on the device.  Scales
+    as matmul_w8a8: the weight's fp16 w_scale unless use_f32_scale."""
+    torch = _torch()
+    if w.layout != W8_TILED:
+        raise McvError("lm_head_argmax_w8a8 needs an MCV_W8_TILED weight")
+    if x_int8.dtype != torch.int8 or x_int8.numel() != w.K or not x_int8.is_contiguous():
+        raise McvError("lm_head_argmax_w8a8 x must be contiguous int8 [1, K]")
+    nslab = -(-vocab // SLAB)
+    if keys is None:
+        keys = torch.empty(nslab, dtype=torch.int64, device=x_int8.device)
+    if token is None:
+        token = torch.empty(1, dtype=torch.int64, device=x_int8.device)
+    if keys.numel() < nslab or token.numel() < 1:
+        raise McvError(f"lm_head_argmax_w8a8: keys need {nslab} int64 and token one")
+    ws = w.w_scale_f32 if use_f32_scale else w.w_scale
+    _check(lib().mcv_w8a8_gemv_argmax_partials(_dev(x_int8), _dev(x_scale), _scale_dtype(x_scale), w.K, w.N, vocab,
+                                               _dev(w.w_int8), _dev(ws), _scale_dtype(ws),
+                                               _dev(logits) if logits is not None else None, _dev(keys),
+                                               _stream(stream)), "mcv_w8a8_gemv_argmax_partials")
+    _check(lib().mcv_argmax_reduce_keys(_dev(keys), nslab, _dev(token), _stream(stream)), "mcv_argmax_reduce_keys")
+    return token
 
 
 class DecodeMlpW8A8:

@@ -54,14 +54,17 @@ int64_t lm_head_greedy_w4a16(const Tensor& last_hidden_1xH, const Tensor* final_
 // The W8A8 lm_head (language_model.cpp:434-467) with the reference's
 // precision: one activation quantisation with its fp16 scale, the fused int8
 // GEMV with the truncated fp16 weight scale, the first-maximum argmax on the
-// device.  The weight stays owned by the caller.
+// device -- for an MCV_W8_TILED weight folded into the GEMV (one key per
+// 64-column slab, then their reduction), otherwise a separate argmax over the
+// logits.  The weight stays owned by the caller.
 struct LmHeadW8A8 {
     const W8A8QuantizedWeight* weight{nullptr};   // [hidden, >= vocab]
     int64_t vocab{0};
     Tensor normed;                 // Float16 [1, hidden]
     Tensor xq;                     // Int8 [1, hidden]
     Tensor xs;                     // Float16 [1]
-    Tensor logits;                 // Float16 [1, weight N]
+    Tensor logits;                 // Float16 [1, weight N]: the last call's logits (columns < vocab)
+    Tensor keys;                   // Int64 [ceil(vocab / 64)] (the fused argmax's per-slab keys)
     Tensor token;                  // Int64 [1]
 };
 LmHeadW8A8 make_lm_head_w8a8(const W8A8QuantizedWeight& weight, int64_t vocab);

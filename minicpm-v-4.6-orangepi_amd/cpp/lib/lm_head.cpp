@@ -112,8 +112,9 @@ LmHeadW8A8 make_lm_head_w8a8(const W8A8QuantizedWeight& weight, int64_t vocab) {
     head.xq = Tensor({1, weight.K}, DType::Int8);
     head.xs = Tensor({1}, DType::Float16);
     head.logits = Tensor({1, weight.N}, DType::Float16);
+    head.keys = Tensor({(vocab + 63) / 64}, DType::Int64);
     head.token = Tensor({1}, DType::Int64);
-    for (Tensor* t : {&head.normed, &head.xq, &head.xs, &head.logits, &head.token}) t->allocate();
+    for (Tensor* t : {&head.normed, &head.xq, &head.xs, &head.logits, &head.keys, &head.token}) t->allocate();
     return head;
 }
 
@@ -128,9 +129,19 @@ int64_t lm_head_greedy_w8a8(const Tensor& last_hidden_1xH, const Tensor* final_n
         x = &head.normed;
     }
     w8a8_quantize(*x, head.xq, head.xs, stream);               // fp16 x_scale, as language_model.cpp:439-441
-    matmul_w8a8(head.xq, head.xs, w, head.logits, stream);     // fp16 w_scale, as :465-466
-    check_mcv(mcv_argmax_f16(head.logits.data(), 1, head.vocab, static_cast<int64_t*>(head.token.data()), stream),
-              "lm_head argmax");
+    int64_t* token = static_cast<int64_t*>(head.token.data());
+    if (w.layout == MCV_W8_TILED) {
+        // fp16 w_scale, as :465-466; the argmax folded into the GEMV
+        check_mcv(mcv_w8a8_gemv_argmax_partials(static_cast<const int8_t*>(head.xq.data()), head.xs.data(), MCV_F16,
+                                                w.K, w.N, head.vocab, static_cast<const int8_t*>(w.w_int8.data()),
+                                                w.w_scale.data(), MCV_F16, head.logits.data(), head.keys.data(),
+                                                stream),
+                  "lm_head W8A8 GEMV");
+        check_mcv(mcv_argmax_reduce_keys(head.keys.data(), head.keys.numel(), token, stream), "lm_head argmax");
+    } else {
+        matmul_w8a8(head.xq, head.xs, w, head.logits, stream);
+        check_mcv(mcv_argmax_f16(head.logits.data(), 1, head.vocab, token, stream), "lm_head argmax");
+    }
     int64_t t = 0;
     check_hip(hipMemcpyAsync(&t, head.token.data(), sizeof(t), hipMemcpyDeviceToHost, stream), "hipMemcpyAsync token");
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");

@@ -14,6 +14,8 @@ int launch_w8a8_tiled_gate_up_silu(const int8_t* xq, int64_t M, int64_t K, int64
                                    int xs16, void* act, hipStream_t stream);
 int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
                       const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
+int launch_w8a8_gemv_argmax(const int8_t* xq, int64_t K, int64_t V, const int8_t* w, void* logits, const void* xs,
+                            int xs16, const void* ws, int ws16, unsigned long long* keys, hipStream_t stream);
 
 namespace {
 
@@ -392,6 +394,21 @@ int mcv_w8a8_gate_up_silu(const int8_t* xq, const void* xs, int xs_dtype, int64_
     if ((rc = require_device()) != MCV_OK) return rc;
     return launch_w8a8_tiled_gate_up_silu(xq, M, K, N, w_gate, ws_gate, w_up, ws_up, ws_dtype == MCV_F16, xs,
                                           xs_dtype == MCV_F16, act, static_cast<hipStream_t>(stream));
+}
+
+int mcv_w8a8_gemv_argmax_partials(const int8_t* xq, const void* xs, int xs_dtype, int64_t K, int64_t N, int64_t V,
+                                  const int8_t* w, const void* ws, int ws_dtype, void* logits, void* keys,
+                                  mcv_stream_t stream) {
+    const char* who = "mcv_w8a8_gemv_argmax_partials";
+    int rc = check_gemm_args(xq, 1, K, N, w, MCV_W8_TILED, keys, who);
+    if (rc != MCV_OK) return rc;
+    if (!xs || !ws) return fail(MCV_ERR_INVALID_ARG, "%s: null scale", who);
+    if (!dtype_ok(xs_dtype) || !dtype_ok(ws_dtype)) return fail(MCV_ERR_INVALID_ARG, "%s: bad scale dtype", who);
+    if (V <= 0 || V > N) return fail(MCV_ERR_SHAPE, "%s: need 0 < V <= N (V=%lld N=%lld)", who, (long long)V, (long long)N);
+    if (reinterpret_cast<uintptr_t>(keys) % 8 != 0) return fail(MCV_ERR_INVALID_ARG, "%s: keys must be 8-byte aligned", who);
+    if ((rc = require_device()) != MCV_OK) return rc;
+    return launch_w8a8_gemv_argmax(xq, K, V, w, logits, xs, xs_dtype == MCV_F16, ws, ws_dtype == MCV_F16,
+                                   static_cast<unsigned long long*>(keys), static_cast<hipStream_t>(stream));
 }
 
 int mcv_w8a8_dequant(const int32_t* acc, const void* xs, int xs_dtype, const void* ws, int ws_dtype, int64_t M, int64_t N,

@@ -338,12 +338,16 @@ __global__ __launch_bounds__(64 * WN * KS) void w8a8_tiled_gemm_kernel(
 // l/32 with v_dot4_i32_i8 (exact int32); the partial sums meet in LDS.  DUAL:
 // the same over a second weight (gate and up) with the fp16 epilogues of both
 // and silu_mul_f16 -- bit-identical to two GEMVs and silu_mul, since the int32
-// sums are exact and the epilogue code is shared.
-template <int MR, int NW, int HALVES, int U, bool OUT_F16, bool DUAL>
+// sums are exact and the epilogue code is shared.  ARG (M = 1, both halves in
+// the workgroup): the fp16 outputs also leave as one first-maximum argmax key
+// per slab (keys[slab], argmax_key64 of the fp16 value and the column), and
+// `out` may be null.
+template <int MR, int NW, int HALVES, int U, bool OUT_F16, bool DUAL, bool ARG = false>
 __global__ __launch_bounds__(64 * NW) void w8a8_tiled_gemv_kernel(
     const int8_t* __restrict__ xq, const int8_t* __restrict__ w, const int8_t* __restrict__ w2, int M, int K, int N,
     int KB, void* __restrict__ out, const void* __restrict__ xs, int xs16, const void* __restrict__ ws,
-    const void* __restrict__ ws2, int ws16, int nslab) {
+    const void* __restrict__ ws2, int ws16, int nslab, unsigned long long* __restrict__ keys) {
+    static_assert(!ARG || (MR == 1 && HALVES == 2 && OUT_F16 && !DUAL), "argmax epilogue: M = 1, whole slabs");
     constexpr int NWT = DUAL ? 2 : 1;
     __shared__ int red[NW][MR][NWT][HALVES][64];
     const int lane = threadIdx.x & 63;
@@ -432,9 +436,18 @@ __global__ __launch_bounds__(64 * NW) void w8a8_tiled_gemv_kernel(
         for (int v = 0; v < NW; ++v) sum[t] += red[v][m][t][jj][l] + red[v][m][t][jj][l + 32];
     }
     const int n = slab * kSlab + 32 * (j0 + jj) + l;
+    const float e_xs = bits_to_f(r_xs, xs16), e_ws = bits_to_f(r_ws, ws16);
+    if constexpr (ARG) {
+        // the 64 threads left are wave 0, one column each (columns past N: key 0)
+        const uint16_t h16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[0]), e_ws), e_xs));
+        if (out != nullptr && n < N) static_cast<uint16_t*>(out)[n] = h16;
+        const unsigned long long key = wave_max_u64(n < N ? argmax_key64(argmax_key16(h16), static_cast<uint32_t>(n))
+                                                          : 0ull);
+        if (lane == 0) keys[slab] = key;
+        return;
+    }
     if (m >= M || n >= N) return;
     const size_t o = static_cast<size_t>(m) * N + n;
-    const float e_xs = bits_to_f(r_xs, xs16), e_ws = bits_to_f(r_ws, ws16);
     if constexpr (DUAL) {
         const float e_ws2 = bits_to_f(r_ws2, ws16);
         const uint16_t g16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum[0]), e_ws), e_xs));
@@ -477,7 +490,7 @@ int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const in
 #define MCV_GEMV8V(R, NW_, H_, U_)                                                                                \
     if (!launched && nw == NW_ && halves == H_ && u == U_) {                                                      \
         hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<R, NW_, H_, U_, OUT_F16, DUAL>), grid, block, 0, stream, xq, w, w2, \
-                           iM, iK, iN, iKB, out, xs, xs16, ws, ws2, ws16, ns);                                    \
+                           iM, iK, iN, iKB, out, xs, xs16, ws, ws2, ws16, ns, nullptr);                           \
         launched = true;                                                                                           \
     }
 #define MCV_GEMV8(R) \
@@ -600,6 +613,21 @@ int launch_w8a8_tiled_gate_up_silu(const int8_t* xq, int64_t M, int64_t K, int64
                                    const void* wsg, const int8_t* wu, const void* wsu, int ws16, const void* xs,
                                    int xs16, void* act, hipStream_t stream) {
     return launch_w8a8_gemv<true, true>(xq, M, K, N, wg, wu, act, xs, xs16, wsg, wsu, ws16, stream);
+}
+
+// The GEMV with the argmax epilogue over the slabs holding columns < V
+// (M = 1): one workgroup per slab, 16 waves, 2 k-blocks in flight -- the wide
+// variant above (V = 248094: the lm_head).
+int launch_w8a8_gemv_argmax(const int8_t* xq, int64_t K, int64_t V, const int8_t* w, void* logits, const void* xs,
+                            int xs16, const void* ws, int ws16, unsigned long long* keys, hipStream_t stream) {
+    const int64_t nslab = ceil_div(V, kSlab);
+    const int64_t KB = ceil_div(K, 128) * 4;
+    if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 32) || nslab > 0x7fffffff)
+        return fail(MCV_ERR_SHAPE, "w8a8 lm_head GEMV: weight exceeds 4 GiB");
+    hipLaunchKernelGGL((w8a8_tiled_gemv_kernel<1, 16, 2, 2, true, false, true>), dim3(static_cast<unsigned>(nslab)),
+                       dim3(64 * 16), 0, stream, xq, w, w, 1, static_cast<int>(K), static_cast<int>(V),
+                       static_cast<int>(KB), logits, xs, xs16, ws, ws, ws16, static_cast<int>(nslab), keys);
+    return check_launch("w8a8_tiled_gemv_kernel<argmax>");
 }
 
 }  // namespace mcv

@@ -128,6 +128,14 @@ int main() {
         std::printf("W8A8 lm_head token=%lld oracle=%lld logit mismatches=%d\n", (long long)t8, (long long)want_tok, bad);
         if (bad != 0 || t8 != want_tok) rc = 1;
         if (bv - second > 5e-2f && t8 != best) rc = 1;
+        // an [K, N] weight takes the separate argmax over the logits: the same token and logits
+        W8A8QuantizedWeight wq8kn = quantize_w8a8_host(w.data(), K, N, MCV_W8_KN);
+        LmHeadW8A8 h8kn = make_lm_head_w8a8(wq8kn, V);
+        const int64_t t8kn = lm_head_greedy_w8a8(x, &gamma, eps, h8kn, ctx.stream());
+        std::vector<uint16_t> got_kn(V);
+        h8kn.logits.copy_to_host(got_kn.data(), V * 2);
+        std::printf("W8A8 lm_head [K, N] weight token=%lld\n", (long long)t8kn);
+        if (t8kn != t8 || got_kn != got) rc = 1;
     }
 
     // Give-up of the device-token route: workgroup 0's call counter (u32 word

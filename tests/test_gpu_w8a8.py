@@ -164,6 +164,8 @@ def test_w8a8_gemm_fused_ragged(mcv, oracle, cuda, M, K, N):
     x = f16_normal(rng, (M, K), 1.0)
     wf = f16_normal(rng, (K, N), 0.02)
     wq = mcv.quantize_dense_weight_w8a8(_f16_dev(wf))
+    wq_np = mcv.quantize_dense_weight_w8a8(wf)            # a host array in: the same weight on the GPU
+    assert wq_np.w_int8.is_cuda and _torch().equal(wq_np.w_int8, wq.w_int8)
     xq, xs, _ = mcv.w8a8_quantize(_f16_dev(x))
     xs16 = xs.half()
     q_o, s_o, s16_o = oracle.w8a8_quantize_act(x)
@@ -361,3 +363,43 @@ def test_decode_mlp_block_falls_back(mcv, oracle, cuda):
     want = mcv.matmul_w8a8(aq, asc, wd)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+# The W8A8 lm_head with the argmax folded into the GEMV: logits bit-identical
+# to matmul_w8a8, the token the first maximum of them, with ragged V (keys for
+# 313 slabs), a tie at the maximum, and the model's vocabulary (3877 slabs).
+@pytest.mark.parametrize("K,N,V", [(1024, 20000, 19997), (256, 4096, 4096), (1024, 248096, 248094)],
+                         ids=lambda v: str(v))
+def test_lm_head_w8a8_fused_argmax(mcv, oracle, cuda, K, N, V):
+    torch = _torch()
+    rng = np.random.default_rng(K + V)
+    x = f16_normal(rng, (1, K), 1.0)
+    wf = f16_normal(rng, (K, N), 0.02)
+    xq, xs, _ = mcv.w8a8_quantize(_f16_dev(x))
+    xs16 = xs.half()
+    if V == 4096:
+        # an exact tie at the maximum: column 50 becomes a copy of the winner
+        wq = mcv.quantize_dense_weight_w8a8(wf)
+        top = int(mcv.lm_head_argmax_w8a8(xq, xs16, wq, V).item())
+        if top != 50:
+            wf[:, 50] = wf[:, top]
+    wq = mcv.quantize_dense_weight_w8a8(wf)
+    logits = torch.empty(V, dtype=torch.float16, device="cuda")
+    tok = int(mcv.lm_head_argmax_w8a8(xq, xs16, wq, V, logits).item())
+    full = mcv.matmul_w8a8(xq, xs16, wq, use_f32_scale=False)
+    assert torch.equal(logits.view(torch.int16), full[0, :V].view(torch.int16))
+    got = _u16(logits)
+    assert tok == oracle.argmax_f16(got)
+    if V == 4096:
+        assert tok == 50
+    if K * N <= 1024 * 20000:
+        q_o, _, s16_o = oracle.w8a8_quantize_act(x)
+        wq_o, _, ws16_o = oracle.w8a8_quantize_weight(wf)
+        want = oracle.w8a8_dequant(oracle.gemm_i32(q_o, wq_o), oracle.h2f(s16_o), oracle.h2f(ws16_o))
+        assert np.array_equal(got, want[0, :V])
+    # without logits: the same token; fp32 scales: the token of their logits
+    assert int(mcv.lm_head_argmax_w8a8(xq, xs16, wq, V).item()) == tok
+    l32 = torch.empty(V, dtype=torch.float16, device="cuda")
+    t32 = int(mcv.lm_head_argmax_w8a8(xq, xs, wq, V, l32, use_f32_scale=True).item())
+    assert torch.equal(l32.view(torch.int16), mcv.matmul_w8a8(xq, xs, wq)[0, :V].view(torch.int16))
+    assert t32 == oracle.argmax_f16(_u16(l32))
