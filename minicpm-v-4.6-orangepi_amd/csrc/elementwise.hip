@@ -12,23 +12,60 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
         out[i] = silu_mul_f16(g[i], u[i]);
 }
 
-// One workgroup per row: 64-bit keys (value, then lowest index) reduced with
-// wave shuffles and LDS.
-__global__ __launch_bounds__(256) void argmax_kernel(const uint16_t* __restrict__ x, int64_t N, int64_t* __restrict__ idx) {
+// One workgroup of 1024 threads per row.  The row is read in 16-byte loads
+// (eight values), four in flight per lane, after a head of at most seven
+// values up to the first 16-byte boundary; each lane keeps the best 16-bit
+// key it saw and the first index holding it (a lane visits its elements in
+// increasing index order, so only a strictly larger key replaces), and the
+// lanes' 64-bit keys (value, then lowest index) meet through wave shuffles
+// and LDS.  A single workgroup of 256 threads with one 2-byte load at a time
+// took 209 us over the 248094 logits of the lm_head shape (MI355X).
+constexpr int kArgThreads = 1024;
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const uint16_t* __restrict__ x, int64_t N,
+                                                             int64_t* __restrict__ idx) {
     const uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * N;
-    unsigned long long best = 0ull;
-    for (int64_t i = threadIdx.x; i < N; i += blockDim.x) {
-        const unsigned long long k = argmax_key64(argmax_key16(xr[i]), static_cast<uint32_t>(i));
-        best = k > best ? k : best;
+    const int tid = threadIdx.x;
+    uint32_t bk = 0, bi = 0;                     // best 16-bit key (0: none yet) and its index
+    auto visit = [&](uint32_t h, uint32_t i) {
+        const uint32_t k = argmax_key16(static_cast<uint16_t>(h));
+        const bool take = k > bk;
+        bk = take ? k : bk;
+        bi = take ? i : bi;
+    };
+    const int64_t head64 = static_cast<int64_t>((16u - (reinterpret_cast<uintptr_t>(xr) & 15u)) & 15u) / 2;
+    const int64_t head = head64 < N ? head64 : N;
+    if (tid < head) visit(xr[tid], static_cast<uint32_t>(tid));
+    const uint4* __restrict__ v = reinterpret_cast<const uint4*>(xr + head);
+    const int64_t nv = (N - head) / 8;
+    constexpr int U = 4;
+    for (int64_t j0 = tid; j0 < nv; j0 += int64_t(kArgThreads) * U) {
+        uint4 q[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = j0 + int64_t(u) * kArgThreads;
+            q[u] = j < nv ? v[j] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = j0 + int64_t(u) * kArgThreads;
+            if (j >= nv) break;
+            const uint32_t base = static_cast<uint32_t>(head + 8 * j);
+            const uint32_t w[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                visit(w[e] & 0xffffu, base + 2 * e);
+                visit(w[e] >> 16, base + 2 * e + 1);
+            }
+        }
     }
-    best = wave_max_u64(best);
-    __shared__ unsigned long long wbest[4];
-    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    for (int64_t i = head + 8 * nv + tid; i < N; i += kArgThreads) visit(xr[i], static_cast<uint32_t>(i));
+    unsigned long long best = wave_max_u64(bk ? argmax_key64(bk, bi) : 0ull);
+    __shared__ unsigned long long wbest[kArgThreads / 64];
+    if ((tid & 63) == 0) wbest[tid >> 6] = best;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) best = wbest[w] > best ? wbest[w] : best;
-        best = wbest[0] > best ? wbest[0] : best;
-        idx[blockIdx.x] = argmax_index(best);
+    if (tid < 64) {
+        best = wave_max_u64(tid < kArgThreads / 64 ? wbest[tid] : 0ull);
+        if (tid == 0) idx[blockIdx.x] = argmax_index(best);
     }
 }
 
@@ -66,7 +103,7 @@ int mcv_argmax_f16(const void* x, int64_t M, int64_t N, int64_t* idx, mcv_stream
         return fail(MCV_ERR_SHAPE, "argmax: bad shape M=%lld N=%lld", (long long)M, (long long)N);
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, static_cast<hipStream_t>(stream),
+    hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(M)), dim3(kArgThreads), 0, static_cast<hipStream_t>(stream),
                        static_cast<const uint16_t*>(x), N, idx);
     return check_launch("argmax_kernel");
 }

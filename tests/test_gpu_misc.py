@@ -54,6 +54,21 @@ def test_argmax_rows(mcv, oracle, cuda):
     assert want[1] == 5000 and want[2] == 0 and want[4] == 0 and want[5] == 12345
 
 
+# Odd row lengths put every row start at another 2-byte offset from a 16-byte
+# boundary (the kernel's head of single loads before the vector loads); a tie
+# between a head element and one in the vector part or the tail.
+@pytest.mark.parametrize("M,N", [(3, 7), (9, 1001), (2, 1), (4, 65537)])
+def test_argmax_ragged_rows(mcv, oracle, cuda, M, N):
+    rng = np.random.default_rng(M * 31 + N)
+    x = f16_normal(rng, (M, N), 1.0)
+    if N > 600:
+        x[1, 3] = x[1, 500] = x[1, N - 1] = 0x7000
+    got = mcv.argmax_last_dim(_f16_dev(x)).cpu().numpy()
+    assert got.tolist() == [oracle.argmax_f16(x[m]) for m in range(M)]
+    if N > 600:
+        assert got[1] == 3
+
+
 @pytest.mark.parametrize("M,H", [(1, 1024), (3, 2048), (64, 1024), (2, 100)])
 def test_rms_norm_vs_oracle(mcv, oracle, cuda, M, H):
     rng = np.random.default_rng(M * 7 + H)
