@@ -331,7 +331,8 @@ int mcv_rms_norm_w8a8_quantize(const void* x_dev, const void* gamma_dev, int64_t
 /* acc[M][N] int32 = xq[M][K] . W exactly.  W is int8 in layout w_layout.
  * Replaces matmul_w8a8_i32 (src/csrc/lib/ops.cpp:1097-1133, kernel
  * op_kernel/matmul_w8a8_i32_custom.cpp:15-48), which accepts M = 1 only.
- * MCV_W8_TILED runs the operand-line GEMM (M > 4) or GEMV (M <= 4); the
+ * MCV_W8_TILED runs the operand-line GEMV (M <= 4; M <= 2 when K > 2048) or
+ * GEMM (larger M); the
  * KN / NK layouts a slower kernel that transposes through LDS. */
 int mcv_w8a8_gemm_i32(const int8_t* xq_dev, int64_t M, int64_t K, int64_t N,
                       const int8_t* w_dev, int w_layout, int32_t* acc_dev, mcv_stream_t stream);

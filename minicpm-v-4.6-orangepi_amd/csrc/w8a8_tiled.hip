@@ -20,7 +20,7 @@
 // output columns per register quad: int32 results leave as 16-byte stores,
 // fp16 results as 16-byte stores after one v_permlane32_swap per pair.
 //
-// GEMV (M <= 4): one workgroup per slab, eight waves splitting K, v_dot4
+// GEMV (M <= 4, or M <= 2 when K > 2048): one workgroup per slab, waves splitting K, v_dot4
 // int8 dot products on the same operand lines, partial sums meeting in LDS.
 //
 // Replaces matmul_w8a8_i32_custom + w8a8_dequant_custom and their host
@@ -576,7 +576,11 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
     const int64_t KB = ceil_div(K, 128) * 4;            // 32-k blocks per slab (padded to whole stages)
     if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 32) || M * K >= (int64_t(1) << 32))
         return fail(MCV_ERR_SHAPE, "w8a8 tiled: weight or activation exceeds 4 GiB");
-    if (M <= 4) {
+    // The GEMV up to M = 4, but only up to M = 2 past K = 2048, where its
+    // serial k-blocks per wave cost more than the GEMM's fixed start
+    // (MI355X, graph-replayed, us: K=3584 N=1024 GEMV M=1/2/4 4.8/6.3/8.4,
+    // GEMM M=5 6.6; K=1024 N=3584 GEMV M=4 3.8, GEMM M=5 4.0).
+    if (M <= 2 || (M <= 4 && KB <= 64)) {
         return f16 ? launch_w8a8_gemv<true, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream)
                    : launch_w8a8_gemv<false, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream);
     }

@@ -76,10 +76,11 @@ def test_gemm_i32_bit_exact(mcv, oracle, cuda, M, K, N, layout):
     assert np.array_equal(acc.cpu().numpy(), oracle.gemm_i32(x, w))
 
 
-# The tiled path's GEMV (M <= 4) and every GEMM tile shape, ragged K and N
+# The tiled path's GEMV (M <= 4; M <= 2 past K = 2048) and every GEMM tile shape, ragged K and N
 # (K padded to 128 with zero weights, N to 64), extreme values.
 @pytest.mark.parametrize("M,K,N", [(2, 1024, 3584), (3, 208, 80), (4, 2048, 1000), (6, 1024, 3584),
-                                   (64, 16, 64), (100, 1040, 3584), (1024, 1024, 3584), (300, 3584, 1024)],
+                                   (64, 16, 64), (100, 1040, 3584), (1024, 1024, 3584), (300, 3584, 1024),
+                                   (2, 3584, 1024), (4, 3584, 1024)],
                          ids=lambda v: str(v))
 def test_tiled_gemm_i32_bit_exact(mcv, oracle, cuda, M, K, N):
     torch = _torch()
