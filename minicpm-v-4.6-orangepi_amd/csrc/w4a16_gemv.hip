@@ -13,6 +13,7 @@
 // Replaces the NPU kernel src/csrc/custom_ops/op_kernel/matmul_w4a16_custom.cpp
 // (8 AICore blocks, int8 tiles, fp16 Axpy accumulation) and its host wrapper
 // src/csrc/lib/ops.cpp:1030-1095.
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
@@ -552,29 +553,132 @@ __global__ __launch_bounds__(64) void w4a16_dequant_kernel(const uint4* __restri
 
 // ------------------------------------------- reference int8 tile format --
 // The reference's own device format (quantized_weight.cpp:41-73): int8 (q - z)
-// in [128][tileLen] tiles ordered (group, block b of 8, tile, k, i).  One thread
-// per output column; consecutive threads read consecutive bytes of a tile row.
-__global__ __launch_bounds__(256) void w4a16_tiled_i8_kernel(const uint16_t* __restrict__ x,
-                                                             const int8_t* __restrict__ w,
-                                                             const uint16_t* __restrict__ scales,
-                                                             uint16_t* __restrict__ out, int K, int N, int blockLen,
-                                                             int tileLen, int tilesPerBlock) {
-    const int n = blockIdx.x * blockDim.x + threadIdx.x;
-    if (n >= N) return;
-    const int b = n / blockLen;
-    const int r = n - b * blockLen;
-    const int t = r / tileLen;
-    const int i = r - t * tileLen;
+// in [128][tileLen] tiles ordered (group, block b of 8, tile t, k, i), column
+// b * blockLen + t * tileLen + i.  A tile's tileLen / 16 chunks of 16 columns
+// are split into slices of CS chunks, one workgroup of kTiWaves waves per
+// (tile, slice): all of a tile when there are >= 64 tiles, down to one chunk
+// per workgroup for the narrow projections (8 tiles).  Lane l of a wave takes
+// chunk l % CS of the slice in row r = l / CS of each R-row band (R = the
+// largest power of two with R * CS <= 64; lanes past R * CS idle), one
+// 16-byte load per band; the waves take the bands of a group in turn, so a
+// lane holds JPG = 128 / (kTiWaves * R) rows of each group (or, when a step
+// of all waves spans several groups, one row of every gstep-th group).  Per
+// group a lane sums x * (q - z) over its rows in fp32, multiplies the sum by
+// its columns' scales and adds it to its accumulators; the next group's loads
+// are in flight meanwhile.  The lanes of one chunk then add up across the
+// rows by shuffles, the waves through LDS.  The same terms as the
+// reference's per-group partial sums, added in another order.  Measured on
+// MI355X (graph-replayed, rotated weights): the former one-thread-per-column
+// kernel took 74 us at K=N=1024, 390 us at K=3584 N=1024 and 140 us at
+// K=1024 N=248064.
+constexpr int kTiWaves = 8;
+constexpr int kTiMaxJ = 8;                               // rows per lane per group: 128 / (8 * 2)
+
+struct Ti8Group {
+    uint4 q[kTiMaxJ];
+    float xv[kTiMaxJ];
+    uint4 s[2];
+};
+
+__global__ __launch_bounds__(64 * kTiWaves) void w4a16_tiled_i8_kernel(const uint16_t* __restrict__ x,
+                                                                      const int8_t* __restrict__ w,
+                                                                      const uint16_t* __restrict__ scales,
+                                                                      uint16_t* __restrict__ out, int K, int N,
+                                                                      int blockLen, int tileLen, int tilesPerBlock,
+                                                                      int CS, int slices) {
+    __shared__ float red[kTiWaves][448];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int CN = tileLen >> 4;
+    int R = 1;
+    while (R * 2 * CS <= 64) R *= 2;
+    const int tile = static_cast<int>(blockIdx.x) / slices, sl = static_cast<int>(blockIdx.x) % slices;
+    const int b = tile / tilesPerBlock, t = tile % tilesPerBlock;
+    const int CSa = CN - sl * CS < CS ? CN - sl * CS : CS;          // chunks of this slice
+    const int cl = lane % CS, r = lane / CS;
+    const int c = sl * CS + cl;
+    // blockLen and tile offsets are multiples of 16, so a chunk lies wholly
+    // inside the block or wholly in the last tile's padding (no scales there)
+    const bool live = r < R && cl < CSa && t * tileLen + 16 * c < blockLen;
+    const int col0 = b * blockLen + t * tileLen + 16 * c;
     const int G = K / kGroup;
-    float acc = 0.f;
-    for (int g = 0; g < G; ++g) {
-        const int8_t* tp = w + (((static_cast<size_t>(g) * 8 + b) * tilesPerBlock + t) * kGroup) * tileLen + i;
-        float partial = 0.f;
-        for (int kk = 0; kk < kGroup; ++kk)
-            partial = fmaf(h2f(x[g * kGroup + kk]), static_cast<float>(tp[static_cast<size_t>(kk) * tileLen]), partial);
-        acc = fmaf(partial, h2f(scales[static_cast<size_t>(g) * N + n]), acc);
+    const int band = kTiWaves * R;                       // rows per step of all waves
+    const int row0 = wave * R + r;
+    // rows of group g this lane holds: g * 128 + rowin + j * band, j < jpg
+    const int jpg = band <= kGroup ? kGroup / band : 1;
+    const int gstep = band <= kGroup ? 1 : band / kGroup;
+    const int gsub = band <= kGroup ? 0 : row0 / kGroup;
+    const int rowin = band <= kGroup ? row0 : row0 % kGroup;
+    const size_t tile_bytes = static_cast<size_t>(kGroup) * tileLen;
+    const int8_t* __restrict__ wl = w + (static_cast<size_t>(b) * tilesPerBlock + t) * tile_bytes + 16 * c +
+                                    static_cast<size_t>(rowin) * tileLen;
+    const size_t gstride = static_cast<size_t>(8) * tilesPerBlock * tile_bytes;    // bytes per group
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    auto load = [&](int g, Ti8Group& d) {
+        const int8_t* p = wl + static_cast<size_t>(g) * gstride;
+#pragma unroll
+        for (int jj = 0; jj < kTiMaxJ; ++jj)
+            if (jj < jpg) {
+                d.q[jj] = *reinterpret_cast<const uint4*>(p + static_cast<size_t>(jj) * band * tileLen);
+                d.xv[jj] = h2f(x[g * kGroup + rowin + jj * band]);
+            }
+        const uint4* sp = reinterpret_cast<const uint4*>(scales + static_cast<size_t>(g) * N + col0);
+        d.s[0] = sp[0];
+        d.s[1] = sp[1];
+    };
+    auto sum = [&](const Ti8Group& d) {
+        float part[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) part[e] = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < kTiMaxJ; ++jj)
+            if (jj < jpg) {
+                const uint32_t words[4] = {d.q[jj].x, d.q[jj].y, d.q[jj].z, d.q[jj].w};
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        part[4 * wd + e] = fmaf(d.xv[jj],
+                                                static_cast<float>(static_cast<int8_t>((words[wd] >> (8 * e)) & 0xffu)),
+                                                part[4 * wd + e]);
+            }
+        const uint32_t sw[8] = {d.s[0].x, d.s[0].y, d.s[0].z, d.s[0].w, d.s[1].x, d.s[1].y, d.s[1].z, d.s[1].w};
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            acc[e] = fmaf(part[e], h2f(static_cast<uint16_t>(sw[e >> 1] >> (16 * (e & 1)))), acc[e]);
+    };
+    if (live && gsub < G) {
+        Ti8Group A, B;
+        load(gsub, A);
+        for (int g = gsub; g < G; g += 2 * gstep) {
+            const int g1 = g + gstep, g2 = g + 2 * gstep;
+            if (g1 < G) load(g1, B);
+            sum(A);
+            if (g1 >= G) break;
+            if (g2 < G) load(g2, A);
+            sum(B);
+        }
     }
-    out[n] = f2h(acc);
+    // rows r of one chunk meet in lane cl (r = 0): a tree over offsets
+    // CS, 2 CS, ... (idle lanes hold zeros; a lane that adds reads r + 2^i < R)
+    for (int m = 1; m < R; m <<= 1)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] += __shfl_down(acc[e], m * CS, 64);
+    if (r == 0 && cl < CSa) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[wave][16 * cl + e] = acc[e];
+    }
+    __syncthreads();
+    for (int col = threadIdx.x; col < 16 * CSa; col += blockDim.x) {
+        float total = 0.f;
+#pragma unroll
+        for (int v = 0; v < kTiWaves; ++v) total += red[v][col];
+        const int i = t * tileLen + 16 * sl * CS + col;
+        const int n = b * blockLen + i;
+        if (i < blockLen && n < N) out[n] = f2h(total);
+    }
 }
 
 // ---- the lm_head's workspace in library memory, for callers that cannot
@@ -934,11 +1038,20 @@ int mcv_w4a16_gemv_tiled_i8(const void* x, int64_t K, int64_t N, int64_t tile_le
         return fail(MCV_ERR_SHAPE, "matmul_w4a16 w packed_rows mismatch");
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    hipLaunchKernelGGL(w4a16_tiled_i8_kernel, dim3(static_cast<unsigned>(ceil_div(N, 256))), dim3(256), 0,
+    if (8 * tilesPerBlock > 0x7fffffff || (K / kGroup) * 8 * tilesPerBlock * kGroup * tile_len >= (int64_t(1) << 40))
+        return fail(MCV_ERR_SHAPE, "matmul_w4a16: weight too large");
+    // chunks of 16 columns per workgroup: a whole tile from 64 tiles on, else
+    // fewer, so the grid reaches ~256 workgroups where it can (MI355X, us per
+    // call: K=N=1024, 8 tiles, 9.9 whole / 6.3 sliced; K=3584 N=1024 29.2 /
+    // 12.5; K=1024 N=31104, 72 tiles, 17.9 whole / 21.6 in 4 slices)
+    const int64_t tiles = 8 * tilesPerBlock, cn = tile_len / 16;
+    const int64_t want = tiles >= 64 ? 1 : std::min<int64_t>(cn, ceil_div(256, tiles));
+    const int64_t cs = ceil_div(cn, want), slices = ceil_div(cn, cs);
+    hipLaunchKernelGGL(w4a16_tiled_i8_kernel, dim3(static_cast<unsigned>(tiles * slices)), dim3(64 * kTiWaves), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), w,
                        static_cast<const uint16_t*>(scales), static_cast<uint16_t*>(out), static_cast<int>(K),
                        static_cast<int>(N), static_cast<int>(blockLen), static_cast<int>(tile_len),
-                       static_cast<int>(tilesPerBlock));
+                       static_cast<int>(tilesPerBlock), static_cast<int>(cs), static_cast<int>(slices));
     return check_launch("w4a16_tiled_i8_kernel");
 }
 

@@ -207,7 +207,10 @@ def _reference_tile_pack(w8, K, N):
     return packed.reshape(-1, tile_len), tile_len
 
 
-@pytest.mark.parametrize("K,N", [(1024, 3584), (1024, 1024), (256, 6144)])
+# tile_len 448, 128, 384 (two tiles per block), 16 and 64 (bands of 16 or 64
+# rows per wave-load, wider than a group), and the lm_head's width (70 tiles
+# per block, the last one part padding).
+@pytest.mark.parametrize("K,N", [(1024, 3584), (1024, 1024), (256, 6144), (256, 128), (384, 512), (128, 248064)])
 def test_reference_int8_tile_format(mcv, oracle, cuda, K, N):
     torch = _torch()
     rng = np.random.default_rng(7)
