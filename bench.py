@@ -552,6 +552,17 @@ class LmHead(Cfg):
     def token(self):
         return int(self.heads[0].launch(self.xd, self.logits).item())
 
+    def greedy_step_us(self, n=200):
+        """The whole greedy step as a decode loop pays it (lm_head_greedy_w4a16):
+        the slots launch, the copy of the 64 slots to the host, which waits
+        for the kernel, and the host fold.  Host wall clock per call."""
+        for i in range(5):
+            self.heads[i % len(self.heads)](self.xd, self.logits)
+        t = time.perf_counter()
+        for i in range(n):
+            self.heads[i % len(self.heads)](self.xd, self.logits)
+        return (time.perf_counter() - t) / n * 1e6
+
     def cpu(self):
         o = load_oracle()
         w8 = o.unpack_awq(self.qweight, self.qzeros)
@@ -575,6 +586,7 @@ def lm_head_entry(lm, args, route, steps, cpu_entry):
     total_ms = lm.gpu_steps(steps, args.warmup, route)
     alt_ms = lm.gpu_steps(max(steps, 200), args.warmup, other)
     pl = lm.per_launch(route)
+    greedy_us = lm.greedy_step_us()
     token = lm.token()
     torch.cuda.synchronize()
     ms = total_ms / steps
@@ -590,6 +602,9 @@ def lm_head_entry(lm, args, route, steps, cpu_entry):
                           "algorithmic_per_launch": lm.bytes},
              "alt_route": {other: {"us_per_call": round(alt_ms / max(steps, 200) * 1e3, 3),
                                    "value": round(lm.bytes / (alt_ms / max(steps, 200) / 1e3) / 1e9, 2)}},
+             "greedy_step": {"us_per_call": round(greedy_us, 2), "calls": 200,
+                             "what": "LmHeadW4A16.__call__ (the Python mirror of lm_head_greedy): slots launch + "
+                                     "copy of the slots to the host + host fold, host wall clock"},
              "config": {"M": 1, "K": lm.K, "V": lm.V, "argmax": route, "launch": "direct",
                         "weight_copies_rotated": len(lm.heads), "rotated_bytes": lm.rotated,
                         "algorithmic_bytes": lm.bytes, "token": token},
