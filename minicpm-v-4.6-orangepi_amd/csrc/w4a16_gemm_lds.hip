@@ -360,6 +360,65 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
     // upper lanes of quad g with the lower lanes of quad g+1 leaves lane l with
     // the 8 consecutive columns 32 j + 8 g + 8 (l/32), g even: one 16-byte store.
     const bool vec_ok = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    auto pack = [&](int i, int j, int g, uint32_t (&p)[4]) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const uint32_t x0 = f2h(acc[i][j][4 * g + 2 * d]) | (uint32_t(f2h(acc[i][j][4 * g + 2 * d + 1])) << 16);
+            const uint32_t x1 = f2h(acc[i][j][4 * g + 4 + 2 * d]) | (uint32_t(f2h(acc[i][j][4 * g + 5 + 2 * d])) << 16);
+            const auto sw = __builtin_amdgcn_permlane32_swap(x0, x1, false, false);
+            p[d] = sw[0];
+            p[2 + d] = sw[1];
+        }
+    };
+    if (vec_ok) {
+        // The wave's TM x 64 fp16 block goes through LDS so that each store
+        // instruction writes whole 128-byte lines of output rows, with
+        // non-temporal stores: full lines go to HBM while other tiles still
+        // compute, and none wait in L2 for the end of the kernel (MI355X,
+        // M=2048 K=1024 N=3584: 20.8-21.2 against 21.2-22.0 us with 16 bytes
+        // per row per store straight from registers; the two-k-part shapes
+        // measured the same either way).  One k-part:
+        // the stage buffers, after a barrier (every wave past the loop).  Two
+        // k-parts: lds1, untouched since the reduction's first barrier (the
+        // waves of k-part 1 have left, so there is no second barrier).
+        constexpr int RB = kSlab * 2 + 16;                 // padded row bytes
+        constexpr int REGION = TM * RB;
+        static_assert(KP == 1 ? ((4 + NS - 1) / NS) * REGION <= C::STAGE : C::WN * REGION <= C::STAGE,
+                      "epilogue staging space");
+        uint8_t* st;
+        if constexpr (KP == 1) {
+            __syncthreads();
+            const int wb = wave % NS;
+            st = (wb == 0 ? lds0 : wb == 1 ? lds1 : wb == 2 ? lds2 : lds3) + (wave / NS) * REGION;
+        } else {
+            st = lds1 + (wave - kp * C::WN) * REGION;
+        }
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; g += 2) {
+                    uint32_t p[4];
+                    pack(i, j, g, p);
+                    *reinterpret_cast<uint4*>(st + (32 * i + (lane & 31)) * RB + (32 * j + 8 * g + 8 * h) * 2) =
+                        make_uint4(p[0], p[1], p[2], p[3]);
+                }
+        // the wave reads back only its own block: its LDS writes are done
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int it = 0; it < TM / 8; ++it) {
+            const int r = it * 8 + (lane >> 3);
+            const int row = m0 + r, col = slab * kSlab + 8 * (lane & 7);
+            const uint4 v = *reinterpret_cast<const uint4*>(st + r * RB + (lane & 7) * 16);
+            if (row < M && col < N)
+                __builtin_nontemporal_store(int4_t{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z),
+                                                   static_cast<int>(v.w)},
+                                            reinterpret_cast<int4_t*>(out + static_cast<size_t>(row) * N + col));
+        }
+        return;
+    }
+    // N not a multiple of 8 (or an unaligned output): element stores
 #pragma unroll
     for (int i = 0; i < C::MB; ++i) {
         const int row = m0 + 32 * i + (lane & 31);
@@ -368,25 +427,13 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
 #pragma unroll
             for (int g = 0; g < 4; g += 2) {
                 uint32_t p[4];
-#pragma unroll
-                for (int d = 0; d < 2; ++d) {
-                    const uint32_t x0 = f2h(acc[i][j][4 * g + 2 * d]) | (uint32_t(f2h(acc[i][j][4 * g + 2 * d + 1])) << 16);
-                    const uint32_t x1 =
-                        f2h(acc[i][j][4 * g + 4 + 2 * d]) | (uint32_t(f2h(acc[i][j][4 * g + 5 + 2 * d])) << 16);
-                    const auto sw = __builtin_amdgcn_permlane32_swap(x0, x1, false, false);
-                    p[d] = sw[0];
-                    p[2 + d] = sw[1];
-                }
+                pack(i, j, g, p);
                 const int col = slab * kSlab + 32 * j + 8 * g + 8 * h;
                 if (row >= M || col >= N) continue;
                 uint16_t* dst = out + static_cast<size_t>(row) * N + col;
-                if (vec_ok) {
-                    *reinterpret_cast<uint4*>(dst) = make_uint4(p[0], p[1], p[2], p[3]);
-                } else {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (col + e < N) dst[e] = static_cast<uint16_t>(p[e >> 1] >> (16 * (e & 1)));
-                }
+                for (int e = 0; e < 8; ++e)
+                    if (col + e < N) dst[e] = static_cast<uint16_t>(p[e >> 1] >> (16 * (e & 1)));
             }
     }
 }
