@@ -192,8 +192,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_kernel(
 // replayed): SPW 16 (243 workgroups) with the tree 26.9-27.2 us, with slots
 // 25.7-26.0 us; SPW 8 27.1-27.3 / 26.4-27.0 us; SPW 1-4 28-30 us; the former
 // one-slab, four-wave kernel ~27.9 us.  Direct launches run ~1 us faster.
-// 256 workgroups with 15 or 16 slabs each (no idle CU) measured the same as
-// 243 with 16 (28.7 against 28.6 us on one box).
+// 256 workgroups with 15 or 16 slabs each (one per CU, the slabs even over
+// the XCDs) measured 0.5-1.1 us slower than 243 with 16 on the full
+// vocabulary, and 0.6 us slower at V = 124047.
 constexpr int kLmWaves = 8;
 constexpr int kLmTree = 0;
 constexpr int kLmSlots = 1;
