@@ -430,7 +430,9 @@ class Prefill(Cfg):
         return gpu_result(self.name, "w4a16_gemm_kernel", self.flops, "TFLOP/s", "mfma",
                           lambda i: pkg.matmul_w4a16(xd, ws[i], out), len(ws), 200,
                           {"config": {"M": self.M, "K": self.K, "N": self.N, "weight_sets_rotated": len(ws),
-                                      "flops": self.flops}})
+                                      "flops": self.flops,
+                                      "k_split_workspace_bytes":
+                                          int(pkg.lib().mcv_w4a16_gemm_workspace_bytes(self.M, self.K, self.N))}})
 
     def cpu(self):
         o = load_oracle()

@@ -140,6 +140,25 @@ int mcv_w4a16_gemm(const void* x_dev, int64_t M, int64_t K, int64_t N,
                    const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                    int zero_bias, void* out_dev, mcv_stream_t stream);
 
+/* mcv_w4a16_gemm with a caller-owned device workspace (no counterpart in the
+ * reference, whose matmul_w4a16 is M = 1 only): where the MFMA tile grid is
+ * small (few rows, long K) the GEMM splits K across workgroups, writes fp32
+ * partial tiles into the workspace and a second launch adds them in a fixed
+ * order and rounds to fp16 (deterministic; the sum order differs from the
+ * unsplit kernel's, within the same fp32 accumulation tolerance).  The
+ * workspace must be 16-byte aligned and hold mcv_w4a16_gemm_workspace_bytes
+ * (M, K, N) bytes, else the call runs unsplit; it is fully written before it
+ * is read, so it needs no clearing.  Calls that share a workspace must be
+ * ordered (one stream). */
+int mcv_w4a16_gemm_ws(const void* x_dev, int64_t M, int64_t K, int64_t N,
+                      const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                      int zero_bias, void* out_dev, void* workspace_dev, int64_t workspace_bytes,
+                      mcv_stream_t stream);
+
+/* Workspace bytes mcv_w4a16_gemm_ws uses for this shape (0: it does not split
+ * K, and any workspace, NULL included, is ignored). */
+int64_t mcv_w4a16_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
+
 /* The two kernels behind mcv_w4a16_gemm, callable directly (same contract). */
 int mcv_w4a16_gemv(const void* x_dev, int64_t M, int64_t K, int64_t N,
                    const void* qw_dev, const void* scales_dev, const void* zeros_dev,

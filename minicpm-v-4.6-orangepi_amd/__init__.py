@@ -58,6 +58,8 @@ _SIGS = {
     "mcv_w4a16_quantize_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int]),
     "mcv_w4a16_unpack_host": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mcv_w4a16_gemm": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
+    "mcv_w4a16_gemm_ws": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64, _vp]),
+    "mcv_w4a16_gemm_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "mcv_w4a16_gemv": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_gemm_mfma": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
@@ -337,8 +339,28 @@ def _w4_call(fn_name: str, x, w: W4A16QuantizedWeight, out, stream):
 
 
 def matmul_w4a16(x, w: W4A16QuantizedWeight, out=None, stream=None):
-    """out[M, N] = x[M, K] . dequant(w), any M (ops.h:104-108 generalised)."""
-    return _w4_call("mcv_w4a16_gemm", x, w, out, stream)
+    """out[M, N] = x[M, K] . dequant(w), any M (ops.h:104-108 generalised).
+    Where the MFMA path splits K across workgroups (few rows, long K) the fp32
+    partial tiles go to a workspace taken from torch's caching allocator on
+    the current stream, so steady-state calls allocate no device memory."""
+    torch = _torch()
+    if x.dtype != torch.float16 or x.dim() != 2 or x.shape[1] != w.K or not x.is_contiguous():
+        raise McvError(f"matmul_w4a16: x must be contiguous fp16 [M, {w.K}]")
+    nb = int(lib().mcv_w4a16_gemm_workspace_bytes(x.shape[0], w.K, w.N))
+    if nb == 0:
+        return _w4_call("mcv_w4a16_gemm", x, w, out, stream)
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, w.N), dtype=torch.float16, device=x.device)
+    if out.dtype != torch.float16 or tuple(out.shape) != (M, w.N) or not out.is_contiguous():
+        raise McvError(f"matmul_w4a16: out must be contiguous fp16 [{M}, {w.N}]")
+    ws = torch.empty(nb, dtype=torch.uint8, device=x.device)
+    if stream is not None:
+        ws.record_stream(stream)                 # not reused until work on `stream` is done
+    q, s, z = w.ptrs()
+    _check(lib().mcv_w4a16_gemm_ws(_dev(x), M, w.K, w.N, q, s, z, w.zero_bias, _dev(out), _dev(ws), nb, _stream(stream)),
+           "matmul_w4a16")
+    return out
 
 
 def matmul_w4a16_gemv(x, w, out=None, stream=None):

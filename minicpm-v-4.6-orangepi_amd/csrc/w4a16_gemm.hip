@@ -34,6 +34,7 @@
 // The reference has no M > 1 quantised path: its prefill runs dense fp16
 // aclnnMm through matmul_b_transposed (src/csrc/lib/decoder_layer.cpp:459-462,
 // 656-659, 857-860; src/csrc/lib/ops.cpp:159-322).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -93,7 +94,7 @@ template <int TM, int WN, int KS, int BK, int DEPTH>
 __global__ __launch_bounds__(64 * WN * KS) void w4a16_gemm_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int M, int K, int N,
-    int nslab, int n_tiles, int total_tiles, int col_major) {
+    int nslab, int n_tiles, int total_tiles, int col_major, int kx, float* __restrict__ part) {
     using C = Cfg<TM, WN, KS, BK, DEPTH>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[C::kLdsBytes];
 
@@ -105,7 +106,11 @@ __global__ __launch_bounds__(64 * WN * KS) void w4a16_gemm_kernel(
     // Each XCD gets a contiguous run of tiles; col_major orders the run down
     // the columns of tiles (an XCD's L2 then holds a few weight slabs and the
     // x rows are what crosses XCDs), row-major along the rows.
-    const int tile = xcd_tile(static_cast<int>(blockIdx.x), total_tiles);
+    // kx > 1: each tile's K is cut into kx contiguous ranges of whole stage
+    // sets (one BK stage per k-part), one workgroup each, and the fp32
+    // partial tiles go to part[split][M][N] for the reduction kernel
+    const int ts = xcd_tile(static_cast<int>(blockIdx.x), total_tiles * kx);
+    const int tile = ts / kx, sx = ts - tile * kx;
     const int m_tiles = total_tiles / n_tiles;
     const int tm = col_major ? tile % m_tiles : tile / n_tiles;
     const int tn = col_major ? tile / m_tiles : tile - tm * n_tiles;
@@ -113,9 +118,10 @@ __global__ __launch_bounds__(64 * WN * KS) void w4a16_gemm_kernel(
     const int slab = tn * WN + wn;
     const int Npad = nslab * kSlab;
     const int CK = K / kChunkK;                // packed chunks per slab
-    const int kpart = K / KS;
-    const int kbeg = kp * kpart;
-    const int KT = kpart / BK;                 // stages
+    const int T = K / (BK * KS);               // stage sets of all of K
+    const int t0 = static_cast<int>(int64_t(sx) * T / kx);
+    const int KT = static_cast<int>(int64_t(sx + 1) * T / kx) - t0;   // stages of this split's k-parts
+    const int kbeg = (t0 * KS + kp * KT) * BK;
 
     uint8_t* As = lds + kp * 2 * C::kAStage;                  // this k-part's two x stage buffers
     uint8_t* Bs = lds + C::kBOff + wave * 2 * C::kBStage;     // this wave's two weight stage buffers
@@ -372,6 +378,35 @@ __global__ __launch_bounds__(64 * WN * KS) void w4a16_gemm_kernel(
         if (kp > 0) return;
     }
 
+    if (part != nullptr) {
+        // the split's fp32 partial tile: register quad g of block (i, j) is
+        // four consecutive columns of one row
+        float* const pd = part + static_cast<size_t>(sx) * M * N;
+        const bool vec4 = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0;
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) {
+            const int row = m0 + 32 * i + (lane & 31);
+            if (row >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int col = slab * kSlab + 32 * j + 8 * g + 4 * (lane >> 5);
+                    if (col >= N) continue;
+                    float* dst = pd + static_cast<size_t>(row) * N + col;
+                    if (vec4) {
+                        *reinterpret_cast<float4*>(dst) =
+                            make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (col + e < N) dst[e] = acc[i][j][4 * g + e];
+                    }
+                }
+        }
+        return;
+    }
+
     // Transposed 32x32 blocks: register r of lane l holds output row
     // 32 i + l%32 and column 32 j + 8 (r/4) + 4 (l/32) + r%4 -- four
     // consecutive columns per register quad.  Swapping the upper lanes of quad
@@ -408,13 +443,60 @@ __global__ __launch_bounds__(64 * WN * KS) void w4a16_gemm_kernel(
     }
 }
 
+// out = fp16 RNE of the KX partial tiles added in split order, four
+// elements per thread (the same order on every call: deterministic).  KX is
+// a compile-time count so every partial's load is issued before the first
+// add.
+template <int KX>
+__global__ __launch_bounds__(256) void w4a16_splitk_reduce_kernel(const float* __restrict__ part, int64_t mn,
+                                                                 uint16_t* __restrict__ out) {
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i0 >= mn) return;
+    if (i0 + 4 <= mn && (mn & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0) {
+        float4 v[KX];
+#pragma unroll
+        for (int s = 0; s < KX; ++s) v[s] = *reinterpret_cast<const float4*>(part + static_cast<size_t>(s) * mn + i0);
+        float4 a = v[0];
+#pragma unroll
+        for (int s = 1; s < KX; ++s) {
+            a.x += v[s].x;
+            a.y += v[s].y;
+            a.z += v[s].z;
+            a.w += v[s].w;
+        }
+        *reinterpret_cast<uint2*>(out + i0) =
+            make_uint2(f2h(a.x) | (uint32_t(f2h(a.y)) << 16), f2h(a.z) | (uint32_t(f2h(a.w)) << 16));
+        return;
+    }
+    for (int64_t i = i0; i < i0 + 4 && i < mn; ++i) {
+        float a = part[i];
+#pragma unroll
+        for (int s = 1; s < KX; ++s) a += part[static_cast<size_t>(s) * mn + i];
+        out[i] = f2h(a);
+    }
+}
+
+using ReduceFn = void (*)(const float*, int64_t, uint16_t*);
+
+ReduceFn pick_reduce(int kx) {
+    switch (kx) {
+        case 2: return w4a16_splitk_reduce_kernel<2>;
+        case 3: return w4a16_splitk_reduce_kernel<3>;
+        case 4: return w4a16_splitk_reduce_kernel<4>;
+        case 5: return w4a16_splitk_reduce_kernel<5>;
+        case 6: return w4a16_splitk_reduce_kernel<6>;
+        case 7: return w4a16_splitk_reduce_kernel<7>;
+        default: return w4a16_splitk_reduce_kernel<8>;
+    }
+}
+
 struct Shape {
     int tm, wn, ks, bk, depth;
     int waves() const { return wn * ks; }
 };
 
 using GemmFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int,
-                        int, int, int, int, int, int);
+                        int, int, int, int, int, int, int, float*);
 
 #define MCV_W4_SHAPES(X)                                                                              \
     X(128, 4, 1, 128, 2) X(128, 4, 2, 64, 1) X(64, 4, 2, 64, 1) X(64, 2, 4, 64, 1) X(64, 2, 2, 128, 2) \
@@ -463,10 +545,41 @@ Shape choose_shape(int64_t M, int64_t K, int64_t nslab) {
     return best;
 }
 
+// Workgroups per tile along K.  A grid far below the 256 CUs (few rows, long
+// K: M=128, K=3584, N=1024 gives 64 tiles) streams each tile's weights and x
+// rows through one CU; cutting K into kx ranges puts kx CUs on every tile,
+// at the cost of kx fp32 partial tiles and a reduction launch.  Up to 8
+// ways, toward 200 workgroups, with at most 8 MB of partial tiles.
+// MCV_W4GEMM_SPLITK=n (1..8) forces n ways where the grid is small (read
+// once per process; tuning sweeps).
+int splitk_ways(const Shape& s, int64_t M, int64_t K, int64_t N) {
+    const int64_t t = tiles_of(s, M, ceil_div(N, kSlab));
+    if (t >= 128) return 1;
+    static const char* const e = std::getenv("MCV_W4GEMM_SPLITK");
+    const int64_t want = e != nullptr && std::atoi(e) >= 1 && std::atoi(e) <= 8 ? std::atoi(e) : ceil_div(200, t);
+    int64_t kx = std::min<int64_t>({want, 8, K / (int64_t(s.bk) * s.ks)});
+    while (kx > 1 && kx * M * N * 4 > (int64_t(8) << 20)) --kx;
+    return static_cast<int>(kx < 1 ? 1 : kx);
+}
+
 }  // namespace
 
+// Bytes of workspace the register-staged path would use for M x K x N (0:
+// no K split, or the LDS kernel or the GEMV takes the shape).
+int64_t w4a16_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    if (M < 1 || K <= 0 || N <= 0 || K % kGroup != 0 || M < 8 || M * N < 65536) return 0;
+    static const char* const which = std::getenv("MCV_W4GEMM_KERNEL");
+    int tm = 0, ns = 0, kp = 1;
+    if ((which == nullptr || std::strcmp(which, "regs") != 0) && choose_w4a16_lds(M, K, N, &tm, &ns, &kp) == 0)
+        return 0;
+    const Shape s = choose_shape(M, K, ceil_div(N, kSlab));
+    const int kx = splitk_ways(s, M, K, N);
+    return kx > 1 ? int64_t(kx) * M * N * 4 : 0;
+}
+
 int launch_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
-                           const void* zeros, int zero_bias, void* out, hipStream_t stream) {
+                           const void* zeros, int zero_bias, void* out, hipStream_t stream, void* ws = nullptr,
+                           int64_t ws_bytes = 0) {
     if (!x || !out || !qw || !scales || !zeros) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_mfma: null pointer");
     if (zero_bias != 0 && zero_bias != 1) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_mfma: zero_bias must be 0 or 1");
     if (K <= 0 || K % kGroup != 0 || K > (int64_t(1) << 24))
@@ -494,17 +607,26 @@ int launch_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const
     if (order != nullptr) col_major = std::atoi(order) ? 1 : 0;
     const int64_t n_tiles = ceil_div(nslab, s.wn);
     const int64_t total = ceil_div(M, s.tm) * n_tiles;
+    // a K split only into a caller's workspace that holds all of it
+    int kx = ws != nullptr ? splitk_ways(s, M, K, N) : 1;
+    if (kx > 1 && (ws_bytes < int64_t(kx) * M * N * 4 || (reinterpret_cast<uintptr_t>(ws) & 15) != 0)) kx = 1;
     // Buffer offsets are 32-bit: x inside one row tile (TM * K * 2 bytes) and
     // the packed weight (K * Npad / 2 bytes).
-    if (total > 0x7fffffff || K > (int64_t(1) << 22) || K * nslab * kSlab / 2 >= (int64_t(1) << 32))
+    if (total * kx > 0x7fffffff || K > (int64_t(1) << 22) || K * nslab * kSlab / 2 >= (int64_t(1) << 32))
         return fail(MCV_ERR_SHAPE, "mcv_w4a16_gemm_mfma: problem too large (M=%lld N=%lld)", (long long)M, (long long)N);
-    hipLaunchKernelGGL(pick(s), dim3(static_cast<unsigned>(total)), dim3(64 * s.waves()), 0, stream,
+    float* const part = kx > 1 ? static_cast<float*>(ws) : nullptr;
+    hipLaunchKernelGGL(pick(s), dim3(static_cast<unsigned>(total * kx)), dim3(64 * s.waves()), 0, stream,
                        static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
                        static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(out), static_cast<int>(M),
                        static_cast<int>(K), static_cast<int>(N), static_cast<int>(nslab), static_cast<int>(n_tiles),
-                       static_cast<int>(total), col_major);
-    return check_launch("w4a16_gemm_kernel");
+                       static_cast<int>(total), col_major, kx, part);
+    if (kx == 1) return check_launch("w4a16_gemm_kernel");
+    if ((rc = check_launch("w4a16_gemm_kernel")) != MCV_OK) return rc;
+    const int64_t mn = M * N;
+    hipLaunchKernelGGL(pick_reduce(kx), dim3(static_cast<unsigned>(ceil_div(ceil_div(mn, 4), 256))), dim3(256), 0,
+                       stream, part, mn, static_cast<uint16_t*>(out));
+    return check_launch("w4a16_splitk_reduce_kernel");
 }
 
 }  // namespace mcv
@@ -516,6 +638,19 @@ extern "C" {
 int mcv_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                         const void* zeros, int zero_bias, void* out, mcv_stream_t stream) {
     return launch_w4a16_gemm_mfma(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
+}
+
+int64_t mcv_w4a16_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) { return w4a16_gemm_workspace_bytes(M, K, N); }
+
+// mcv_w4a16_gemm with a caller-owned workspace, which lets the MFMA path
+// split K across workgroups where the tile grid is small.
+int mcv_w4a16_gemm_ws(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
+                      const void* zeros, int zero_bias, void* out, void* workspace, int64_t workspace_bytes,
+                      mcv_stream_t stream) {
+    if (M >= 1 && (M < 8 || int64_t(M) * N < 65536))
+        return launch_w4a16_gemv(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
+    return launch_w4a16_gemm_mfma(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream),
+                                  workspace, workspace_bytes);
 }
 
 // Decode-sized M streams the weights once per row through the GEMV; larger M

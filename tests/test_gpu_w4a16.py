@@ -128,6 +128,36 @@ def test_gemm_mfma_full_size(mcv, oracle, cuda, M, K, N):
     _check(_host_f32(out), ref, f"mfma full M={M} K={K} N={N}")
 
 
+# K split across workgroups (mcv_w4a16_gemm_ws, the Python mirror's route):
+# few rows and a long K leave the tile grid far below the CU count.  K=3584's
+# 7 stage sets over 4 workgroups (uneven), seven ways at M=64, ragged rows
+# and an odd N (element stores of the partial tiles, the reduction's scalar
+# path).
+@pytest.mark.parametrize("M,K,N", [(128, 3584, 1024), (64, 3584, 1024), (200, 3584, 1024), (97, 2048, 1001),
+                                   (128, 1024, 1024)], ids=lambda v: str(v))
+def test_gemm_split_k_vs_oracle(mcv, oracle, cuda, M, K, N):
+    torch = _torch()
+    x, qweight, qzeros, scales, _ = _case(6000 + M + K + N, M, K, N)
+    w = _dev_weight(mcv, qweight, qzeros, scales)
+    nb = int(mcv.lib().mcv_w4a16_gemm_workspace_bytes(M, w.K, w.N))           # (N padded to 8 columns)
+    assert nb > 0
+    xd = _to_dev(x)
+    out = mcv.matmul_w4a16(xd, w)
+    again = mcv.matmul_w4a16(xd, w)
+    ref = oracle.w4a16_matmul(x, oracle.unpack_awq(qweight, qzeros), scales)
+    _check(_host_f32(out), ref, f"split-K M={M} K={K} N={N}")
+    # the partials are added in split order: the same bits on every call
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    # a workspace one byte short runs unsplit: the MFMA kernel's own bits
+    short = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    got = torch.empty_like(out)
+    q, sc, z = w.ptrs()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert mcv.lib().mcv_w4a16_gemm_ws(xd.data_ptr(), M, w.K, w.N, q, sc, z, w.zero_bias, got.data_ptr(),
+                                       short.data_ptr(), nb - 1, stream) == 0
+    assert torch.equal(got.view(torch.int16), mcv.matmul_w4a16_mfma(xd, w).view(torch.int16))
+
+
 def test_gemv_and_mfma_agree(mcv, cuda):
     x, qweight, qzeros, scales, _ = _case(5, 8, 1024, 520)
     w = _dev_weight(mcv, qweight, qzeros, scales)
