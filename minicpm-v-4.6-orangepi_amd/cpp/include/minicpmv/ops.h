@@ -36,6 +36,12 @@ void matmul_w4a16(const Tensor& x, const Tensor& w_int8, const Tensor& scales, T
 // LDS-dequant fp16 MFMA GEMM otherwise).
 void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream);
 
+// The same with a caller-owned workspace (mcv_w4a16_gemm_ws): where the MFMA
+// path splits K across workgroups (few rows, long K) its fp32 partial tiles go
+// there.  `workspace` (Int8) is reallocated only when a shape needs more than
+// it holds; calls that share it must be ordered on one stream.
+void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream, Tensor& workspace);
+
 // Decode MLP front half in one launch: act [M, I] = silu(x . gate) * (x . up),
 // gate/up rounded to fp16 first -- bit-identical to two matmul_w4a16 calls and
 // silu_mul (the reference's sequence, decoder_layer.cpp:1029-1046).

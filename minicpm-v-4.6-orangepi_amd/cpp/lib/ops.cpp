@@ -73,6 +73,21 @@ void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, h
               "matmul_w4a16");
 }
 
+void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream, Tensor& workspace) {
+    require(x.dtype() == DType::Float16 && out.dtype() == DType::Float16, "matmul_w4a16 x and out must be fp16");
+    require(x.shape().size() == 2 && x.shape()[1] == w.K, "matmul_w4a16 x must be [M, K]");
+    require(out.shape() == std::vector<int64_t>{x.shape()[0], w.N}, "matmul_w4a16 out must be [M, N]");
+    require(w.w_int8.data() && w.scales.data() && w.zeros.data(), "matmul_w4a16 weight is not loaded");
+    const int64_t nb = mcv_w4a16_gemm_workspace_bytes(x.shape()[0], w.K, w.N);
+    if (nb > 0 && static_cast<int64_t>(workspace.numel()) < nb) {
+        workspace = Tensor({nb}, DType::Int8);
+        workspace.allocate();
+    }
+    check_mcv(mcv_w4a16_gemm_ws(x.data(), x.shape()[0], w.K, w.N, w.w_int8.data(), w.scales.data(), w.zeros.data(),
+                                w.zero_bias, out.data(), nb > 0 ? workspace.data() : nullptr, nb, stream),
+              "matmul_w4a16");
+}
+
 void mlp_gate_up_silu_w4a16(const Tensor& x, const W4A16QuantizedWeight& gate, const W4A16QuantizedWeight& up,
                             Tensor& act, hipStream_t stream) {
     require(x.dtype() == DType::Float16 && act.dtype() == DType::Float16, "mlp_gate_up_silu x and act must be fp16");

@@ -161,6 +161,38 @@ int main() {
         std::printf("decode MLP give-up: workspace flag %u, status %d, threw %d, exact after reset %d\n", ws_flag,
                     int(status), int(threw), int(h1 == h2));
         if (ws_flag == 0 || !status || !threw || h1 != h2) return 1;
+
+        // The K split across workgroups into a caller-owned workspace, on the
+        // down projection's shape (K=3584, N=1024) at M = 128: within fp16
+        // rounding of the unsplit kernel (only the fp32 summation order
+        // differs), the same bits on every call, the workspace allocated once.
+        constexpr int MR = 128;
+        Tensor a({MR, N}, DType::Float16), o1({MR, K}, DType::Float16), o2({MR, K}, DType::Float16), wsp;
+        a.allocate();
+        o1.allocate();
+        o2.allocate();
+        std::vector<uint16_t> ha(static_cast<size_t>(MR) * N), r1(static_cast<size_t>(MR) * K), r2(r1.size()),
+            r3(r1.size());
+        for (auto& v : ha) v = t::f2h(xd(rng));
+        a.copy_from_host(ha.data(), ha.size() * 2);
+        matmul_w4a16(a, down, o1, ctx.stream());
+        matmul_w4a16(a, down, o2, ctx.stream(), wsp);
+        const int64_t nb = mcv_w4a16_gemm_workspace_bytes(MR, N, K);
+        const void* const first = wsp.data();
+        o1.copy_to_host(r1.data(), r1.size() * 2);
+        o2.copy_to_host(r2.data(), r2.size() * 2);
+        matmul_w4a16(a, down, o2, ctx.stream(), wsp);
+        o2.copy_to_host(r3.data(), r3.size() * 2);
+        double worst = 0.0;
+        for (size_t i = 0; i < r1.size(); ++i) {
+            const double u = t::h2f(r1[i]), v = t::h2f(r2[i]);
+            worst = std::max(worst, std::fabs(u - v) / (std::fabs(u) + 1e-2));
+        }
+        std::printf("split-K M=%d: workspace %lld bytes (allocated %zu), max rel diff vs unsplit %.2e, repeat %d, "
+                    "reused %d\n", MR, static_cast<long long>(nb), wsp.numel(), worst, int(r2 == r3),
+                    int(wsp.data() == first));
+        if (nb <= 0 || static_cast<int64_t>(wsp.numel()) < nb || worst > 2e-3 || r2 != r3 || wsp.data() != first)
+            return 1;
     }
 
     // 4) shape validation mirrors the reference's host wrapper

@@ -158,6 +158,36 @@ def test_gemm_split_k_vs_oracle(mcv, oracle, cuda, M, K, N):
     assert torch.equal(got.view(torch.int16), mcv.matmul_w4a16_mfma(xd, w).view(torch.int16))
 
 
+def test_gemm_split_k_graph_replays(mcv, cuda):
+    """The split path under HIP graph capture (workspace from the graph's
+    pool, no memset anywhere): every replay, with eager work and host
+    synchronisation between them, gives the eager call's bits."""
+    torch = _torch()
+    M, K, N = 128, 3584, 1024
+    x, qweight, qzeros, scales, _ = _case(77, M, K, N)
+    w = _dev_weight(mcv, qweight, qzeros, scales)
+    assert int(mcv.lib().mcv_w4a16_gemm_workspace_bytes(M, w.K, w.N)) > 0
+    xd = _to_dev(x)
+    want = mcv.matmul_w4a16(xd, w)
+    out = torch.empty_like(want)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mcv.matmul_w4a16(xd, w, out)                       # warm the pool on the capture stream
+        with torch.cuda.graph(g, stream=s):
+            mcv.matmul_w4a16(xd, w, out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        mcv.matmul_w4a16(_to_dev(x[: M // 2]), w)          # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {i}"
+
+
 def test_gemv_and_mfma_agree(mcv, cuda):
     x, qweight, qzeros, scales, _ = _case(5, 8, 1024, 520)
     w = _dev_weight(mcv, qweight, qzeros, scales)
