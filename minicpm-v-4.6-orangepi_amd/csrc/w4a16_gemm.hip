@@ -555,11 +555,33 @@ Shape choose_shape(int64_t M, int64_t K, int64_t nslab) {
 int splitk_ways(const Shape& s, int64_t M, int64_t K, int64_t N) {
     const int64_t t = tiles_of(s, M, ceil_div(N, kSlab));
     if (t >= 128) return 1;
-    static const char* const e = std::getenv("MCV_W4GEMM_SPLITK");
-    const int64_t want = e != nullptr && std::atoi(e) >= 1 && std::atoi(e) <= 8 ? std::atoi(e) : ceil_div(200, t);
+    static const int forced = [] {
+        const char* const e = std::getenv("MCV_W4GEMM_SPLITK");
+        const int v = e != nullptr ? std::atoi(e) : 0;
+        return v >= 1 && v <= 8 ? v : 0;
+    }();
+    const int64_t want = forced > 0 ? forced : ceil_div(200, t);
     int64_t kx = std::min<int64_t>({want, 8, K / (int64_t(s.bk) * s.ks)});
     while (kx > 1 && kx * M * N * 4 > (int64_t(8) << 20)) --kx;
     return static_cast<int>(kx < 1 ? 1 : kx);
+}
+
+// Few rows: the GEMV streams the weights once per row and still beats the
+// MFMA GEMM, whose tile count is M/TM * N/TN, until the output reaches about
+// 64K elements (MI355X, graph-replayed, rotated weights: K=1024 N=3584 M=16
+// 5.7 us against 7.0; K=3584 N=1024 M=48 12.4 against 12.5; K=1024 N=6144
+// crosses over near M=11).
+bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N < 65536); }
+
+// The LDS-staged kernel (w4a16_gemm_lds.hip) where its tall tiles fill the
+// chip, the register-staged one otherwise; MCV_W4GEMM_KERNEL=regs forces the
+// latter (read once per process).
+bool w4a16_uses_lds(int64_t M, int64_t K, int64_t N, int* tm, int* ns, int* kp) {
+    static const bool regs_only = [] {
+        const char* const e = std::getenv("MCV_W4GEMM_KERNEL");
+        return e != nullptr && std::strcmp(e, "regs") == 0;
+    }();
+    return !regs_only && choose_w4a16_lds(M, K, N, tm, ns, kp) == 0;
 }
 
 }  // namespace
@@ -567,11 +589,9 @@ int splitk_ways(const Shape& s, int64_t M, int64_t K, int64_t N) {
 // Bytes of workspace the register-staged path would use for M x K x N (0:
 // no K split, or the LDS kernel or the GEMV takes the shape).
 int64_t w4a16_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
-    if (M < 1 || K <= 0 || N <= 0 || K % kGroup != 0 || M < 8 || M * N < 65536) return 0;
-    static const char* const which = std::getenv("MCV_W4GEMM_KERNEL");
+    if (M < 1 || K <= 0 || N <= 0 || K % kGroup != 0 || w4a16_prefers_gemv(M, N)) return 0;
     int tm = 0, ns = 0, kp = 1;
-    if ((which == nullptr || std::strcmp(which, "regs") != 0) && choose_w4a16_lds(M, K, N, &tm, &ns, &kp) == 0)
-        return 0;
+    if (w4a16_uses_lds(M, K, N, &tm, &ns, &kp)) return 0;
     const Shape s = choose_shape(M, K, ceil_div(N, kSlab));
     const int kx = splitk_ways(s, M, K, N);
     return kx > 1 ? int64_t(kx) * M * N * 4 : 0;
@@ -589,12 +609,8 @@ int launch_w4a16_gemm_mfma(const void* x, int64_t M, int64_t K, int64_t N, const
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_mfma: x must be 16-byte aligned");
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    // The LDS-staged kernel (w4a16_gemm_lds.hip) where its tall tiles fill
-    // the chip, the register-staged one below otherwise;
-    // MCV_W4GEMM_KERNEL=regs forces the latter (read once per process).
-    static const char* const which = std::getenv("MCV_W4GEMM_KERNEL");
     int tm = 0, ns = 0, kp = 1;
-    if ((which == nullptr || std::strcmp(which, "regs") != 0) && choose_w4a16_lds(M, K, N, &tm, &ns, &kp) == 0)
+    if (w4a16_uses_lds(M, K, N, &tm, &ns, &kp))
         return launch_w4a16_gemm_lds(x, M, K, N, qw, scales, zeros, zero_bias, out, tm, ns, kp, stream);
     const int64_t nslab = ceil_div(N, kSlab);
     const Shape s = choose_shape(M, K, nslab);
@@ -647,7 +663,7 @@ int64_t mcv_w4a16_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) { return
 int mcv_w4a16_gemm_ws(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                       const void* zeros, int zero_bias, void* out, void* workspace, int64_t workspace_bytes,
                       mcv_stream_t stream) {
-    if (M >= 1 && (M < 8 || int64_t(M) * N < 65536))
+    if (w4a16_prefers_gemv(M, N))
         return launch_w4a16_gemv(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
     return launch_w4a16_gemm_mfma(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream),
                                   workspace, workspace_bytes);
@@ -657,12 +673,7 @@ int mcv_w4a16_gemm_ws(const void* x, int64_t M, int64_t K, int64_t N, const void
 // goes to the MFMA kernel, which reuses each dequantised operand across rows.
 int mcv_w4a16_gemm(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                    const void* zeros, int zero_bias, void* out, mcv_stream_t stream) {
-    // Few rows: the GEMV streams the weights once per row and still beats the
-    // MFMA GEMM, whose tile count is M/TM * N/TN, until the output reaches
-    // about 64K elements (MI355X, graph-replayed, rotated weights: K=1024
-    // N=3584 M=16 5.7 us against 7.0; K=3584 N=1024 M=48 12.4 against 12.5;
-    // K=1024 N=6144 crosses over near M=11).
-    if (M >= 1 && (M < 8 || int64_t(M) * N < 65536))
+    if (w4a16_prefers_gemv(M, N))
         return launch_w4a16_gemv(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
     return launch_w4a16_gemm_mfma(x, M, K, N, qw, scales, zeros, zero_bias, out, static_cast<hipStream_t>(stream));
 }
