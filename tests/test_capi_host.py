@@ -308,6 +308,22 @@ def test_lm_head_slots_token_known_answer(mcv):
     assert L.mcv_w4a16_lm_head_argmax_slots(fake, 128, big, big, fake, fake, fake, 0, None, fake, 1, None) == 2
 
 
+def test_w4a16_gemm_workspace_query(mcv):
+    """Workspace of the K split across workgroups: none where the GEMV
+    (few rows) or the LDS kernel (tall tiles fill the chip) takes the shape,
+    or for an invalid K; otherwise kx fp32 partial tiles of M x N, kx the
+    split toward 200 workgroups (M=128, K=3584, N=1024: 64 tiles of 32 rows
+    x one slab, 4 ways; M=64: 32 tiles, 7 ways -- K=3584 has 7 stage sets of
+    4 x 128)."""
+    q = mcv.lib().mcv_w4a16_gemm_workspace_bytes
+    assert q(128, 3584, 1024) == 4 * 128 * 1024 * 4
+    assert q(64, 3584, 1024) == 7 * 64 * 1024 * 4
+    assert q(128, 1024, 1024) == 2 * 128 * 1024 * 4                 # K=1024: only 2 stage sets
+    for shape in [(4, 1024, 1024), (32, 1024, 1024), (2048, 1024, 3584), (2048, 3584, 1024), (128, 1024, 3584),
+                  (512, 3584, 1024), (128, 1000, 1024), (0, 1024, 1024), (128, 0, 1024)]:
+        assert q(*shape) == 0, shape
+
+
 def test_lm_head_grid_choice(mcv):
     """Slabs per workgroup by vocabulary: 16 on the full vocabulary (243
     workgroups), fewer on a GPU's share of a column split, one slab per

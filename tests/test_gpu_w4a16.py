@@ -156,6 +156,12 @@ def test_gemm_split_k_vs_oracle(mcv, oracle, cuda, M, K, N):
     assert mcv.lib().mcv_w4a16_gemm_ws(xd.data_ptr(), M, w.K, w.N, q, sc, z, w.zero_bias, got.data_ptr(),
                                        short.data_ptr(), nb - 1, stream) == 0
     assert torch.equal(got.view(torch.int16), mcv.matmul_w4a16_mfma(xd, w).view(torch.int16))
+    # so does a large enough workspace that is not 16-byte aligned
+    got.zero_()
+    big = torch.empty(nb + 16, dtype=torch.uint8, device="cuda")
+    assert mcv.lib().mcv_w4a16_gemm_ws(xd.data_ptr(), M, w.K, w.N, q, sc, z, w.zero_bias, got.data_ptr(),
+                                       big.data_ptr() + 4, nb, stream) == 0
+    assert torch.equal(got.view(torch.int16), mcv.matmul_w4a16_mfma(xd, w).view(torch.int16))
 
 
 def test_gemm_split_k_graph_replays(mcv, cuda):
