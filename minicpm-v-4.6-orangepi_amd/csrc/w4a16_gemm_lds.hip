@@ -471,8 +471,8 @@ GemmWFn pick_w(const ShapeW& s) {
 // for it (M=1024: 15.4 against 14.7 us; M=2048 K=1024: equal with random
 // data, 1 us slower with constant data).  So: the first of 128-row, 64-row,
 // 64-row-two-k-parts tiles whose grid still covers most of the 256 CUs, else
-// -1.  MCV_W4LDS_SHAPE="TM,NS,KP" forces a shape (read once per process;
-// tuning sweeps).
+// -1, except at a short K (below).  MCV_W4LDS_SHAPE="TM,NS,KP" forces a
+// shape (read once per process; tuning sweeps).
 int choose_w4a16_lds(int64_t M, int64_t K, int64_t N, int* tm, int* ns, int* kp) {
     static const char* const e = std::getenv("MCV_W4LDS_SHAPE");
     ShapeW s{0, 0, 1};
@@ -492,6 +492,20 @@ int choose_w4a16_lds(int64_t M, int64_t K, int64_t N, int* tm, int* ns, int* kp)
             *kp = c.kp;
             return 0;
         }
+    }
+    // No tall tile fills the chip: at a short K, 32-row tiles over two
+    // k-parts still beat the register-staged kernel, whatever their grid
+    // (graph-replayed, rotated weights, us per call, register-staged kernel
+    // in brackets): M=128 K=1024 N=3584 7.4 (8.05); M=256 7.8 (9.8); M=192
+    // 7.6 (14.0); M=64 7.2 (8.8); M=128 N=6144 7.8 (14.2); M=128 K=1024
+    // N=1024 6.7 (7.9); M=128 K=2048 N=2048 10.1 (10.4).  At K=3584 they
+    // lose: M=128 N=1024 14.5 against 10.9 for the register kernel's K split,
+    // M=512 15.3 against 14.4.
+    if (M >= 32 && K <= 2048 && K % (int64_t(kGroup) * 2) == 0) {
+        *tm = 32;
+        *ns = 3;
+        *kp = 2;
+        return 0;
     }
     return -1;
 }

@@ -314,13 +314,15 @@ def test_w4a16_gemm_workspace_query(mcv):
     or for an invalid K; otherwise kx fp32 partial tiles of M x N, kx the
     split toward 200 workgroups (M=128, K=3584, N=1024: 64 tiles of 32 rows
     x one slab, 4 ways; M=64: 32 tiles, 7 ways -- K=3584 has 7 stage sets of
-    4 x 128)."""
+    4 x 128).  Splits happen only past K=2048."""
     q = mcv.lib().mcv_w4a16_gemm_workspace_bytes
     assert q(128, 3584, 1024) == 4 * 128 * 1024 * 4
     assert q(64, 3584, 1024) == 7 * 64 * 1024 * 4
-    assert q(128, 1024, 1024) == 2 * 128 * 1024 * 4                 # K=1024: only 2 stage sets
+    assert q(96, 3584, 2048) == 3 * 96 * 2048 * 4                   # 96 tiles: 3 ways
+    # K <= 2048 goes to the LDS kernel's 32-row, two-k-part tiles
     for shape in [(4, 1024, 1024), (32, 1024, 1024), (2048, 1024, 3584), (2048, 3584, 1024), (128, 1024, 3584),
-                  (512, 3584, 1024), (128, 1000, 1024), (0, 1024, 1024), (128, 0, 1024)]:
+                  (128, 1024, 1024), (128, 2048, 2048), (512, 3584, 1024), (128, 1000, 1024), (0, 1024, 1024),
+                  (128, 0, 1024)]:
         assert q(*shape) == 0, shape
 
 

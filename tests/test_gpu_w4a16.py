@@ -95,6 +95,10 @@ def test_dequant_bit_exact(mcv, oracle, cuda):
 
 
 @pytest.mark.parametrize("M,K,N", [
+    # (128, 1024, 3584), (130, 1024, 1000) ragged and (256, 256, 264), one
+    # stage per k-part: the LDS kernel's 32-row tiles over two k-parts
+    # (K <= 2048 with no tall tile filling the chip); (8, ...) and
+    # (128, 3584, 1024): the register-staged kernel
     (8, 1024, 3584), (128, 1024, 3584), (130, 1024, 1000), (128, 3584, 1024), (256, 256, 264),
     # LDS-staged kernel: 128-row tiles, ragged M and N (57 slabs, the last
     # tile's fourth slab past the end), one k stage (fewer stages than buffers)
@@ -130,11 +134,11 @@ def test_gemm_mfma_full_size(mcv, oracle, cuda, M, K, N):
 
 # K split across workgroups (mcv_w4a16_gemm_ws, the Python mirror's route):
 # few rows and a long K leave the tile grid far below the CU count.  K=3584's
-# 7 stage sets over 4 workgroups (uneven), seven ways at M=64, ragged rows
-# and an odd N (element stores of the partial tiles, the reduction's scalar
-# path).
-@pytest.mark.parametrize("M,K,N", [(128, 3584, 1024), (64, 3584, 1024), (200, 3584, 1024), (97, 2048, 1001),
-                                   (128, 1024, 1024)], ids=lambda v: str(v))
+# 7 stage sets over 4 workgroups (uneven), seven ways at M=64, three at
+# M=96 N=2048, ragged rows and an odd N (element stores of the partial
+# tiles, the reduction's scalar path).
+@pytest.mark.parametrize("M,K,N", [(128, 3584, 1024), (64, 3584, 1024), (200, 3584, 1024), (97, 3584, 1001),
+                                   (96, 3584, 2048)], ids=lambda v: str(v))
 def test_gemm_split_k_vs_oracle(mcv, oracle, cuda, M, K, N):
     torch = _torch()
     x, qweight, qzeros, scales, _ = _case(6000 + M + K + N, M, K, N)
