@@ -16,9 +16,11 @@ carries every configuration of the north star, each measured in the same run:
   4  W4A16 prefill GEMM, M in {128,512,2048} x (K,N) in {(1024,3584),(3584,1024)}
   5  W8A8 GEMM M in {1,256,1024}, K=1024, N=3584 (fused fp16 epilogue)
 
-For each: `us_per_call` = mean duration of back-to-back launches (HIP graphs of
-100 launches, so the host's launch rate does not gate short kernels), from
-which `value` and `roofline.achieved` follow; `kernel_us_median` /
+For each: `us_per_call` = mean duration of 200 back-to-back launches, enqueued
+directly while a spin kernel holds the stream (so the host's launch rate does
+not gate short kernels, and a rocprofv3 kernel trace of the same launches
+sees them back to back as well), from which `value` and `roofline.achieved`
+follow; `kernel_us_median` /
 `kernel_us_mean` = per-launch HIP event pairs around each of >= 100 launches
 (the queue is kept full by a sleep kernel, so each pair brackets one kernel);
 `cpu_baseline` = the oracle's restatement of the reference's CPU path on this
@@ -44,8 +46,8 @@ METRIC = "W4A16 M=1 GEMV HBM GB/s (% peak) + µs/call; prefill GEMM TFLOPS (% MF
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 INT8_MFMA_PEAK_TOPS = 5000.0
-GRAPH_CHUNK = 100          # launches per captured graph
 PER_LAUNCH = 200           # event-bracketed launches per configuration
+ARGS = None                # the parsed command line
 
 
 def log(*a):
@@ -83,47 +85,45 @@ def w4a16_bytes(K, N):
 # --------------------------------------------------------------------------- #
 # GPU timing                                                                   #
 # --------------------------------------------------------------------------- #
-def _capture(launch, first, count, n_sets):
-    """A HIP graph of `count` launches (weight sets rotating from `first`),
-    captured on a side stream."""
-    import torch
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(g, stream=s):
-            for i in range(count):
-                launch((first + i) % n_sets)
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    return g
-
-
-def time_graph(launch, n_sets, steps, warmup=3):
-    """Mean ms per launch over `steps` back-to-back launches replayed from HIP
-    graphs on torch's current stream, between one event pair."""
+def time_queued(launch, n_sets, steps, warmup=3):
+    """Mean ms per launch over `steps` back-to-back launches enqueued directly
+    on torch's current stream while a spin kernel holds it, between one event
+    pair: the GPU runs them back to back however slowly the host enqueues
+    (rocprofv3's kernel trace of the same launches shows them back to back
+    too, so its per-kernel durations match this figure).  Returns (ms per
+    launch, host enqueue ms)."""
     import torch
     for i in range(warmup):
         launch(i % n_sets)
     torch.cuda.synchronize()
-    chunks, done = [], 0
-    while done < steps:
-        n = min(GRAPH_CHUNK, steps - done)
-        chunks.append(_capture(launch, warmup + done, n, n_sets))
-        done += n
+    t = time.perf_counter()
+    for i in range(20):
+        launch(i % n_sets)
+    host_ms = (time.perf_counter() - t) / 20 * 1e3
+    torch.cuda.synchronize()
     # one untimed pass over exactly the launches timed below: every weight
     # set they use is read once before the clock starts (a set's first read
     # after it was written costs extra: page-table walks on fresh memory)
-    for g in chunks:
-        g.replay()
+    for i in range(steps):
+        launch(i % n_sets)
     torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for g in chunks:
-        g.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+    hold = steps * host_ms * 1.5 + 1.0
+    for _ in range(3):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _sleep_ms(hold)
+        t0.record()
+        th = time.perf_counter()
+        for i in range(steps):
+            launch(i % n_sets)
+        t1.record()
+        enq_ms = (time.perf_counter() - th) * 1e3
+        torch.cuda.synchronize()
+        if enq_ms < 0.8 * hold:          # the spin kernel outlasted the enqueue
+            break
+        hold *= 2.0
+    else:
+        raise RuntimeError(f"time_queued: the host could not enqueue {steps} launches within the hold")
+    return t0.elapsed_time(t1) / steps, enq_ms
 
 
 def time_direct(launch, n_sets, steps, warmup):
@@ -238,8 +238,10 @@ def traffic_from_profiles(workload: str):
 def gpu_result(name, kernel, amount, unit, bound, launch, n_sets, steps, extra=None):
     """Times one configuration: back-to-back mean (value, roofline) and the
     per-launch median."""
-    per = time_graph(launch, n_sets, steps)
-    pl = np.array(time_per_launch(launch, n_sets))
+    per, _ = time_queued(launch, n_sets, steps)
+    # (--no-per-launch: profiling runs, whose kernel trace should hold only
+    # the back-to-back launches)
+    pl = np.array([per] if ARGS.no_per_launch else time_per_launch(launch, n_sets))
     scale = 1e9 if unit == "GB/s" else 1e12
     value = amount / (per / 1e3) / scale
     peak = HBM_PEAK_GBS if bound == "hbm" else (INT8_MFMA_PEAK_TOPS if unit == "TOP/s" else FP16_MFMA_PEAK_TFLOPS)
@@ -893,9 +895,13 @@ def main():
     ap.add_argument("--N", type=int, default=0)
     ap.add_argument("--V", type=int, default=0, help="lm_head vocabulary (default 248094)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-per-launch", action="store_true",
+                    help="skip the event-bracketed per-launch timing (profiling runs)")
     ap.add_argument("--argmax", default="tree", choices=["tree", "slots"],
                     help="lm_head: token on the device (tree) or host-finished tagged slots")
     args = ap.parse_args()
+    global ARGS
+    ARGS = args
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: every box in this build has a single MI355X, and this run has no "

@@ -242,12 +242,12 @@ int mcv_w4a16_gemv_multi(const void* x_dev, int64_t M, int64_t K, const mcv_w4a1
 
 /* Workspace for mcv_w4a16_lm_head_argmax over V columns (0 < V < 2^24):
  * device memory of this many bytes, 128-byte aligned, zero-filled once before
- * its first use.  It holds per-workgroup call counters and the call-tagged key
- * words of the fused argmax, which every call keeps consistent; one workspace
- * serves one V, and calls sharing it must not overlap.  The u32 at byte 0
- * turns non-zero if the wait for the keys ever gave up (~40 ms); that call's
- * token is then -1, and the workspace must be zero-filled again before the
- * next call.  Returns 0 for an unsupported V. */
+ * its first use.  It holds a generation word and the call-tagged key words of
+ * the fused argmax, which every call keeps consistent: a workspace sized for
+ * the largest V serves every smaller V too, eager calls and HIP-graph replays
+ * alike, but calls sharing it must not overlap.  The u32 at byte 0 turns
+ * non-zero if the wait for the keys ever gave up (~40 ms); that call's token
+ * is then -1, and later calls need no reset.  Returns 0 for an unsupported V. */
 int64_t mcv_lm_head_workspace_bytes(int64_t V);
 
 /* Slabs of 64 columns per workgroup that the lm_head entry points launch for
@@ -280,11 +280,14 @@ int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
  * and results to mcv_w4a16_lm_head_argmax, minus the workspace: the
  * workspace lives in a library-owned array in device memory, one per GPU,
  * held until the process ends, for V <= mcv_lm_head_noalloc_max_vocab()
- * (2^20; larger V is MCV_ERR_SHAPE).  The call allocates nothing.  Every
+ * (2^20; larger V is MCV_ERR_SHAPE).  The call allocates nothing and
+ * launches only the lm_head kernel, so it may be captured into a HIP graph;
+ * captured replays and eager calls at other V may interleave, because the
+ * array's state lives in device memory and is valid for every V.  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU
- * (other streams, other threads) race and give undefined tokens.  The first
- * call on a GPU, and every call whose V differs from the previous call's,
- * zero-fills the array first with a fill kernel on `stream`. */
+ * (other streams, other threads) race and give undefined tokens.  A bounded
+ * wait that gives up shows as token -1 and *status (when not NULL); the next
+ * call needs no reset. */
 int64_t mcv_lm_head_noalloc_max_vocab(void);
 int mcv_w4a16_lm_head_argmax_noalloc(const void* x_dev, int64_t K, int64_t N, int64_t V,
                                      const void* qw_dev, const void* scales_dev, const void* zeros_dev,

@@ -528,7 +528,7 @@ class LmHeadW4A16:
             raise McvError(f"vocab {vocab} exceeds weight width {w.N}")
         self.w, self.vocab = w, vocab
         dev = w.qweight.device
-        # zero-filled once; the fused calls keep its call counters and tagged keys consistent
+        # zero-filled once; the fused calls keep its generation word and tagged keys consistent
         self.workspace = torch.zeros(lib().mcv_lm_head_workspace_bytes(vocab), dtype=torch.uint8, device=dev)
         self.slots = torch.zeros(lib().mcv_lm_head_slots_bytes() // 8, dtype=torch.int64, device=dev)
         self.tag = 0

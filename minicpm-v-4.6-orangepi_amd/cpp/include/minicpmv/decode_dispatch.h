@@ -34,12 +34,15 @@ bool w8a8_weight_ready(const W8A8QuantizedWeight* w8_weight);
 void matmul_decode_w8a8_prequant(const Tensor& x_int8, const Tensor& x_scale, const W8A8QuantizedWeight& w8_weight,
                                  Tensor& out, hipStream_t stream);
 
-// Device scratch of the W8A8 branch: the quantised row and its fp16 scale.
-// Grown (allocated) only when a call needs more than it holds, so a decode
-// loop allocates on its first call and never again.  One stream at a time.
+// Device scratch of the dispatcher: the W8A8 branch's quantised row and its
+// fp16 scale, and the W4A16 GEMM's K-split workspace (fp32 partial tiles and
+// their arrival counters).  Grown (allocated) only when a call needs more than
+// it holds, so a decode loop allocates on its first call and never again.
+// One stream at a time.
 struct DecodeScratch {
     Tensor x_int8;       // Int8 [capacity]
     Tensor x_scale;      // Float16 [rows capacity]
+    Tensor gemm_ws;      // Int8 [bytes], see matmul_w4a16's workspace overload
     // Makes room for an [M, K] activation (reallocates only on growth).
     void reserve(int64_t M, int64_t K);
 };
@@ -54,7 +57,8 @@ struct DecodeScratch {
 void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W4A16QuantizedWeight* quant_weight,
                             const W8A8QuantizedWeight* w8_weight, Tensor& out, hipStream_t stream,
                             DecodeScratch& scratch);
-// The reference's signature: the scratch is this thread's, one per device.
+// The reference's signature: the scratch is this thread's, one per (device,
+// stream), so dispatches on two streams never share temporaries.
 void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W4A16QuantizedWeight* quant_weight,
                             const W8A8QuantizedWeight* w8_weight, Tensor& out, hipStream_t stream);
 

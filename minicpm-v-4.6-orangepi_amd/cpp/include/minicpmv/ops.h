@@ -33,7 +33,10 @@ void argmax_last_dim(const Tensor& self, Tensor& out, hipStream_t stream);
 void matmul_w4a16(const Tensor& x, const Tensor& w_int8, const Tensor& scales, Tensor& out, hipStream_t stream);
 
 // x fp16 [M, K] . dequant(w) -> out fp16 [M, N], any M (GEMV for small M,
-// LDS-dequant fp16 MFMA GEMM otherwise).
+// LDS-dequant fp16 MFMA GEMM otherwise).  Where the GEMM splits K across
+// workgroups it uses a workspace the library keeps per (device, stream) of
+// the calling thread: allocated on the first call that needs it (or more of
+// it), reused after that.
 void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream);
 
 // The same with a caller-owned workspace (mcv_w4a16_gemm_ws): where the MFMA

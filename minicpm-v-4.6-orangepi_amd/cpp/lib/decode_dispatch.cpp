@@ -6,7 +6,8 @@
 
 #include <cstdlib>
 #include <stdexcept>
-#include <unordered_map>
+#include <map>
+#include <utility>
 
 namespace minicpmv {
 
@@ -87,7 +88,7 @@ void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W
         return;
     }
     if (q4_ready && one_row) {
-        matmul_w4a16(x, *quant_weight, out, stream);
+        matmul_w4a16(x, *quant_weight, out, stream, scratch.gemm_ws);
         return;
     }
     if (dense_weight != nullptr) {
@@ -95,7 +96,7 @@ void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W
         return;
     }
     if (q4_ready && rank2(x)) {
-        matmul_w4a16(x, *quant_weight, out, stream);
+        matmul_w4a16(x, *quant_weight, out, stream, scratch.gemm_ws);
         return;
     }
     if (w8a8_weight_ready(w8_weight) && rank2(x)) {
@@ -107,10 +108,10 @@ void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W
 
 void matmul_decode_dispatch(const Tensor& x, const Tensor* dense_weight, const W4A16QuantizedWeight* quant_weight,
                             const W8A8QuantizedWeight* w8_weight, Tensor& out, hipStream_t stream) {
-    thread_local std::unordered_map<int, DecodeScratch> per_device;
+    thread_local std::map<std::pair<int, hipStream_t>, DecodeScratch> per_stream;
     int dev = 0;
     check_hip(hipGetDevice(&dev), "hipGetDevice");
-    matmul_decode_dispatch(x, dense_weight, quant_weight, w8_weight, out, stream, per_device[dev]);
+    matmul_decode_dispatch(x, dense_weight, quant_weight, w8_weight, out, stream, per_stream[{dev, stream}]);
 }
 
 }  // namespace minicpmv

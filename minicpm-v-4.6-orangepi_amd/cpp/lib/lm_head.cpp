@@ -34,9 +34,10 @@ void check_io(const Tensor& hidden_1xH, const LmHeadW4A16& head, const Tensor* l
         throw std::runtime_error("lm_head logits must be fp16 [1, vocab]");
 }
 
-// A give-up leaves the workgroups' call counters out of step, so the
-// workspace is zero-filled (after the stream drains) before the error is
-// raised; the next call starts consistent.
+// A give-up is reported once: the workspace (whose u32 at byte 0 holds the
+// sticky give-up flag) is zero-filled after the stream drains and the status
+// word cleared before the error is raised, so the next call reports only its
+// own outcome.
 [[noreturn]] void raise_gave_up(LmHeadW4A16& head, hipStream_t stream) {
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
     head.workspace.zero();

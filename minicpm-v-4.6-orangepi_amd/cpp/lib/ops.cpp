@@ -10,6 +10,7 @@
 
 #include <rocblas/rocblas.h>
 
+#include <map>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -20,6 +21,16 @@ namespace {
 
 void require(bool ok, const std::string& msg) {
     if (!ok) throw std::runtime_error(msg);
+}
+
+// The workspace of the 4-argument matmul_w4a16: one per (device, stream) of
+// this thread, grown on demand and kept, so calls on one stream reuse it in
+// stream order and calls on two streams never share one.
+Tensor& implicit_gemm_workspace(hipStream_t stream) {
+    thread_local std::map<std::pair<int, hipStream_t>, Tensor> per_stream;
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    return per_stream[{dev, stream}];
 }
 
 int scale_dtype(const Tensor& t, const char* what) {
@@ -64,13 +75,7 @@ void matmul_w4a16(const Tensor& x, const Tensor& w_int8, const Tensor& scales, T
 }
 
 void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream) {
-    require(x.dtype() == DType::Float16 && out.dtype() == DType::Float16, "matmul_w4a16 x and out must be fp16");
-    require(x.shape().size() == 2 && x.shape()[1] == w.K, "matmul_w4a16 x must be [M, K]");
-    require(out.shape() == std::vector<int64_t>{x.shape()[0], w.N}, "matmul_w4a16 out must be [M, N]");
-    require(w.w_int8.data() && w.scales.data() && w.zeros.data(), "matmul_w4a16 weight is not loaded");
-    check_mcv(mcv_w4a16_gemm(x.data(), x.shape()[0], w.K, w.N, w.w_int8.data(), w.scales.data(), w.zeros.data(),
-                             w.zero_bias, out.data(), stream),
-              "matmul_w4a16");
+    matmul_w4a16(x, w, out, stream, implicit_gemm_workspace(stream));
 }
 
 void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, hipStream_t stream, Tensor& workspace) {

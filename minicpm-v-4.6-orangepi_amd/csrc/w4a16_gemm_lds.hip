@@ -175,8 +175,15 @@ __global__ __launch_bounds__(256) void w4a16_gemm_lds_kernel(
         xoff[j] = static_cast<uint32_t>(row * K + kb * C::BK) * 2u +
                   static_cast<uint32_t>((lane & 15) ^ (row & 15)) * 16u;
     }
-    const uint32_t zoff = (static_cast<uint32_t>(slab) * 32u + lane * 4u) | (lane < 8 ? 0u : 0x80000000u);
-    const uint32_t soff = (static_cast<uint32_t>(slab) * 128u + lane * 4u) | (lane < 32 ? 0u : 0x80000000u);
+    // The buffer range check covers the vector offset only (the group's
+    // stride rides in the scalar offset), so a padding slab past nslab -- the
+    // last tile's when nslab % WN != 0 -- must put its copies out of range by
+    // the vector offset alone, like the idle lanes.
+    const bool slab_live = slab < nslab;
+    const uint32_t zoff =
+        (static_cast<uint32_t>(slab) * 32u + lane * 4u) | (lane < 8 && slab_live ? 0u : 0x80000000u);
+    const uint32_t soff =
+        (static_cast<uint32_t>(slab) * 128u + lane * 4u) | (lane < 32 && slab_live ? 0u : 0x80000000u);
     // Copy `it` (0 .. P-1: x rows, packed chunks, zero words, scales) of
     // stage kt into dst.
     auto issue_item = [&](int kt, uint8_t* dst, int it) {

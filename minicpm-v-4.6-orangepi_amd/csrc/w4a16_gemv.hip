@@ -31,35 +31,40 @@ namespace {
 // goes through to the coherent point; the grid's last workgroup polls all the
 // words with device-scope loads until each carries this call's tag, takes
 // the maximum and writes the token -- one store's visibility plus one poll
-// after the last workgroup.  The tag comes from a per-workgroup call counter:
-// each workgroup reads its own counter once and bumps it, so a call's
-// workgroups agree on the tag without talking to each other, and a graph
-// replay reads the counters afresh.  Workspace (zero-filled once, kept
-// consistent by every call): u32 give-up flag at word 0, u32 call counters at
-// words 64.., then the u64 keys, both sized for one workgroup per slab.
+// after the last workgroup.  The tag comes from the workspace's generation
+// word: every workgroup reads it at its start, and the poller advances it
+// once it has seen every key of the call (so no workgroup of the call can
+// still be about to read it).  The next call is stream-ordered after this
+// kernel and reads the advanced value; a graph replay reads it afresh from
+// device memory.  The key words sit at a fixed offset whatever the grid, so
+// calls over different V may share one workspace (one at a time).
+// Workspace (zero-filled once): u32 give-up flag at word 0, u32 generation
+// at word 1, the u64 keys from byte kLmKeysByte, one per workgroup.
 // Measured on MI355X with the lm_head's workgroups: 3877 atomics on one
 // address serialise to 45 us, a __threadfence per workgroup adds ~30 us,
 // CAS-combined (key, count) words 22-39 us, and the fence-free 64-slot
 // arrival tree this replaces (atomicMax, then slot and global counts, then a
 // read of the slot maxima) ~1.8 us: four device round trips.
 constexpr int kSlotWords = 64;                                // slots of the host-finished route
-constexpr int kLmEpoch = 64;                                  // u32 index of the first call counter
+constexpr int kLmGen = 1;                                     // u32 index of the generation word
+constexpr int kLmKeysByte = 128;                              // byte offset of the key words
 constexpr int kLmPollVec = 8;                                 // key words per lane per poll
 constexpr int kLmSpinLimit = 1 << 18;
 
-__host__ __device__ inline int64_t lm_keys_index(int64_t nslab) { return (kLmEpoch + nslab + 1) / 2; }
+// The call's tag from a generation: 1 .. 2^24 - 1 (a zero-filled key, tag 0,
+// never matches).
+__device__ __forceinline__ unsigned long long lm_tag(unsigned gen) { return (gen % 0xffffffu) + 1u; }
 
 // Run by one full wave of each workgroup after its columns are final; `key`
-// is the workgroup's best argmax_key64 (wave-uniform), `epoch` its call
-// counter as read at the start of the kernel.
+// is the workgroup's best argmax_key64 (wave-uniform), `gen` the generation
+// word as read at the start of the kernel.
 __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ ws, unsigned long long key,
-                                               unsigned epoch, int b, int nblk, int nslab, int lane,
+                                               unsigned gen, int b, int nblk, int lane,
                                                int64_t* __restrict__ token, unsigned* status) {
     unsigned* ws32 = reinterpret_cast<unsigned*>(ws);
-    unsigned long long* keys = ws + lm_keys_index(nslab);
-    const unsigned long long tag = (epoch + 1u) & 0xffffffu;
+    unsigned long long* keys = ws + kLmKeysByte / 8;
+    const unsigned long long tag = lm_tag(gen);
     if (lane == 0) {
-        __hip_atomic_store(ws32 + kLmEpoch + b, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long k16 = key >> 32, idx = key & 0xffffffull;
         __hip_atomic_store(keys + b, (tag << 40) | (k16 << 24) | (k16 ? idx : 0ull), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -93,10 +98,14 @@ __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ 
         }
     }
     best = wave_max_u64(best);
-    // -1: the keys of this call never all arrived, so no token is known
-    if (lane == 0)
+    if (lane == 0) {
+        // -1: the keys of this call never all arrived, so no token is known
         *token = gave_up ? int64_t(-1)
                  : (best >> 24) ? static_cast<int64_t>(0xffffffu - static_cast<uint32_t>(best & 0xffffffu)) : 0;
+        // the next call's tag (also after a give-up: this call's late keys
+        // then carry a tag the next call does not accept)
+        __hip_atomic_store(ws32 + kLmGen, gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ARGMAX modes of the GEMV epilogue (M == 1 only).
@@ -216,13 +225,13 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
     asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
     const int s0 = static_cast<int>(blockIdx.x) * SPW;
-    // this workgroup's call counter (device-token route), issued before the
+    // the call's generation word (device-token route), issued before the
     // weight loads and needed only at the end
-    unsigned epoch = 0;
+    unsigned gen = 0;
     if constexpr (MODE == kLmTree)
         if (wave == 0)
-            epoch = __hip_atomic_load(reinterpret_cast<unsigned*>(ws) + kLmEpoch + blockIdx.x, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
+            gen = __hip_atomic_load(reinterpret_cast<unsigned*>(ws) + kLmGen, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
     const int ns = nslab - s0 < SPW ? nslab - s0 : SPW;                  // workgroup-uniform
     const uint32_t zshift = (lane & 7) * 4;                              // slab bases are multiples of 8 columns
     const uint4* __restrict__ wbase = qw + lane;
@@ -290,8 +299,7 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     if (wave != 0) return;
     best = wave_max_u64(lane < kLmWaves ? wbest[lane] : 0ull);
     if constexpr (MODE == kLmTree) {
-        argmax_publish(ws, best, epoch, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), nslab, lane, token,
-                       status);
+        argmax_publish(ws, best, gen, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token, status);
     } else {
         if (lane == 0) {
             // argmax_key64 -> slot key: the fp16 key moves to bits 39..24, the
@@ -438,24 +446,15 @@ template <int ARGMAX>
 using GemvFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int,
                         int, int, unsigned long long*, int64_t*);
 
-template <int ARGMAX, int KS>
-GemvFn<ARGMAX> pick_gpw(int gpw) {
-    switch (gpw) {
-        case 1: return w4a16_gemv_kernel<KS, 1, ARGMAX>;
-        case 2: return w4a16_gemv_kernel<KS, 2, ARGMAX>;
-        case 4: return w4a16_gemv_kernel<KS, 4, ARGMAX>;
-        default: return w4a16_gemv_kernel<KS, 8, ARGMAX>;
-    }
-}
-
 template <int ARGMAX>
 GemvFn<ARGMAX> pick_kernel(int ks, int gpw) {
+    if (gpw != 1) return nullptr;                 // one group per wave per trip (choose_gemv)
     switch (ks) {
-        case 1: return pick_gpw<ARGMAX, 1>(gpw);
-        case 2: return pick_gpw<ARGMAX, 2>(gpw);
-        case 4: return pick_gpw<ARGMAX, 4>(gpw);
-        case 8: return pick_gpw<ARGMAX, 8>(gpw);
-        default: return pick_gpw<ARGMAX, 16>(gpw);
+        case 1: return w4a16_gemv_kernel<1, 1, ARGMAX>;
+        case 2: return w4a16_gemv_kernel<2, 1, ARGMAX>;
+        case 4: return w4a16_gemv_kernel<4, 1, ARGMAX>;
+        case 8: return w4a16_gemv_kernel<8, 1, ARGMAX>;
+        default: return w4a16_gemv_kernel<16, 1, ARGMAX>;
     }
 }
 
@@ -463,27 +462,6 @@ struct GemvCfg {
     int ksplit;
     int gpw;
 };
-
-int env_int(const char* name, int fallback) {
-    const char* v = std::getenv(name);
-    if (v == nullptr || *v == '\0') return fallback;
-    return std::atoi(v);
-}
-
-// Sweep overrides of the GEMV k-split and the lm_head's slabs per workgroup,
-// read once per process: the tagged-word kernels index per-workgroup call
-// counters by blockIdx, so the grid of one shape must not change while its
-// workspace is in use.
-struct GemvOverrides {
-    int ksplit;
-    int gpw;
-    int lm_spw;
-};
-const GemvOverrides& gemv_overrides() {
-    static const GemvOverrides o{env_int("MCV_GEMV_KSPLIT", 0), env_int("MCV_GEMV_GPW", 0),
-                                 env_int("MCV_LMHEAD_SPW", 0)};
-    return o;
-}
 
 // One quantisation group (four 16-byte loads per lane) per wave per trip,
 // and enough waves per workgroup (up to 16, at most one per group) that the
@@ -493,16 +471,11 @@ const GemvOverrides& gemv_overrides() {
 // heavy, so more loads in flight per wave do not pay.  On the decoder's
 // narrow projections the grid is tiny and the serial trips per wave set the
 // time: K=3584 N=1024 8 x 1 6.45 us, 16 x 1 5.39 us; K=2048 N=1024 4.56 us
-// vs 4.07 us.  MCV_GEMV_KSPLIT / MCV_GEMV_GPW override the choice.
+// vs 4.07 us.
 GemvCfg choose_gemv(int64_t G, int64_t blocks) {
     int ks = 1;
     while (ks < 16 && blocks * ks < 8192 && ks * 2 <= G) ks *= 2;
-    const int gpw = 1;
-    const GemvOverrides& o = gemv_overrides();
-    GemvCfg c{o.ksplit ? o.ksplit : ks, o.gpw ? o.gpw : gpw};
-    if (c.ksplit != 1 && c.ksplit != 2 && c.ksplit != 4 && c.ksplit != 8 && c.ksplit != 16) c.ksplit = ks;
-    if (c.gpw != 1 && c.gpw != 2 && c.gpw != 4 && c.gpw != 8) c.gpw = gpw;
-    return c;
+    return GemvCfg{ks, 1};
 }
 
 bool w4_args_ok(const void* qw, const void* scales, const void* zeros, int zero_bias, int64_t K, int64_t N,
@@ -688,17 +661,8 @@ __global__ __launch_bounds__(64 * kTiWaves) void w4a16_tiled_i8_kernel(const uin
 // passes the array's name to a kernel (on the host it is only a stand-in):
 // it uses the device address hipGetSymbolAddress returns for the current GPU.
 constexpr int64_t kNoallocMaxV = int64_t(1) << 20;
-constexpr int64_t kNoallocWords = (kLmEpoch + (kNoallocMaxV + kSlab - 1) / kSlab + 1) / 2 +
-                                  (kNoallocMaxV + kSlab - 1) / kSlab;   // u64 words for V = kNoallocMaxV
+constexpr int64_t kNoallocWords = kLmKeysByte / 8 + (kNoallocMaxV + kSlab - 1) / kSlab;   // u64 words for V = kNoallocMaxV
 static __device__ __align__(256) unsigned long long scratch[kNoallocWords];
-
-// Zero-fills n u64 words (a kernel, not hipMemsetAsync, so a caller may
-// capture it in a graph).
-__global__ __launch_bounds__(256) void zero_words_kernel(unsigned long long* __restrict__ p, int64_t n) {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-        p[i] = 0ull;
-}
 
 }  // namespace
 
@@ -735,11 +699,8 @@ int launch_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void
 // double-buffered runs of slabs pay while the grid still covers the CUs,
 // and at a few slabs per workgroup more workgroups hide more latency.  A
 // function of V alone, so a workspace (sized for one workgroup per slab)
-// always meets the same grid.  MCV_LMHEAD_SPW (1, 2, 4, 8, 16) overrides it
-// for sweeps.
+// always meets the same grid.
 int lm_head_spw(int64_t nslab) {
-    const int o = gemv_overrides().lm_spw;
-    if (o == 1 || o == 2 || o == 4 || o == 8 || o == 16) return o;
     int spw = 16;
     while (spw > 1 && ceil_div(nslab, spw) < 240) spw /= 2;
     if (spw == 2 && nslab <= 512) spw = 1;
@@ -775,16 +736,13 @@ int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* q
 namespace {
 
 // Per-GPU state of the no-allocation route: the scratch array's device
-// address on that GPU and the vocabulary size of its last call (the
-// per-workgroup call counters and key words are laid out for one grid, so a
-// call with another V first zero-fills the array).  Fixed-size, so looking a
-// device up allocates nothing.
+// address on that GPU (fixed-size, so looking a device up allocates nothing).
+// The array needs no host-side bookkeeping beyond that: it starts zero-filled
+// with the code object, and its generation word and fixed-offset key words
+// stay consistent from call to call, for any V, in eager calls and graph
+// replays alike.
 constexpr int kNoallocMaxDevices = 64;
-struct NoallocSlot {
-    unsigned long long* ptr;
-    int64_t last_v;
-};
-NoallocSlot g_noalloc[kNoallocMaxDevices];
+unsigned long long* g_noalloc[kNoallocMaxDevices];
 std::mutex g_noalloc_mu;
 
 }  // namespace
@@ -802,8 +760,8 @@ int mcv_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t N, const void* q
 
 int64_t mcv_lm_head_workspace_bytes(int64_t V) {
     if (V <= 0 || V >= (int64_t(1) << 24)) return 0;
-    const int64_t nslab = ceil_div(V, kSlab);
-    return (lm_keys_index(nslab) + nslab) * 8;
+    // one key word per slab: room for the grid of this V and of every smaller one
+    return kLmKeysByte + ceil_div(V, kSlab) * 8;
 }
 
 int64_t mcv_lm_head_slabs_per_workgroup(int64_t V) {
@@ -881,26 +839,20 @@ int mcv_w4a16_lm_head_argmax_noalloc(const void* x, int64_t K, int64_t N, int64_
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoallocMaxDevices)
         return fail(MCV_ERR_HIP, "%s: no usable current device (%d)", who, dev);
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    std::lock_guard<std::mutex> lock(g_noalloc_mu);
-    NoallocSlot& slot = g_noalloc[dev];
-    if (slot.ptr == nullptr) {
-        // once per GPU, with that GPU current: the array's address on it
-        void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || p == nullptr)
-            return fail(MCV_ERR_HIP, "%s: hipGetSymbolAddress failed (%s)", who, hipGetErrorString(e));
-        slot.ptr = static_cast<unsigned long long*>(p);
-        slot.last_v = 0;
+    unsigned long long* ptr = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        if (g_noalloc[dev] == nullptr) {
+            // once per GPU, with that GPU current: the array's address on it
+            void* p = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || p == nullptr)
+                return fail(MCV_ERR_HIP, "%s: hipGetSymbolAddress failed (%s)", who, hipGetErrorString(e));
+            g_noalloc[dev] = static_cast<unsigned long long*>(p);
+        }
+        ptr = g_noalloc[dev];
     }
-    if (slot.last_v != V) {
-        // first call on this GPU, or a new grid: every counter and key word from zero
-        const int64_t words = mcv_lm_head_workspace_bytes(V) / 8;
-        hipLaunchKernelGGL(zero_words_kernel, dim3(static_cast<unsigned>(ceil_div(words, 256) < 64 ? ceil_div(words, 256) : 64)),
-                           dim3(256), 0, st, slot.ptr, words);
-        if ((rc = check_launch("zero_words_kernel")) != MCV_OK) return rc;
-        slot.last_v = V;
-    }
-    return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, token, slot.ptr, 0u, kLmTree,
+    return launch_lm_head(x, K, N, V, qw, scales, zeros, zero_bias, logits, token, ptr, 0u, kLmTree,
                           static_cast<unsigned*>(status), st);
 }
 

@@ -329,8 +329,9 @@ def test_w4a16_gemm_workspace_query(mcv):
 def test_lm_head_grid_choice(mcv):
     """Slabs per workgroup by vocabulary: 16 on the full vocabulary (243
     workgroups), fewer on a GPU's share of a column split, one slab per
-    workgroup once that grid fits two workgroups per CU; the workspace always
-    covers one workgroup per slab."""
+    workgroup once that grid fits two workgroups per CU; the workspace holds
+    a 128-byte header and one key word per slab, so a workspace serves every
+    V up to the one it was sized for."""
     L = mcv.lib()
     spw = L.mcv_lm_head_slabs_per_workgroup
     cases = {248094: 16, 124047: 8, 100000: 4, 62024: 4, 40000: 2, 31012: 1, 8320: 1, 4097: 1, 1: 1}
@@ -339,7 +340,8 @@ def test_lm_head_grid_choice(mcv):
         assert mcv.lm_head_slabs_per_workgroup(V) == want
         nslab = -(-V // 64)
         assert -(-nslab // want) >= min(nslab, 240) or want == 1
-        assert L.mcv_lm_head_workspace_bytes(V) >= nslab * 8
+        assert L.mcv_lm_head_workspace_bytes(V) == 128 + 8 * nslab
+        assert L.mcv_lm_head_workspace_bytes(V) <= L.mcv_lm_head_workspace_bytes(248094)
     assert spw(0) == 0 and spw(1 << 24) == 0
 
 

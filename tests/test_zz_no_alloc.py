@@ -69,3 +69,41 @@ def test_noalloc_lm_head_matches_workspace_route(mcv, cuda):
     rc = L.mcv_w4a16_lm_head_argmax_noalloc(fake, 128, (1 << 20) + 64, (1 << 20) + 1, fake, fake, fake, 0, None,
                                             fake, None, None)
     assert rc == 2 and b"scratch" in L.mcv_last_error()
+
+
+def test_noalloc_lm_head_graph_replays_interleaved(mcv, cuda):
+    """A captured noalloc call replays correctly between eager noalloc calls at
+    another V: the array's generation word and fixed-offset keys live in
+    device memory, so no host-side decision is baked into the graph."""
+    import torch
+    rng = np.random.default_rng(77)
+    L = mcv.lib()
+    big, small = (1024, 40000, 39999), (256, 4096, 3001)
+    cases = {shape: _case(mcv, rng, shape[0], shape[1]) for shape in (big, small)}
+    want = {shape: _workspace_route(mcv, *cases[shape], shape[2]) for shape in (big, small)}
+    wq, x = cases[big]
+    V = big[2]
+    q, s, z = wq.ptrs()
+    tok = torch.full((1,), -7, dtype=torch.int64, device="cuda")
+    lg = torch.empty(V, dtype=torch.float16, device="cuda")
+    _noalloc_route(mcv, wq, x, V)                       # an eager call before the capture
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            rc = L.mcv_w4a16_lm_head_argmax_noalloc(x.data_ptr(), wq.K, wq.N, V, q, s, z, wq.zero_bias,
+                                                    lg.data_ptr(), tok.data_ptr(), None, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert rc == 0, L.mcv_last_error()
+    for rep in range(4):
+        got_small = _noalloc_route(mcv, *cases[small], small[2])      # eager, another V
+        assert got_small[0] == want[small][0], (rep, got_small[0], want[small][0])
+        tok.fill_(-7)
+        lg.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want[big][0], (rep, int(tok.item()), want[big][0])
+        assert torch.equal(lg.cpu().view(torch.int16), want[big][1].view(torch.int16)), rep
