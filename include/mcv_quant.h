@@ -289,6 +289,11 @@ int mcv_w4a16_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V,
  * wait that gives up shows as token -1 and *status (when not NULL); the next
  * call needs no reset. */
 int64_t mcv_lm_head_noalloc_max_vocab(void);
+/* Test hook, no use in production: while on, the device-token lm_head's
+ * poller (mcv_w4a16_lm_head_argmax and _noalloc) expects a tag no key carries,
+ * so its bounded wait gives up (token -1, give-up word and *status set) and
+ * the kernel still ends normally.  Process-wide; off by default. */
+void mcv_testing_lm_head_skew_poll(int on);
 int mcv_w4a16_lm_head_argmax_noalloc(const void* x_dev, int64_t K, int64_t N, int64_t V,
                                      const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                                      int zero_bias, void* logits_dev, int64_t* token_dev,

@@ -75,6 +75,7 @@ _SIGS = {
     "mcv_w4a16_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp,
                                           _vp]),
     "mcv_lm_head_noalloc_max_vocab": (_c_i64, []),
+    "mcv_testing_lm_head_skew_poll": (None, [_c_int]),
     "mcv_w4a16_lm_head_argmax_noalloc": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _vp,
                                                   _vp]),
     "mcv_lm_head_slots_bytes": (_c_i64, []),

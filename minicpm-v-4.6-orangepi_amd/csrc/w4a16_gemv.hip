@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -57,13 +58,16 @@ __device__ __forceinline__ unsigned long long lm_tag(unsigned gen) { return (gen
 
 // Run by one full wave of each workgroup after its columns are final; `key`
 // is the workgroup's best argmax_key64 (wave-uniform), `gen` the generation
-// word as read at the start of the kernel.
+// word as read at the start of the kernel.  `skew` is 0 except under
+// mcv_testing_lm_head_skew_poll, where the poller expects a tag no key
+// carries, so its bounded wait gives up (the give-up path's test).
 __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ ws, unsigned long long key,
-                                               unsigned gen, int b, int nblk, int lane,
+                                               unsigned gen, unsigned skew, int b, int nblk, int lane,
                                                int64_t* __restrict__ token, unsigned* status) {
     unsigned* ws32 = reinterpret_cast<unsigned*>(ws);
     unsigned long long* keys = ws + kLmKeysByte / 8;
     const unsigned long long tag = lm_tag(gen);
+    const unsigned long long want = (tag + skew) & 0xffffffull;
     if (lane == 0) {
         const unsigned long long k16 = key >> 32, idx = key & 0xffffffull;
         __hip_atomic_store(keys + b, (tag << 40) | (k16 << 24) | (k16 ? idx : 0ull), __ATOMIC_RELAXED,
@@ -82,7 +86,7 @@ __device__ __forceinline__ void argmax_publish(unsigned long long* __restrict__ 
             }
             unsigned long long bad = 0;
 #pragma unroll
-            for (int i = 0; i < kLmPollVec; ++i) bad |= (v[i] >> 40) ^ tag;
+            for (int i = 0; i < kLmPollVec; ++i) bad |= (v[i] >> 40) ^ want;
             if (__all(bad == 0)) break;
             if (spins > kLmSpinLimit) {
                 if (lane == 0) flag_gave_up(ws32, status);
@@ -299,7 +303,8 @@ __global__ __launch_bounds__(64 * kLmWaves) void w4a16_lm_head_kernel(
     if (wave != 0) return;
     best = wave_max_u64(lane < kLmWaves ? wbest[lane] : 0ull);
     if constexpr (MODE == kLmTree) {
-        argmax_publish(ws, best, gen, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token, status);
+        argmax_publish(ws, best, gen, tag, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token,
+                       status);
     } else {
         if (lane == 0) {
             // argmax_key64 -> slot key: the fp16 key moves to bits 39..24, the
@@ -707,7 +712,12 @@ int lm_head_spw(int64_t nslab) {
     return spw;
 }
 
-// Shared launcher of both argmax routes.
+// Test hook (mcv_testing_lm_head_skew_poll): the device-token route's poller
+// expects a tag no key carries.
+std::atomic<unsigned> g_lm_poll_skew{0};
+
+// Shared launcher of both argmax routes (`tag`: the slots route's call tag;
+// the device-token route passes the poll skew in its place).
 int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* qw, const void* scales,
                    const void* zeros, int zero_bias, void* logits, int64_t* token, void* ws, uint32_t tag, int mode,
                    unsigned* status, hipStream_t stream) {
@@ -728,7 +738,8 @@ int launch_lm_head(const void* x, int64_t K, int64_t N, int64_t V, const void* q
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
                        static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(logits), static_cast<int>(K),
                        static_cast<int>(V), static_cast<int>(npad), static_cast<int>(nslab),
-                       static_cast<unsigned long long*>(ws), token, tag, status);
+                       static_cast<unsigned long long*>(ws), token,
+                       mode == kLmTree ? g_lm_poll_skew.load(std::memory_order_relaxed) : tag, status);
     return check_launch("w4a16_lm_head_kernel");
 }
 
@@ -822,6 +833,8 @@ int mcv_w4a16_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, con
 }
 
 int64_t mcv_lm_head_noalloc_max_vocab(void) { return kNoallocMaxV; }
+
+void mcv_testing_lm_head_skew_poll(int on) { g_lm_poll_skew.store(on ? 1u : 0u, std::memory_order_relaxed); }
 
 int mcv_w4a16_lm_head_argmax_noalloc(const void* x, int64_t K, int64_t N, int64_t V, const void* qw,
                                      const void* scales, const void* zeros, int zero_bias, void* logits,

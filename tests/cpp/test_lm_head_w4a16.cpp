@@ -5,9 +5,10 @@
 // the first index, the workspace is reusable, the W8A8 variant's logits are
 // bit-exact against the oracle's composition of the reference's steps
 // (language_model.cpp:434-467: fp16 x_scale, truncated fp16 w_scale), and a
-// give-up of the device-token route's bounded wait -- forced from the host by
-// putting one workgroup's call counter out of step -- yields token -1, the
-// status word and a thrown error, after which the head works again.
+// give-up of the device-token route's bounded wait -- forced from the host
+// through the library's test hook, which has the poller expect a tag no key
+// carries -- yields token -1, the status word and a thrown error, after which
+// the head works again.
 #include "mcv_oracle.h"
 #include "mcv_quant.h"
 #include "minicpmv/hip_context.h"
@@ -138,21 +139,19 @@ int main() {
         if (t8kn != t8 || got_kn != got) rc = 1;
     }
 
-    // Give-up of the device-token route: workgroup 0's call counter (u32 word
-    // 64 of the workspace) five ahead of the others, so its key never carries
-    // the tag the last workgroup polls for.  The kernel still ends (bounded
-    // wait), writes token -1 and sets the status word; the next call throws
-    // and resets the workspace, after which the head works again.
+    // Give-up of the device-token route: the poller expects a tag no key
+    // carries.  The kernel still ends (bounded wait), writes token -1 and sets
+    // the status word; the next call throws and resets the workspace, after
+    // which the head works again.
     {
         lm_head_argmax_w4a16(x2, head, nullptr, ctx.stream());
         const int64_t before = lm_head_read_token(head, ctx.stream());
-        uint32_t counters[2] = {0, 0};
-        check_hip(hipMemcpy(counters, static_cast<uint8_t*>(head.workspace.data()) + 64 * 4, 8, hipMemcpyDeviceToHost),
-                  "hipMemcpy");
-        const uint32_t ahead = counters[0] + 5;
-        check_hip(hipMemcpy(static_cast<uint8_t*>(head.workspace.data()) + 64 * 4, &ahead, 4, hipMemcpyHostToDevice),
-                  "hipMemcpy");
+        uint32_t gen[2] = {0, 0};
+        check_hip(hipMemcpy(gen, head.workspace.data(), 8, hipMemcpyDeviceToHost), "hipMemcpy");
+        mcv_testing_lm_head_skew_poll(1);
         lm_head_argmax_w4a16(x2, head, nullptr, ctx.stream());
+        check_hip(hipStreamSynchronize(ctx.stream()), "hipStreamSynchronize");
+        mcv_testing_lm_head_skew_poll(0);
         int64_t sentinel = 0;
         check_hip(hipMemcpy(&sentinel, head.token.data(), 8, hipMemcpyDeviceToHost), "hipMemcpy");
         uint32_t ws_flag = 0;
@@ -166,9 +165,8 @@ int main() {
         }
         lm_head_argmax_w4a16(x2, head, nullptr, ctx.stream());      // the workspace was reset: works again
         const int64_t after = lm_head_read_token(head, ctx.stream());
-        std::printf("give-up: counters %u %u, token %lld, workspace flag %u, status %d, threw %d, recovered %d\n",
-                    counters[0], counters[1], (long long)sentinel, ws_flag, int(status), int(threw),
-                    int(after == before));
+        std::printf("give-up: generation %u, token %lld, workspace flag %u, status %d, threw %d, recovered %d\n",
+                    gen[1], (long long)sentinel, ws_flag, int(status), int(threw), int(after == before));
         if (sentinel != -1 || ws_flag == 0 || !status || !threw || after != before || before != 777) rc = 1;
     }
     return rc;
