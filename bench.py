@@ -429,7 +429,10 @@ class Prefill(Cfg):
 
     def gpu(self):
         pkg, ws, xd, out = self.pkg, self.ws, self.xd, self.out
-        return gpu_result(self.name, "w4a16_gemm_kernel", self.flops, "TFLOP/s", "mfma",
+        # the kernel the dispatch launches for this shape (with the workspace
+        # the Python mirror passes), as the library names it
+        kernel = pkg.lib().mcv_w4a16_gemm_kernel_name(self.M, self.K, self.N, 1).decode()
+        return gpu_result(self.name, kernel, self.flops, "TFLOP/s", "mfma",
                           lambda i: pkg.matmul_w4a16(xd, ws[i], out), len(ws), 200,
                           {"config": {"M": self.M, "K": self.K, "N": self.N, "weight_sets_rotated": len(ws),
                                       "flops": self.flops,
@@ -477,10 +480,11 @@ class W8a8(Cfg):
     def gpu(self):
         pkg, ws, xq, xs, out = self.pkg, self.ws, self.xq, self.xs, self.out
         M = self.M
+        kernel = pkg.lib().mcv_w8a8_gemm_kernel_name(M, self.K, self.N, ws[0].layout, 1).decode()
         if M <= 4:
-            kernel, amount, unit, bound = "w8a8_tiled_gemv_kernel (v_dot4, fused fp16 epilogue)", self.bytes, "GB/s", "hbm"
+            amount, unit, bound = self.bytes, "GB/s", "hbm"
         else:
-            kernel, amount, unit, bound = "w8a8_tiled_gemm_kernel (int8 MFMA, fused fp16 epilogue)", self.flops, "TOP/s", "mfma"
+            amount, unit, bound = self.flops, "TOP/s", "mfma"
         r = gpu_result(self.name, kernel, amount, unit, bound, lambda i: pkg.matmul_w8a8(xq, xs, ws[i], out), len(ws),
                        200, {"config": {"M": M, "K": self.K, "N": self.N, "weight_sets_rotated": len(ws),
                                         "scales": "fp32 per-token and per-channel", "flops": self.flops,

@@ -123,6 +123,16 @@ int mcv_w4a16_pack_gptq(const int32_t* qweight_host, const int32_t* qzeros_host,
 int mcv_w4a16_quantize_host(const uint16_t* w_kn_host, int64_t K, int64_t N, int32_t* qweight_host,
                             int32_t* qzeros_host, uint16_t* scales_host, int nthreads);
 
+/* The same quantiser fed from an [N_src][K] (out, in) fp16 or bf16 tensor --
+ * the tied embedding [vocab, hidden] that the lm_head reuses as its
+ * projection -- with the output padded to N columns (N % 8 == 0, N >= N_src):
+ * columns from N_src on are zero weights (q = z = 0).  Outputs as above,
+ * [K][N/8] / [K/128][N/8] / [K/128][N].  Bit-identical to
+ * mcv_w4a16_quantize_host on the transposed, zero-padded [K][N] (bf16 source
+ * values converted as mcv_w8a8_quantize_weight_nk_host converts them). */
+int mcv_w4a16_quantize_nk_host(const uint16_t* w_nk_host, int src_dtype, int64_t K, int64_t N_src, int64_t N,
+                               int32_t* qweight_host, int32_t* qzeros_host, uint16_t* scales_host, int nthreads);
+
 /* Inverse of the packers, for round trips and inspection: writes the nibble q
  * ([K][N] uint8, may be NULL), the effective zero z + zero_bias ([K/128][N]
  * uint8, may be NULL) and the unpadded scales ([K/128][N] fp16, may be NULL). */
@@ -135,21 +145,24 @@ int mcv_w4a16_unpack_host(const void* qw_host, const uint16_t* scales_host,
  * Replaces matmul_w4a16 / aclnnMatmulW4a16Custom (src/csrc/lib/ops.cpp:1030-1095,
  * kernel src/csrc/custom_ops/op_kernel/matmul_w4a16_custom.cpp:157-168), which
  * accepts M = 1 only; any M >= 1 is accepted here.  Small M runs the streaming
- * GEMV kernel, larger M the LDS-dequant + fp16 MFMA GEMM kernel. */
+ * GEMV kernel, larger M the LDS-dequant fp16 MFMA GEMM, unsplit (without a
+ * workspace it never splits K; mcv_w4a16_gemm_ws may). */
 int mcv_w4a16_gemm(const void* x_dev, int64_t M, int64_t K, int64_t N,
                    const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                    int zero_bias, void* out_dev, mcv_stream_t stream);
 
 /* mcv_w4a16_gemm with a caller-owned device workspace (no counterpart in the
  * reference, whose matmul_w4a16 is M = 1 only): where the MFMA tile grid is
- * small (few rows, long K) the GEMM splits K across workgroups, writes fp32
- * partial tiles into the workspace and a second launch adds them in a fixed
- * order and rounds to fp16 (deterministic; the sum order differs from the
- * unsplit kernel's, within the same fp32 accumulation tolerance).  The
- * workspace must be 16-byte aligned and hold mcv_w4a16_gemm_workspace_bytes
- * (M, K, N) bytes, else the call runs unsplit; it is fully written before it
- * is read, so it needs no clearing.  Calls that share a workspace must be
- * ordered (one stream). */
+ * small (few rows, long K) the GEMM splits K across workgroups inside the
+ * same launch -- each writes an fp32 partial tile, the last of a tile adds
+ * them in split order and rounds to fp16 (deterministic; the sum order
+ * differs from the unsplit kernel's, within the same fp32 accumulation
+ * tolerance).  The workspace must be 256-byte aligned, hold
+ * mcv_w4a16_gemm_workspace_bytes(M, K, N) bytes (else the call runs
+ * unsplit) and be zero-filled once before its first use: its first 4 KiB hold
+ * the tiles' arrival counters, which every call leaves zero, so one workspace
+ * serves calls of every shape.  Calls that share a workspace must be ordered
+ * (one stream). */
 int mcv_w4a16_gemm_ws(const void* x_dev, int64_t M, int64_t K, int64_t N,
                       const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                       int zero_bias, void* out_dev, void* workspace_dev, int64_t workspace_bytes,
@@ -158,6 +171,30 @@ int mcv_w4a16_gemm_ws(const void* x_dev, int64_t M, int64_t K, int64_t N,
 /* Workspace bytes mcv_w4a16_gemm_ws uses for this shape (0: it does not split
  * K, and any workspace, NULL included, is ignored). */
 int64_t mcv_w4a16_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
+
+/* The kernel (and configuration) mcv_w4a16_gemm (with_workspace = 0) or
+ * mcv_w4a16_gemm_ws (1) launches for M x K x N, as text, for labels in
+ * reports; valid until the next call on this thread.  No reference
+ * counterpart. */
+const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with_workspace);
+
+/* The half-slab GEMM with an explicit configuration (what mcv_w4a16_gemm_ws
+ * picks by shape; exposed so every configuration can be tested and timed):
+ * tile tm x 32 * waves (tm in {32, 64, 128}, waves in {4, 8}), `stages`
+ * copy stages in flight, K split `splits` ways across workgroups (splits
+ * divides K / 128), the partial tiles added inside the same launch by the
+ * last workgroup of each tile, in split order (deterministic).  Splits > 1
+ * need a 256-byte aligned workspace of mcv_w4a16_gemm_sk_workspace_bytes
+ * bytes, zero-filled once before its first use: its first 4 KiB hold the
+ * tile arrival counters (at most 1024 tiles per split call), which every
+ * call leaves zero, so one workspace serves calls of every shape.
+ * MCV_ERR_INVALID_ARG for a configuration that is not built.
+ * No reference counterpart (the reference has no quantised M > 1 path). */
+int64_t mcv_w4a16_gemm_sk_workspace_bytes(int64_t M, int64_t N, int tm, int waves, int splits);
+int mcv_w4a16_gemm_sk(const void* x_dev, int64_t M, int64_t K, int64_t N,
+                      const void* qw_dev, const void* scales_dev, const void* zeros_dev,
+                      int zero_bias, void* out_dev, int tm, int waves, int stages, int splits,
+                      void* workspace_dev, int64_t workspace_bytes, mcv_stream_t stream);
 
 /* The two kernels behind mcv_w4a16_gemm, callable directly (same contract). */
 int mcv_w4a16_gemv(const void* x_dev, int64_t M, int64_t K, int64_t N,
@@ -457,11 +494,24 @@ enum mcv_src_dtype {
 int mcv_w8a8_quantize_weight_nk_host(const uint16_t* w_nk_host, int src_dtype, int64_t K, int64_t N,
                                      int8_t* q_host, int out_layout, float* scale_f32_host,
                                      uint16_t* scale_f16_host);
+/* The same from [N_src][K] rows into N >= N_src output channels, channels
+ * from N_src on zero (scale 1e-8, q = 0): the tied embedding [vocab, hidden]
+ * quantised as the reference quantises its zero-padded lm_head chunks
+ * (src/csrc/lib/language_model.cpp:238-270). */
+int mcv_w8a8_quantize_weight_nk_pad_host(const uint16_t* w_nk_host, int src_dtype, int64_t K, int64_t N_src,
+                                         int64_t N, int8_t* q_host, int out_layout, float* scale_f32_host,
+                                         uint16_t* scale_f16_host);
 
 /* Re-lays a pre-quantised int8 [N][K] checkpoint tensor (safetensors I8, no
  * counterpart in the reference, whose loader has no I8 dtype,
  * src/csrc/lib/weights.cpp:15-23) into MCV_W8_TILED on the host. */
 int mcv_w8a8_pack_tiled_nk_host(const int8_t* q_nk_host, int64_t K, int64_t N, int8_t* tiled_host);
+
+/* The kernel the W8A8 GEMM entry points launch for M x K x N with a weight in
+ * `w_layout` (fp16 output through the fused epilogue when out_f16, else
+ * int32), as text, for labels in reports; valid until the next call on this
+ * thread.  No reference counterpart. */
+const char* mcv_w8a8_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int w_layout, int out_f16);
 
 /* ------------------------------------------------------------ elementwise -- */
 /* out = fp16 RNE(silu(g) * u) in fp32, n elements.  Replaces silu_mul

@@ -56,10 +56,16 @@ _SIGS = {
     "mcv_w4a16_pack_awq": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mcv_w4a16_pack_gptq": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mcv_w4a16_quantize_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int]),
+    "mcv_w4a16_quantize_nk_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int]),
     "mcv_w4a16_unpack_host": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mcv_w4a16_gemm": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_gemm_ws": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64, _vp]),
     "mcv_w4a16_gemm_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "mcv_w4a16_gemm_kernel_name": (ctypes.c_char_p, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "mcv_w8a8_gemm_kernel_name": (ctypes.c_char_p, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "mcv_w4a16_gemm_sk_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_int, _c_int, _c_int]),
+    "mcv_w4a16_gemm_sk": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int,
+                                   _c_int, _vp, _c_i64, _vp]),
     "mcv_w4a16_gemv": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_gemm_mfma": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
@@ -98,6 +104,7 @@ _SIGS = {
     "mcv_w8a8_mlp_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
     "mcv_w8a8_mlp": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]),
     "mcv_w8a8_quantize_weight_nk_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
+    "mcv_w8a8_quantize_weight_nk_pad_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_pack_tiled_nk_host": (_c_int, [_vp, _c_i64, _c_i64, _vp]),
     "mcv_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
     "mcv_argmax_f16": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp]),
@@ -199,6 +206,20 @@ def quantize_int4(w_kn_f16: np.ndarray, nthreads: int = 0):
     return qweight, qzeros, scales
 
 
+def quantize_int4_embedding(emb_vk: np.ndarray, N: int, src_dtype: int = 0, nthreads: int = 0):
+    """The synthetic int4 quantiser over a tied embedding [V, H] (fp16 or bf16
+    bits) as the lm_head's [H, N] projection, columns from V on zero ->
+    AutoAWQ (qweight, qzeros, scales u16)."""
+    w = np.ascontiguousarray(emb_vk).view(np.uint16)
+    V, K = w.shape
+    qweight = np.empty((K, N // 8), np.int32)
+    qzeros = np.empty((K // GROUP, N // 8), np.int32)
+    scales = np.empty((K // GROUP, N), np.uint16)
+    _check(lib().mcv_w4a16_quantize_nk_host(_np_ptr(w), src_dtype, K, V, N, _np_ptr(qweight), _np_ptr(qzeros),
+                                            _np_ptr(scales), nthreads), "mcv_w4a16_quantize_nk_host")
+    return qweight, qzeros, scales
+
+
 def w8a8_tiled_bytes(K: int, N: int) -> int:
     return lib().mcv_w8a8_tiled_bytes(K, N)
 
@@ -250,6 +271,23 @@ def quantize_w8a8_weight_nk_host(w_nk: np.ndarray, src_dtype: int = SRC_F16, lay
     s16 = np.empty(N, np.uint16)
     _check(lib().mcv_w8a8_quantize_weight_nk_host(_np_ptr(w), src_dtype, K, N, _np_ptr(q), layout, _np_ptr(s32),
                                                   _np_ptr(s16)), "mcv_w8a8_quantize_weight_nk_host")
+    return q, s32, s16
+
+
+def quantize_w8a8_embedding(emb_vk: np.ndarray, N: int, src_dtype: int = SRC_F16, layout: int = W8_TILED):
+    """The per-channel quantiser over a tied embedding [V, H] as the lm_head's
+    [H, N] projection, channels from V on zero (the reference's zero-padded
+    chunks, language_model.cpp:238-270) -> (q, s32, s16)."""
+    w = np.ascontiguousarray(emb_vk).view(np.uint16)
+    V, K = w.shape
+    if layout == W8_TILED:
+        q = np.empty(w8a8_tiled_bytes(K, N), np.int8)
+    else:
+        q = np.empty((K, N) if layout == W8_KN else (N, K), np.int8)
+    s32 = np.empty(N, np.float32)
+    s16 = np.empty(N, np.uint16)
+    _check(lib().mcv_w8a8_quantize_weight_nk_pad_host(_np_ptr(w), src_dtype, K, V, N, _np_ptr(q), layout,
+                                                      _np_ptr(s32), _np_ptr(s16)), "mcv_w8a8_quantize_weight_nk_pad_host")
     return q, s32, s16
 
 
@@ -339,11 +377,29 @@ def _w4_call(fn_name: str, x, w: W4A16QuantizedWeight, out, stream):
     return out
 
 
+_GEMM_WS: dict = {}
+
+
+def gemm_workspace(nbytes: int, device, stream=None):
+    """The K-split workspace of the W4A16 GEMM for calls on one stream: kept
+    per (device, stream), zero-filled when (re)allocated -- its tile counters
+    must start at zero, and every call leaves them zero -- and grown only when
+    a shape needs more, so steady-state calls allocate nothing.  Calls on one
+    stream are ordered, so they may share it; two streams never do."""
+    torch = _torch()
+    dev = torch.device(device)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(stream))
+    ws = _GEMM_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _GEMM_WS[key] = ws
+    return ws
+
+
 def matmul_w4a16(x, w: W4A16QuantizedWeight, out=None, stream=None):
     """out[M, N] = x[M, K] . dequant(w), any M (ops.h:104-108 generalised).
-    Where the MFMA path splits K across workgroups (few rows, long K) the fp32
-    partial tiles go to a workspace taken from torch's caching allocator on
-    the current stream, so steady-state calls allocate no device memory."""
+    Where the MFMA GEMM splits K across workgroups (few rows, long K) it takes
+    the per-stream workspace of gemm_workspace()."""
     torch = _torch()
     if x.dtype != torch.float16 or x.dim() != 2 or x.shape[1] != w.K or not x.is_contiguous():
         raise McvError(f"matmul_w4a16: x must be contiguous fp16 [M, {w.K}]")
@@ -355,12 +411,10 @@ def matmul_w4a16(x, w: W4A16QuantizedWeight, out=None, stream=None):
         out = torch.empty((M, w.N), dtype=torch.float16, device=x.device)
     if out.dtype != torch.float16 or tuple(out.shape) != (M, w.N) or not out.is_contiguous():
         raise McvError(f"matmul_w4a16: out must be contiguous fp16 [{M}, {w.N}]")
-    ws = torch.empty(nb, dtype=torch.uint8, device=x.device)
-    if stream is not None:
-        ws.record_stream(stream)                 # not reused until work on `stream` is done
+    ws = gemm_workspace(nb, x.device, stream)
     q, s, z = w.ptrs()
-    _check(lib().mcv_w4a16_gemm_ws(_dev(x), M, w.K, w.N, q, s, z, w.zero_bias, _dev(out), _dev(ws), nb, _stream(stream)),
-           "matmul_w4a16")
+    _check(lib().mcv_w4a16_gemm_ws(_dev(x), M, w.K, w.N, q, s, z, w.zero_bias, _dev(out), _dev(ws), ws.numel(),
+                                   _stream(stream)), "matmul_w4a16")
     return out
 
 

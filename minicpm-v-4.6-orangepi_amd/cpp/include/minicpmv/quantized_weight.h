@@ -67,4 +67,20 @@ bool has_w8a8_quantized_weight(const WeightsIndex& index, const std::string& bas
 W8A8QuantizedWeight load_w8a8_quantized_weight(const WeightsIndex& index, const std::string& base,
                                                int layout = MCV_W8_TILED);
 
+// The lm_head's vocabulary projection from the tied token embedding, read
+// from the checkpoint (`name`, e.g. "model.language_model.embed_tokens.weight",
+// [vocab, hidden] F16 or BF16, bf16 converted as the reference loads it) in
+// one host pass: the embedding's rows become the projection's columns,
+// padded with zero columns to N = vocab rounded up to 64 (the reference
+// transposes it into 16384-wide chunks, the last padded with zero columns,
+// language_model.cpp:170,238-270).  W4A16: the build's synthetic int4
+// quantiser per (group, column) -- the reference has no int4 lm_head.  W8A8:
+// the reference's per-channel quantiser (quantize_dense_weight_w8a8 of each
+// chunk, language_model.cpp:264-266), bit-identical to it; the zero columns get
+// the 1e-8 scale floor and q = 0.  Columns from vocab on are ignored by the
+// lm_head entry points (vocab is passed to them).
+W4A16QuantizedWeight load_lm_head_w4a16(const WeightsIndex& index, const std::string& name, int64_t vocab);
+W8A8QuantizedWeight load_lm_head_w8a8(const WeightsIndex& index, const std::string& name, int64_t vocab,
+                                      int layout = MCV_W8_TILED);
+
 }  // namespace minicpmv

@@ -85,8 +85,9 @@ void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, h
     require(w.w_int8.data() && w.scales.data() && w.zeros.data(), "matmul_w4a16 weight is not loaded");
     const int64_t nb = mcv_w4a16_gemm_workspace_bytes(x.shape()[0], w.K, w.N);
     if (nb > 0 && static_cast<int64_t>(workspace.numel()) < nb) {
+        // the split's tile counters must start at zero (calls leave them zero)
         workspace = Tensor({nb}, DType::Int8);
-        workspace.allocate();
+        workspace.zero();
     }
     check_mcv(mcv_w4a16_gemm_ws(x.data(), x.shape()[0], w.K, w.N, w.w_int8.data(), w.scales.data(), w.zeros.data(),
                                 w.zero_bias, out.data(), nb > 0 ? workspace.data() : nullptr, nb, stream),

@@ -253,4 +253,58 @@ W8A8QuantizedWeight load_w8a8_quantized_weight(const WeightsIndex& index, const 
     return upload_w8a8(q, s32, s16, K, N, layout);
 }
 
+namespace {
+
+// The tied embedding [vocab, hidden] (F16 or BF16) of the checkpoint: its
+// host bytes, hidden size and source dtype, checked against `vocab`.
+struct EmbeddingSource {
+    const uint16_t* data;
+    int64_t V;
+    int64_t H;
+    int src_dtype;
+};
+
+EmbeddingSource embedding_source(const WeightsIndex& index, const std::string& name, int64_t vocab) {
+    const TensorInfo& info = index.at(name);
+    if (info.shape.size() != 2) throw std::runtime_error("lm_head embedding " + name + " must be 2-D [vocab, hidden]");
+    if (info.dtype != DType::Float16 && info.dtype != DType::BFloat16)
+        throw std::runtime_error("lm_head embedding " + name + " must be F16 or BF16");
+    const int64_t V = info.shape[0], H = info.shape[1];
+    if (vocab != V) throw std::runtime_error("lm_head embedding " + name + " has " + std::to_string(V) +
+                                             " rows, expected vocab " + std::to_string(vocab));
+    if (H <= 0 || H % MCV_W4_GROUP != 0)
+        throw std::runtime_error("lm_head embedding hidden size must be a positive multiple of 128");
+    return {reinterpret_cast<const uint16_t*>(index.host_data(name)), V, H,
+            info.dtype == DType::BFloat16 ? MCV_SRC_BF16 : MCV_SRC_F16};
+}
+
+}  // namespace
+
+W4A16QuantizedWeight load_lm_head_w4a16(const WeightsIndex& index, const std::string& name, int64_t vocab) {
+    const EmbeddingSource e = embedding_source(index, name, vocab);
+    const int64_t N = (e.V + 63) / 64 * 64;
+    std::vector<int32_t> qweight(static_cast<size_t>(e.H * (N / 8)));
+    std::vector<int32_t> qzeros(static_cast<size_t>((e.H / MCV_W4_GROUP) * (N / 8)));
+    std::vector<uint16_t> scales(static_cast<size_t>((e.H / MCV_W4_GROUP) * N));
+    check_mcv(mcv_w4a16_quantize_nk_host(e.data, e.src_dtype, e.H, e.V, N, qweight.data(), qzeros.data(),
+                                         scales.data(), 0),
+              "load_lm_head_w4a16");
+    return pack_w4a16_awq(qweight.data(), qzeros.data(), scales.data(), e.H, N);
+}
+
+W8A8QuantizedWeight load_lm_head_w8a8(const WeightsIndex& index, const std::string& name, int64_t vocab, int layout) {
+    if (layout != MCV_W8_TILED && layout != MCV_W8_KN)
+        throw std::runtime_error("load_lm_head_w8a8: layout must be MCV_W8_TILED or MCV_W8_KN");
+    const EmbeddingSource e = embedding_source(index, name, vocab);
+    const int64_t N = (e.V + 63) / 64 * 64;
+    const int64_t bytes = layout == MCV_W8_TILED ? mcv_w8a8_tiled_bytes(e.H, N) : e.H * N;
+    std::vector<int8_t> q(static_cast<size_t>(bytes));
+    std::vector<float> s32(static_cast<size_t>(N));
+    std::vector<uint16_t> s16(static_cast<size_t>(N));
+    check_mcv(mcv_w8a8_quantize_weight_nk_pad_host(e.data, e.src_dtype, e.H, e.V, N, q.data(), layout, s32.data(),
+                                                   s16.data()),
+              "load_lm_head_w8a8");
+    return upload_w8a8(q, s32, s16, e.H, N, layout);
+}
+
 }  // namespace minicpmv

@@ -411,26 +411,32 @@ extern "C" int mcv_w8a8_pack_tiled_nk_host(const int8_t* q_nk, int64_t K, int64_
     return MCV_OK;
 }
 
-extern "C" int mcv_w8a8_quantize_weight_nk_host(const uint16_t* w_nk, int src_dtype, int64_t K, int64_t N, int8_t* q,
-                                                int out_layout, float* scale_f32, uint16_t* scale_f16) {
-    if (!w_nk || !q || !scale_f32) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_nk_host: null pointer");
-    if (K <= 0 || N <= 0) return fail(MCV_ERR_SHAPE, "mcv_w8a8_quantize_weight_nk_host: K and N must be positive");
+extern "C" int mcv_w8a8_quantize_weight_nk_pad_host(const uint16_t* w_nk, int src_dtype, int64_t K, int64_t N_src,
+                                                    int64_t N, int8_t* q, int out_layout, float* scale_f32,
+                                                    uint16_t* scale_f16) {
+    const char* who = "mcv_w8a8_quantize_weight_nk_pad_host";
+    if (!w_nk || !q || !scale_f32) return fail(MCV_ERR_INVALID_ARG, "%s: null pointer", who);
+    if (K <= 0 || N <= 0 || N_src <= 0 || N_src > N)
+        return fail(MCV_ERR_SHAPE, "%s: need K > 0 and 0 < N_src <= N (K=%lld N_src=%lld N=%lld)", who, (long long)K,
+                    (long long)N_src, (long long)N);
     if (src_dtype != MCV_SRC_F16 && src_dtype != MCV_SRC_BF16)
-        return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_nk_host: bad source dtype %d", src_dtype);
+        return fail(MCV_ERR_INVALID_ARG, "%s: bad source dtype %d", who, src_dtype);
     if (out_layout != MCV_W8_KN && out_layout != MCV_W8_NK && out_layout != MCV_W8_TILED)
-        return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_nk_host: bad layout %d", out_layout);
+        return fail(MCV_ERR_INVALID_ARG, "%s: bad layout %d", who, out_layout);
     const int64_t kblocks = ceil_div(K, 128) * 4;
     if (out_layout == MCV_W8_TILED) std::memset(q, 0, static_cast<size_t>(mcv_w8a8_tiled_bytes(K, N)));
     const bool bf = src_dtype == MCV_SRC_BF16;
     // Output channel n is row n of the checkpoint's [N][K]: the same values,
-    // the same per-channel formula as the [K][N] quantiser above.
+    // the same per-channel formula as the [K][N] quantiser above.  Channels
+    // from N_src on are zero columns (scale floored at 1e-8, every q zero),
+    // what the quantiser makes of the zero padding the reference appends.
     parallel_columns(N, K, [&](int64_t n0, int64_t n1) {
         std::vector<float> row(static_cast<size_t>(K));
         for (int64_t n = n0; n < n1; ++n) {
             const uint16_t* src = w_nk + n * K;
             float max_abs = 0.0f;
             for (int64_t k = 0; k < K; ++k) {
-                row[k] = h2f_host(bf ? bf16_to_f16_trunc_host(src[k]) : src[k]);
+                row[k] = n < N_src ? h2f_host(bf ? bf16_to_f16_trunc_host(src[k]) : src[k]) : 0.0f;
                 max_abs = std::max(max_abs, std::fabs(row[k]));
             }
             float scale = max_abs / 127.0f;
@@ -449,6 +455,93 @@ extern "C" int mcv_w8a8_quantize_weight_nk_host(const uint16_t* w_nk, int src_dt
     return MCV_OK;
 }
 
+extern "C" int mcv_w8a8_quantize_weight_nk_host(const uint16_t* w_nk, int src_dtype, int64_t K, int64_t N, int8_t* q,
+                                                int out_layout, float* scale_f32, uint16_t* scale_f16) {
+    return mcv_w8a8_quantize_weight_nk_pad_host(w_nk, src_dtype, K, N, N, q, out_layout, scale_f32, scale_f16);
+}
+
+namespace {
+
+// The build's synthetic int4 quantiser for one (group, column): the 128
+// values v[0..127] -> scale bits, zero, and the 128 nibbles q[].
+void quantize_group_int4(const float* v, uint16_t* s16_out, uint32_t* z_out, uint8_t* q) {
+    float lo = INFINITY, hi = -INFINITY;
+    for (int kk = 0; kk < kGroup; ++kk) {
+        lo = v[kk] < lo ? v[kk] : lo;
+        hi = v[kk] > hi ? v[kk] : hi;
+    }
+    float range = hi - lo;
+    if (range < 1e-5f) range = 1e-5f;
+    const uint16_t s16 = f2h_rne_host(range / 15.0f);
+    const float sc = h2f_host(s16);
+    float zf = std::nearbyint(-lo / sc);
+    zf = zf < 0.0f ? 0.0f : (zf > 15.0f ? 15.0f : zf);
+    for (int kk = 0; kk < kGroup; ++kk) {
+        float qf = std::nearbyint(v[kk] / sc) + zf;
+        qf = qf < 0.0f ? 0.0f : (qf > 15.0f ? 15.0f : qf);
+        q[kk] = static_cast<uint8_t>(qf);
+    }
+    *s16_out = s16;
+    *z_out = static_cast<uint32_t>(zf);
+}
+
+}  // namespace
+
+extern "C" int mcv_w4a16_quantize_nk_host(const uint16_t* w_nk, int src_dtype, int64_t K, int64_t N_src, int64_t N,
+                                          int32_t* qweight, int32_t* qzeros, uint16_t* scales, int nthreads) {
+    const char* who = "mcv_w4a16_quantize_nk_host";
+    if (!w_nk || !qweight || !qzeros || !scales) return fail(MCV_ERR_INVALID_ARG, "%s: null pointer", who);
+    if (K <= 0 || K % kGroup != 0 || N <= 0 || N % 8 != 0 || N_src <= 0 || N_src > N)
+        return fail(MCV_ERR_SHAPE, "%s: need K %% 128 == 0, N %% 8 == 0 and 0 < N_src <= N (K=%lld N_src=%lld N=%lld)",
+                    who, (long long)K, (long long)N_src, (long long)N);
+    if (src_dtype != MCV_SRC_F16 && src_dtype != MCV_SRC_BF16)
+        return fail(MCV_ERR_INVALID_ARG, "%s: bad source dtype %d", who, src_dtype);
+    const bool bf = src_dtype == MCV_SRC_BF16;
+    const int64_t np = N / 8, G = K / kGroup;
+    constexpr int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    int nt = nthreads > 0 ? nthreads : static_cast<int>(std::thread::hardware_concurrency());
+    if (nt < 1) nt = 1;
+    if (nt > 64) nt = 64;
+    // Each worker owns a contiguous range of 8-column words: disjoint outputs.
+    // Column n is row n of the [N_src][K] source (zero from N_src on).
+    auto work = [&](int64_t j0, int64_t j1) {
+        std::vector<float> col(static_cast<size_t>(K));
+        uint8_t q[8][kGroup];
+        uint32_t z[8];
+        for (int64_t j = j0; j < j1; ++j) {
+            for (int64_t g = 0; g < G; ++g) {
+                uint32_t zword = 0;
+                for (int sl = 0; sl < 8; ++sl) {
+                    const int64_t n = j * 8 + order[sl];
+                    const uint16_t* src = w_nk + n * K + g * kGroup;
+                    for (int kk = 0; kk < kGroup; ++kk)
+                        col[kk] = n < N_src ? h2f_host(bf ? bf16_to_f16_trunc_host(src[kk]) : src[kk]) : 0.0f;
+                    quantize_group_int4(col.data(), &scales[g * N + n], &z[sl], q[sl]);
+                    zword |= z[sl] << (4 * sl);
+                }
+                qzeros[g * np + j] = static_cast<int32_t>(zword);
+                for (int kk = 0; kk < kGroup; ++kk) {
+                    uint32_t word = 0;
+                    for (int sl = 0; sl < 8; ++sl) word |= static_cast<uint32_t>(q[sl][kk]) << (4 * sl);
+                    qweight[(g * kGroup + kk) * np + j] = static_cast<int32_t>(word);
+                }
+            }
+        }
+    };
+    if (nt == 1 || np < 64) {
+        work(0, np);
+    } else {
+        std::vector<std::thread> th;
+        const int64_t per = ceil_div(np, nt);
+        for (int t = 0; t < nt; ++t) {
+            const int64_t j0 = t * per, j1 = std::min<int64_t>(np, j0 + per);
+            if (j0 < j1) th.emplace_back(work, j0, j1);
+        }
+        for (auto& t : th) t.join();
+    }
+    return MCV_OK;
+}
+
 extern "C" int mcv_w4a16_quantize_host(const uint16_t* w_kn, int64_t K, int64_t N, int32_t* qweight, int32_t* qzeros,
                                        uint16_t* scales, int nthreads) {
     if (!w_kn || !qweight || !qzeros || !scales) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_quantize_host: null pointer");
@@ -462,37 +555,22 @@ extern "C" int mcv_w4a16_quantize_host(const uint16_t* w_kn, int64_t K, int64_t 
     if (nt > 64) nt = 64;
     // Each worker owns a contiguous range of 8-column words: disjoint outputs.
     auto work = [&](int64_t j0, int64_t j1) {
-        uint8_t q[kGroup][8];
+        float col[kGroup];
+        uint8_t q[8][kGroup];
         for (int64_t g = 0; g < G; ++g)
             for (int64_t j = j0; j < j1; ++j) {
                 uint32_t zword = 0;
                 for (int s = 0; s < 8; ++s) {
                     const int64_t n = j * 8 + order[s];
-                    float lo = INFINITY, hi = -INFINITY;
-                    for (int kk = 0; kk < kGroup; ++kk) {
-                        const float v = h2f_host(w_kn[(g * kGroup + kk) * N + n]);
-                        lo = v < lo ? v : lo;
-                        hi = v > hi ? v : hi;
-                    }
-                    float range = hi - lo;
-                    if (range < 1e-5f) range = 1e-5f;
-                    const uint16_t s16 = f2h_rne_host(range / 15.0f);
-                    const float sc = h2f_host(s16);
-                    float zf = std::nearbyint(-lo / sc);
-                    zf = zf < 0.0f ? 0.0f : (zf > 15.0f ? 15.0f : zf);
-                    scales[g * N + n] = s16;
-                    zword |= static_cast<uint32_t>(zf) << (4 * s);
-                    for (int kk = 0; kk < kGroup; ++kk) {
-                        const float v = h2f_host(w_kn[(g * kGroup + kk) * N + n]);
-                        float qf = std::nearbyint(v / sc) + zf;
-                        qf = qf < 0.0f ? 0.0f : (qf > 15.0f ? 15.0f : qf);
-                        q[kk][s] = static_cast<uint8_t>(qf);
-                    }
+                    for (int kk = 0; kk < kGroup; ++kk) col[kk] = h2f_host(w_kn[(g * kGroup + kk) * N + n]);
+                    uint32_t z = 0;
+                    quantize_group_int4(col, &scales[g * N + n], &z, q[s]);
+                    zword |= z << (4 * s);
                 }
                 qzeros[g * np + j] = static_cast<int32_t>(zword);
                 for (int kk = 0; kk < kGroup; ++kk) {
                     uint32_t word = 0;
-                    for (int s = 0; s < 8; ++s) word |= static_cast<uint32_t>(q[kk][s]) << (4 * s);
+                    for (int s = 0; s < 8; ++s) word |= static_cast<uint32_t>(q[s][kk]) << (4 * s);
                     qweight[(g * kGroup + kk) * np + j] = static_cast<int32_t>(word);
                 }
             }

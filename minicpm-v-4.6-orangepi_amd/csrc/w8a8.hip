@@ -5,6 +5,8 @@
 // Replaces the NPU operators w8a8_quantize_custom, matmul_w8a8_i32_custom and
 // w8a8_dequant_custom (src/csrc/custom_ops/op_kernel/*.cpp) and their host
 // wrappers (src/csrc/lib/ops.cpp:1097-1210).
+#include <string>
+
 #include "common.h"
 
 namespace mcv {
@@ -12,6 +14,7 @@ namespace mcv {
 int launch_w8a8_tiled_gate_up_silu(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* wg,
                                    const void* wsg, const int8_t* wu, const void* wsu, int ws16, const void* xs,
                                    int xs16, void* act, hipStream_t stream);
+std::string w8a8_tiled_name(int64_t M, int64_t K, int64_t N, bool f16);
 int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
                       const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
 int launch_w8a8_gemv_argmax(const int8_t* xq, int64_t K, int64_t V, const int8_t* w, void* logits, const void* xs,
@@ -334,7 +337,24 @@ bool dtype_ok(int d) { return d == MCV_F32 || d == MCV_F16; }
 
 using namespace mcv;
 
+namespace {
+thread_local std::string g_w8_kernel_name;
+}
+
 extern "C" {
+
+const char* mcv_w8a8_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int w_layout, int out_f16) {
+    if (M <= 0 || K <= 0 || N <= 0) {
+        g_w8_kernel_name = "none (bad shape)";
+    } else if (w_layout == MCV_W8_TILED) {
+        g_w8_kernel_name = w8a8_tiled_name(M, K, N, out_f16 != 0);
+    } else {
+        g_w8_kernel_name = std::string("w8a8_gemm_kernel<") + (w_layout == MCV_W8_KN ? "true" : "false") + ", " +
+                           (out_f16 ? "true" : "false") + "> (VALU dot4, " +
+                           (w_layout == MCV_W8_KN ? "[K, N]" : "[N, K]") + " weight)";
+    }
+    return g_w8_kernel_name.c_str();
+}
 
 int mcv_w8a8_quantize_act(const void* x, int64_t M, int64_t K, int8_t* xq, float* s32, void* s16, mcv_stream_t stream) {
     if (!x || !xq || (!s32 && !s16)) return fail(MCV_ERR_INVALID_ARG, "w8a8_quantize: null pointer");

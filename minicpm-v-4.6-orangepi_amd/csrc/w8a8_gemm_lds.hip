@@ -44,7 +44,9 @@
 // (src/csrc/custom_ops/op_kernel/matmul_w8a8_i32_custom.cpp:15-48,
 // w8a8_dequant_custom.cpp:33-69) for weights packed by
 // quantize_dense_weight_w8a8 (src/csrc/lib/quantized_weight.cpp:231-268).
+#include <cstdio>
 #include <cstdlib>
+#include <string>
 
 #include "common.h"
 
@@ -531,19 +533,13 @@ GemmLFn pick_l(const ShapeL& s, int epi) {
 
 // Largest tiles first; the first shape whose grid covers most of the 256
 // CUs, else the one with the most workgroups.  Measured on MI355X (K=1024,
-// N=3584, graph-replayed, rotated weights): M=1024 128x128 with 3 stages
-// 9.5 us (4 stages 9.8, 64x128 12.2, 64x64 13.1); M=256 64x64 5.3 us
-// (64x128 6.6, 128x128 8.4).  The K loop there runs at ~0.58 us per
-// 32 KiB stage: a plain L2 -> LDS stream sustains ~104 GB/s per CU
-// (0.32 us per stage) and the stage's MFMAs take ~0.21 us, so the copies and
-// the operand reads contend for the LDS.  MCV_W8LDS_SHAPE="BM,BN,NS"
-// overrides the choice (read once per process; tuning sweeps).
+// N=3584, rotated weights): M=1024 128x128 with 3 stages 9.5 us (4 stages
+// 9.8, 64x128 12.2, 64x64 13.1); M=256 64x64 5.3 us (64x128 6.6, 128x128
+// 8.4).  The K loop there runs at ~0.58 us per 32 KiB stage: a plain L2 ->
+// LDS stream sustains ~104 GB/s per CU (0.32 us per stage) and the stage's
+// MFMAs take ~0.21 us, so the copies and the operand reads contend for the
+// LDS.
 ShapeL choose_l(int64_t M, int64_t N) {
-    static const char* const e = std::getenv("MCV_W8LDS_SHAPE");
-    if (e != nullptr) {
-        ShapeL s{0, 0, 0};
-        if (std::sscanf(e, "%d,%d,%d", &s.bm, &s.bn, &s.ns) == 3 && pick_l(s, 0)) return s;
-    }
     constexpr ShapeL kOrder[] = {{128, 128, 3}, {64, 128, 4}, {64, 64, 4}};
     ShapeL best = kOrder[0];
     int64_t best_t = -1;
@@ -559,6 +555,15 @@ ShapeL choose_l(int64_t M, int64_t N) {
 }
 
 }  // namespace
+
+// The kernel launch_w8a8_gemm_lds picks for M x N, as text (report labels).
+std::string w8a8_gemm_lds_name(int64_t M, int64_t N, bool f16) {
+    const ShapeL s = choose_l(M, N);
+    char buf[128];
+    std::snprintf(buf, sizeof(buf), "w8a8_gemm_lds_kernel<%d, %d, %d> (%s, %lld workgroups)", s.bm, s.bn, s.ns,
+                  f16 ? "fused fp16 epilogue" : "int32 out", (long long)(ceil_div(M, s.bm) * ceil_div(N, s.bn)));
+    return buf;
+}
 
 // xq [M][K] int8 (K % 16 == 0), w tiled; out int32 or fp16 [M][N].  Shapes
 // were validated by the caller.
@@ -576,17 +581,10 @@ int launch_w8a8_gemm_lds(const int8_t* xq, int64_t M, int64_t K, int64_t N, cons
     const int KT = static_cast<int>(KB / 4);
     const int epi = f16 ? 4 | (xs16 ? 1 : 0) | (ws16 ? 2 : 0) : 0;
     // Tile order: a contiguous run of tiles per XCD, down the tile columns.
-    // Cutting the grid into one 2-D block per XCD halves the x bytes each L2
-    // sees but doubles the weight columns, which come from HBM: slower at
-    // M = 1024 (8.7 against 8.4 us).  MCV_W8LDS_XCDM=a forces the a x (8 / a)
-    // blocking (read once per process; tuning sweeps).
-    const int64_t m_tiles = ceil_div(M, s.bm);
-    int xcd_m = 0;
-    static const char* const xe = std::getenv("MCV_W8LDS_XCDM");
-    if (xe != nullptr) {
-        const int a = std::atoi(xe);
-        if ((a == 1 || a == 2 || a == 4 || a == 8) && m_tiles % a == 0 && n_tiles % (8 / a) == 0) xcd_m = a;
-    }
+    // Cutting the grid into one 2-D block per XCD (the kernel's xcd_m > 0)
+    // halves the x bytes each L2 sees but doubles the weight columns, which
+    // come from HBM: slower at M = 1024 (8.7 against 8.4 us).
+    const int xcd_m = 0;
     hipLaunchKernelGGL(pick_l(s, epi), dim3(static_cast<unsigned>(total)),
                        dim3(256), 0, stream, xq, w, static_cast<int>(M), static_cast<int>(K), static_cast<int>(N),
                        static_cast<int>(KB), out, xs, ws, static_cast<int>(nslab), static_cast<int>(n_tiles),

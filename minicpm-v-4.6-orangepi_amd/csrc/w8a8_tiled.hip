@@ -18,6 +18,7 @@
 // quantize_dense_weight_w8a8 (src/csrc/lib/quantized_weight.cpp:231-268).
 #include <cstdlib>
 #include <cstring>
+#include <string>
 
 #include "common.h"
 
@@ -212,6 +213,25 @@ int64_t w8a8_tiled_bytes(int64_t K, int64_t N) {
 
 int launch_w8a8_gemm_lds(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
                          const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
+std::string w8a8_gemm_lds_name(int64_t M, int64_t N, bool f16);
+
+// The GEMV takes M <= 4, and M <= 2 past K = 2048 (launch_w8a8_tiled).
+bool w8a8_uses_gemv(int64_t M, int64_t K) {
+    const int64_t KB = ceil_div(K, 128) * 4;
+    return M <= 2 || (M <= 4 && KB <= 64);
+}
+
+// The kernel launch_w8a8_tiled runs for M x K x N, as text (report labels).
+std::string w8a8_tiled_name(int64_t M, int64_t K, int64_t N, bool f16) {
+    if (!w8a8_uses_gemv(M, K)) return w8a8_gemm_lds_name(M, N, f16);
+    const int64_t nslab = ceil_div(N, kSlab), KB = ceil_div(K, 128) * 4;
+    const bool narrow = nslab < 128;
+    const int nw = narrow && KB <= 64 ? 8 : 16, halves = narrow ? 1 : 2, u = narrow && KB <= 64 ? 4 : 2;
+    char buf[160];
+    std::snprintf(buf, sizeof(buf), "w8a8_tiled_gemv_kernel<%lld, %d, %d, %d> (v_dot4, %s)", (long long)(M < 4 ? M : 4),
+                  nw, halves, u, f16 ? "fused fp16 epilogue" : "int32 out");
+    return buf;
+}
 
 // xq [M][K] int8 (16-byte aligned rows not required), w tiled; out int32 or
 // fp16 [M][N].  Shapes were validated by the caller.
@@ -225,7 +245,7 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
     // serial k-blocks per wave cost more than the GEMM's fixed start
     // (MI355X, graph-replayed, us: K=3584 N=1024 GEMV M=1/2/4 4.8/6.3/8.4,
     // GEMM M=5 6.6; K=1024 N=3584 GEMV M=4 3.8, GEMM M=5 4.0).
-    if (M <= 2 || (M <= 4 && KB <= 64)) {
+    if (w8a8_uses_gemv(M, K)) {
         return f16 ? launch_w8a8_gemv<true, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream)
                    : launch_w8a8_gemv<false, false>(xq, M, K, N, w, nullptr, out, xs, xs16, ws, nullptr, ws16, stream);
     }

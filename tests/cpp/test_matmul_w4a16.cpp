@@ -164,8 +164,9 @@ int main() {
 
         // The K split across workgroups into a caller-owned workspace, on the
         // down projection's shape (K=3584, N=1024) at M = 128: within fp16
-        // rounding of the unsplit kernel (only the fp32 summation order
-        // differs), the same bits on every call, the workspace allocated once.
+        // rounding of the unsplit kernel (the C-ABI without a workspace; only
+        // the fp32 summation order differs), the same bits on every call, the
+        // workspace allocated once.
         constexpr int MR = 128;
         Tensor a({MR, N}, DType::Float16), o1({MR, K}, DType::Float16), o2({MR, K}, DType::Float16), wsp;
         a.allocate();
@@ -175,7 +176,9 @@ int main() {
             r3(r1.size());
         for (auto& v : ha) v = t::f2h(xd(rng));
         a.copy_from_host(ha.data(), ha.size() * 2);
-        matmul_w4a16(a, down, o1, ctx.stream());
+        check_mcv(mcv_w4a16_gemm(a.data(), MR, down.K, down.N, down.w_int8.data(), down.scales.data(),
+                                 down.zeros.data(), down.zero_bias, o1.data(), ctx.stream()),
+                  "unsplit GEMM");
         matmul_w4a16(a, down, o2, ctx.stream(), wsp);
         const int64_t nb = mcv_w4a16_gemm_workspace_bytes(MR, N, K);
         const void* const first = wsp.data();

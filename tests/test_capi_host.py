@@ -309,21 +309,26 @@ def test_lm_head_slots_token_known_answer(mcv):
 
 
 def test_w4a16_gemm_workspace_query(mcv):
-    """Workspace of the K split across workgroups: none where the GEMV
-    (few rows) or the LDS kernel (tall tiles fill the chip) takes the shape,
-    or for an invalid K; otherwise kx fp32 partial tiles of M x N, kx the
-    split toward 200 workgroups (M=128, K=3584, N=1024: 64 tiles of 32 rows
-    x one slab, 4 ways; M=64: 32 tiles, 7 ways -- K=3584 has 7 stage sets of
-    4 x 128).  Splits happen only past K=2048."""
-    q = mcv.lib().mcv_w4a16_gemm_workspace_bytes
-    assert q(128, 3584, 1024) == 4 * 128 * 1024 * 4
-    assert q(64, 3584, 1024) == 7 * 64 * 1024 * 4
-    assert q(96, 3584, 2048) == 3 * 96 * 2048 * 4                   # 96 tiles: 3 ways
-    # K <= 2048 goes to the LDS kernel's 32-row, two-k-part tiles
+    """Workspace of the K split across workgroups: none where the GEMV (few
+    rows) or an unsplit tile grid (it covers most of the chip) takes the
+    shape, or for an invalid K; otherwise the 4 KiB counter region plus S fp32
+    partial tiles of 32 x 128 per tile, S the most ways (dividing K/128) that
+    keep the grid within 256 workgroups and >= 7 stages per workgroup; the
+    kernel label names the same configuration."""
+    L = mcv.lib()
+    q = L.mcv_w4a16_gemm_workspace_bytes
+    part = 32 * 128 * 4
+    for (M, K, N), S in [((128, 3584, 1024), 4), ((64, 3584, 1024), 4), ((512, 3584, 1024), 2),
+                         ((96, 3584, 2048), 4), ((128, 2048, 2048), 2)]:
+        tiles = -(-M // 32) * -(-N // 128)
+        assert q(M, K, N) == 4096 + tiles * S * part, (M, K, N)
+        assert f"K split {S} ways".encode() in L.mcv_w4a16_gemm_kernel_name(M, K, N, 1)
+        assert b"K split 1 ways" in L.mcv_w4a16_gemm_kernel_name(M, K, N, 0)      # no workspace: unsplit
     for shape in [(4, 1024, 1024), (32, 1024, 1024), (2048, 1024, 3584), (2048, 3584, 1024), (128, 1024, 3584),
-                  (128, 1024, 1024), (128, 2048, 2048), (512, 3584, 1024), (128, 1000, 1024), (0, 1024, 1024),
-                  (128, 0, 1024)]:
+                  (128, 1024, 1024), (512, 1024, 3584), (128, 1000, 1024), (0, 1024, 1024), (128, 0, 1024)]:
         assert q(*shape) == 0, shape
+    assert b"w4a16_gemv_kernel" in L.mcv_w4a16_gemm_kernel_name(4, 1024, 1024, 1)
+    assert b"<128, 8, 3>" in L.mcv_w4a16_gemm_kernel_name(2048, 1024, 3584, 1)
 
 
 def test_lm_head_grid_choice(mcv):
@@ -373,3 +378,37 @@ def test_w8a8_checkpoint_quantiser(mcv, oracle, K, N):
     # pre-quantised int8 [N, K] (safetensors I8) -> tiled
     q_nk = rng.integers(-128, 128, (N, K)).astype(np.int8)
     assert np.array_equal(mcv.pack_w8a8_tiled_nk(q_nk), mcv.pack_w8a8_tiled(np.ascontiguousarray(q_nk.T)))
+
+
+@pytest.mark.parametrize("V,H,N", [(1000, 256, 1024), (61, 128, 64), (4097, 384, 4160)])
+def test_embedding_quantisers(mcv, oracle, V, H, N):
+    """The tied embedding [V, H] as the lm_head's [H, N] projection, columns
+    from V on zero: the int4 quantiser equals mcv_w4a16_quantize_host on the
+    transposed, zero-padded matrix, and the int8 one the oracle's per-channel
+    quantiser on it (the reference's padded chunks, language_model.cpp:
+    238-270), bit for bit, from fp16 and from bf16 bits."""
+    rng = np.random.default_rng(V + H)
+    emb = f16_normal(rng, (V, H), 0.02)
+    pad = np.zeros((H, N), np.uint16)
+    pad[:, :V] = emb.T
+    got = mcv.quantize_int4_embedding(emb, N)
+    want = mcv.quantize_int4(pad)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+    q, s32, s16 = mcv.quantize_w8a8_embedding(emb, N, mcv.SRC_F16, mcv.W8_TILED)
+    q_o, s_o, s16_o = oracle.w8a8_quantize_weight(pad)
+    assert np.array_equal(q, mcv.pack_w8a8_tiled(q_o))
+    assert np.array_equal(s32.view(np.uint32), s_o.view(np.uint32))
+    assert np.array_equal(s16, s16_o)
+    assert np.all(s32[V:] == np.float32(1e-8))                 # zero columns: the scale floor
+    # bf16 bits: converted as the reference loads bf16 (truncating to fp16)
+    f = rng.standard_normal((V, H)).astype(np.float32) * np.float32(0.02)
+    bf = (f.view(np.uint32) >> 16).astype(np.uint16)
+    as16 = oracle.bf16_to_f16_trunc(bf)
+    pad16 = np.zeros((H, N), np.uint16)
+    pad16[:, :V] = as16.T
+    for g, w in zip(mcv.quantize_int4_embedding(bf, N, mcv.SRC_BF16), mcv.quantize_int4(pad16)):
+        assert np.array_equal(g, w)
+    q, s32, _ = mcv.quantize_w8a8_embedding(bf, N, mcv.SRC_BF16, mcv.W8_KN)
+    q_o, s_o, _ = oracle.w8a8_quantize_weight(pad16)
+    assert np.array_equal(q, q_o) and np.array_equal(s32.view(np.uint32), s_o.view(np.uint32))

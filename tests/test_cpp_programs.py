@@ -79,6 +79,14 @@ def test_cpp_lm_head():
 
 
 @pytest.mark.gpu
+@pytest.mark.timeout(400)
+def test_cpp_lm_head_from_embedding(tmp_path):
+    """load_lm_head_w4a16 / _w8a8 over a synthetic [248094, 1024] embedding in a
+    safetensors file, through lm_head_greedy_w4a16 / _w8a8, against the oracle."""
+    run("test_lm_head_embedding", str(tmp_path), timeout=360)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("mode", [None, "all"])
 def test_cpp_decode_dispatch(mode):
     run("test_decode_dispatch", "dispatch", env={} if mode is None else {"MINICPM_W8A8_DECODE": mode})

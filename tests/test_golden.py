@@ -73,3 +73,19 @@ def test_kernels_reproduce_fixtures(mcv, cuda):
     d = load("w8a8_dequant_reference.npz")
     out = mcv.w8a8_dequant(torch.from_numpy(d["acc"]).cuda(), f16(d["xs16"]), f16(d["ws16"]))
     assert np.array_equal(u16(out), d["out16"])
+
+
+@pytest.mark.gpu
+def test_lm_head_pipeline_fixture_on_gpu(mcv, cuda):
+    """The reference's deterministic lm_head pipeline (tests/test_lm_head_pipeline.cpp:
+    51-120: four rows whose maximum logit is shared by four columns each) through
+    this build's argmax kernel: the logits on the device (fp32 products of the
+    fp16 operands, rounded to fp16 -- equal columns give equal logits), then
+    mcv_argmax_f16, whose first-maximum rule must return the fixture's tokens."""
+    import torch
+    lm = load("lm_head_pipeline_reference.npz")
+    h = torch.from_numpy(lm["hidden16"].view(np.int16)).cuda().view(torch.float16)
+    w = torch.from_numpy(lm["weight16"].view(np.int16)).cuda().view(torch.float16)
+    logits = (h.float() @ w.float()).half()
+    tok = mcv.argmax_last_dim(logits)
+    assert tok.cpu().tolist() == lm["tokens"].tolist()

@@ -95,18 +95,14 @@ def test_dequant_bit_exact(mcv, oracle, cuda):
 
 
 @pytest.mark.parametrize("M,K,N", [
-    # (128, 1024, 3584), (130, 1024, 1000) ragged and (256, 256, 264), one
-    # stage per k-part: the LDS kernel's 32-row tiles over two k-parts
-    # (K <= 2048 with no tall tile filling the chip); (8, ...) and
-    # (128, 3584, 1024): the register-staged kernel
+    # the dispatch's unsplit configurations: 32 x 128 tiles (few rows), ragged
+    # M and N, one stage (fewer stages than buffers)
     (8, 1024, 3584), (128, 1024, 3584), (130, 1024, 1000), (128, 3584, 1024), (256, 256, 264),
-    # LDS-staged kernel: 128-row tiles, ragged M and N (57 slabs, the last
-    # tile's fourth slab past the end), one k stage (fewer stages than buffers)
+    # 128 x 256 tiles (eight waves), ragged M and N (57 slabs: the last tile's
+    # fourth slab past the end), one k stage
     (2050, 128, 3592),
-    # 64-row tiles, ragged M and N
-    (1100, 256, 3000),
-    # 64-row tiles over two k-parts (128-column tiles), ragged M and N
-    (1700, 512, 1000),
+    # 64 x 128 tiles, ragged M and N
+    (1100, 256, 3000), (1700, 512, 1000),
 ], ids=lambda v: str(v))
 def test_gemm_mfma_vs_oracle(mcv, oracle, cuda, M, K, N):
     x, qweight, qzeros, scales, _ = _case(3000 + M + K + N, M, K, N)
@@ -133,10 +129,10 @@ def test_gemm_mfma_full_size(mcv, oracle, cuda, M, K, N):
 
 
 # K split across workgroups (mcv_w4a16_gemm_ws, the Python mirror's route):
-# few rows and a long K leave the tile grid far below the CU count.  K=3584's
-# 7 stage sets over 4 workgroups (uneven), seven ways at M=64, three at
-# M=96 N=2048, ragged rows and an odd N (element stores of the partial
-# tiles, the reduction's scalar path).
+# few rows and a long K leave the tile grid far below the CU count; the
+# partial tiles are added inside the launch by the last workgroup of each
+# tile.  K=3584 four ways at M=128, M=64 and M=96 N=2048, two at M=200,
+# ragged rows and an odd N (the element-store epilogue).
 @pytest.mark.parametrize("M,K,N", [(128, 3584, 1024), (64, 3584, 1024), (200, 3584, 1024), (97, 3584, 1001),
                                    (96, 3584, 2048)], ids=lambda v: str(v))
 def test_gemm_split_k_vs_oracle(mcv, oracle, cuda, M, K, N):
@@ -169,9 +165,11 @@ def test_gemm_split_k_vs_oracle(mcv, oracle, cuda, M, K, N):
 
 
 def test_gemm_split_k_graph_replays(mcv, cuda):
-    """The split path under HIP graph capture (workspace from the graph's
-    pool, no memset anywhere): every replay, with eager work and host
-    synchronisation between them, gives the eager call's bits."""
+    """The split path under HIP graph capture (the capture stream's own
+    zero-filled workspace, made by the call before the capture; no memset in
+    the graph): every replay, with eager work and host synchronisation
+    between them, gives the eager call's bits -- the tile counters are back at
+    zero after every call."""
     torch = _torch()
     M, K, N = 128, 3584, 1024
     x, qweight, qzeros, scales, _ = _case(77, M, K, N)
@@ -196,6 +194,50 @@ def test_gemm_split_k_graph_replays(mcv, cuda):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {i}"
+
+
+# Every built configuration of the half-slab GEMM (mcv_w4a16_gemm_sk), the
+# dispatch's and the rest, against the oracle on ragged shapes, all through
+# ONE zero-filled workspace (calls of different shapes and splits must leave
+# its counters zero for each other), each split twice for identical bits.
+SK_CONFIGS = [(128, 8, 3), (128, 4, 3), (64, 8, 3), (64, 4, 3), (32, 4, 3)]
+
+
+@pytest.mark.parametrize("M,K,N", [(200, 1024, 1000), (70, 2048, 520)], ids=lambda v: str(v))
+def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
+    torch = _torch()
+    L = mcv.lib()
+    x, qweight, qzeros, scales, _ = _case(8000 + M + K + N, M, K, N)
+    w = _dev_weight(mcv, qweight, qzeros, scales)
+    xd = _to_dev(x)
+    ref = oracle.w4a16_matmul(x, oracle.unpack_awq(qweight, qzeros), scales)
+    ws = torch.zeros(32 << 20, dtype=torch.uint8, device="cuda")
+    q, sc, z = w.ptrs()
+    stream = torch.cuda.current_stream().cuda_stream
+    G = K // 128
+    for tm, nwv, ns in SK_CONFIGS:
+        for S in [s for s in (1, 2, 4, 8, 16) if G % s == 0]:
+            assert L.mcv_w4a16_gemm_sk_workspace_bytes(M, w.N, tm, nwv, S) <= ws.numel()
+            outs = []
+            for _ in range(2 if S > 1 else 1):
+                out = torch.full((M, N), 7.0, dtype=torch.float16, device="cuda")
+                rc = L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, w.zero_bias, out.data_ptr(), tm, nwv,
+                                         ns, S, ws.data_ptr(), ws.numel(), stream)
+                assert rc == 0, L.mcv_last_error()
+                outs.append(out)
+            torch.cuda.synchronize()
+            _check(_host_f32(outs[0]), ref, f"sk tm={tm} waves={nwv} S={S} M={M} K={K} N={N}")
+            if S > 1:
+                assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (tm, nwv, S)
+    # the counters are zero after every call
+    assert int(ws[:4096].count_nonzero().item()) == 0
+    # an unbuilt configuration, a split that does not divide K/128, a missing workspace: clear errors
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 96, 4, 3, 1, None, 0,
+                               stream) == 1
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 3, ws.data_ptr(),
+                               ws.numel(), stream) == 1
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 2, None, 0,
+                               stream) == 1
 
 
 def test_gemv_and_mfma_agree(mcv, cuda):
