@@ -181,8 +181,11 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
 /* The half-slab GEMM with an explicit configuration (what mcv_w4a16_gemm_ws
  * picks by shape; exposed so every configuration can be tested and timed):
  * tile tm x 32 * waves (tm in {32, 64, 128}, waves in {4, 8}), `stages`
- * copy stages in flight, K split `splits` ways across workgroups (splits
- * divides K / 128), the partial tiles added inside the same launch by the
+ * copy stages in flight of `groups_per_stage` quantisation groups (128 k)
+ * each, `k_parts` waves per half-slab (1, or 2 with groups_per_stage 2:
+ * each takes one group of every stage), K split `splits` ways across
+ * workgroups (splits divides K / 128, groups_per_stage divides
+ * K / 128 / splits), the partial tiles added inside the same launch by the
  * last workgroup of each tile, in split order (deterministic).  Splits > 1
  * need a 256-byte aligned workspace of mcv_w4a16_gemm_sk_workspace_bytes
  * bytes, zero-filled once before its first use: its first 4 KiB hold the
@@ -193,8 +196,9 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
 int64_t mcv_w4a16_gemm_sk_workspace_bytes(int64_t M, int64_t N, int tm, int waves, int splits);
 int mcv_w4a16_gemm_sk(const void* x_dev, int64_t M, int64_t K, int64_t N,
                       const void* qw_dev, const void* scales_dev, const void* zeros_dev,
-                      int zero_bias, void* out_dev, int tm, int waves, int stages, int splits,
-                      void* workspace_dev, int64_t workspace_bytes, mcv_stream_t stream);
+                      int zero_bias, void* out_dev, int tm, int waves, int stages,
+                      int groups_per_stage, int k_parts, int splits, void* workspace_dev,
+                      int64_t workspace_bytes, mcv_stream_t stream);
 
 /* The two kernels behind mcv_w4a16_gemm, callable directly (same contract). */
 int mcv_w4a16_gemv(const void* x_dev, int64_t M, int64_t K, int64_t N,

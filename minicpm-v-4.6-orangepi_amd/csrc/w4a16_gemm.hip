@@ -37,22 +37,32 @@ bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N
 // widths), with a workspace, K is split across workgroups on 32 x 128 tiles:
 // the most ways that keep the grid within one workgroup per CU and at least
 // seven 128-k stages per workgroup (the partial tiles' exchange costs ~1-2 us,
-// which a shorter loop does not pay back).  Measured on MI355X (rotated
-// weights, us per call, back to back): M=2048 K=1024 N=3584 128x256 21.8;
-// M=2048 K=3584 N=1024 64x128 23.0-24.7; M=512 K=1024 N=3584 64x128 8.9;
-// M=512 K=3584 N=1024 32x128 split 2 ways 13.1 (unsplit 17.6, 4 ways 13.5,
-// 64x128 2 ways 14.9); M=128 K=1024 N=3584 32x128 7.4 (2 ways 7.9); M=128
-// K=3584 N=1024 32x128 split 4 ways 10.2 (7 ways 11.5, 64x128 7 ways 13.7).
+// which a shorter loop does not pay back).  A workgroup with a long K loop
+// (14 or more groups, an even count) on a four-wave tile takes two k-parts
+// (eight waves, two groups per stage): two waves per SIMD cover each
+// other's copy issue, worth ~2% there and a loss on shorter loops.
+// Measured on MI355X (rotated weights, us per call, back to back): M=2048
+// K=1024 N=3584 128x256 21.3 (64x128 25.4); M=2048 K=3584 N=1024 64x128 two
+// k-parts 22.4 (one 22.8); M=512 K=1024 N=3584 64x128 9.0 (two k-parts 9.2);
+// M=512 K=3584 N=1024 32x128 split 2 ways, two k-parts 12.5 (one 12.8,
+// unsplit 16.5, 4 ways 14.1); M=128 K=1024 N=3584 32x128 7.1 (2 ways 7.9);
+// M=128 K=3584 N=1024 32x128 split 4 ways 9.9 (7 ways 11.1).
 SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
     constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {32, 4, 3, 1}};
+    const int64_t G = K / kGroup;
+    auto k_parts = [&](SkConfig c) {
+        const int64_t per = G / c.splits;
+        if (c.nwv == 4 && c.tm <= 64 && per >= 14 && per % 2 == 0) c.kg = c.kw = 2;
+        return c;
+    };
     for (const SkConfig& c : kOne)
-        if (w4a16_sk_tiles(M, N, c) >= 200) return c;
+        if (w4a16_sk_tiles(M, N, c) >= 200) return k_parts(c);
     SkConfig c{32, 4, 3, 1};
-    const int64_t tiles = w4a16_sk_tiles(M, N, c), G = K / kGroup;
-    if (!can_split || tiles > kSkMaxSplitTiles) return c;
+    const int64_t tiles = w4a16_sk_tiles(M, N, c);
+    if (!can_split || tiles > kSkMaxSplitTiles) return k_parts(c);
     for (int64_t s = 2; s <= G && s <= 64; ++s)
         if (G % s == 0 && tiles * s <= 256 && G / s >= 7) c.splits = static_cast<int>(s);
-    return c;
+    return k_parts(c);
 }
 
 int check_gemm_args(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
@@ -132,8 +142,8 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
         g_kernel_name = buf;
     } else {
         const SkConfig c = choose_gemm(M, K, N, with_workspace != 0);
-        std::snprintf(buf, sizeof(buf), "w4a16_gemm_sk_kernel<%d, %d, %d> (K split %d ways, %lld workgroups)", c.tm,
-                      c.nwv, c.ns, c.splits, (long long)(w4a16_sk_tiles(M, N, c) * c.splits));
+        std::snprintf(buf, sizeof(buf), "w4a16_gemm_sk_kernel<%d, %d, %d, %d, %d> (K split %d ways, %lld workgroups)",
+                      c.tm, c.nwv, c.ns, c.kg, c.kw, c.splits, (long long)(w4a16_sk_tiles(M, N, c) * c.splits));
         g_kernel_name = buf;
     }
     return g_kernel_name.c_str();

@@ -8,14 +8,18 @@
 
 namespace mcv {
 
-// Tile TM rows x 32 * nwv columns (nwv waves, one 32-column half-slab each),
-// ns stages in flight, K split `splits` ways across workgroups (splits must
-// divide K / 128).
+// Tile TM rows x 32 * nwv columns (nwv half-slabs of 32 columns), ns stages
+// in flight, K split `splits` ways across workgroups, kg quantisation groups
+// (128 k each) per stage (kg must divide the groups of every split:
+// K / 128 / splits), kw k-parts: nwv * kw waves, k-part j taking group j of
+// every stage (kw = 2 needs kg = 2), their sums added in LDS at the end.
 struct SkConfig {
     int tm;
     int nwv;
     int ns;
     int splits;
+    int kg = 1;
+    int kw = 1;
 };
 
 // The workspace starts with the tile arrival counters, a fixed region for

@@ -4,38 +4,45 @@
 // out[M][N] = x[M][K] . W[K][N], W in the slab-64 int4 layout, fp32
 // accumulation, fp16 RNE output.
 //
-// Workgroup: NWV waves; wave w owns the 32-column half-slab w of the tile
-// (columns 32 w .. 32 w + 31) over all TM rows: TM/32 blocks of
-// v_mfma_f32_32x32x16_f16, so every widened weight operand feeds TM/32 MFMAs
-// (the widening is ~15 VALU per k16 step per wave, the same per MFMA as a
-// full-slab wave over the same rows).  Tile TM x 32 NWV.  Each wave reads all
-// TM x-rows of every k16 step from LDS, twice the LDS reads per MFMA of a
-// full-slab wave: gfx950's LDS serves them (measured ds_read_b128 throughput
-// ~340 GB/s per CU from four waves, ~500 from eight, against ~100 GB/s per CU
-// that the whole kernel needs).
+// Workgroup: NWV x KW waves; wave w owns the 32-column half-slab w % NWV of
+// the tile (columns 32 (w % NWV) .. + 31) over all TM rows, for k-part
+// w / NWV: TM/32 blocks of v_mfma_f32_32x32x16_f16, so every widened weight
+// operand feeds TM/32 MFMAs (the widening is ~15 VALU per k16 step per wave,
+// the same per MFMA as a full-slab wave over the same rows).  Tile TM x
+// 32 NWV.  Each wave reads all TM x-rows of every k16 step from LDS, twice
+// the LDS reads per MFMA of a full-slab wave: gfx950's LDS serves them
+// (measured ds_read_b128 throughput ~340 GB/s per CU from four waves, ~500
+// from eight, against ~100 GB/s per CU that the whole kernel needs).
 //
-// K advances in stages of 128 (one quantisation group, so a lane's scale and
-// zero are constant over a stage).  Per stage, every wave copies global ->
-// LDS with gfx950's direct-to-LDS buffer loads (no VGPR staging), P copies
-// of 1 KiB (or 4 B per lane for zero and scale words), spread over the k16
-// steps of the stage NS - 1 earlier:
-//   - x rows (TM x 256 bytes), 4 rows per copy, the 16-byte chunk index XORed
-//     with the row's low 4 bits (by choosing which global chunk each lane
-//     fetches), so one ds_read_b128 pass over 16 rows at one k offset covers
-//     all banks; rows past M read as zero;
+// K advances in stages of KG quantisation groups (128 k each; a lane's scale
+// and zero are constant over a group).  With KW = 2 (KG = 2) k-part j takes
+// group j of every stage and the two partial sums meet in LDS after the
+// loop: the copies of a stage then come from eight waves, two per SIMD, so
+// one wave's MFMAs run while the other issues copies (MI355X: an LDS-DMA
+// load from a wave that also issues MFMAs holds that wave ~90 ns; a second
+// wave on the SIMD hides it).  Per stage, the waves copy global -> LDS with
+// gfx950's direct-to-LDS buffer loads (no VGPR staging; staging through
+// registers measured no faster), P copies per wave of 1 KiB (or 4 B per
+// lane for zero and scale words), spread over the k16 steps of the stage
+// NS - 1 earlier:
+//   - x rows (TM x 256 KG bytes), 4 / KG rows per copy, the 16-byte chunk
+//     index XORed with the row's low 4 bits (by choosing which global chunk
+//     each lane fetches), so one ds_read_b128 pass over 16 rows at one k
+//     offset covers all banks; rows past M read as zero;
 //   - the packed chunks of the tile's slabs (32 k x 64 columns, 1 KiB each,
 //     contiguous in the slab layout) verbatim;
 //   - the slabs' zero words (lanes 0-7) and scales (lanes 0-31, two per
-//     dword) of the stage's group.
+//     dword) of the stage's groups.
 // A lane of half-slab h reads column 32 h + l%32 of its slab: per 32-k chunk
 // the two 4-byte words of its k-octet parity (l/32) with one ds_read2_b32,
-// eight words per stage, one per k16 step, each widened into the 8-value
+// eight words per group, one per k16 step, each widened into the 8-value
 // fp16 operand RNE((q - z) * s) -- the values mcv_w4a16_dequant materialises
 // ((1024 + q) - (1024 + z) exact through the fp16 exponent, times s, one
 // rounding).
 //
 // K split (S > 1): workgroup (tile, p) runs k-groups [p G/S, (p+1) G/S).
-// Each writes its fp32 partial tile to the workspace with device-scope
+// Each writes its fp32 partial tile (after the k-parts' sum) to the
+// workspace with device-scope
 // stores (written through to the point of coherence of all XCDs; a plain
 // store plus one device-scope release, an L2 write-back, measured 1.5-2x
 // slower on MI355X), waits for them, and adds 1 to the tile's arrival
@@ -89,35 +96,48 @@ __device__ __forceinline__ int xcd_run(int b, int total) {
     return x * per + (x < rem ? x : rem) + i;
 }
 
-template <int TM, int NWV, int NS>
+template <int TM, int NWV, int NS, int KG, int KW>
 struct CfgS {
     static constexpr int WS = NWV / 2;                   // slabs per tile
     static constexpr int TN = 32 * NWV;                  // columns per tile
+    static constexpr int NWT = NWV * KW;                 // waves: NWV half-slabs x KW k-parts
     static constexpr int MB = TM / 32;                   // 32-row blocks per wave
-    static constexpr int A_BYTES = TM * 256;             // x rows, 128 k of fp16
-    static constexpr int B_BYTES = WS * 4 * kLine;       // packed chunks
-    static constexpr int Z_OFF = A_BYTES + B_BYTES;      // per slab: 8 zero words at +0, 32 scale words at +256
-    static constexpr int STAGE = Z_OFF + WS * 512;
-    static constexpr int PA = (TM / 4) / NWV;            // x copies per wave per stage
-    static constexpr int PB = (4 * WS) / NWV;            // chunk copies per wave: 2
-    static constexpr int PZ = (2 * WS) / NWV;            // zero-or-scale copies per wave: 1
+    static constexpr int RP = 256 * KG;                  // bytes of one x row per stage (KG groups of 128 k)
+    static constexpr int GW = KG / KW;                   // groups of a stage per wave
+    static constexpr int STEPS = 8 * GW;                 // k16 steps per stage per wave
+    static constexpr int A_BYTES = TM * RP;              // x rows
+    static constexpr int B_BYTES = WS * 4 * KG * kLine;  // packed chunks, per slab group-major
+    static constexpr int Z_OFF = A_BYTES + B_BYTES;      // per group and slab: 8 zero words at +0, 32 scale words at +256
+    static constexpr int STAGE = Z_OFF + KG * WS * 512;
+    // copy items of a stage, spread evenly over all NWT waves
+    static constexpr int PA = (TM * RP / kLine) / NWT;   // x rows, 1 KiB each
+    static constexpr int PB = (4 * KG * WS) / NWT;       // packed chunks, 1 KiB each
+    static constexpr int PZ = (2 * KG * WS) / NWT;       // zero words or scales of one (group, slab)
     static constexpr int P = PA + PB + PZ;
+    // after the K loop each wave owns OB of the tile's MB row blocks of its
+    // half-slab (k-part kp owns blocks kp * OB ..), the KW partial sums added
+    static constexpr int OB = MB >= KW ? MB / KW : 1;
     static_assert(TM == 32 || TM == 64 || TM == 128, "TM");
     static_assert(NWV == 4 || NWV == 8, "NWV");
-    static_assert(PA * NWV == TM / 4 && PB == 2 && PZ == 1, "copies split evenly over the waves");
+    static_assert(KG == 1 || KG == 2, "KG");
+    static_assert(KW == 1 || (KW == 2 && KG == 2 && NWV == 4), "KW: each k-part takes one group of a stage");
+    static_assert(PA * NWT * kLine == TM * RP && PB * NWT == 4 * KG * WS && PZ * NWT == 2 * KG * WS,
+                  "copies split evenly over the waves");
+    static_assert((4 * KG) % PB == 0 && KG % PZ == 0, "a wave's chunk copies share one slab, its zero/scale copies one kind");
     static_assert(NS >= 2 && NS <= 4 && P * (NS - 1) < 64, "stages");
     static_assert(NS * STAGE <= 160 * 1024, "LDS");
     static constexpr int RB = TN * 2 + 16;               // padded bytes of one staged output row
     static constexpr int RPA = (STAGE / RB) / 32 * 32 < TM ? (STAGE / RB) / 32 * 32 : TM;   // staged rows per stage buffer
     static_assert(RPA >= 32 && (TM + RPA - 1) / RPA <= NS, "epilogue staging space");
+    static_assert(KW == 1 || NWV * MB * 16 * 64 * 4 <= STAGE, "k-part exchange space");
 };
 
-template <int TM, int NWV, int NS>
-__global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
+template <int TM, int NWV, int NS, int KG, int KW>
+__global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int M, int K, int N,
     int nslab, int m_tiles, int n_tiles, int S, int col_major, uint8_t* __restrict__ ws, uint32_t ws_bytes) {
-    using C = CfgS<TM, NWV, NS>;
+    using C = CfgS<TM, NWV, NS, KG, KW>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds2[NS > 2 ? C::STAGE : 16];
@@ -126,7 +146,9 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     uint8_t* const bufs[4] = {lds0, lds1, lds2, lds3};
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // 0 .. NWT-1: copies
+    const int hw = wave % NWV;                           // half-slab of the tile: compute and output
+    const int kp = wave / NWV;                           // k-part: groups kp * GW .. of every stage
     const int h = lane >> 5;
 
     // (tile, split): the split index is the slowest, then the tile order --
@@ -143,7 +165,7 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     const int CK = K / kChunkK;
     const int G = K / kGroup;
     const int g0 = static_cast<int>(int64_t(p) * G / S);
-    const int KT = static_cast<int>(int64_t(p + 1) * G / S) - g0;   // stages of this split
+    const int KT = (static_cast<int>(int64_t(p + 1) * G / S) - g0) / KG;   // stages of this split
 
     const int rows_here = M - m0 < TM ? M - m0 : TM;
     const __amdgpu_buffer_rsrc_t xr =
@@ -162,33 +184,45 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     uint32_t xoff[C::PA];
 #pragma unroll
     for (int j = 0; j < C::PA; ++j) {
-        const int row = 4 * (wave * C::PA + j) + (lane >> 4);
-        xoff[j] = static_cast<uint32_t>(row * K) * 2u + static_cast<uint32_t>((lane & 15) ^ (row & 15)) * 16u;
+        // copy j of this wave: 4 / KG rows of RP bytes
+        constexpr int kRowsPerCopy = kLine / C::RP, kLanesPerRow = 64 / kRowsPerCopy;
+        const int row = kRowsPerCopy * (wave * C::PA + j) + lane / kLanesPerRow;
+        const int chunk = lane % kLanesPerRow;
+        xoff[j] = static_cast<uint32_t>(row * K) * 2u + static_cast<uint32_t>(chunk ^ (row & 15)) * 16u;
     }
-    // chunks 2 (wave & 1), +1 of slab wave / 2 (PB = 2: the slab's four chunks
-    // over its two waves)
-    const int bslab = tn * C::WS + (wave >> 1);
+    // chunk items wave * PB .. + PB - 1 of the stage's 4 KG WS: slab t / (4 KG),
+    // chunk t % (4 KG) of that slab's stage (group c / 4, 32-k chunk c % 4)
+    const int bitem = wave * C::PB;
+    const int bslab_t = bitem / (4 * KG);
+    const int bslab = tn * C::WS + bslab_t;
     const bool bslab_live = bslab < nslab;
     const uint32_t qoff = (static_cast<uint32_t>(bslab) * CK * kSlab * 16u + lane * 16u) | (bslab_live ? 0u : 0x80000000u);
-    const int bchunk = 2 * (wave & 1);
-    // zero words (even wave) or scales (odd wave) of slab wave / 2
-    const bool zkind = (wave & 1) == 0;
-    const uint32_t zsoff = zkind ? ((static_cast<uint32_t>(bslab) * 32u + lane * 4u) | (lane < 8 && bslab_live ? 0u : 0x80000000u))
-                                 : ((static_cast<uint32_t>(bslab) * 128u + lane * 4u) | (lane < 32 && bslab_live ? 0u : 0x80000000u));
+    const int bchunk = bitem % (4 * KG);
+    // zero/scale items wave * PZ .. + PZ - 1 of the stage's 2 KG WS: slab
+    // t / (2 KG), then zero words (kind 0) or scales (kind 1), then group
+    const int zitem = wave * C::PZ;
+    const int zslab_t = zitem / (2 * KG);
+    const int zslab = tn * C::WS + zslab_t;
+    const bool zslab_live = zslab < nslab;
+    const bool zkind = (zitem % (2 * KG)) / KG == 0;
+    const int zgrp = zitem % KG;                         // first group of this wave's items
+    const uint32_t zsoff = zkind ? ((static_cast<uint32_t>(zslab) * 32u + lane * 4u) | (lane < 8 && zslab_live ? 0u : 0x80000000u))
+                                 : ((static_cast<uint32_t>(zslab) * 128u + lane * 4u) | (lane < 32 && zslab_live ? 0u : 0x80000000u));
     const int zsstride = zkind ? (Npad >> 3) * 4 : Npad * 2;
     const __amdgpu_buffer_rsrc_t zsr = zkind ? zr : sr;
-    const int zsdst = C::Z_OFF + (wave >> 1) * 512 + (zkind ? 0 : 256);
+    const int zsdst = C::Z_OFF + zslab_t * 512 + (zkind ? 0 : 256);   // + group * WS * 512
 
     auto issue_item = [&](int kt, uint8_t* dst, int it) {
         const int kc = kt < KT ? kt : KT - 1;
-        const int g = g0 + kc;
+        const int g = g0 + kc * KG;                      // the stage's first group
         if (it < C::PA) {
             dma16_s(xr, dst + (wave * C::PA + it) * kLine, xoff[it], g * 256);
         } else if (it < C::PA + C::PB) {
             const int c = bchunk + (it - C::PA);
-            dma16_s(qr, dst + C::A_BYTES + ((wave >> 1) * 4 + c) * kLine, qoff, (g * 4 + c) * kSlab * 16);
+            dma16_s(qr, dst + C::A_BYTES + (bslab_t * 4 * KG + c) * kLine, qoff, (g * 4 + c) * kSlab * 16);
         } else {
-            dma4_s(zsr, dst + zsdst, zsoff, g * zsstride);
+            const int j = zgrp + (it - C::PA - C::PB);   // group j of the stage
+            dma4_s(zsr, dst + zsdst + j * C::WS * 512, zsoff, (g + j) * zsstride);
         }
     };
     auto issue = [&](int kt, uint8_t* dst) {
@@ -199,7 +233,7 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     uint32_t vmagic;
     asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
     const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
-    const int col = 32 * (wave & 1) + (lane & 31);       // this lane's column inside its slab
+    const int col = 32 * (hw & 1) + (lane & 31);         // this lane's column inside its slab
     const uint32_t zsh = (col & 7) * 4;
 
     float16_t acc[C::MB];
@@ -208,21 +242,27 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
 
-    // x operand of k16 step s, block i: row 32 i + l%32, 16-byte chunk
-    // 2 s + l/32, XOR-swizzled by the row's low 4 bits; block i is 8 KiB on.
-    int a_off[8];
+    // x operand of this wave's k16 step s (step 8 kp GW + s of the stage),
+    // block i: row 32 i + l%32, 16-byte chunk 2 (8 kp GW + s) + l/32,
+    // XOR-swizzled by the row's low 4 bits; block i is 32 rows on.
+    int a_off[C::STEPS];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) a_off[s] = (lane & 31) * 256 + (((2 * s + h) ^ (lane & 15)) << 4);
-    // the lane's two words of chunk c: word h (k-octet 4c + h) and word 2 + h
-    const int b_off = C::A_BYTES + (wave >> 1) * 4 * kLine + col * 16 + h * 4;
-    const int z_off = C::Z_OFF + (wave >> 1) * 512 + (col >> 3) * 4;
-    const int s_off = C::Z_OFF + (wave >> 1) * 512 + 256 + col * 2;
+    for (int s = 0; s < C::STEPS; ++s)
+        a_off[s] = (lane & 31) * C::RP + (((2 * (8 * kp * C::GW + s) + h) ^ (lane & 15)) << 4);
+    // the lane's two words of chunk c: word h (k-octet 4c + h) and word 2 + h;
+    // this wave's chunks start at group kp GW of its slab's stage
+    const int b_off = C::A_BYTES + ((hw >> 1) * 4 * KG + 4 * kp * C::GW) * kLine + col * 16 + h * 4;
+    const int z_off = C::Z_OFF + kp * C::GW * C::WS * 512 + (hw >> 1) * 512 + (col >> 3) * 4;
+    const int s_off = C::Z_OFF + kp * C::GW * C::WS * 512 + (hw >> 1) * 512 + 256 + col * 2;
 
-    uint32_t q[8];                                       // the stage's eight words, one per k16 step
-    uint32_t zz = 0, ss = 0;
+    uint32_t q[C::STEPS];                                // the wave's words of a stage, one per k16 step
+    uint32_t zza[C::GW], ssa[C::GW];                     // per group of the wave's part of a stage
+#pragma unroll
+    for (int j = 0; j < C::GW; ++j) zza[j] = ssa[j] = 0;
     half8_t af[2][C::MB], bf[2];
     auto widen = [&](int s, half8_t& b) {
         const uint32_t w = q[s];
+        const uint32_t zz = zza[s / 8], ss = ssa[s / 8];
         uint32_t t[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) t[j] = and_or_b32(j ? w >> (4 * j) : w, mlo, vmagic);
@@ -239,20 +279,27 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     };
     auto read_a = [&](const uint8_t* src, int s, half8_t* dst) {
 #pragma unroll
-        for (int i = 0; i < C::MB; ++i) dst[i] = *reinterpret_cast<const half8_t*>(src + a_off[s] + i * 32 * 256);
+        for (int i = 0; i < C::MB; ++i) dst[i] = *reinterpret_cast<const half8_t*>(src + a_off[s] + i * 32 * C::RP);
     };
     auto head = [&](const uint8_t* src) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < 4 * C::GW; ++c) {
             const uint32_t* wp = reinterpret_cast<const uint32_t*>(src + b_off + c * kLine);
             q[2 * c] = wp[0];
             q[2 * c + 1] = wp[2];
         }
-        const uint32_t zw = *reinterpret_cast<const uint32_t*>(src + z_off);
-        const uint32_t sh = *reinterpret_cast<const uint16_t*>(src + s_off);
+        uint32_t zw[C::GW], sh[C::GW];
+#pragma unroll
+        for (int j = 0; j < C::GW; ++j) {
+            zw[j] = *reinterpret_cast<const uint32_t*>(src + z_off + j * C::WS * 512);
+            sh[j] = *reinterpret_cast<const uint16_t*>(src + s_off + j * C::WS * 512);
+        }
         read_a(src, 0, af[0]);
-        zz = (0x6400u + ((zw >> zsh) & 15u) + zero_bias) * 0x10001u;
-        ss = sh * 0x10001u;
+#pragma unroll
+        for (int j = 0; j < C::GW; ++j) {
+            zza[j] = (0x6400u + ((zw[j] >> zsh) & 15u) + zero_bias) * 0x10001u;
+            ssa[j] = sh[j] * 0x10001u;
+        }
     };
     auto mfmas = [&](int cur, int lo, int hi) {
 #pragma unroll
@@ -267,24 +314,25 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     // between its MFMAs (wait for the copies, barrier, the next stage's head).
     auto run_stage = [&](int kt, const uint8_t* cur, const uint8_t* nxt, uint8_t* prv) {
 #pragma unroll
-        for (int s = 0; s < 7; ++s) {
+        for (int s = 0; s < C::STEPS - 1; ++s) {
             const int c = s & 1, n = c ^ 1;
-            constexpr int kLo[8] = {0, C::P * 1 / 7, C::P * 2 / 7, C::P * 3 / 7, C::P * 4 / 7, C::P * 5 / 7,
-                                    C::P * 6 / 7, C::P};
+            // copies of this step: [lo, hi) of the stage's P, spread evenly
+            const int lo = C::P * s / (C::STEPS - 1), hi = C::P * (s + 1) / (C::STEPS - 1);
 #pragma unroll
-            for (int it = kLo[s]; it < kLo[s + 1]; ++it) issue_item(kt + NS - 1, prv, it);
+            for (int it = lo; it < hi; ++it) issue_item(kt + NS - 1, prv, it);
             read_a(cur, s + 1, af[n]);
             widen(s + 1, bf[n]);
             mfmas(c, 0, C::MB);
 #pragma unroll
             for (int i = 0; i < C::MB; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  // DS read
-                if (i < kLo[s + 1] - kLo[s]) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // copy
+                if (i < hi - lo) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // copy
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, kV, 0);                 // VALU
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        static_assert(C::STEPS % 2 == 0, "the last step uses operand set 1");
         mfmas(1, 0, (C::MB + 1) / 2);
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -318,20 +366,58 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     // no copy may land in LDS after this point (the stage buffers are reused)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+    // ---- The wave's owned row blocks ib0 .. ib0 + OB - 1 of half-slab hw
+    // (all MB with one k-part).  With KW k-parts the partial sums meet in
+    // LDS: k-part 0's + k-part 1's, the same sum whichever wave adds it.
+    const int ib0 = KW > 1 && C::MB >= KW ? kp * C::OB : 0;
+    const bool owns = KW == 1 || C::MB >= KW || kp == 0;
+    float16_t own[C::OB];
+    if constexpr (KW == 1) {
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) own[i] = acc[i];
+    } else {
+        // [half-slab][block][register quad][lane] float4 in the first stage buffer
+        auto roff = [&](int i, int rq) { return ((hw * C::MB + i) * 4 + rq) * 1024 + lane * 16; };
+        __syncthreads();                                 // every wave is past its last operand read
+#pragma unroll
+        for (int i = 0; i < C::MB; ++i) {
+            const bool mine = owns && i >= ib0 && i < ib0 + C::OB;
+            if (!mine)
+#pragma unroll
+                for (int rq = 0; rq < 4; ++rq)
+                    *reinterpret_cast<float4*>(lds0 + roff(i, rq)) =
+                        make_float4(acc[i][4 * rq], acc[i][4 * rq + 1], acc[i][4 * rq + 2], acc[i][4 * rq + 3]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ii = 0; ii < C::OB; ++ii) {
+            const int i = ib0 + ii;
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const float4 o = *reinterpret_cast<const float4*>(lds0 + roff(i, rq));
+                own[ii][4 * rq] = acc[i][4 * rq] + o.x;
+                own[ii][4 * rq + 1] = acc[i][4 * rq + 1] + o.y;
+                own[ii][4 * rq + 2] = acc[i][4 * rq + 2] + o.z;
+                own[ii][4 * rq + 3] = acc[i][4 * rq + 3] + o.w;
+            }
+        }
+    }
+
     if (S > 1) {
         // ---- K split: publish this split's partial tile, the last arriver adds all S.
-        // Partial layout per (tile, split): [wave][block i][register quad rq][lane] float4.
+        // Partial layout per (tile, split): [half-slab][block i][register quad rq][lane] float4.
         constexpr uint32_t kPart = TM * C::TN * 4;
         const __amdgpu_buffer_rsrc_t wr = rsrc_s(ws, ws_bytes);
         unsigned* const counters = reinterpret_cast<unsigned*>(ws);
         const uint32_t base = kSkCounterBytes + static_cast<uint32_t>(tile * S) * kPart;
-        const uint32_t lo = (static_cast<uint32_t>(wave) * C::MB * 4) * 1024u + lane * 16u;
+        const uint32_t lo = (static_cast<uint32_t>(hw) * C::MB * 4 + ib0 * 4) * 1024u + lane * 16u;
 #pragma unroll
-        for (int i = 0; i < C::MB; ++i)
+        for (int i = 0; i < C::OB; ++i)
 #pragma unroll
             for (int rq = 0; rq < 4; ++rq) {
-                const int4_t v = {__float_as_int(acc[i][4 * rq]), __float_as_int(acc[i][4 * rq + 1]),
-                                  __float_as_int(acc[i][4 * rq + 2]), __float_as_int(acc[i][4 * rq + 3])};
+                if (!owns) continue;
+                const int4_t v = {__float_as_int(own[i][4 * rq]), __float_as_int(own[i][4 * rq + 1]),
+                                  __float_as_int(own[i][4 * rq + 2]), __float_as_int(own[i][4 * rq + 3])};
                 // device scope (sc1): written through to where every XCD reads it
                 __builtin_amdgcn_raw_buffer_store_b128(v, wr, lo + (i * 4 + rq) * 1024u, base + p * kPart, 16);
             }
@@ -348,14 +434,14 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
         // sum in split order 0 .. S-1, this split's own partial from
         // registers; the next partial's loads are in flight while the
         // current one is added
-        auto fetch = [&](int q2, float16_t (&dst)[C::MB]) {
+        auto fetch = [&](int q2, float16_t (&dst)[C::OB]) {
             if (q2 == p) {
 #pragma unroll
-                for (int i = 0; i < C::MB; ++i) dst[i] = acc[i];
+                for (int i = 0; i < C::OB; ++i) dst[i] = own[i];
                 return;
             }
 #pragma unroll
-            for (int i = 0; i < C::MB; ++i)
+            for (int i = 0; i < C::OB; ++i)
 #pragma unroll
                 for (int rq = 0; rq < 4; ++rq) {
                     const int4_t t =
@@ -364,12 +450,12 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
                     for (int e = 0; e < 4; ++e) dst[i][4 * rq + e] = __int_as_float(t[e]);
                 }
         };
-        float16_t sum[C::MB], cur[C::MB], nxt[C::MB];
-        fetch(0, cur);
-        for (int q2 = 0; q2 < S; ++q2) {
+        float16_t sum[C::OB], cur[C::OB], nxt[C::OB];
+        if (owns) fetch(0, cur);
+        for (int q2 = 0; q2 < S && owns; ++q2) {
             if (q2 + 1 < S) fetch(q2 + 1, nxt);
 #pragma unroll
-            for (int i = 0; i < C::MB; ++i) {
+            for (int i = 0; i < C::OB; ++i) {
                 if (q2 == 0) {
                     sum[i] = cur[i];
                 } else {
@@ -379,19 +465,21 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
                 cur[i] = nxt[i];
             }
         }
+        if (owns)
 #pragma unroll
-        for (int i = 0; i < C::MB; ++i) acc[i] = sum[i];
+            for (int i = 0; i < C::OB; ++i) own[i] = sum[i];
     }
 
-    // ---- fp16 epilogue.  Block i: register r of lane l holds output row
-    // 32 i + l%32 and column 8 (r/4) + 4 (l/32) + r%4 of the wave's 32;
-    // swapping the upper lanes of quad g with the lower lanes of quad g+1
-    // leaves lane l with the 8 consecutive columns 8 g + 8 (l/32), g even.
-    auto pack = [&](int i, int g, uint32_t (&pk)[4]) {
+    // ---- fp16 epilogue.  Owned block ii (row block ib0 + ii): register r of
+    // lane l holds output row 32 (ib0 + ii) + l%32 and column 8 (r/4) +
+    // 4 (l/32) + r%4 of the half-slab's 32; swapping the upper lanes of quad g
+    // with the lower lanes of quad g+1 leaves lane l with the 8 consecutive
+    // columns 8 g + 8 (l/32), g even.
+    auto pack = [&](int ii, int g, uint32_t (&pk)[4]) {
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
-            const uint32_t x0 = f2h(acc[i][4 * g + 2 * d]) | (uint32_t(f2h(acc[i][4 * g + 2 * d + 1])) << 16);
-            const uint32_t x1 = f2h(acc[i][4 * g + 4 + 2 * d]) | (uint32_t(f2h(acc[i][4 * g + 5 + 2 * d])) << 16);
+            const uint32_t x0 = f2h(own[ii][4 * g + 2 * d]) | (uint32_t(f2h(own[ii][4 * g + 2 * d + 1])) << 16);
+            const uint32_t x1 = f2h(own[ii][4 * g + 4 + 2 * d]) | (uint32_t(f2h(own[ii][4 * g + 5 + 2 * d])) << 16);
             const auto sw = __builtin_amdgcn_permlane32_swap(x0, x1, false, false);
             pk[d] = sw[0];
             pk[2 + d] = sw[1];
@@ -410,17 +498,19 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
             return (a == 0 ? lds0 : a == 1 ? lds1 : a == 2 ? lds2 : lds3) + (r - a * C::RPA) * C::RB;
         };
 #pragma unroll
-        for (int i = 0; i < C::MB; ++i)
+        for (int ii = 0; ii < C::OB; ++ii)
 #pragma unroll
             for (int g = 0; g < 4; g += 2) {
+                if (!owns) continue;
                 uint32_t pk[4];
-                pack(i, g, pk);
-                *reinterpret_cast<uint4*>(srow(32 * i + (lane & 31)) + (32 * wave + 8 * g + 8 * h) * 2) =
+                pack(ii, g, pk);
+                *reinterpret_cast<uint4*>(srow(32 * (ib0 + ii) + (lane & 31)) + (32 * hw + 8 * g + 8 * h) * 2) =
                     make_uint4(pk[0], pk[1], pk[2], pk[3]);
             }
         __syncthreads();
         constexpr int CPR = C::TN / 8;                   // 16-byte chunks per row
-        constexpr int RPI = 64 * NWV / CPR;              // rows per workgroup-wide pass
+        constexpr int RPI = 64 * C::NWT / CPR;           // rows per workgroup-wide pass
+        static_assert(TM % RPI == 0, "row passes");
         const int cl = static_cast<int>(threadIdx.x) % CPR, rl = static_cast<int>(threadIdx.x) / CPR;
 #pragma unroll
         for (int it = 0; it < TM / RPI; ++it) {
@@ -436,13 +526,14 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
     }
     // N not a multiple of 8 (or an unaligned output): element stores
 #pragma unroll
-    for (int i = 0; i < C::MB; ++i) {
-        const int row = m0 + 32 * i + (lane & 31);
+    for (int ii = 0; ii < C::OB; ++ii) {
+        if (!owns) break;
+        const int row = m0 + 32 * (ib0 + ii) + (lane & 31);
 #pragma unroll
         for (int g = 0; g < 4; g += 2) {
             uint32_t pk[4];
-            pack(i, g, pk);
-            const int c0 = n0 + 32 * wave + 8 * g + 8 * h;
+            pack(ii, g, pk);
+            const int c0 = n0 + 32 * hw + 8 * g + 8 * h;
             if (row >= M || c0 >= N) continue;
             uint16_t* dst = out + static_cast<size_t>(row) * N + c0;
 #pragma unroll
@@ -455,11 +546,13 @@ __global__ __launch_bounds__(64 * NWV) void w4a16_gemm_sk_kernel(
 using SkFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int,
                       int, int, int, int, int, int, uint8_t*, uint32_t);
 
-#define MCV_SK_SHAPES(X) X(128, 8, 3) X(128, 4, 3) X(64, 8, 3) X(64, 4, 3) X(32, 4, 3)
+#define MCV_SK_SHAPES(X)                                                                               \
+    X(128, 8, 3, 1, 1) X(128, 4, 3, 1, 1) X(64, 8, 3, 1, 1) X(64, 4, 3, 1, 1) X(32, 4, 3, 1, 1) X(64, 4, 3, 2, 1) \
+    X(32, 4, 3, 2, 1) X(64, 4, 3, 2, 2) X(32, 4, 3, 2, 2)
 
-SkFn pick_sk(int tm, int nwv, int ns) {
-#define MCV_SK_PICK(a, b, c) \
-    if (tm == a && nwv == b && ns == c) return w4a16_gemm_sk_kernel<a, b, c>;
+SkFn pick_sk(int tm, int nwv, int ns, int kg, int kw) {
+#define MCV_SK_PICK(a, b, c, d, e) \
+    if (tm == a && nwv == b && ns == c && kg == d && kw == e) return w4a16_gemm_sk_kernel<a, b, c, d, e>;
     MCV_SK_SHAPES(MCV_SK_PICK)
 #undef MCV_SK_PICK
     return nullptr;
@@ -478,19 +571,21 @@ int64_t w4a16_sk_workspace_bytes(int64_t M, int64_t N, const SkConfig& c) {
 }
 
 bool w4a16_sk_config_valid(int64_t M, int64_t K, int64_t N, const SkConfig& c) {
-    return pick_sk(c.tm, c.nwv, c.ns) != nullptr && c.splits >= 1 && c.splits <= 64 && K % kGroup == 0 &&
-           (K / kGroup) % c.splits == 0 && (c.splits == 1 || w4a16_sk_tiles(M, N, c) <= kSkMaxSplitTiles);
+    return pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw) != nullptr && c.splits >= 1 && c.splits <= 64 && K % kGroup == 0 &&
+           (K / kGroup) % c.splits == 0 && (K / kGroup / c.splits) % c.kg == 0 &&
+           (c.splits == 1 || w4a16_sk_tiles(M, N, c) <= kSkMaxSplitTiles);
 }
 
 int launch_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                          const void* zeros, int zero_bias, void* out, const SkConfig& c, void* ws, int64_t ws_bytes,
                          hipStream_t stream) {
-    SkFn fn = pick_sk(c.tm, c.nwv, c.ns);
+    SkFn fn = pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw);
     if (fn == nullptr || !w4a16_sk_config_valid(M, K, N, c))
         return fail(MCV_ERR_INVALID_ARG,
-                    "w4a16 GEMM: no split-K kernel for TM=%d waves=%d NS=%d S=%d at M=%lld K=%lld N=%lld (S must divide "
-                    "K/128, and a split needs at most %d tiles)",
-                    c.tm, c.nwv, c.ns, c.splits, (long long)M, (long long)K, (long long)N, kSkMaxSplitTiles);
+                    "w4a16 GEMM: no kernel for TM=%d waves=%d NS=%d KG=%d KW=%d S=%d at M=%lld K=%lld N=%lld (S must "
+                    "divide K/128, KG the groups of a split, and a split needs at most %d tiles)",
+                    c.tm, c.nwv, c.ns, c.kg, c.kw, c.splits, (long long)M, (long long)K, (long long)N,
+                    kSkMaxSplitTiles);
     const int64_t nslab = ceil_div(N, kSlab);
     const int64_t m_tiles = ceil_div(M, c.tm), n_tiles = ceil_div(nslab, c.nwv / 2);
     const int64_t total = m_tiles * n_tiles * c.splits;
@@ -504,7 +599,7 @@ int launch_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const v
         int64_t(c.tm) * K * 2 >= (int64_t(1) << 31) || need >= (int64_t(1) << 31))
         return fail(MCV_ERR_SHAPE, "w4a16 GEMM: problem too large (M=%lld N=%lld)", (long long)M, (long long)N);
     const int col_major = M < N ? 1 : 0;
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(total)), dim3(64 * c.nwv), 0, stream,
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(total)), dim3(64 * c.nwv * c.kw), 0, stream,
                        static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
                        static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(out), static_cast<int>(M),
@@ -526,8 +621,9 @@ int64_t mcv_w4a16_gemm_sk_workspace_bytes(int64_t M, int64_t N, int tm, int wave
 }
 
 int mcv_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
-                      const void* zeros, int zero_bias, void* out, int tm, int waves, int stages, int splits,
-                      void* workspace, int64_t workspace_bytes, mcv_stream_t stream) {
+                      const void* zeros, int zero_bias, void* out, int tm, int waves, int stages,
+                      int groups_per_stage, int k_parts, int splits, void* workspace, int64_t workspace_bytes,
+                      mcv_stream_t stream) {
     if (!x || !out || !qw || !scales || !zeros) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: null pointer");
     if (zero_bias != 0 && zero_bias != 1) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: zero_bias must be 0 or 1");
     if (K <= 0 || K % kGroup != 0 || M <= 0 || M > (int64_t(1) << 30) || N <= 0 || N > (int64_t(1) << 30))
@@ -536,8 +632,9 @@ int mcv_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: x must be 16-byte aligned");
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    return launch_w4a16_gemm_sk(x, M, K, N, qw, scales, zeros, zero_bias, out, SkConfig{tm, waves, stages, splits},
-                                workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+    return launch_w4a16_gemm_sk(x, M, K, N, qw, scales, zeros, zero_bias, out,
+                                SkConfig{tm, waves, stages, splits, groups_per_stage, k_parts}, workspace, workspace_bytes,
+                                static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"
