@@ -339,7 +339,8 @@ class Gemv1(Cfg):
 
     def gpu(self):
         pkg, ws, xd, out = self.pkg, self.ws, self.xd, self.out
-        return gpu_result(self.name, "w4a16_gemv_kernel<8,1,none>", self.bytes, "GB/s", "hbm",
+        kernel = pkg.lib().mcv_w4a16_gemm_kernel_name(1, self.K, self.N, 0).decode()
+        return gpu_result(self.name, kernel, self.bytes, "GB/s", "hbm",
                           lambda i: pkg.matmul_w4a16(xd, ws[i], out), len(ws), 200,
                           {"config": {"M": 1, "K": self.K, "N": self.N, "weight_sets_rotated": len(ws),
                                       "algorithmic_bytes": self.bytes}})
@@ -866,7 +867,23 @@ def _copy(pkg, args):
             **gpu_result("copy", "torch copy kernel", 2 * n, "GB/s", "hbm", lambda i: dst.copy_(src[i]), 4, 100)}
 
 
+def _tiny(pkg, args):
+    """The per-dispatch cost of the kernel trace itself: the library's
+    smallest kernel (silu_mul over 64 elements, one workgroup) back to back.
+    Its duration is almost all launch and completion, so the difference
+    between this line's us_per_call and a rocprofv3 --kernel-trace average of
+    the same command is the trace's own per-dispatch cost."""
+    import torch
+    g = torch.zeros(64, dtype=torch.float16, device="cuda")
+    u = torch.zeros(64, dtype=torch.float16, device="cuda")
+    o = torch.empty(64, dtype=torch.float16, device="cuda")
+    return {"workload": "tiny_kernel_dispatch",
+            **gpu_result("tiny", "silu_mul_kernel (64 elements)", 64 * 6, "GB/s", "hbm",
+                         lambda i: pkg.silu_mul(g, u, o), 1, 200)}
+
+
 EXTRA = {
+    "tiny": _tiny,
     "mlp_2launch": lambda p, a: _mlp_variant(p, a, "two"),
     "mlp_unfused": lambda p, a: _mlp_variant(p, a, "unfused"),
     "mlp_w8a8": lambda p, a: _mlp_w8a8(p, a, "block"),

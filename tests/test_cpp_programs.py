@@ -64,8 +64,17 @@ def test_cpp_matmul_w8a8_i32():
 
 
 @pytest.mark.gpu
-def test_cpp_w8a8_dequant():
-    run("test_w8a8_dequant")
+def test_cpp_w8a8_dequant(tmp_path):
+    """The reference's deterministic dequant vectors (the committed fixture)
+    through the C++ surface, as raw files the program reads."""
+    import numpy as np
+    g = np.load(Path(__file__).resolve().parent / "golden" / "w8a8_dequant_reference.npz")
+    g["acc"].reshape(-1).astype("<i4").tofile(tmp_path / "acc.i32")
+    g["ws16"].reshape(-1).astype("<u2").tofile(tmp_path / "ws.f16")
+    g["xs16"].reshape(-1).astype("<u2").tofile(tmp_path / "xs.f16")
+    g["out16"].reshape(-1).astype("<u2").tofile(tmp_path / "out.f16")
+    out = run("test_w8a8_dequant", str(tmp_path))
+    assert out.strip().endswith("ok")
 
 
 @pytest.mark.gpu
