@@ -601,7 +601,8 @@ def lm_head_entry(lm, args, route, steps, cpu_entry):
     ms = total_ms / steps
     value = lm.bytes / (ms / 1e3) / 1e9
     spw = lm.pkg.lm_head_slabs_per_workgroup(lm.V)
-    kernel = f"w4a16_lm_head_kernel<{spw},{'kLmTree' if route == 'tree' else 'kLmSlots'}> (GEMV + fused argmax)"
+    kernel = (f"w4a16_lm_head_kernel<{spw}, {0 if route == 'tree' else 1}> (GEMV + fused argmax, "
+              f"{'device-token' if route == 'tree' else 'host-finished slots'} route)")
     entry = {"kernel": kernel, "us_per_call": round(ms * 1e3, 3), "value": round(value, 2), "unit": "GB/s",
              "kernel_us_median": round(float(np.median(pl)) * 1e3, 3),
              "kernel_us_mean": round(float(pl.mean()) * 1e3, 3), "per_launch_samples": int(pl.size),

@@ -513,8 +513,10 @@ int mcv_w8a8_pack_tiled_nk_host(const int8_t* q_nk_host, int64_t K, int64_t N, i
 
 /* The kernel the W8A8 GEMM entry points launch for M x K x N with a weight in
  * `w_layout` (fp16 output through the fused epilogue when out_f16, else
- * int32), as text, for labels in reports; valid until the next call on this
- * thread.  No reference counterpart. */
+ * int32), as text with its template arguments as a kernel trace names them
+ * (the epilogue argument as launched with fp32 scales), for labels in
+ * reports; valid until the next call on this thread.  No reference
+ * counterpart. */
 const char* mcv_w8a8_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int w_layout, int out_f16);
 
 /* ------------------------------------------------------------ elementwise -- */

@@ -37,22 +37,23 @@ bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N
 // widths), with a workspace, K is split across workgroups on 32 x 128 tiles:
 // the most ways that keep the grid within one workgroup per CU and at least
 // seven 128-k stages per workgroup (the partial tiles' exchange costs ~1-2 us,
-// which a shorter loop does not pay back).  A workgroup with a long K loop
-// (14 or more groups, an even count) on a four-wave tile takes two k-parts
-// (eight waves, two groups per stage): two waves per SIMD cover each
-// other's copy issue, worth ~2% there and a loss on shorter loops.
-// Measured on MI355X (rotated weights, us per call, back to back): M=2048
-// K=1024 N=3584 128x256 21.3 (64x128 25.4); M=2048 K=3584 N=1024 64x128 two
-// k-parts 22.4 (one 22.8); M=512 K=1024 N=3584 64x128 9.0 (two k-parts 9.2);
-// M=512 K=3584 N=1024 32x128 split 2 ways, two k-parts 12.5 (one 12.8,
-// unsplit 16.5, 4 ways 14.1); M=128 K=1024 N=3584 32x128 7.1 (2 ways 7.9);
-// M=128 K=3584 N=1024 32x128 split 4 ways 9.9 (7 ways 11.1).
+// which a shorter loop does not pay back).  A four-wave tile takes two
+// k-parts (eight waves, two groups per stage) when its workgroups' group
+// count is even and at least 8 (64-row tiles) or 14 (32-row tiles): two
+// waves per SIMD cover each other's copy issue, a gain there and a loss on
+// the shorter loops of the thinner tiles.  Measured on MI355X (rotated
+// weights, us per call, back to back): M=2048 K=1024 N=3584 128x256 20.4
+// (64x128 25.4); M=2048 K=3584 N=1024 64x128 two k-parts 21.0 (one 23.2);
+// M=512 K=1024 N=3584 64x128 two k-parts 8.5 (one 8.8); M=512 K=3584 N=1024
+// 32x128 split 2 ways, two k-parts 12.0 (one 12.4, unsplit 15.8, 4 ways
+// 13.5); M=128 K=1024 N=3584 32x128 6.9 (two k-parts 7.0, 2 ways 7.8); M=128
+// K=3584 N=1024 32x128 split 4 ways 9.7 (7 ways 10.8).
 SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
     constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {32, 4, 3, 1}};
     const int64_t G = K / kGroup;
     auto k_parts = [&](SkConfig c) {
         const int64_t per = G / c.splits;
-        if (c.nwv == 4 && c.tm <= 64 && per >= 14 && per % 2 == 0) c.kg = c.kw = 2;
+        if (c.nwv == 4 && per % 2 == 0 && ((c.tm == 64 && per >= 8) || (c.tm == 32 && per >= 14))) c.kg = c.kw = 2;
         return c;
     };
     for (const SkConfig& c : kOne)

@@ -34,7 +34,9 @@
 //   - the slabs' zero words (lanes 0-7) and scales (lanes 0-31, two per
 //     dword) of the stage's groups.
 // A lane of half-slab h reads column 32 h + l%32 of its slab: per 32-k chunk
-// the two 4-byte words of its k-octet parity (l/32) with one ds_read2_b32,
+// the two 4-byte words of its k-octet parity (l/32) -- a pair of chunks in one
+// ds_read_b128 (the half-waves read one chunk each) and two v_permlane32_swap
+// (a lane-per-word read, 16 bytes apart, costs ~12 bank-conflict cycles) --
 // eight words per group, one per k16 step, each widened into the 8-value
 // fp16 operand RNE((q - z) * s) -- the values mcv_w4a16_dequant materialises
 // ((1024 + q) - (1024 + z) exact through the fp16 exponent, times s, one
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
         a_off[s] = (lane & 31) * C::RP + (((2 * (8 * kp * C::GW + s) + h) ^ (lane & 15)) << 4);
     // the lane's two words of chunk c: word h (k-octet 4c + h) and word 2 + h;
     // this wave's chunks start at group kp GW of its slab's stage
-    const int b_off = C::A_BYTES + ((hw >> 1) * 4 * KG + 4 * kp * C::GW) * kLine + col * 16 + h * 4;
+    const int b_off = C::A_BYTES + ((hw >> 1) * 4 * KG + 4 * kp * C::GW + h) * kLine + col * 16;
     const int z_off = C::Z_OFF + kp * C::GW * C::WS * 512 + (hw >> 1) * 512 + (col >> 3) * 4;
     const int s_off = C::Z_OFF + kp * C::GW * C::WS * 512 + (hw >> 1) * 512 + 256 + col * 2;
 
@@ -282,11 +284,19 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
         for (int i = 0; i < C::MB; ++i) dst[i] = *reinterpret_cast<const half8_t*>(src + a_off[s] + i * 32 * C::RP);
     };
     auto head = [&](const uint8_t* src) {
+        // Chunks c, c+1 (c even) in one conflict-free ds_read_b128: the lower
+        // half-wave reads column col of chunk c, the upper half of chunk c+1;
+        // two lane-half swaps then leave each lane its k-octet parity's words
+        // (h and 2 + h) of both chunks.
 #pragma unroll
-        for (int c = 0; c < 4 * C::GW; ++c) {
-            const uint32_t* wp = reinterpret_cast<const uint32_t*>(src + b_off + c * kLine);
-            q[2 * c] = wp[0];
-            q[2 * c + 1] = wp[2];
+        for (int c = 0; c < 4 * C::GW; c += 2) {
+            const uint4 w = *reinterpret_cast<const uint4*>(src + b_off + c * kLine);
+            const auto s0 = __builtin_amdgcn_permlane32_swap(w.x, w.y, false, false);
+            const auto s2 = __builtin_amdgcn_permlane32_swap(w.z, w.w, false, false);
+            q[2 * c] = s0[0];                            // word h of chunk c
+            q[2 * c + 2] = s0[1];                        // word h of chunk c + 1
+            q[2 * c + 1] = s2[0];                        // word 2 + h of chunk c
+            q[2 * c + 3] = s2[1];                        // word 2 + h of chunk c + 1
         }
         uint32_t zw[C::GW], sh[C::GW];
 #pragma unroll

@@ -560,8 +560,10 @@ ShapeL choose_l(int64_t M, int64_t N) {
 std::string w8a8_gemm_lds_name(int64_t M, int64_t N, bool f16) {
     const ShapeL s = choose_l(M, N);
     char buf[128];
-    std::snprintf(buf, sizeof(buf), "w8a8_gemm_lds_kernel<%d, %d, %d> (%s, %lld workgroups)", s.bm, s.bn, s.ns,
-                  f16 ? "fused fp16 epilogue" : "int32 out", (long long)(ceil_div(M, s.bm) * ceil_div(N, s.bn)));
+    // EPI as launched with fp32 scales (fp16 ones add 1 and 2)
+    std::snprintf(buf, sizeof(buf), "w8a8_gemm_lds_kernel<%d, %d, %d, %d> (%s, %lld workgroups)", s.bm, s.bn, s.ns,
+                  f16 ? 4 : 0, f16 ? "fused fp16 epilogue" : "int32 out",
+                  (long long)(ceil_div(M, s.bm) * ceil_div(N, s.bn)));
     return buf;
 }
 

@@ -228,8 +228,9 @@ std::string w8a8_tiled_name(int64_t M, int64_t K, int64_t N, bool f16) {
     const bool narrow = nslab < 128;
     const int nw = narrow && KB <= 64 ? 8 : 16, halves = narrow ? 1 : 2, u = narrow && KB <= 64 ? 4 : 2;
     char buf[160];
-    std::snprintf(buf, sizeof(buf), "w8a8_tiled_gemv_kernel<%lld, %d, %d, %d> (v_dot4, %s)", (long long)(M < 4 ? M : 4),
-                  nw, halves, u, f16 ? "fused fp16 epilogue" : "int32 out");
+    std::snprintf(buf, sizeof(buf), "w8a8_tiled_gemv_kernel<%lld, %d, %d, %d, %s, false, false> (v_dot4, %s)",
+                  (long long)(M < 4 ? M : 4), nw, halves, u, f16 ? "true" : "false",
+                  f16 ? "fused fp16 epilogue" : "int32 out");
     return buf;
 }
 
