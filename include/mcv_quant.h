@@ -183,7 +183,9 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
  * tile tm x 32 * waves (tm in {32, 64, 128}, waves in {4, 8}), `stages`
  * copy stages in flight of `groups_per_stage` quantisation groups (128 k)
  * each, `k_parts` waves per half-slab (1, or 2 with groups_per_stage 2:
- * each takes one group of every stage), K split `splits` ways across
+ * each takes one group of every stage), `weights_in_registers` 1 to load
+ * each wave's packed weights, zeros and scales straight into registers (the
+ * stage buffers in LDS then hold x rows only), K split `splits` ways across
  * workgroups (splits divides K / 128, groups_per_stage divides
  * K / 128 / splits), the partial tiles added inside the same launch by the
  * last workgroup of each tile, in split order (deterministic).  Splits > 1
@@ -197,8 +199,8 @@ int64_t mcv_w4a16_gemm_sk_workspace_bytes(int64_t M, int64_t N, int tm, int wave
 int mcv_w4a16_gemm_sk(const void* x_dev, int64_t M, int64_t K, int64_t N,
                       const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                       int zero_bias, void* out_dev, int tm, int waves, int stages,
-                      int groups_per_stage, int k_parts, int splits, void* workspace_dev,
-                      int64_t workspace_bytes, mcv_stream_t stream);
+                      int groups_per_stage, int k_parts, int weights_in_registers, int splits,
+                      void* workspace_dev, int64_t workspace_bytes, mcv_stream_t stream);
 
 /* The two kernels behind mcv_w4a16_gemm, callable directly (same contract). */
 int mcv_w4a16_gemv(const void* x_dev, int64_t M, int64_t K, int64_t N,

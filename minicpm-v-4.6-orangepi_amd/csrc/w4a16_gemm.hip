@@ -41,19 +41,26 @@ bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N
 // k-parts (eight waves, two groups per stage) when its workgroups' group
 // count is even and at least 8 (64-row tiles) or 14 (32-row tiles): two
 // waves per SIMD cover each other's copy issue, a gain there and a loss on
-// the shorter loops of the thinner tiles.  Measured on MI355X (rotated
-// weights, us per call, back to back): M=2048 K=1024 N=3584 128x256 20.4
-// (64x128 25.4); M=2048 K=3584 N=1024 64x128 two k-parts 21.0 (one 23.2);
-// M=512 K=1024 N=3584 64x128 two k-parts 8.5 (one 8.8); M=512 K=3584 N=1024
-// 32x128 split 2 ways, two k-parts 12.0 (one 12.4, unsplit 15.8, 4 ways
-// 13.5); M=128 K=1024 N=3584 32x128 6.9 (two k-parts 7.0, 2 ways 7.8); M=128
-// K=3584 N=1024 32x128 split 4 ways 9.7 (7 ways 10.8).
+// the shorter loops of the thinner tiles.  The 64- and 32-row tiles load
+// their weights, zeros and scales straight into registers (each wave's
+// columns are its own; LDS then stages x only): 0-9 % faster than staging
+// them in LDS in two sweeps, never slower; the 128 x 256 tile measured the
+// same either way and keeps the LDS path.  Measured on MI355X (rotated
+// weights, us per call, back to back; the same launch varies by up to +-7 %
+// from one 200-launch region to the next): M=2048 K=1024 N=3584 128x256
+// 20.0-20.5 (64x128 24-25); M=2048 K=3584 N=1024 64x128 two k-parts 19.6-19.8
+// (LDS weights 20.1-21.6, one k-part 21.6-22.6); M=512 K=1024 N=3584 64x128
+// two k-parts 8.4-8.5 (LDS weights 8.8); M=512 K=3584 N=1024 32x128 split 2
+// ways, two k-parts 11.5 (LDS weights 12.1, one k-part 12.4, unsplit 12.8-15.6,
+// 4 ways 13.6); M=128 K=1024 N=3584 32x128 6.9 (two k-parts 6.8-6.9, 2 ways
+// 7.8); M=128 K=3584 N=1024 32x128 split 4 ways 9.7 (7 ways 10.8).
 SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
     constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {32, 4, 3, 1}};
     const int64_t G = K / kGroup;
     auto k_parts = [&](SkConfig c) {
         const int64_t per = G / c.splits;
         if (c.nwv == 4 && per % 2 == 0 && ((c.tm == 64 && per >= 8) || (c.tm == 32 && per >= 14))) c.kg = c.kw = 2;
+        c.wr = c.tm != 128;
         return c;
     };
     for (const SkConfig& c : kOne)
@@ -143,8 +150,8 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
         g_kernel_name = buf;
     } else {
         const SkConfig c = choose_gemm(M, K, N, with_workspace != 0);
-        std::snprintf(buf, sizeof(buf), "w4a16_gemm_sk_kernel<%d, %d, %d, %d, %d> (K split %d ways, %lld workgroups)",
-                      c.tm, c.nwv, c.ns, c.kg, c.kw, c.splits, (long long)(w4a16_sk_tiles(M, N, c) * c.splits));
+        std::snprintf(buf, sizeof(buf), "w4a16_gemm_sk_kernel<%d, %d, %d, %d, %d, %d> (K split %d ways, %lld workgroups)",
+                      c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr, c.splits, (long long)(w4a16_sk_tiles(M, N, c) * c.splits));
         g_kernel_name = buf;
     }
     return g_kernel_name.c_str();

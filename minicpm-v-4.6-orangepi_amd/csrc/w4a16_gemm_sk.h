@@ -20,6 +20,7 @@ struct SkConfig {
     int splits;
     int kg = 1;
     int kw = 1;
+    int wr = 0;             // 1: each wave loads its weights, zeros and scales into registers (LDS holds x only)
 };
 
 // The workspace starts with the tile arrival counters, a fixed region for

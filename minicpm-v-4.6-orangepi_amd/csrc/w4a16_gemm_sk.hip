@@ -98,7 +98,7 @@ __device__ __forceinline__ int xcd_run(int b, int total) {
     return x * per + (x < rem ? x : rem) + i;
 }
 
-template <int TM, int NWV, int NS, int KG, int KW>
+template <int TM, int NWV, int NS, int KG, int KW, int WR>
 struct CfgS {
     static constexpr int WS = NWV / 2;                   // slabs per tile
     static constexpr int TN = 32 * NWV;                  // columns per tile
@@ -108,14 +108,17 @@ struct CfgS {
     static constexpr int GW = KG / KW;                   // groups of a stage per wave
     static constexpr int STEPS = 8 * GW;                 // k16 steps per stage per wave
     static constexpr int A_BYTES = TM * RP;              // x rows
-    static constexpr int B_BYTES = WS * 4 * KG * kLine;  // packed chunks, per slab group-major
+    static constexpr int B_BYTES = WR ? 0 : WS * 4 * KG * kLine;   // packed chunks, per slab group-major
     static constexpr int Z_OFF = A_BYTES + B_BYTES;      // per group and slab: 8 zero words at +0, 32 scale words at +256
-    static constexpr int STAGE = Z_OFF + KG * WS * 512;
+    static constexpr int STAGE = Z_OFF + (WR ? 0 : KG * WS * 512);
     // copy items of a stage, spread evenly over all NWT waves
     static constexpr int PA = (TM * RP / kLine) / NWT;   // x rows, 1 KiB each
-    static constexpr int PB = (4 * KG * WS) / NWT;       // packed chunks, 1 KiB each
-    static constexpr int PZ = (2 * KG * WS) / NWT;       // zero words or scales of one (group, slab)
-    static constexpr int P = PA + PB + PZ;
+    static constexpr int PB = WR ? 0 : (4 * KG * WS) / NWT;   // packed chunks, 1 KiB each
+    static constexpr int PZ = WR ? 0 : (2 * KG * WS) / NWT;   // zero words or scales of one (group, slab)
+    // WR: each wave loads its own part of the stage's weights into registers
+    // instead (per group: two chunk pairs, the zero word, the scale)
+    static constexpr int PR = WR ? 4 * GW : 0;
+    static constexpr int P = PA + PB + PZ + PR;
     // after the K loop each wave owns OB of the tile's MB row blocks of its
     // half-slab (k-part kp owns blocks kp * OB ..), the KW partial sums added
     static constexpr int OB = MB >= KW ? MB / KW : 1;
@@ -123,23 +126,28 @@ struct CfgS {
     static_assert(NWV == 4 || NWV == 8, "NWV");
     static_assert(KG == 1 || KG == 2, "KG");
     static_assert(KW == 1 || (KW == 2 && KG == 2 && NWV == 4), "KW: each k-part takes one group of a stage");
-    static_assert(PA * NWT * kLine == TM * RP && PB * NWT == 4 * KG * WS && PZ * NWT == 2 * KG * WS,
+    static_assert(PA * NWT * kLine == TM * RP && (WR || (PB * NWT == 4 * KG * WS && PZ * NWT == 2 * KG * WS)),
                   "copies split evenly over the waves");
-    static_assert((4 * KG) % PB == 0 && KG % PZ == 0, "a wave's chunk copies share one slab, its zero/scale copies one kind");
+    static_assert(WR || ((4 * KG) % (PB ? PB : 1) == 0 && KG % (PZ ? PZ : 1) == 0 && PB > 0 && PZ > 0),
+                  "a wave's chunk copies share one slab, its zero/scale copies one kind");
+    static_assert(WR == 0 || WR == 1, "WR");
     static_assert(NS >= 2 && NS <= 4 && P * (NS - 1) < 64, "stages");
     static_assert(NS * STAGE <= 160 * 1024, "LDS");
     static constexpr int RB = TN * 2 + 16;               // padded bytes of one staged output row
-    static constexpr int RPA = (STAGE / RB) / 32 * 32 < TM ? (STAGE / RB) / 32 * 32 : TM;   // staged rows per stage buffer
-    static_assert(RPA >= 32 && (TM + RPA - 1) / RPA <= NS, "epilogue staging space");
+    // staged output rows per stage buffer: whole 32-row blocks where a buffer
+    // holds one (a wave's rows then share a buffer), else what fits
+    static constexpr int R32 = (STAGE / RB) / 32 * 32;
+    static constexpr int RPA = R32 >= 32 ? (R32 < TM ? R32 : TM) : (STAGE / RB < TM ? STAGE / RB : TM);
+    static_assert(RPA >= 8 && (TM + RPA - 1) / RPA <= NS, "epilogue staging space");
     static_assert(KW == 1 || NWV * MB * 16 * 64 * 4 <= STAGE, "k-part exchange space");
 };
 
-template <int TM, int NWV, int NS, int KG, int KW>
+template <int TM, int NWV, int NS, int KG, int KW, int WR>
 __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int M, int K, int N,
     int nslab, int m_tiles, int n_tiles, int S, int col_major, uint8_t* __restrict__ ws, uint32_t ws_bytes) {
-    using C = CfgS<TM, NWV, NS, KG, KW>;
+    using C = CfgS<TM, NWV, NS, KG, KW, WR>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds2[NS > 2 ? C::STAGE : 16];
@@ -214,11 +222,36 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
     const __amdgpu_buffer_rsrc_t zsr = zkind ? zr : sr;
     const int zsdst = C::Z_OFF + zslab_t * 512 + (zkind ? 0 : 256);   // + group * WS * 512
 
-    auto issue_item = [&](int kt, uint8_t* dst, int it) {
+    // WR: this wave's weights of stage kt land in register slot kt % NS (the
+    // slot index is a compile-time constant wherever the stages are unrolled):
+    // per group j of its part, chunk pairs (4j, 4j+1) and (4j+2, 4j+3) of
+    // its column -- the lower half-wave fetches the first chunk of a pair,
+    // the upper half the second, as the LDS path's ds_read_b128 does -- plus
+    // the column's zero word and scale.  Padding slabs get bit 31 (read zero).
+    const int col = 32 * (hw & 1) + (lane & 31);         // this lane's column inside its slab
+    const int wslab = tn * C::WS + (hw >> 1);
+    const uint32_t wdead = wslab < nslab ? 0u : 0x80000000u;
+    const uint32_t wq_off = (static_cast<uint32_t>(wslab) * CK * kSlab * 16u + h * 1024u + col * 16u) | wdead;
+    const uint32_t wz_off = (static_cast<uint32_t>(wslab) * 32u + (col >> 3) * 4u) | wdead;
+    const uint32_t ws_off = (static_cast<uint32_t>(wslab) * 128u + col * 2u) | wdead;
+    uint4 rq[WR ? NS : 1][2 * C::GW];
+    uint32_t rz[WR ? NS : 1][C::GW], rs[WR ? NS : 1][C::GW];
+
+    auto issue_item = [&](int kt, uint8_t* dst, int it, int slot) {
         const int kc = kt < KT ? kt : KT - 1;
         const int g = g0 + kc * KG;                      // the stage's first group
         if (it < C::PA) {
             dma16_s(xr, dst + (wave * C::PA + it) * kLine, xoff[it], g * 256);
+        } else if (WR) {
+            const int r = it - C::PA, j = r / 4, kind = r % 4;
+            const int grp = g + kp * C::GW + j;
+            if (kind < 2)
+                rq[slot][2 * j + kind] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(qr, wq_off, (grp * 4 + 2 * kind) * kSlab * 16, 0));
+            else if (kind == 2)
+                rz[slot][j] = __builtin_amdgcn_raw_buffer_load_b32(zr, wz_off, grp * (Npad >> 3) * 4, 0);
+            else
+                rs[slot][j] = __builtin_amdgcn_raw_buffer_load_b16(sr, ws_off, grp * Npad * 2, 0);
         } else if (it < C::PA + C::PB) {
             const int c = bchunk + (it - C::PA);
             dma16_s(qr, dst + C::A_BYTES + (bslab_t * 4 * KG + c) * kLine, qoff, (g * 4 + c) * kSlab * 16);
@@ -227,15 +260,14 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
             dma4_s(zsr, dst + zsdst + j * C::WS * 512, zsoff, (g + j) * zsstride);
         }
     };
-    auto issue = [&](int kt, uint8_t* dst) {
+    auto issue = [&](int kt, uint8_t* dst, int slot) {
 #pragma unroll
-        for (int it = 0; it < C::P; ++it) issue_item(kt, dst, it);
+        for (int it = 0; it < C::P; ++it) issue_item(kt, dst, it, slot);
     };
 
     uint32_t vmagic;
     asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
     const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
-    const int col = 32 * (hw & 1) + (lane & 31);         // this lane's column inside its slab
     const uint32_t zsh = (col & 7) * 4;
 
     float16_t acc[C::MB];
@@ -283,14 +315,14 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
 #pragma unroll
         for (int i = 0; i < C::MB; ++i) dst[i] = *reinterpret_cast<const half8_t*>(src + a_off[s] + i * 32 * C::RP);
     };
-    auto head = [&](const uint8_t* src) {
+    auto head = [&](const uint8_t* src, int slot) {
         // Chunks c, c+1 (c even) in one conflict-free ds_read_b128: the lower
         // half-wave reads column col of chunk c, the upper half of chunk c+1;
         // two lane-half swaps then leave each lane its k-octet parity's words
         // (h and 2 + h) of both chunks.
 #pragma unroll
         for (int c = 0; c < 4 * C::GW; c += 2) {
-            const uint4 w = *reinterpret_cast<const uint4*>(src + b_off + c * kLine);
+            const uint4 w = WR ? rq[slot][c / 2] : *reinterpret_cast<const uint4*>(src + b_off + c * kLine);
             const auto s0 = __builtin_amdgcn_permlane32_swap(w.x, w.y, false, false);
             const auto s2 = __builtin_amdgcn_permlane32_swap(w.z, w.w, false, false);
             q[2 * c] = s0[0];                            // word h of chunk c
@@ -301,8 +333,8 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
         uint32_t zw[C::GW], sh[C::GW];
 #pragma unroll
         for (int j = 0; j < C::GW; ++j) {
-            zw[j] = *reinterpret_cast<const uint32_t*>(src + z_off + j * C::WS * 512);
-            sh[j] = *reinterpret_cast<const uint16_t*>(src + s_off + j * C::WS * 512);
+            zw[j] = WR ? rz[slot][j] : *reinterpret_cast<const uint32_t*>(src + z_off + j * C::WS * 512);
+            sh[j] = WR ? rs[slot][j] & 0xffffu : *reinterpret_cast<const uint16_t*>(src + s_off + j * C::WS * 512);
         }
         read_a(src, 0, af[0]);
 #pragma unroll
@@ -322,14 +354,14 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
     // s's MFMAs run and spread the copies of stage kt + NS - 1 into `prv`
     // (free since the last barrier); step 7 crosses into the next stage
     // between its MFMAs (wait for the copies, barrier, the next stage's head).
-    auto run_stage = [&](int kt, const uint8_t* cur, const uint8_t* nxt, uint8_t* prv) {
+    auto run_stage = [&](int kt, const uint8_t* cur, const uint8_t* nxt, uint8_t* prv, int u) {
 #pragma unroll
         for (int s = 0; s < C::STEPS - 1; ++s) {
             const int c = s & 1, n = c ^ 1;
             // copies of this step: [lo, hi) of the stage's P, spread evenly
             const int lo = C::P * s / (C::STEPS - 1), hi = C::P * (s + 1) / (C::STEPS - 1);
 #pragma unroll
-            for (int it = lo; it < hi; ++it) issue_item(kt + NS - 1, prv, it);
+            for (int it = lo; it < hi; ++it) issue_item(kt + NS - 1, prv, it, (u + NS - 1) % NS);
             read_a(cur, s + 1, af[n]);
             widen(s + 1, bf[n]);
             mfmas(c, 0, C::MB);
@@ -349,29 +381,29 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
         wait_vmcnt_s<C::P * (NS - 2)>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        head(nxt);
+        head(nxt, (u + 1) % NS);
         mfmas(1, (C::MB + 1) / 2, C::MB);
         __builtin_amdgcn_sched_barrier(0);
         widen(0, bf[0]);
     };
 
 #pragma unroll
-    for (int d = 0; d < NS - 1; ++d) issue(d, bufs[d]);
+    for (int d = 0; d < NS - 1; ++d) issue(d, bufs[d], d);
     wait_vmcnt_s<C::P * (NS - 2)>();
     __builtin_amdgcn_s_barrier();
-    head(bufs[0]);
+    head(bufs[0], 0);
     widen(0, bf[0]);
     int kt = 0;
     for (; kt + NS <= KT; kt += NS) {
 #pragma unroll
-        for (int u = 0; u < NS; ++u) run_stage(kt + u, bufs[u], bufs[(u + 1) % NS], bufs[(u + NS - 1) % NS]);
+        for (int u = 0; u < NS; ++u) run_stage(kt + u, bufs[u], bufs[(u + 1) % NS], bufs[(u + NS - 1) % NS], u);
     }
     // (the tail leaves by `break`, so each tail stage is reached only from
     // the one before and the copy accounting stays exact)
 #pragma unroll
     for (int u = 0; u < NS - 1; ++u) {
         if (kt + u >= KT) break;
-        run_stage(kt + u, bufs[u], bufs[(u + 1) % NS], bufs[(u + NS - 1) % NS]);
+        run_stage(kt + u, bufs[u], bufs[(u + 1) % NS], bufs[(u + NS - 1) % NS], u);
     }
     // no copy may land in LDS after this point (the stage buffers are reused)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -556,13 +588,15 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
 using SkFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint32_t*, uint32_t, uint16_t*, int, int,
                       int, int, int, int, int, int, uint8_t*, uint32_t);
 
-#define MCV_SK_SHAPES(X)                                                                               \
-    X(128, 8, 3, 1, 1) X(128, 4, 3, 1, 1) X(64, 8, 3, 1, 1) X(64, 4, 3, 1, 1) X(32, 4, 3, 1, 1) X(64, 4, 3, 2, 1) \
-    X(32, 4, 3, 2, 1) X(64, 4, 3, 2, 2) X(32, 4, 3, 2, 2)
+#define MCV_SK_SHAPES(X)                                                                                   \
+    X(128, 8, 3, 1, 1, 0) X(128, 4, 3, 1, 1, 0) X(64, 8, 3, 1, 1, 0) X(64, 4, 3, 1, 1, 0) X(32, 4, 3, 1, 1, 0)   \
+    X(64, 4, 3, 2, 1, 0) X(32, 4, 3, 2, 1, 0) X(64, 4, 3, 2, 2, 0) X(32, 4, 3, 2, 2, 0) X(128, 8, 4, 1, 1, 1)   \
+    X(64, 4, 3, 1, 1, 1) X(64, 4, 3, 2, 2, 1) X(64, 4, 4, 2, 2, 1) X(32, 4, 3, 1, 1, 1) X(32, 4, 3, 2, 1, 1)   \
+    X(32, 4, 3, 2, 2, 1)
 
-SkFn pick_sk(int tm, int nwv, int ns, int kg, int kw) {
-#define MCV_SK_PICK(a, b, c, d, e) \
-    if (tm == a && nwv == b && ns == c && kg == d && kw == e) return w4a16_gemm_sk_kernel<a, b, c, d, e>;
+SkFn pick_sk(int tm, int nwv, int ns, int kg, int kw, int wr) {
+#define MCV_SK_PICK(a, b, c, d, e, f) \
+    if (tm == a && nwv == b && ns == c && kg == d && kw == e && wr == f) return w4a16_gemm_sk_kernel<a, b, c, d, e, f>;
     MCV_SK_SHAPES(MCV_SK_PICK)
 #undef MCV_SK_PICK
     return nullptr;
@@ -581,7 +615,7 @@ int64_t w4a16_sk_workspace_bytes(int64_t M, int64_t N, const SkConfig& c) {
 }
 
 bool w4a16_sk_config_valid(int64_t M, int64_t K, int64_t N, const SkConfig& c) {
-    return pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw) != nullptr && c.splits >= 1 && c.splits <= 64 && K % kGroup == 0 &&
+    return pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr) != nullptr && c.splits >= 1 && c.splits <= 64 && K % kGroup == 0 &&
            (K / kGroup) % c.splits == 0 && (K / kGroup / c.splits) % c.kg == 0 &&
            (c.splits == 1 || w4a16_sk_tiles(M, N, c) <= kSkMaxSplitTiles);
 }
@@ -589,12 +623,12 @@ bool w4a16_sk_config_valid(int64_t M, int64_t K, int64_t N, const SkConfig& c) {
 int launch_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                          const void* zeros, int zero_bias, void* out, const SkConfig& c, void* ws, int64_t ws_bytes,
                          hipStream_t stream) {
-    SkFn fn = pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw);
+    SkFn fn = pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr);
     if (fn == nullptr || !w4a16_sk_config_valid(M, K, N, c))
         return fail(MCV_ERR_INVALID_ARG,
-                    "w4a16 GEMM: no kernel for TM=%d waves=%d NS=%d KG=%d KW=%d S=%d at M=%lld K=%lld N=%lld (S must "
+                    "w4a16 GEMM: no kernel for TM=%d waves=%d NS=%d KG=%d KW=%d WR=%d S=%d at M=%lld K=%lld N=%lld (S must "
                     "divide K/128, KG the groups of a split, and a split needs at most %d tiles)",
-                    c.tm, c.nwv, c.ns, c.kg, c.kw, c.splits, (long long)M, (long long)K, (long long)N,
+                    c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr, c.splits, (long long)M, (long long)K, (long long)N,
                     kSkMaxSplitTiles);
     const int64_t nslab = ceil_div(N, kSlab);
     const int64_t m_tiles = ceil_div(M, c.tm), n_tiles = ceil_div(nslab, c.nwv / 2);
@@ -632,8 +666,8 @@ int64_t mcv_w4a16_gemm_sk_workspace_bytes(int64_t M, int64_t N, int tm, int wave
 
 int mcv_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                       const void* zeros, int zero_bias, void* out, int tm, int waves, int stages,
-                      int groups_per_stage, int k_parts, int splits, void* workspace, int64_t workspace_bytes,
-                      mcv_stream_t stream) {
+                      int groups_per_stage, int k_parts, int weights_in_registers, int splits, void* workspace,
+                      int64_t workspace_bytes, mcv_stream_t stream) {
     if (!x || !out || !qw || !scales || !zeros) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: null pointer");
     if (zero_bias != 0 && zero_bias != 1) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: zero_bias must be 0 or 1");
     if (K <= 0 || K % kGroup != 0 || M <= 0 || M > (int64_t(1) << 30) || N <= 0 || N > (int64_t(1) << 30))
@@ -643,7 +677,8 @@ int mcv_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void
     int rc = require_device();
     if (rc != MCV_OK) return rc;
     return launch_w4a16_gemm_sk(x, M, K, N, qw, scales, zeros, zero_bias, out,
-                                SkConfig{tm, waves, stages, splits, groups_per_stage, k_parts}, workspace, workspace_bytes,
+                                SkConfig{tm, waves, stages, splits, groups_per_stage, k_parts, weights_in_registers},
+                                workspace, workspace_bytes,
                                 static_cast<hipStream_t>(stream));
 }
 

@@ -328,13 +328,13 @@ def test_w4a16_gemm_workspace_query(mcv):
                   (128, 1024, 1024), (512, 1024, 3584), (128, 1000, 1024), (0, 1024, 1024), (128, 0, 1024)]:
         assert q(*shape) == 0, shape
     assert b"w4a16_gemv_kernel" in L.mcv_w4a16_gemm_kernel_name(4, 1024, 1024, 1)
-    assert b"<128, 8, 3, 1, 1>" in L.mcv_w4a16_gemm_kernel_name(2048, 1024, 3584, 1)
+    assert b"<128, 8, 3, 1, 1, 0>" in L.mcv_w4a16_gemm_kernel_name(2048, 1024, 3584, 1)
     # even group counts of at least 8 (64-row tiles) or 14 (32-row tiles) take two k-parts
-    assert b"<64, 4, 3, 2, 2>" in L.mcv_w4a16_gemm_kernel_name(2048, 3584, 1024, 1)
-    assert b"<32, 4, 3, 2, 2> (K split 2 ways" in L.mcv_w4a16_gemm_kernel_name(512, 3584, 1024, 1)
-    assert b"<32, 4, 3, 1, 1> (K split 4 ways" in L.mcv_w4a16_gemm_kernel_name(128, 3584, 1024, 1)
-    assert b"<64, 4, 3, 2, 2>" in L.mcv_w4a16_gemm_kernel_name(512, 1024, 3584, 1)
-    assert b"<32, 4, 3, 1, 1> (K split 1 ways" in L.mcv_w4a16_gemm_kernel_name(128, 1024, 3584, 1)
+    assert b"<64, 4, 3, 2, 2, 1>" in L.mcv_w4a16_gemm_kernel_name(2048, 3584, 1024, 1)
+    assert b"<32, 4, 3, 2, 2, 1> (K split 2 ways" in L.mcv_w4a16_gemm_kernel_name(512, 3584, 1024, 1)
+    assert b"<32, 4, 3, 1, 1, 1> (K split 4 ways" in L.mcv_w4a16_gemm_kernel_name(128, 3584, 1024, 1)
+    assert b"<64, 4, 3, 2, 2, 1>" in L.mcv_w4a16_gemm_kernel_name(512, 1024, 3584, 1)
+    assert b"<32, 4, 3, 1, 1, 1> (K split 1 ways" in L.mcv_w4a16_gemm_kernel_name(128, 1024, 3584, 1)
 
 
 def test_lm_head_grid_choice(mcv):

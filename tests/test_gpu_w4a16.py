@@ -200,8 +200,10 @@ def test_gemm_split_k_graph_replays(mcv, cuda):
 # dispatch's and the rest, against the oracle on ragged shapes, all through
 # ONE zero-filled workspace (calls of different shapes and splits must leave
 # its counters zero for each other), each split twice for identical bits.
-SK_CONFIGS = [(128, 8, 3, 1, 1), (128, 4, 3, 1, 1), (64, 8, 3, 1, 1), (64, 4, 3, 1, 1), (32, 4, 3, 1, 1), (64, 4, 3, 2, 1),
-              (32, 4, 3, 2, 1), (64, 4, 3, 2, 2), (32, 4, 3, 2, 2)]
+SK_CONFIGS = [(128, 8, 3, 1, 1, 0), (128, 4, 3, 1, 1, 0), (64, 8, 3, 1, 1, 0), (64, 4, 3, 1, 1, 0), (32, 4, 3, 1, 1, 0),
+              (64, 4, 3, 2, 1, 0), (32, 4, 3, 2, 1, 0), (64, 4, 3, 2, 2, 0), (32, 4, 3, 2, 2, 0), (128, 8, 4, 1, 1, 1),
+              (64, 4, 3, 1, 1, 1), (64, 4, 3, 2, 2, 1), (64, 4, 4, 2, 2, 1), (32, 4, 3, 1, 1, 1), (32, 4, 3, 2, 1, 1),
+              (32, 4, 3, 2, 2, 1)]
 
 
 @pytest.mark.parametrize("M,K,N", [(200, 1024, 1000), (70, 2048, 520)], ids=lambda v: str(v))
@@ -216,33 +218,33 @@ def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
     q, sc, z = w.ptrs()
     stream = torch.cuda.current_stream().cuda_stream
     G = K // 128
-    for tm, nwv, ns, kg, kw in SK_CONFIGS:
+    for tm, nwv, ns, kg, kw, wr in SK_CONFIGS:
         for S in [s for s in (1, 2, 4, 8, 16) if G % s == 0 and (G // s) % kg == 0]:
             assert L.mcv_w4a16_gemm_sk_workspace_bytes(M, w.N, tm, nwv, S) <= ws.numel()
             outs = []
             for _ in range(2 if S > 1 else 1):
                 out = torch.full((M, N), 7.0, dtype=torch.float16, device="cuda")
                 rc = L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, w.zero_bias, out.data_ptr(), tm, nwv,
-                                         ns, kg, kw, S, ws.data_ptr(), ws.numel(), stream)
+                                         ns, kg, kw, wr, S, ws.data_ptr(), ws.numel(), stream)
                 assert rc == 0, L.mcv_last_error()
                 outs.append(out)
             torch.cuda.synchronize()
-            _check(_host_f32(outs[0]), ref, f"sk tm={tm} waves={nwv} kg={kg} kw={kw} S={S} M={M} K={K} N={N}")
+            _check(_host_f32(outs[0]), ref, f"sk tm={tm} waves={nwv} ns={ns} kg={kg} kw={kw} wr={wr} S={S} M={M} K={K} N={N}")
             if S > 1:
-                assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (tm, nwv, kg, kw, S)
+                assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (tm, nwv, ns, kg, kw, wr, S)
     # the counters are zero after every call
     assert int(ws[:4096].count_nonzero().item()) == 0
     # an unbuilt configuration, a split that does not divide K/128, groups per
     # stage that do not divide a split's groups, a missing workspace: clear errors
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 96, 4, 3, 1, 1, 1, None, 0,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 96, 4, 3, 1, 1, 0, 1, None, 0,
                                stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 3,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 3,
                                ws.data_ptr(), ws.numel(), stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 2, 1, G,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 2, 1, 0, G,
                                ws.data_ptr(), ws.numel(), stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 2, 1,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 2, 0, 1,
                                ws.data_ptr(), ws.numel(), stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 2, None, 0,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 2, None, 0,
                                stream) == 1
 
 
