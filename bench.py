@@ -19,8 +19,9 @@ carries every configuration of the north star, each measured in the same run:
 For each: `us_per_call` = mean duration of 200 back-to-back launches, enqueued
 directly while a spin kernel holds the stream (so the host's launch rate does
 not gate short kernels, and a rocprofv3 kernel trace of the same launches
-sees them back to back as well), from which `value` and `roofline.achieved`
-follow; `kernel_us_median` /
+sees them back to back as well), the median of five such timed regions
+(`regions_us_per_call` lists all five), from which `value` and
+`roofline.achieved` follow; `kernel_us_median` /
 `kernel_us_mean` = per-launch HIP event pairs around each of >= 100 launches
 (the queue is kept full by a sleep kernel, so each pair brackets one kernel);
 `cpu_baseline` = the oracle's restatement of the reference's CPU path on this
@@ -85,13 +86,14 @@ def w4a16_bytes(K, N):
 # --------------------------------------------------------------------------- #
 # GPU timing                                                                   #
 # --------------------------------------------------------------------------- #
-def time_queued(launch, n_sets, steps, warmup=3):
+def time_queued(launch, n_sets, steps, warmup=3, regions=1):
     """Mean ms per launch over `steps` back-to-back launches enqueued directly
     on torch's current stream while a spin kernel holds it, between one event
     pair: the GPU runs them back to back however slowly the host enqueues
     (rocprofv3's kernel trace of the same launches shows them back to back
     too, so its per-kernel durations match this figure).  Returns (ms per
-    launch, host enqueue ms)."""
+    launch, host enqueue ms); with regions > 1, `regions` such timed regions
+    one after another and the list of their ms per launch instead."""
     import torch
     for i in range(warmup):
         launch(i % n_sets)
@@ -108,22 +110,25 @@ def time_queued(launch, n_sets, steps, warmup=3):
         launch(i % n_sets)
     torch.cuda.synchronize()
     hold = steps * host_ms * 1.5 + 1.0
-    for _ in range(3):
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        _sleep_ms(hold)
-        t0.record()
-        th = time.perf_counter()
-        for i in range(steps):
-            launch(i % n_sets)
-        t1.record()
-        enq_ms = (time.perf_counter() - th) * 1e3
-        torch.cuda.synchronize()
-        if enq_ms < 0.8 * hold:          # the spin kernel outlasted the enqueue
-            break
-        hold *= 2.0
-    else:
-        raise RuntimeError(f"time_queued: the host could not enqueue {steps} launches within the hold")
-    return t0.elapsed_time(t1) / steps, enq_ms
+    out = []
+    while len(out) < regions:
+        for _ in range(3):
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            _sleep_ms(hold)
+            t0.record()
+            th = time.perf_counter()
+            for i in range(steps):
+                launch(i % n_sets)
+            t1.record()
+            enq_ms = (time.perf_counter() - th) * 1e3
+            torch.cuda.synchronize()
+            if enq_ms < 0.8 * hold:          # the spin kernel outlasted the enqueue
+                break
+            hold *= 2.0
+        else:
+            raise RuntimeError(f"time_queued: the host could not enqueue {steps} launches within the hold")
+        out.append(t0.elapsed_time(t1) / steps)
+    return (out[0], enq_ms) if regions == 1 else (out, enq_ms)
 
 
 def time_direct(launch, n_sets, steps, warmup):
@@ -235,10 +240,17 @@ def traffic_from_profiles(workload: str):
         return None
 
 
+REGIONS = 5
+
+
 def gpu_result(name, kernel, amount, unit, bound, launch, n_sets, steps, extra=None):
-    """Times one configuration: back-to-back mean (value, roofline) and the
-    per-launch median."""
-    per, _ = time_queued(launch, n_sets, steps)
+    """Times one configuration: REGIONS timed regions of `steps` back-to-back
+    launches each, the median region's mean per launch (value, roofline), and
+    the per-launch median.  One MI355X region of a few ms can differ from the
+    next by up to ~7 % for the same launches (the clocks and the memory system
+    change on that scale), so one region alone is a noisy figure."""
+    per_r, _ = time_queued(launch, n_sets, steps, regions=REGIONS)
+    per = float(np.median(per_r))
     # (--no-per-launch: profiling runs, whose kernel trace should hold only
     # the back-to-back launches)
     pl = np.array([per] if ARGS.no_per_launch else time_per_launch(launch, n_sets))
@@ -248,6 +260,7 @@ def gpu_result(name, kernel, amount, unit, bound, launch, n_sets, steps, extra=N
     r = {"kernel": kernel, "us_per_call": round(per * 1e3, 3), "value": round(value, 2), "unit": unit,
          "kernel_us_median": round(float(np.median(pl)) * 1e3, 3), "kernel_us_mean": round(float(pl.mean()) * 1e3, 3),
          "per_launch_samples": int(pl.size), "back_to_back_launches": steps,
+         "regions_us_per_call": [round(v * 1e3, 3) for v in per_r],
          "roofline": {"bound": bound, "achieved": round(value, 2), "peak": peak, "unit": unit,
                       "frac": round(value / peak, 4), "traffic": traffic_from_profiles(name),
                       "algorithmic_per_launch": amount}}
