@@ -423,6 +423,21 @@ int mcv_w8a8_gemm_f16(const int8_t* xq_dev, const void* x_scale_dev, int x_scale
                       const void* w_scale_dev, int w_scale_dtype, void* out_dev,
                       mcv_stream_t stream);
 
+/* The int8 MFMA GEMM behind mcv_w8a8_gemm_i32 / _f16 for M > 4 on
+ * MCV_W8_TILED weights, with an explicit tile configuration instead of the
+ * dispatch's (no counterpart in the reference; exposed so every built
+ * configuration can be tested and timed): bm x bn tiles (128x128, 64x128,
+ * 128x64, 64x64), `stages` 128-k stages in flight (3 or 4),
+ * `weights_in_registers` 1 to have each of the four waves load its own weight
+ * columns into registers (128x128 and 64x128 only; LDS then stages x alone).
+ * f16_out 1: fp16 out through the fused epilogue (scales as mcv_w8a8_gemm_f16),
+ * 0: int32 out (scales unused).  An unbuilt configuration fails with
+ * MCV_ERR_INVALID_ARG. */
+int mcv_w8a8_gemm_lds(const int8_t* xq_dev, const void* x_scale_dev, int x_scale_dtype,
+                      int64_t M, int64_t K, int64_t N, const int8_t* w_dev, const void* w_scale_dev,
+                      int w_scale_dtype, void* out_dev, int f16_out, int bm, int bn, int stages,
+                      int weights_in_registers, mcv_stream_t stream);
+
 /* The whole W8A8 decode MLP block, M = 1, in one launch, from the normed fp16
  * row x [1][H]: quantise x, gate and up int8 GEMVs with the fused epilogue,
  * silu * mul, quantise the act row, the down int8 GEMV with its epilogue ->

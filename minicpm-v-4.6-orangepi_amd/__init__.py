@@ -94,6 +94,8 @@ _SIGS = {
     "mcv_w8a8_gemm_i32": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_dequant": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_i64, _c_i64, _vp, _vp]),
     "mcv_w8a8_gemm_f16": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp, _c_int, _vp, _vp]),
+    "mcv_w8a8_gemm_lds": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int,
+                                   _c_int, _c_int, _vp]),
     "mcv_w8a8_gemv_argmax_partials": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_int, _vp, _vp,
                                                _vp]),
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),

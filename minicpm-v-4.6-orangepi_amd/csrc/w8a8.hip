@@ -19,6 +19,9 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
                       const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
 int launch_w8a8_gemv_argmax(const int8_t* xq, int64_t K, int64_t V, const int8_t* w, void* logits, const void* xs,
                             int xs16, const void* ws, int ws16, unsigned long long* keys, hipStream_t stream);
+int launch_w8a8_gemm_lds_cfg(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
+                             const void* xs, int xs16, const void* ws, int ws16, int bm, int bn, int ns, int wr,
+                             hipStream_t stream);
 
 namespace {
 
@@ -399,6 +402,20 @@ int mcv_w8a8_gemm_f16(const int8_t* xq, const void* xs, int xs_dtype, int64_t M,
     if ((rc = require_device()) != MCV_OK) return rc;
     return launch_gemm<true>(xq, M, K, N, w, w_layout, out, xs, xs_dtype == MCV_F16, ws, ws_dtype == MCV_F16,
                              static_cast<hipStream_t>(stream));
+}
+
+int mcv_w8a8_gemm_lds(const int8_t* xq, const void* xs, int xs_dtype, int64_t M, int64_t K, int64_t N, const int8_t* w,
+                      const void* ws, int ws_dtype, void* out, int f16_out, int bm, int bn, int stages,
+                      int weights_in_registers, mcv_stream_t stream) {
+    int rc = check_gemm_args(xq, M, K, N, w, MCV_W8_TILED, out, "mcv_w8a8_gemm_lds");
+    if (rc != MCV_OK) return rc;
+    if (f16_out && (!xs || !ws)) return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_gemm_lds: null scale");
+    if (f16_out && (!dtype_ok(xs_dtype) || !dtype_ok(ws_dtype)))
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_gemm_lds: bad scale dtype");
+    if ((rc = require_device()) != MCV_OK) return rc;
+    return launch_w8a8_gemm_lds_cfg(xq, M, K, N, w, out, f16_out != 0, xs, xs_dtype == MCV_F16, ws,
+                                    ws_dtype == MCV_F16, bm, bn, stages, weights_in_registers,
+                                    static_cast<hipStream_t>(stream));
 }
 
 int mcv_w8a8_gate_up_silu(const int8_t* xq, const void* xs, int xs_dtype, int64_t M, int64_t K, int64_t N,

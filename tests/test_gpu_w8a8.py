@@ -179,6 +179,54 @@ def test_w8a8_gemm_fused_ragged(mcv, oracle, cuda, M, K, N):
     assert np.array_equal(got16, oracle.w8a8_dequant(acc_o, oracle.h2f(s16_o), oracle.h2f(ws16_o)))
 
 
+# Every built tile configuration of the M > 4 GEMM through mcv_w8a8_gemm_lds
+# (the dispatch runs one per shape): int32 accumulators bit-exact against the
+# oracle's product, the fused epilogue bit-exact with fp32 and with fp16
+# scales, on ragged shapes (a last tile past M and N, K padded with zero
+# weights, N % 4 != 0); then unbuilt configurations fail cleanly.
+W8_LDS_CONFIGS = [(128, 128, 3, 0), (128, 128, 4, 0), (64, 128, 4, 0), (128, 64, 4, 0), (64, 64, 4, 0),
+                  (128, 128, 3, 1), (128, 128, 4, 1), (64, 128, 4, 1)]
+
+
+@pytest.mark.parametrize("M,K,N", [(257, 1040, 1000), (70, 384, 1003)], ids=lambda v: str(v))
+def test_w8a8_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
+    torch = _torch()
+    L = mcv.lib()
+    rng = np.random.default_rng(1300 + M + N)
+    x = f16_normal(rng, (M, K), 1.0)
+    wf = f16_normal(rng, (K, N), 0.02)
+    wq = mcv.quantize_dense_weight_w8a8(_f16_dev(wf))
+    xq, xs, _ = mcv.w8a8_quantize(_f16_dev(x))
+    xs16 = xs.half()
+    q_o, s_o, s16_o = oracle.w8a8_quantize_act(x)
+    wq_o, ws_o, ws16_o = oracle.w8a8_quantize_weight(wf)
+    acc_o = oracle.gemm_i32(q_o, wq_o)
+    want32 = oracle.w8a8_dequant(acc_o, s_o, ws_o)
+    want16 = oracle.w8a8_dequant(acc_o, oracle.h2f(s16_o), oracle.h2f(ws16_o))
+    stream = torch.cuda.current_stream().cuda_stream
+    for bm, bn, ns, wr in W8_LDS_CONFIGS:
+        tag = f"{bm}x{bn} ns={ns} wr={wr} M={M} K={K} N={N}"
+        acc = torch.full((M, N), 7, dtype=torch.int32, device="cuda")
+        rc = L.mcv_w8a8_gemm_lds(xq.data_ptr(), None, 0, M, K, N, wq.w_int8.data_ptr(), None, 0, acc.data_ptr(), 0,
+                                 bm, bn, ns, wr, stream)
+        assert rc == 0, (tag, L.mcv_last_error())
+        out = torch.full((M, N), 7.0, dtype=torch.float16, device="cuda")
+        rc = L.mcv_w8a8_gemm_lds(xq.data_ptr(), xs.data_ptr(), mcv.MCV_F32, M, K, N, wq.w_int8.data_ptr(),
+                                 wq.w_scale_f32.data_ptr(), mcv.MCV_F32, out.data_ptr(), 1, bm, bn, ns, wr, stream)
+        assert rc == 0, (tag, L.mcv_last_error())
+        out16 = torch.full((M, N), 7.0, dtype=torch.float16, device="cuda")
+        rc = L.mcv_w8a8_gemm_lds(xq.data_ptr(), xs16.data_ptr(), mcv.MCV_F16, M, K, N, wq.w_int8.data_ptr(),
+                                 wq.w_scale.data_ptr(), mcv.MCV_F16, out16.data_ptr(), 1, bm, bn, ns, wr, stream)
+        assert rc == 0, (tag, L.mcv_last_error())
+        torch.cuda.synchronize()
+        assert np.array_equal(acc.cpu().numpy(), acc_o), tag
+        assert np.array_equal(_u16(out), want32), tag
+        assert np.array_equal(_u16(out16), want16), tag
+    for bm, bn, ns, wr in [(96, 128, 3, 0), (64, 64, 4, 1), (128, 128, 2, 0)]:
+        assert L.mcv_w8a8_gemm_lds(xq.data_ptr(), None, 0, M, K, N, wq.w_int8.data_ptr(), None, 0,
+                                   xq.data_ptr(), 0, bm, bn, ns, wr, stream) == 1, (bm, bn, ns, wr)
+
+
 def test_nk_layout_fused(mcv, cuda):
     torch = _torch()
     rng = np.random.default_rng(77)
