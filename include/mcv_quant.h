@@ -185,7 +185,10 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
  * each, `k_parts` waves per half-slab (1, or 2 with groups_per_stage 2:
  * each takes one group of every stage), `weights_in_registers` 1 to load
  * each wave's packed weights, zeros and scales straight into registers (the
- * stage buffers in LDS then hold x rows only), K split `splits` ways across
+ * stage buffers in LDS then hold x rows only), `tile_order` the order in
+ * which the XCDs take the tiles (0 as the dispatch: down the tile columns when
+ * x has fewer bytes than the packed weights, else along the rows; 1 along the
+ * rows; 2 down the columns), K split `splits` ways across
  * workgroups (splits divides K / 128, groups_per_stage divides
  * K / 128 / splits), the partial tiles added inside the same launch by the
  * last workgroup of each tile, in split order (deterministic).  Splits > 1
@@ -199,8 +202,8 @@ int64_t mcv_w4a16_gemm_sk_workspace_bytes(int64_t M, int64_t N, int tm, int wave
 int mcv_w4a16_gemm_sk(const void* x_dev, int64_t M, int64_t K, int64_t N,
                       const void* qw_dev, const void* scales_dev, const void* zeros_dev,
                       int zero_bias, void* out_dev, int tm, int waves, int stages,
-                      int groups_per_stage, int k_parts, int weights_in_registers, int splits,
-                      void* workspace_dev, int64_t workspace_bytes, mcv_stream_t stream);
+                      int groups_per_stage, int k_parts, int weights_in_registers, int tile_order,
+                      int splits, void* workspace_dev, int64_t workspace_bytes, mcv_stream_t stream);
 
 /* The two kernels behind mcv_w4a16_gemm, callable directly (same contract). */
 int mcv_w4a16_gemv(const void* x_dev, int64_t M, int64_t K, int64_t N,

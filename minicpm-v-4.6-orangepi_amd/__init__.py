@@ -65,7 +65,7 @@ _SIGS = {
     "mcv_w8a8_gemm_kernel_name": (ctypes.c_char_p, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "mcv_w4a16_gemm_sk_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_int, _c_int, _c_int]),
     "mcv_w4a16_gemm_sk": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int,
-                                   _c_int, _c_int, _c_int, _c_int, _vp, _c_i64, _vp]),
+                                   _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _c_i64, _vp]),
     "mcv_w4a16_gemv": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_gemm_mfma": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "mcv_w4a16_dequant": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),

@@ -654,7 +654,14 @@ int launch_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const v
     if (total > 0x7fffffff || K > (int64_t(1) << 22) || K * nslab * kSlab / 2 >= (int64_t(1) << 31) ||
         int64_t(c.tm) * K * 2 >= (int64_t(1) << 31) || need >= (int64_t(1) << 31))
         return fail(MCV_ERR_SHAPE, "w4a16 GEMM: problem too large (M=%lld N=%lld)", (long long)M, (long long)N);
-    const int col_major = M < N ? 1 : 0;
+    // Each XCD takes a contiguous run of the tile order.  Down the columns,
+    // an XCD's tiles share few weight columns but need (nearly) every x row;
+    // along the rows, the reverse; so the order goes down the columns only
+    // when x is the smaller operand (every XCD re-reads it from beyond its
+    // L2 instead of the weights).  MI355X, M=2048 K=1024 N=3584 (x 4.2 MB,
+    // weights 2.3 MB): the column order fetched 36 MB per call.
+    const int64_t x_bytes = M * K * 2, w_bytes = K * N / 2 + (K / kGroup) * N * 5 / 2;
+    const int col_major = c.order == 2 || (c.order == 0 && x_bytes < w_bytes) ? 1 : 0;
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(total)), dim3(64 * c.nwv * c.kw), 0, stream,
                        static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
@@ -678,8 +685,8 @@ int64_t mcv_w4a16_gemm_sk_workspace_bytes(int64_t M, int64_t N, int tm, int wave
 
 int mcv_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,
                       const void* zeros, int zero_bias, void* out, int tm, int waves, int stages,
-                      int groups_per_stage, int k_parts, int weights_in_registers, int splits, void* workspace,
-                      int64_t workspace_bytes, mcv_stream_t stream) {
+                      int groups_per_stage, int k_parts, int weights_in_registers, int tile_order, int splits,
+                      void* workspace, int64_t workspace_bytes, mcv_stream_t stream) {
     if (!x || !out || !qw || !scales || !zeros) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: null pointer");
     if (zero_bias != 0 && zero_bias != 1) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: zero_bias must be 0 or 1");
     if (K <= 0 || K % kGroup != 0 || M <= 0 || M > (int64_t(1) << 30) || N <= 0 || N > (int64_t(1) << 30))
@@ -688,8 +695,11 @@ int mcv_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: x must be 16-byte aligned");
     int rc = require_device();
     if (rc != MCV_OK) return rc;
+    if (tile_order < 0 || tile_order > 2)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: tile_order must be 0, 1 or 2 (%d)", tile_order);
     return launch_w4a16_gemm_sk(x, M, K, N, qw, scales, zeros, zero_bias, out,
-                                SkConfig{tm, waves, stages, splits, groups_per_stage, k_parts, weights_in_registers},
+                                SkConfig{tm, waves, stages, splits, groups_per_stage, k_parts, weights_in_registers,
+                                         tile_order},
                                 workspace, workspace_bytes,
                                 static_cast<hipStream_t>(stream));
 }

@@ -225,7 +225,7 @@ def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
             for _ in range(2 if S > 1 else 1):
                 out = torch.full((M, N), 7.0, dtype=torch.float16, device="cuda")
                 rc = L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, w.zero_bias, out.data_ptr(), tm, nwv,
-                                         ns, kg, kw, wr, S, ws.data_ptr(), ws.numel(), stream)
+                                         ns, kg, kw, wr, 1 + (S + tm) % 2, S, ws.data_ptr(), ws.numel(), stream)
                 assert rc == 0, L.mcv_last_error()
                 outs.append(out)
             torch.cuda.synchronize()
@@ -236,15 +236,17 @@ def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
     assert int(ws[:4096].count_nonzero().item()) == 0
     # an unbuilt configuration, a split that does not divide K/128, groups per
     # stage that do not divide a split's groups, a missing workspace: clear errors
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 96, 4, 3, 1, 1, 0, 1, None, 0,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 96, 4, 3, 1, 1, 0, 0, 1, None, 0,
                                stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 3,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 0, 3,
                                ws.data_ptr(), ws.numel(), stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 2, 1, 0, G,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 2, 1, 0, 0, G,
                                ws.data_ptr(), ws.numel(), stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 2, 0, 1,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 2, 0, 0, 1,
                                ws.data_ptr(), ws.numel(), stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 2, None, 0,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 0, 2, None, 0,
+                               stream) == 1
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 3, 1, None, 0,
                                stream) == 1
 
 
