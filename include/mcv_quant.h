@@ -180,7 +180,7 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
 
 /* The half-slab GEMM with an explicit configuration (what mcv_w4a16_gemm_ws
  * picks by shape; exposed so every configuration can be tested and timed):
- * tile tm x 32 * waves (tm in {32, 64, 128}, waves in {4, 8}), `stages`
+ * tile tm x 32 * waves (tm in {32, 64, 128}, waves in {2, 4, 8}), `stages`
  * copy stages in flight of `groups_per_stage` quantisation groups (128 k)
  * each, `k_parts` waves per half-slab (1, or 2 with groups_per_stage 2:
  * each takes one group of every stage), `weights_in_registers` 1 to load

@@ -33,44 +33,58 @@ bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N
 
 // The GEMM's configuration for M x K x N.  First the largest tile whose grid
 // covers most of the 256 CUs with one tile per workgroup: 128 x 256 (eight
-// waves), 64 x 128, 32 x 128.  Failing that (few rows and N = 1024-like
-// widths), with a workspace, K is split across workgroups on 32 x 128 tiles:
-// the most ways that keep the grid within one workgroup per CU and at least
-// seven 128-k stages per workgroup (the partial tiles' exchange costs ~1-2 us,
-// which a shorter loop does not pay back).  A four-wave tile takes two
-// k-parts (eight waves, two groups per stage) when its workgroups' group
-// count is even and at least 8 (64-row tiles) or 14 (32-row tiles): two
-// waves per SIMD cover each other's copy issue, a gain there and a loss on
-// the shorter loops of the thinner tiles.  The 64- and 32-row tiles load
-// their weights, zeros and scales straight into registers (each wave's
-// columns are its own; LDS then stages x only): 0-9 % faster than staging
-// them in LDS in two sweeps, never slower; the 128 x 256 tile measured the
-// same either way and keeps the LDS path.  Measured on MI355X (rotated
-// weights, us per call, back to back; the same launch varies by up to +-7 %
-// from one 200-launch region to the next): M=2048 K=1024 N=3584 128x256
-// 20.0-20.5 (64x128 24-25); M=2048 K=3584 N=1024 64x128 two k-parts 19.6-19.8
-// (LDS weights 20.1-21.6, one k-part 21.6-22.6); M=512 K=1024 N=3584 64x128
-// two k-parts 8.4-8.5 (LDS weights 8.8); M=512 K=3584 N=1024 32x128 split 2
-// ways, two k-parts 11.5 (LDS weights 12.1, one k-part 12.4, unsplit 12.8-15.6,
-// 4 ways 13.6); M=128 K=1024 N=3584 32x128 6.9 (two k-parts 6.8-6.9, 2 ways
-// 7.8); M=128 K=3584 N=1024 32x128 split 4 ways 9.7 (7 ways 10.8).
+// waves), 64 x 128, 32 x 128, 32 x 64.  Failing that (few rows and N =
+// 1024-like widths), with a workspace, K is split across workgroups on 32 x 64
+// tiles: the most ways that keep the grid within one workgroup per CU and
+// leave each workgroup an even number of at least 8 quantisation groups (two
+// k-parts; else the most ways with at least 7, one k-part) -- the partial
+// tiles' exchange costs ~1-2 us, which a shorter loop does not pay back.  A
+// tile of four half-slabs takes two k-parts (eight waves, two groups per
+// stage) when its workgroups' group count is even and at least 8 (64-row
+// tiles) or 14 (32-row tiles); the 32 x 64 tile (two half-slabs) whenever the
+// count is even: two waves per SIMD cover each other's copy issue.  The 64-
+// and 32-row tiles load their weights, zeros and scales straight into
+// registers (each wave's columns are its own; LDS then stages x only): 0-9 %
+// faster than staging them in LDS in two sweeps, never slower; the 128 x 256
+// tile measured the same either way and keeps the LDS path.  Measured on
+// MI355X (rotated weights, us per call, back to back; the same launch varies
+// by up to +-7 % from one 200-launch region to the next on the long shapes):
+// M=2048 K=1024 N=3584 128x256 20.0-20.6 (64x128 24-25); M=2048 K=3584 N=1024
+// 64x128 two k-parts 19.6-22.3 (LDS weights 20.1-21.6, one k-part 21.6-22.6);
+// M=512 K=1024 N=3584 64x128 two k-parts 8.3-8.5 (32x64 10.0-11.6); M=512
+// K=3584 N=1024 32x64 two k-parts 10.1 (32x128 split 2 ways 11.4-12.1, 64x64
+// split 2 ways 10.8); M=128 K=1024 N=3584 32x64 two k-parts 5.5 (one k-part
+// 6.6, 32x128 6.7-7.0); M=128 K=3584 N=1024 32x64 split 2 ways, two k-parts
+// 8.7 (4 ways, one k-part 9.7; 32x128 split 4 ways 9.6-9.8).  Against the
+// rule before the 32 x 64 tile, over M = 48..512 and (K, N) = (1024, 3584),
+// (3584, 1024), (1024, 6144), (1024, 2048), (2048, 1024): 10-25 % faster
+// where it changes the configuration, except 0.05-0.15 us slower where its
+// grid passes 256 workgroups (M = 96-192 at N = 3584-6144).
 SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
-    constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {32, 4, 3, 1}};
+    constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {32, 4, 3, 1}, {32, 2, 3, 1}};
     const int64_t G = K / kGroup;
-    auto k_parts = [&](SkConfig c) {
+    auto finish = [&](SkConfig c) {
         const int64_t per = G / c.splits;
-        if (c.nwv == 4 && per % 2 == 0 && ((c.tm == 64 && per >= 8) || (c.tm == 32 && per >= 14))) c.kg = c.kw = 2;
+        const bool even = per % 2 == 0;
+        if (even && ((c.nwv == 2 && per >= 2) ||
+                     (c.nwv == 4 && ((c.tm == 64 && per >= 8) || (c.tm == 32 && per >= 14)))))
+            c.kg = c.kw = 2;
         c.wr = c.tm != 128;
         return c;
     };
     for (const SkConfig& c : kOne)
-        if (w4a16_sk_tiles(M, N, c) >= 200) return k_parts(c);
-    SkConfig c{32, 4, 3, 1};
+        if (w4a16_sk_tiles(M, N, c) >= 200) return finish(c);
+    SkConfig c{32, 2, 3, 1};
     const int64_t tiles = w4a16_sk_tiles(M, N, c);
-    if (!can_split || tiles > kSkMaxSplitTiles) return k_parts(c);
-    for (int64_t s = 2; s <= G && s <= 64; ++s)
-        if (G % s == 0 && tiles * s <= 256 && G / s >= 7) c.splits = static_cast<int>(s);
-    return k_parts(c);
+    if (!can_split || tiles > kSkMaxSplitTiles) return finish(c);
+    int s_even = 1, s_any = 1;
+    for (int64_t s = 2; s <= G && s <= 64; ++s) {
+        if (G % s != 0 || tiles * s > 256) continue;
+        if ((G / s) % 2 == 0 && G / s >= 8) s_even = static_cast<int>(s);
+        if (G / s >= 7) s_any = static_cast<int>(s);
+    }
+    c.splits = s_even > 1 ? s_even : s_any;
+    return finish(c);
 }
 
 int check_gemm_args(const void* x, int64_t M, int64_t K, int64_t N, const void* qw, const void* scales,

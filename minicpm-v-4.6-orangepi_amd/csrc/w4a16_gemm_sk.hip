@@ -132,9 +132,9 @@ struct CfgS {
     // half-slab (k-part kp owns blocks kp * OB ..), the KW partial sums added
     static constexpr int OB = MB >= KW ? MB / KW : 1;
     static_assert(TM == 32 || TM == 64 || TM == 128, "TM");
-    static_assert(NWV == 4 || NWV == 8, "NWV");
+    static_assert(NWV == 2 || NWV == 4 || NWV == 8, "NWV");
     static_assert(KG == 1 || KG == 2, "KG");
-    static_assert(KW == 1 || (KW == 2 && KG == 2 && NWV == 4), "KW: each k-part takes one group of a stage");
+    static_assert(KW == 1 || (KW == 2 && KG == 2 && NWV <= 4), "KW: each k-part takes one group of a stage");
     static_assert(PA * NWT * kLine == TM * RP && (WR || (PB * NWT == 4 * KG * WS && PZ * NWT == 2 * KG * WS)),
                   "copies split evenly over the waves");
     static_assert(WR || ((4 * KG) % (PB ? PB : 1) == 0 && KG % (PZ ? PZ : 1) == 0 && PB > 0 && PZ > 0),
@@ -604,7 +604,7 @@ using SkFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint
     X(128, 8, 3, 1, 1, 0) X(128, 4, 3, 1, 1, 0) X(64, 8, 3, 1, 1, 0) X(64, 4, 3, 1, 1, 0) X(32, 4, 3, 1, 1, 0)   \
     X(64, 4, 3, 2, 1, 0) X(32, 4, 3, 2, 1, 0) X(64, 4, 3, 2, 2, 0) X(32, 4, 3, 2, 2, 0) X(128, 8, 4, 1, 1, 1)   \
     X(64, 4, 3, 1, 1, 1) X(64, 4, 3, 2, 2, 1) X(64, 4, 4, 2, 2, 1) X(32, 4, 3, 1, 1, 1) X(32, 4, 3, 2, 1, 1)   \
-    X(32, 4, 3, 2, 2, 1)
+    X(32, 4, 3, 2, 2, 1) X(32, 2, 3, 1, 1, 1) X(32, 2, 3, 2, 2, 1) X(64, 2, 3, 2, 2, 1) X(32, 2, 4, 2, 2, 1)
 
 SkFn pick_sk(int tm, int nwv, int ns, int kg, int kw, int wr) {
 #define MCV_SK_PICK(a, b, c, d, e, f) \
