@@ -32,8 +32,9 @@ namespace {
 bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N < 65536); }
 
 // The GEMM's configuration for M x K x N.  First the largest tile whose grid
-// covers most of the 256 CUs with one tile per workgroup: 128 x 256 (eight
-// waves), 64 x 128, 32 x 128, 32 x 64.  Failing that (few rows and N =
+// gives 200-256 workgroups, one tile each (a workgroup per CU): 128 x 256
+// (eight waves), 64 x 128, 64 x 64, 32 x 128, 32 x 64; past 256, the largest
+// that reaches 200 other than 64 x 64.  Failing that (few rows and N =
 // 1024-like widths), with a workspace, K is split across workgroups on 32 x 64
 // tiles: the most ways that keep the grid within one workgroup per CU and
 // leave each workgroup an even number of at least 8 quantisation groups (two
@@ -55,13 +56,17 @@ bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N
 // K=3584 N=1024 32x64 two k-parts 10.1 (32x128 split 2 ways 11.4-12.1, 64x64
 // split 2 ways 10.8); M=128 K=1024 N=3584 32x64 two k-parts 5.5 (one k-part
 // 6.6, 32x128 6.7-7.0); M=128 K=3584 N=1024 32x64 split 2 ways, two k-parts
-// 8.7 (4 ways, one k-part 9.7; 32x128 split 4 ways 9.6-9.8).  Against the
+// 8.7 (4 ways, one k-part 9.7; 32x128 split 4 ways 9.6-9.8); 64x64 two
+// k-parts against 32x128 at 224-256 tiles: M=256 K=1024 N=3584 6.6 / 7.3,
+// M=1024 K=3584 N=1024 13.9 / 15.6, M=512 K=1024 N=2048 6.5 / 7.1, M=1024
+// K=2048 N=1024 9.3 / 9.9, M=512 K=3584 N=2048 14.1 / 15.9; at 288-384
+// tiles 64x64 is 0.1-2 us slower.  Against the
 // rule before the 32 x 64 tile, over M = 48..512 and (K, N) = (1024, 3584),
 // (3584, 1024), (1024, 6144), (1024, 2048), (2048, 1024): 10-25 % faster
 // where it changes the configuration, except 0.05-0.15 us slower where its
 // grid passes 256 workgroups (M = 96-192 at N = 3584-6144).
 SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
-    constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {32, 4, 3, 1}, {32, 2, 3, 1}};
+    constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {64, 2, 3, 1}, {32, 4, 3, 1}, {32, 2, 3, 1}};
     const int64_t G = K / kGroup;
     auto finish = [&](SkConfig c) {
         const int64_t per = G / c.splits;
@@ -72,8 +77,15 @@ SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
         c.wr = c.tm != 128;
         return c;
     };
+    // one tile per workgroup and one workgroup per CU where a tile fits that
+    // (200-256 tiles); else the largest tile that still covers most CUs,
+    // 64 x 64 aside (past 256 tiles it trails 32 x 128 by 5-20 %)
+    for (const SkConfig& c : kOne) {
+        const int64_t t = w4a16_sk_tiles(M, N, c);
+        if (t >= 200 && t <= 256) return finish(c);
+    }
     for (const SkConfig& c : kOne)
-        if (w4a16_sk_tiles(M, N, c) >= 200) return finish(c);
+        if (w4a16_sk_tiles(M, N, c) >= 200 && !(c.tm == 64 && c.nwv == 2)) return finish(c);
     SkConfig c{32, 2, 3, 1};
     const int64_t tiles = w4a16_sk_tiles(M, N, c);
     if (!can_split || tiles > kSkMaxSplitTiles) return finish(c);
@@ -164,8 +176,9 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
         g_kernel_name = buf;
     } else {
         const SkConfig c = choose_gemm(M, K, N, with_workspace != 0);
-        std::snprintf(buf, sizeof(buf), "w4a16_gemm_sk_kernel<%d, %d, %d, %d, %d, %d> (K split %d ways, %lld workgroups)",
-                      c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr, c.splits, (long long)(w4a16_sk_tiles(M, N, c) * c.splits));
+        std::snprintf(buf, sizeof(buf), "w4a16_gemm_sk_kernel<%d, %d, %d, %d, %d, %d> (K split %d ways, %lld workgroups)%s",
+                      c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr, c.splits, (long long)(w4a16_sk_tiles(M, N, c) * c.splits),
+                      w4a16_sk_config_valid(M, K, N, c) ? "" : " NOT BUILT");
         g_kernel_name = buf;
     }
     return g_kernel_name.c_str();

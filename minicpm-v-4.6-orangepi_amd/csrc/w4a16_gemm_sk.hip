@@ -604,7 +604,8 @@ using SkFn = void (*)(const uint16_t*, const uint4*, const uint16_t*, const uint
     X(128, 8, 3, 1, 1, 0) X(128, 4, 3, 1, 1, 0) X(64, 8, 3, 1, 1, 0) X(64, 4, 3, 1, 1, 0) X(32, 4, 3, 1, 1, 0)   \
     X(64, 4, 3, 2, 1, 0) X(32, 4, 3, 2, 1, 0) X(64, 4, 3, 2, 2, 0) X(32, 4, 3, 2, 2, 0) X(128, 8, 4, 1, 1, 1)   \
     X(64, 4, 3, 1, 1, 1) X(64, 4, 3, 2, 2, 1) X(64, 4, 4, 2, 2, 1) X(32, 4, 3, 1, 1, 1) X(32, 4, 3, 2, 1, 1)   \
-    X(32, 4, 3, 2, 2, 1) X(32, 2, 3, 1, 1, 1) X(32, 2, 3, 2, 2, 1) X(64, 2, 3, 2, 2, 1) X(32, 2, 4, 2, 2, 1)
+    X(32, 4, 3, 2, 2, 1) X(32, 2, 3, 1, 1, 1) X(32, 2, 3, 2, 2, 1) X(64, 2, 3, 2, 2, 1) X(32, 2, 4, 2, 2, 1)   \
+    X(128, 2, 3, 1, 1, 1) X(128, 2, 2, 2, 2, 1) X(64, 2, 3, 1, 1, 1)
 
 SkFn pick_sk(int tm, int nwv, int ns, int kg, int kw, int wr) {
 #define MCV_SK_PICK(a, b, c, d, e, f) \

@@ -338,6 +338,22 @@ def test_w4a16_gemm_workspace_query(mcv):
     assert b"<32, 2, 3, 2, 2, 1> (K split 1 ways, 224 workgroups" in L.mcv_w4a16_gemm_kernel_name(128, 1024, 3584, 1)
 
 
+def test_w4a16_gemm_dispatch_builds(mcv):
+    """Every configuration the GEMM dispatch picks, with and without a
+    workspace, over a grid of shapes, is one the library built (the label
+    says NOT BUILT otherwise, and the launch would fail)."""
+    L = mcv.lib()
+    seen = set()
+    for K in (128, 256, 384, 1024, 1152, 2048, 2688, 3584, 4096, 8192):
+        for N in (8, 64, 200, 1000, 1024, 2048, 3584, 6144, 18944):
+            for M in (8, 16, 33, 48, 64, 96, 128, 192, 256, 384, 512, 768, 1024, 1536, 2048, 4096, 8192):
+                for ws in (0, 1):
+                    name = L.mcv_w4a16_gemm_kernel_name(M, K, N, ws).decode()
+                    assert "NOT BUILT" not in name, (M, K, N, ws, name)
+                    seen.add(name.split(" (")[0])
+    assert any("<64, 2, 3, 2, 2, 1>" in s for s in seen) and any("<32, 2, 3, 2, 2, 1>" in s for s in seen), seen
+
+
 def test_lm_head_grid_choice(mcv):
     """Slabs per workgroup by vocabulary: 16 on the full vocabulary (243
     workgroups), fewer on a GPU's share of a column split, one slab per

@@ -203,7 +203,8 @@ def test_gemm_split_k_graph_replays(mcv, cuda):
 SK_CONFIGS = [(128, 8, 3, 1, 1, 0), (128, 4, 3, 1, 1, 0), (64, 8, 3, 1, 1, 0), (64, 4, 3, 1, 1, 0), (32, 4, 3, 1, 1, 0),
               (64, 4, 3, 2, 1, 0), (32, 4, 3, 2, 1, 0), (64, 4, 3, 2, 2, 0), (32, 4, 3, 2, 2, 0), (128, 8, 4, 1, 1, 1),
               (64, 4, 3, 1, 1, 1), (64, 4, 3, 2, 2, 1), (64, 4, 4, 2, 2, 1), (32, 4, 3, 1, 1, 1), (32, 4, 3, 2, 1, 1),
-              (32, 4, 3, 2, 2, 1), (32, 2, 3, 1, 1, 1), (32, 2, 3, 2, 2, 1), (64, 2, 3, 2, 2, 1), (32, 2, 4, 2, 2, 1)]
+              (32, 4, 3, 2, 2, 1), (32, 2, 3, 1, 1, 1), (32, 2, 3, 2, 2, 1), (64, 2, 3, 2, 2, 1), (32, 2, 4, 2, 2, 1),
+              (128, 2, 3, 1, 1, 1), (128, 2, 2, 2, 2, 1), (64, 2, 3, 1, 1, 1)]
 
 
 @pytest.mark.parametrize("M,K,N", [(200, 1024, 1000), (70, 2048, 520)], ids=lambda v: str(v))
