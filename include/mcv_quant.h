@@ -189,8 +189,9 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
  * which the XCDs take the tiles (0 as the dispatch: down the tile columns when
  * x has fewer bytes than the packed weights, else along the rows; 1 along the
  * rows; 2 down the columns), K split `splits` ways across
- * workgroups (splits divides K / 128, groups_per_stage divides
- * K / 128 / splits), the partial tiles added inside the same launch by the
+ * workgroups (groups_per_stage divides K / 128, splits at most
+ * K / 128 / groups_per_stage; split p takes stages [p U / S, (p+1) U / S) of
+ * the U = K / 128 / groups_per_stage), the partial tiles added inside the same launch by the
  * last workgroup of each tile, in split order (deterministic).  Splits > 1
  * need a 256-byte aligned workspace of mcv_w4a16_gemm_sk_workspace_bytes
  * bytes, zero-filled once before its first use: its first 4 KiB hold the

@@ -37,13 +37,14 @@ bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N
 // that reaches 200 other than 64 x 64.  Failing that (few rows and N =
 // 1024-like widths), with a workspace, K is split across workgroups on 32 x 64
 // tiles: the most ways that keep the grid within one workgroup per CU and
-// leave each workgroup an even number of at least 8 quantisation groups (two
-// k-parts; else the most ways with at least 7, one k-part) -- the partial
-// tiles' exchange costs ~1-2 us, which a shorter loop does not pay back.  A
+// leave each workgroup at least 7 quantisation groups on average (splits are
+// cut in whole stages, so they differ by at most one) -- the partial tiles'
+// exchange costs ~1-2 us, which a shorter loop does not pay back.  A
 // tile of four half-slabs takes two k-parts (eight waves, two groups per
 // stage) when its workgroups' group count is even and at least 8 (64-row
-// tiles) or 14 (32-row tiles); the 32 x 64 tile (two half-slabs) whenever the
-// count is even: two waves per SIMD cover each other's copy issue.  The 64-
+// tiles) or 14 (32-row tiles); the 32 x 64 and 64 x 64 tiles (two
+// half-slabs) whenever K/128 is even: two waves per SIMD cover each other's
+// copy issue.  The 64-
 // and 32-row tiles load their weights, zeros and scales straight into
 // registers (each wave's columns are its own; LDS then stages x only): 0-9 %
 // faster than staging them in LDS in two sweeps, never slower; the 128 x 256
@@ -56,7 +57,9 @@ bool w4a16_prefers_gemv(int64_t M, int64_t N) { return M >= 1 && (M < 8 || M * N
 // K=3584 N=1024 32x64 two k-parts 10.1 (32x128 split 2 ways 11.4-12.1, 64x64
 // split 2 ways 10.8); M=128 K=1024 N=3584 32x64 two k-parts 5.5 (one k-part
 // 6.6, 32x128 6.7-7.0); M=128 K=3584 N=1024 32x64 split 2 ways, two k-parts
-// 8.7 (4 ways, one k-part 9.7; 32x128 split 4 ways 9.6-9.8); 64x64 two
+// 7.96 (3 ways 7.93, 2 ways 8.8; one k-part 4 ways 9.7; 32x128 split 4 ways
+// 9.6-9.8); M=64 K=3584 N=1024 32x64 split 4 ways 7.2 (3 ways 7.4, 8 ways
+// 8.0); M=128 K=2048 N=1024 2 ways 7.1 (3 ways 6.85); 64x64 two
 // k-parts against 32x128 at 224-256 tiles: M=256 K=1024 N=3584 6.6 / 7.3,
 // M=1024 K=3584 N=1024 13.9 / 15.6, M=512 K=1024 N=2048 6.5 / 7.1, M=1024
 // K=2048 N=1024 9.3 / 9.9, M=512 K=3584 N=2048 14.1 / 15.9; at 288-384
@@ -69,10 +72,7 @@ SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
     constexpr SkConfig kOne[] = {{128, 8, 3, 1}, {64, 4, 3, 1}, {64, 2, 3, 1}, {32, 4, 3, 1}, {32, 2, 3, 1}};
     const int64_t G = K / kGroup;
     auto finish = [&](SkConfig c) {
-        const int64_t per = G / c.splits;
-        const bool even = per % 2 == 0;
-        if (even && ((c.nwv == 2 && per >= 2) ||
-                     (c.nwv == 4 && ((c.tm == 64 && per >= 8) || (c.tm == 32 && per >= 14)))))
+        if (G % 2 == 0 && (c.nwv == 2 || (c.nwv == 4 && ((c.tm == 64 && G >= 8) || (c.tm == 32 && G >= 14)))))
             c.kg = c.kw = 2;
         c.wr = c.tm != 128;
         return c;
@@ -89,13 +89,12 @@ SkConfig choose_gemm(int64_t M, int64_t K, int64_t N, bool can_split) {
     SkConfig c{32, 2, 3, 1};
     const int64_t tiles = w4a16_sk_tiles(M, N, c);
     if (!can_split || tiles > kSkMaxSplitTiles) return finish(c);
-    int s_even = 1, s_any = 1;
-    for (int64_t s = 2; s <= G && s <= 64; ++s) {
-        if (G % s != 0 || tiles * s > 256) continue;
-        if ((G / s) % 2 == 0 && G / s >= 8) s_even = static_cast<int>(s);
-        if (G / s >= 7) s_any = static_cast<int>(s);
-    }
-    c.splits = s_even > 1 ? s_even : s_any;
+    // the K split: the most ways within 256 workgroups that leave at least 7
+    // groups per workgroup on average, cut in whole stages (two groups each
+    // where K/128 is even)
+    const int64_t U = G % 2 == 0 ? G / 2 : G;
+    for (int64_t s = 2; s <= U && s <= 64; ++s)
+        if (tiles * s <= 256 && G >= 7 * s) c.splits = static_cast<int>(s);
     return finish(c);
 }
 

@@ -51,7 +51,8 @@
 // MI355X this measured 0-9 % faster on 64- and 32-row tiles and the same on
 // 128 x 256 (whose LDS path stays).
 //
-// K split (S > 1): workgroup (tile, p) runs k-groups [p G/S, (p+1) G/S).
+// K split (S > 1): workgroup (tile, p) runs the stages [p U/S, (p+1) U/S)
+// of the U = G/KG stages over K (S need not divide U).
 // Each writes its fp32 partial tile (after the k-parts' sum) to the
 // workspace with device-scope
 // stores (written through to the point of coherence of all XCDs; a plain
@@ -183,8 +184,12 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
     const int Npad = nslab * kSlab;
     const int CK = K / kChunkK;
     const int G = K / kGroup;
-    const int g0 = static_cast<int>(int64_t(p) * G / S);
-    const int KT = (static_cast<int>(int64_t(p + 1) * G / S) - g0) / KG;   // stages of this split
+    // split p takes stages [p U / S, (p+1) U / S) of the U = G / KG stages
+    // over all of K (S need not divide U: the splits differ by one stage)
+    const int U = G / KG;
+    const int u0 = static_cast<int>(int64_t(p) * U / S);
+    const int g0 = u0 * KG;
+    const int KT = static_cast<int>(int64_t(p + 1) * U / S) - u0;   // stages of this split
 
     const int rows_here = M - m0 < TM ? M - m0 : TM;
     const __amdgpu_buffer_rsrc_t xr =
@@ -629,7 +634,7 @@ int64_t w4a16_sk_workspace_bytes(int64_t M, int64_t N, const SkConfig& c) {
 
 bool w4a16_sk_config_valid(int64_t M, int64_t K, int64_t N, const SkConfig& c) {
     return pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr) != nullptr && c.splits >= 1 && c.splits <= 64 && K % kGroup == 0 &&
-           (K / kGroup) % c.splits == 0 && (K / kGroup / c.splits) % c.kg == 0 &&
+           (K / kGroup) % c.kg == 0 && c.splits <= K / kGroup / c.kg &&
            (c.splits == 1 || w4a16_sk_tiles(M, N, c) <= kSkMaxSplitTiles);
 }
 
@@ -639,8 +644,8 @@ int launch_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const v
     SkFn fn = pick_sk(c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr);
     if (fn == nullptr || !w4a16_sk_config_valid(M, K, N, c))
         return fail(MCV_ERR_INVALID_ARG,
-                    "w4a16 GEMM: no kernel for TM=%d waves=%d NS=%d KG=%d KW=%d WR=%d S=%d at M=%lld K=%lld N=%lld (S must "
-                    "divide K/128, KG the groups of a split, and a split needs at most %d tiles)",
+                    "w4a16 GEMM: no kernel for TM=%d waves=%d NS=%d KG=%d KW=%d WR=%d S=%d at M=%lld K=%lld N=%lld (KG must "
+                    "divide K/128, S be at most K/128/KG, and a split needs at most %d tiles)",
                     c.tm, c.nwv, c.ns, c.kg, c.kw, c.wr, c.splits, (long long)M, (long long)K, (long long)N,
                     kSkMaxSplitTiles);
     const int64_t nslab = ceil_div(N, kSlab);

@@ -312,15 +312,16 @@ def test_w4a16_gemm_workspace_query(mcv):
     """Workspace of the K split across workgroups: none where the GEMV (few
     rows) or an unsplit tile grid (it covers most of the chip) takes the
     shape, or for an invalid K; otherwise the 4 KiB counter region plus S fp32
-    partial tiles of 32 x 64 per tile, S the most ways (dividing K/128) that
-    keep the grid within 256 workgroups and leave an even number of at least 8
-    groups per workgroup, else the most that leave at least 7; the kernel
-    label names the same configuration."""
+    partial tiles of 32 x 64 per tile, S the most ways that keep the grid
+    within 256 workgroups and leave at least 7 groups per workgroup on average
+    (S need not divide K/128); the kernel label names the same
+    configuration."""
     L = mcv.lib()
     q = L.mcv_w4a16_gemm_workspace_bytes
     part = 32 * 64 * 4
-    for (M, K, N), S in [((128, 3584, 1024), 2), ((64, 3584, 1024), 2), ((96, 3584, 2048), 2),
-                         ((128, 2048, 2048), 2), ((128, 4096, 1024), 4), ((128, 2688, 1024), 3)]:
+    for (M, K, N), S in [((128, 3584, 1024), 4), ((64, 3584, 1024), 4), ((96, 3584, 2048), 2),
+                         ((128, 2048, 2048), 2), ((128, 4096, 1024), 4), ((128, 2688, 1024), 3),
+                         ((128, 2048, 1024), 2), ((64, 8192, 1024), 8)]:
         tiles = -(-M // 32) * -(-N // 64)
         assert q(M, K, N) == 4096 + tiles * S * part, (M, K, N)
         assert f"K split {S} ways".encode() in L.mcv_w4a16_gemm_kernel_name(M, K, N, 1)
@@ -333,7 +334,7 @@ def test_w4a16_gemm_workspace_query(mcv):
     # even group counts of at least 8 (64-row tiles) or 14 (32-row tiles) take two k-parts
     assert b"<64, 4, 3, 2, 2, 1>" in L.mcv_w4a16_gemm_kernel_name(2048, 3584, 1024, 1)
     assert b"<32, 2, 3, 2, 2, 1> (K split 1 ways, 256 workgroups" in L.mcv_w4a16_gemm_kernel_name(512, 3584, 1024, 1)
-    assert b"<32, 2, 3, 2, 2, 1> (K split 2 ways, 128 workgroups" in L.mcv_w4a16_gemm_kernel_name(128, 3584, 1024, 1)
+    assert b"<32, 2, 3, 2, 2, 1> (K split 4 ways, 256 workgroups" in L.mcv_w4a16_gemm_kernel_name(128, 3584, 1024, 1)
     assert b"<64, 4, 3, 2, 2, 1>" in L.mcv_w4a16_gemm_kernel_name(512, 1024, 3584, 1)
     assert b"<32, 2, 3, 2, 2, 1> (K split 1 ways, 224 workgroups" in L.mcv_w4a16_gemm_kernel_name(128, 1024, 3584, 1)
 

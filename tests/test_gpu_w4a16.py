@@ -220,7 +220,7 @@ def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
     stream = torch.cuda.current_stream().cuda_stream
     G = K // 128
     for tm, nwv, ns, kg, kw, wr in SK_CONFIGS:
-        for S in [s for s in (1, 2, 4, 8, 16) if G % s == 0 and (G // s) % kg == 0]:
+        for S in [s for s in (1, 2, 3, 4, 8, 16) if G % kg == 0 and s <= G // kg]:
             assert L.mcv_w4a16_gemm_sk_workspace_bytes(M, w.N, tm, nwv, S) <= ws.numel()
             outs = []
             for _ in range(2 if S > 1 else 1):
@@ -235,11 +235,12 @@ def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
                 assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), (tm, nwv, ns, kg, kw, wr, S)
     # the counters are zero after every call
     assert int(ws[:4096].count_nonzero().item()) == 0
-    # an unbuilt configuration, a split that does not divide K/128, groups per
-    # stage that do not divide a split's groups, a missing workspace: clear errors
+    # an unbuilt configuration, more splits than groups, more splits than
+    # stages, two k-parts with one group per stage, a missing workspace, a bad
+    # tile order: clear errors
     assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 96, 4, 3, 1, 1, 0, 0, 1, None, 0,
                                stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 0, 3,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 0, G + 1,
                                ws.data_ptr(), ws.numel(), stream) == 1
     assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 2, 1, 0, 0, G,
                                ws.data_ptr(), ws.numel(), stream) == 1
