@@ -105,11 +105,22 @@ int mcv_w4a16_pack_awq(const int32_t* qweight_host, const int32_t* qzeros_host,
  * q - zero are kept exact by re-basing each (k/128 group, column) on one
  * common zero (unchanged nibbles when the rows' zeros agree, as in every
  * sym=True checkpoint).  MCV_ERR_SHAPE for g_idx outside [0, G);
- * MCV_ERR_UNSUPPORTED when one group's values span more than 16 levels. */
+ * MCV_ERR_UNSUPPORTED when one group's values span more than 16 levels (the
+ * loaders then keep the weight dense: mcv_w4a16_dequant_gptq_host). */
 int mcv_w4a16_pack_gptq(const int32_t* qweight_host, const int32_t* qzeros_host,
                         const int32_t* g_idx_host, const uint16_t* scales_host,
                         int64_t K, int64_t N, int64_t groups,
                         void* qw_host, uint16_t* scales_out_host, uint32_t* zeros_out_host);
+
+/* When mcv_w4a16_pack_gptq returns MCV_ERR_UNSUPPORTED (an act-order block's
+ * values span more than 16 levels): the dense fp16 weight w_kn_host [K][N],
+ * element (k, n) = RNE((q - zero[g_idx[k]]) * scale[k/128][n]), the
+ * reference's values (quantized_weight.cpp:98-117 with the kernel's scale by
+ * position), for a plain fp16 GEMM.  Same tensors and errors as
+ * mcv_w4a16_pack_gptq; g_idx may be NULL. */
+int mcv_w4a16_dequant_gptq_host(const int32_t* qweight_host, const int32_t* qzeros_host,
+                                const int32_t* g_idx_host, const uint16_t* scales_host, int64_t K,
+                                int64_t N, int64_t groups, uint16_t* w_kn_host);
 
 /* Build-defined synthetic int4 quantiser (the reference has none; it only
  * unpacks AutoAWQ/GPTQ checkpoints).  Per (group g, column n) over the 128

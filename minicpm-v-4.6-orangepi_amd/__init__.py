@@ -35,7 +35,13 @@ _vp = ctypes.c_void_p
 
 
 class McvError(RuntimeError):
-    """Raised when a C-ABI call returns a non-zero status."""
+    """Raised when a C-ABI call returns a non-zero status (`status`, one of
+    the mcv_status codes; None for an error raised in Python)."""
+
+    status: Optional[int] = None
+
+
+MCV_ERR_UNSUPPORTED = 4
 
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -55,6 +61,7 @@ _SIGS = {
     "mcv_w4a16_packed_zero_bytes": (_c_i64, [_c_i64, _c_i64]),
     "mcv_w4a16_pack_awq": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp]),
     "mcv_w4a16_pack_gptq": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp]),
+    "mcv_w4a16_dequant_gptq_host": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp]),
     "mcv_w4a16_quantize_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_int]),
     "mcv_w4a16_quantize_nk_host": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_int]),
     "mcv_w4a16_unpack_host": (_c_int, [_vp, _vp, _vp, _c_int, _c_i64, _c_i64, _vp, _vp, _vp]),
@@ -132,7 +139,9 @@ def lib() -> ctypes.CDLL:
 
 def _check(rc: int, what: str) -> None:
     if rc != 0:
-        raise McvError(f"{what} failed (status {rc}): {lib().mcv_last_error().decode()}")
+        e = McvError(f"{what} failed (status {rc}): {lib().mcv_last_error().decode()}")
+        e.status = rc
+        raise e
 
 
 def _np_ptr(a: np.ndarray) -> int:
@@ -183,6 +192,23 @@ def pack_gptq(qweight: np.ndarray, qzeros: np.ndarray, g_idx: Optional[np.ndarra
     _check(lib().mcv_w4a16_pack_gptq(_np_ptr(qweight), _np_ptr(qzeros), gp, _np_ptr(scales), K, N, groups,
                                      _np_ptr(qw), _np_ptr(sc), _np_ptr(zr)), "mcv_w4a16_pack_gptq")
     return qw, sc, zr
+
+
+def dequant_gptq(qweight: np.ndarray, qzeros: np.ndarray, g_idx: Optional[np.ndarray], scales: np.ndarray):
+    """GPTQ v1 tensors -> the dense fp16 weight [K][N] (u16 bits), RNE((q -
+    zero[g_idx[k]]) * scale[k/128]): for act-order weights pack_gptq refuses."""
+    qweight = np.ascontiguousarray(qweight, np.int32)
+    qzeros = np.ascontiguousarray(qzeros, np.int32)
+    scales = np.ascontiguousarray(scales).view(np.uint16)
+    K, N = qweight.shape[0] * 8, qweight.shape[1]
+    gp = 0
+    if g_idx is not None:
+        g_idx = np.ascontiguousarray(g_idx, np.int32)
+        gp = _np_ptr(g_idx)
+    w = np.empty((K, N), np.uint16)
+    _check(lib().mcv_w4a16_dequant_gptq_host(_np_ptr(qweight), _np_ptr(qzeros), gp, _np_ptr(scales), K, N,
+                                             scales.shape[0], _np_ptr(w)), "mcv_w4a16_dequant_gptq_host")
+    return w
 
 
 def unpack(qw: np.ndarray, scales: np.ndarray, zeros: np.ndarray, zero_bias: int, K: int, N: int):
@@ -327,6 +353,11 @@ class W4A16QuantizedWeight:
     N: int
     zero_bias: int = 0
     group_size: int = GROUP
+    # torch.float16 [K, N], set instead of the slab tensors for a GPTQ
+    # act-order weight whose 128-row blocks span more than 16 levels (the
+    # exact dequantised values; matmul_w4a16 runs it as a dense fp16 GEMM,
+    # every fused W4A16 entry point refuses it)
+    dense: "object" = None
 
     @classmethod
     def from_packed(cls, qw, sc, zr, K, N, zero_bias=0, device="cuda"):
@@ -344,9 +375,19 @@ class W4A16QuantizedWeight:
     def from_gptq(cls, qweight, qzeros, g_idx, scales, device="cuda"):
         qweight = np.asarray(qweight)
         K, N = qweight.shape[0] * 8, qweight.shape[1]
-        return cls.from_packed(*pack_gptq(qweight, qzeros, g_idx, scales), K, N, 1, device)
+        try:
+            return cls.from_packed(*pack_gptq(qweight, qzeros, g_idx, scales), K, N, 1, device)
+        except McvError as e:
+            if e.status != MCV_ERR_UNSUPPORTED:
+                raise
+        torch = _torch()
+        w = dequant_gptq(qweight, qzeros, g_idx, scales)
+        return cls(None, None, None, K, N, 1, dense=torch.from_numpy(w.view(np.int16)).to(device).view(torch.float16))
 
     def ptrs(self):
+        if self.dense is not None:
+            raise McvError("this GPTQ act-order weight is kept dense (its 128-row blocks span more than 16 "
+                           "levels); only matmul_w4a16 takes it")
         return _dev(self.qweight), _dev(self.scales), _dev(self.zeros)
 
 
@@ -405,6 +446,15 @@ def matmul_w4a16(x, w: W4A16QuantizedWeight, out=None, stream=None):
     torch = _torch()
     if x.dtype != torch.float16 or x.dim() != 2 or x.shape[1] != w.K or not x.is_contiguous():
         raise McvError(f"matmul_w4a16: x must be contiguous fp16 [M, {w.K}]")
+    if w.dense is not None:                  # act-order weight kept dense: the vendor's fp16 GEMM
+        if out is None:
+            out = torch.empty((x.shape[0], w.N), dtype=torch.float16, device=x.device)
+        if stream is None:
+            torch.matmul(x, w.dense, out=out)
+        else:
+            with torch.cuda.stream(stream):
+                torch.matmul(x, w.dense, out=out)
+        return out
     nb = int(lib().mcv_w4a16_gemm_workspace_bytes(x.shape[0], w.K, w.N))
     if nb == 0:
         return _w4_call("mcv_w4a16_gemm", x, w, out, stream)

@@ -31,6 +31,11 @@ struct W4A16QuantizedWeight {
     int64_t N{0};
     int64_t group_size{128};
     int zero_bias{0};       // 0: AutoAWQ / synthetic, 1: GPTQ v1 (stored zero - 1)
+    // Float16 [K, N], set instead of the three tensors above for a GPTQ
+    // act-order weight whose 128-row blocks span more than 16 levels (no
+    // 4-bit zero per block holds them): the exact dequantised values, run by
+    // matmul_w4a16 as a dense fp16 GEMM; the fused W4A16 entry points refuse it
+    Tensor dense_kn;
 };
 
 struct W8A8QuantizedWeight {

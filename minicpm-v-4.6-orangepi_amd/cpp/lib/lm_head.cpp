@@ -10,6 +10,9 @@ namespace minicpmv {
 
 LmHeadW4A16 make_lm_head_w4a16(W4A16QuantizedWeight weight, int64_t vocab) {
     if (vocab <= 0 || vocab > weight.N) throw std::runtime_error("lm_head vocab must be in [1, weight N]");
+    if (weight.dense_kn.numel() > 0)
+        throw std::runtime_error("make_lm_head_w4a16: the weight is kept dense (GPTQ act-order blocks span more than "
+                                 "16 levels); the lm_head takes slab-layout weights");
     LmHeadW4A16 head;
     head.weight = std::move(weight);
     head.vocab = vocab;

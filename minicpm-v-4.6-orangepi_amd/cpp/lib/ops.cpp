@@ -23,6 +23,13 @@ void require(bool ok, const std::string& msg) {
     if (!ok) throw std::runtime_error(msg);
 }
 
+// The fused W4A16 entry points take slab-layout weights only.
+void require_slab(const W4A16QuantizedWeight& w, const char* what) {
+    require(w.dense_kn.numel() == 0, std::string(what) +
+                                         ": this GPTQ act-order weight is kept dense (its 128-row blocks span more "
+                                         "than 16 levels); only matmul_w4a16 takes it");
+}
+
 // The workspace of the 4-argument matmul_w4a16: one per (device, stream) of
 // this thread, grown on demand and kept, so calls on one stream reuse it in
 // stream order and calls on two streams never share one.
@@ -82,6 +89,10 @@ void matmul_w4a16(const Tensor& x, const W4A16QuantizedWeight& w, Tensor& out, h
     require(x.dtype() == DType::Float16 && out.dtype() == DType::Float16, "matmul_w4a16 x and out must be fp16");
     require(x.shape().size() == 2 && x.shape()[1] == w.K, "matmul_w4a16 x must be [M, K]");
     require(out.shape() == std::vector<int64_t>{x.shape()[0], w.N}, "matmul_w4a16 out must be [M, N]");
+    if (w.dense_kn.numel() > 0) {                // act-order weight kept dense (quantized_weight.h)
+        matmul_b_transposed(x, w.dense_kn, out, stream);
+        return;
+    }
     require(w.w_int8.data() && w.scales.data() && w.zeros.data(), "matmul_w4a16 weight is not loaded");
     const int64_t nb = mcv_w4a16_gemm_workspace_bytes(x.shape()[0], w.K, w.N);
     if (nb > 0 && static_cast<int64_t>(workspace.numel()) < nb) {
@@ -99,6 +110,8 @@ void mlp_gate_up_silu_w4a16(const Tensor& x, const W4A16QuantizedWeight& gate, c
     require(x.dtype() == DType::Float16 && act.dtype() == DType::Float16, "mlp_gate_up_silu x and act must be fp16");
     require(x.shape().size() == 2 && x.shape()[1] == gate.K, "mlp_gate_up_silu x must be [M, K]");
     require(up.K == gate.K && up.N == gate.N, "mlp_gate_up_silu gate and up must have the same shape");
+    require_slab(gate, "mlp_gate_up_silu");
+    require_slab(up, "mlp_gate_up_silu");
     require(act.shape() == std::vector<int64_t>{x.shape()[0], gate.N}, "mlp_gate_up_silu act must be [M, N]");
     check_mcv(mcv_w4a16_gate_up_silu(x.data(), x.shape()[0], gate.K, gate.N, gate.w_int8.data(), gate.scales.data(),
                                      gate.zeros.data(), gate.zero_bias, up.w_int8.data(), up.scales.data(),
@@ -110,6 +123,9 @@ DecodeMlpW4A16 make_decode_mlp_w4a16(const W4A16QuantizedWeight& gate, const W4A
                                      const W4A16QuantizedWeight& down) {
     require(up.K == gate.K && up.N == gate.N, "decode MLP gate and up must have the same shape");
     require(down.K == gate.N && down.N == gate.K, "decode MLP down must be [I, H] for gate [H, I]");
+    require_slab(gate, "make_decode_mlp_w4a16");
+    require_slab(up, "make_decode_mlp_w4a16");
+    require_slab(down, "make_decode_mlp_w4a16");
     DecodeMlpW4A16 mlp;
     mlp.gate = &gate;
     mlp.up = &up;
@@ -314,6 +330,7 @@ void matmul_w4a16_multi(const Tensor& x, const std::vector<const W4A16QuantizedW
     require(x.dtype() == DType::Float16 && x.shape().size() == 2, "matmul_w4a16_multi x must be fp16 [M, K]");
     require(!weights.empty() && weights.size() <= 4 && weights.size() == outs.size(),
             "matmul_w4a16_multi takes 1..4 weights and as many outputs");
+    for (const W4A16QuantizedWeight* w : weights) require_slab(*w, "matmul_w4a16_multi");
     const int64_t M = x.shape()[0], K = x.shape()[1];
     std::vector<mcv_w4a16_part> parts(weights.size());
     for (size_t i = 0; i < weights.size(); ++i) {
@@ -358,6 +375,7 @@ void mlp_gate_up_silu_w8a8(const Tensor& x_int8, const Tensor& x_scale, const W8
 }
 
 void w4a16_dequant(const W4A16QuantizedWeight& w, Tensor* w_f16, Tensor* w_i8, hipStream_t stream) {
+    require_slab(w, "w4a16_dequant");
     const std::vector<int64_t> kn{w.K, w.N};
     if (w_f16) require(w_f16->dtype() == DType::Float16 && w_f16->shape() == kn, "w4a16_dequant f16 out must be [K, N]");
     if (w_i8) require(w_i8->dtype() == DType::Int8 && w_i8->shape() == kn, "w4a16_dequant i8 out must be [K, N]");

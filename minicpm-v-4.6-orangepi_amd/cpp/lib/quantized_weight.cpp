@@ -68,8 +68,23 @@ W4A16QuantizedWeight pack_w4a16_awq(const int32_t* qweight, const int32_t* qzero
 W4A16QuantizedWeight pack_w4a16_gptq(const int32_t* qweight, const int32_t* qzeros, const int32_t* g_idx,
                                      const uint16_t* scales, int64_t K, int64_t N, int64_t groups) {
     PackedHost p = alloc_packed(K, N);
-    check_mcv(mcv_w4a16_pack_gptq(qweight, qzeros, g_idx, scales, K, N, groups, p.qw.data(), p.sc.data(), p.zr.data()),
-              "pack_w4a16_gptq");
+    const int rc =
+        mcv_w4a16_pack_gptq(qweight, qzeros, g_idx, scales, K, N, groups, p.qw.data(), p.sc.data(), p.zr.data());
+    if (rc == MCV_ERR_UNSUPPORTED) {
+        // an act-order block spans more than 16 levels: the dense fp16 weight
+        std::vector<uint16_t> w(static_cast<size_t>(K * N));
+        check_mcv(mcv_w4a16_dequant_gptq_host(qweight, qzeros, g_idx, scales, K, N, groups, w.data()),
+                  "pack_w4a16_gptq (dense)");
+        W4A16QuantizedWeight out;
+        out.K = K;
+        out.N = N;
+        out.group_size = MCV_W4_GROUP;
+        out.zero_bias = 1;
+        out.dense_kn = Tensor({K, N}, DType::Float16);
+        out.dense_kn.copy_from_host(w.data(), w.size() * 2);
+        return out;
+    }
+    check_mcv(rc, "pack_w4a16_gptq");
     return upload_packed(p.qw, p.sc, p.zr, K, N, 1);
 }
 

@@ -588,3 +588,33 @@ extern "C" int mcv_w4a16_quantize_host(const uint16_t* w_kn, int64_t K, int64_t 
     }
     return MCV_OK;
 }
+
+// GPTQ act-order weights whose 128-row blocks a single 4-bit zero cannot
+// hold: the dense fp16 weight, each element the reference's int8 value
+// q - zero[g_idx[k]] (quantized_weight.cpp:98-117) times the scale of group
+// k / 128, rounded once to fp16 (the value the slab path widens to).  The
+// product of an integer in [-16, 15] and an fp16 scale is exact in fp32, so
+// the one rounding is f2h_rne_host's.
+extern "C" int mcv_w4a16_dequant_gptq_host(const int32_t* qweight, const int32_t* qzeros, const int32_t* g_idx,
+                                           const uint16_t* scales, int64_t K, int64_t N, int64_t groups,
+                                           uint16_t* w_kn) {
+    if (!qweight || !qzeros || !scales || !w_kn) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_dequant_gptq_host: null pointer");
+    if (K <= 0 || N <= 0 || K % kGroup != 0 || N % 8 != 0 || groups * kGroup != K || K > (int64_t(1) << 24) ||
+        N > (int64_t(1) << 24))
+        return fail(MCV_ERR_SHAPE, "mcv_w4a16_dequant_gptq_host: need K %% 128 == 0, N %% 8 == 0, groups*128 == K "
+                    "(K=%lld N=%lld groups=%lld)", (long long)K, (long long)N, (long long)groups);
+    if (g_idx)
+        for (int64_t k = 0; k < K; ++k)
+            if (g_idx[k] < 0 || g_idx[k] >= groups)
+                return fail(MCV_ERR_SHAPE, "mcv_w4a16_dequant_gptq_host: g_idx out of range (g_idx[%lld]=%d)",
+                            (long long)k, g_idx[k]);
+    for (int64_t k = 0; k < K; ++k) {
+        const int64_t gz = g_idx ? g_idx[k] : k / kGroup, gs = k / kGroup;
+        for (int64_t n = 0; n < N; ++n) {
+            const int q = static_cast<int>((static_cast<uint32_t>(qweight[(k / 8) * N + n]) >> (4 * (k % 8))) & 15u);
+            const int z = static_cast<int>((static_cast<uint32_t>(qzeros[gz * (N / 8) + n / 8]) >> (4 * (n % 8))) & 15u) + 1;
+            w_kn[k * N + n] = f2h_rne_host(static_cast<float>(q - z) * h2f_host(scales[gs * N + n]));
+        }
+    }
+    return MCV_OK;
+}

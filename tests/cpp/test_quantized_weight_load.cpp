@@ -44,12 +44,24 @@ static int check(HipContext& ctx, const W4A16QuantizedWeight& w, const std::vect
         num += d * d;
         den += double(ref) * ref;
     }
-    Tensor wi8({K, N}, DType::Int8);
-    wi8.allocate();
-    w4a16_dequant(w, nullptr, &wi8, ctx.stream());
-    std::vector<int8_t> hw8(static_cast<size_t>(K * N));
-    wi8.copy_to_host(hw8.data(), hw8.size());
-    const bool exact = hw8 == w8;
+    bool exact = true;
+    if (w.dense_kn.numel() > 0) {
+        // kept dense (an act-order block spans more than 16 levels): every
+        // value is RNE(w8 * scale of its k / 128 group)
+        std::vector<uint16_t> hd(static_cast<size_t>(K * N));
+        w.dense_kn.copy_to_host(hd.data(), hd.size() * 2);
+        for (int64_t k = 0; k < K; ++k)
+            for (int64_t n = 0; n < N; ++n)
+                exact &= hd[k * N + n] ==
+                         t::f2h_rne(static_cast<float>(w8[k * N + n]) * t::h2f(scales[(k / 128) * N + n]));
+    } else {
+        Tensor wi8({K, N}, DType::Int8);
+        wi8.allocate();
+        w4a16_dequant(w, nullptr, &wi8, ctx.stream());
+        std::vector<int8_t> hw8(static_cast<size_t>(K * N));
+        wi8.copy_to_host(hw8.data(), hw8.size());
+        exact = hw8 == w8;
+    }
     std::printf("%s K=%lld N=%lld max_abs=%.2e rel_l2=%.2e dequant_exact=%d\n", what, (long long)K, (long long)N, max_abs,
                 std::sqrt(num / den), int(exact));
     return (max_abs <= 2e-2 && std::sqrt(num / den) <= 1e-3 && exact) ? 0 : 1;
@@ -245,6 +257,28 @@ int main(int argc, char** argv) {
                               {"m.proj.scales", "F16", {G, N}, t::bytes_of(scales)}});
     WeightsIndex ig2(pg);
     rc |= check(ctx, load_w4a16_quantized_weight(ig2, "m.proj"), w8g, scales, "GPTQ act-order");
+
+    // act-order rows drawn from zero-1 and zero-16 groups (stored zeros 0 and
+    // 15) with the full nibble range: the blocks' values span 31 levels, which
+    // one 4-bit zero per block cannot hold, so the loader keeps the weight as
+    // its dense fp16 values and matmul_w4a16 runs a dense GEMM over it
+    std::vector<int32_t> gz3(gz.size()), gidx3(static_cast<size_t>(K));
+    for (int64_t g = 0; g < G; ++g)
+        for (int64_t j = 0; j < N / 8; ++j) gz3[g * (N / 8) + j] = static_cast<int32_t>(g % 2 ? 0xFFFFFFFFu : 0u);
+    for (int64_t k = 0; k < K; ++k) gidx3[k] = static_cast<int32_t>(k % 2);
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t n = 0; n < N; ++n) w8g[k * N + n] = static_cast<int8_t>(int(q[k * N + n]) - (k % 2 ? 16 : 1));
+    t::write_safetensors(pg, {{"m.proj.qweight", "I32", {K / 8, N}, t::bytes_of(gq)},
+                              {"m.proj.qzeros", "I32", {G, N / 8}, t::bytes_of(gz3)},
+                              {"m.proj.g_idx", "I32", {K}, t::bytes_of(gidx3)},
+                              {"m.proj.scales", "F16", {G, N}, t::bytes_of(scales)}});
+    WeightsIndex ig3(pg);
+    const W4A16QuantizedWeight wd = load_w4a16_quantized_weight(ig3, "m.proj");
+    if (wd.dense_kn.numel() != static_cast<size_t>(K * N) || wd.w_int8.numel() != 0) {
+        std::printf("GPTQ act-order, 31 levels: not kept dense\n");
+        rc |= 1;
+    }
+    rc |= check(ctx, wd, w8g, scales, "GPTQ act-order, 31 levels (dense)");
     rc |= check_w8a8(ctx, dir);
     return rc;
 }

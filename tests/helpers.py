@@ -244,3 +244,19 @@ def rel_l2(a: np.ndarray, b: np.ndarray) -> float:
     a = a.astype(np.float64)
     b = b.astype(np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def too_wide_gptq(rng, K, N):
+    """GPTQ tensors whose act-order g_idx makes every 128-row block draw rows
+    from a zero-1 group and a zero-16 group: values up to 31 levels apart."""
+    G = K // 128
+    qn = rng.integers(0, 16, (K, N)).astype(np.uint32)
+    qweight = np.zeros((K // 8, N), np.uint32)
+    for i in range(8):
+        qweight |= qn[i::8] << (4 * i)
+    zn = np.where(np.arange(G)[:, None] % 2 == 0, 0, 15) * np.ones((G, N), np.uint32)   # stored zeros 0 / 15
+    qzeros = np.zeros((G, N // 8), np.uint32)
+    for sl in range(8):
+        qzeros |= zn[:, sl::8].astype(np.uint32) << (4 * sl)
+    g_idx = (np.arange(K) % 2).astype(np.int32)
+    return qweight.view(np.int32), qzeros.view(np.int32), g_idx

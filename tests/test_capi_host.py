@@ -8,7 +8,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from helpers import ROOT, f16_normal, synth_w4a16
+from helpers import ROOT, f16_normal, synth_w4a16, too_wide_gptq
 
 
 def _declared_functions():
@@ -134,19 +134,25 @@ def test_gptq_act_order_rebased(mcv, oracle):
         assert np.array_equal(s, scales)
 
 
-def test_gptq_act_order_too_wide_refused(mcv):
-    # one block draws rows from a zero-1 group and a zero-16 group: its values
-    # span 31 levels, more than one zero per block can express
-    K, N, G = 256, 8, 2
-    qn = np.zeros((K, N), np.uint32)
-    qn[0::2] = 15
-    qweight = np.zeros((K // 8, N), np.uint32)
-    for i in range(8):
-        qweight |= qn[i::8] << (4 * i)
-    qzeros = np.array([[0x00000000], [0xFFFFFFFF]], np.uint32)      # stored zeros 0 and 15
-    g_idx = (np.arange(K) % 2).astype(np.int32)
-    with pytest.raises(mcv.McvError, match="levels"):
-        mcv.pack_gptq(qweight.view(np.int32), qzeros.view(np.int32), g_idx, np.zeros((G, N), np.uint16))
+def test_gptq_act_order_too_wide_dense(mcv, oracle):
+    # blocks whose values span more than 16 levels: the slab packer refuses
+    # them (MCV_ERR_UNSUPPORTED), and the dense fp16 weight the loaders then
+    # use is RNE((q - zero[g_idx[k]]) * scale[k/128]) bit for bit
+    rng = np.random.default_rng(26)
+    K, N = 512, 72
+    qweight, qzeros, g_idx = too_wide_gptq(rng, K, N)
+    scales = f16_normal(rng, (K // 128, N), 0.01)
+    with pytest.raises(mcv.McvError, match="levels") as e:
+        mcv.pack_gptq(qweight, qzeros, g_idx, scales)
+    assert e.value.status == mcv.MCV_ERR_UNSUPPORTED
+    w8 = oracle.unpack_gptq(qweight, qzeros, g_idx, K // 128)
+    assert w8.min() < -8 and w8.max() > 8                    # more than 16 levels in use
+    want = (w8.astype(np.float32) * np.repeat(oracle.h2f(scales), 128, axis=0)).astype(np.float16).view(np.uint16)
+    assert np.array_equal(mcv.dequant_gptq(qweight, qzeros, g_idx, scales), want)
+    # without g_idx (or a trivial one) the same function gives the in-order values
+    w8t = oracle.unpack_gptq(qweight, qzeros, (np.arange(K) // 128).astype(np.int32), K // 128)
+    want_t = (w8t.astype(np.float32) * np.repeat(oracle.h2f(scales), 128, axis=0)).astype(np.float16).view(np.uint16)
+    assert np.array_equal(mcv.dequant_gptq(qweight, qzeros, None, scales), want_t)
 
 
 def test_gptq_g_idx_out_of_range(mcv):

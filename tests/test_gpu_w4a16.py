@@ -9,7 +9,7 @@ checked against an fp64 product of the oracle-exact dequantised weights.
 import numpy as np
 import pytest
 
-from helpers import f16_normal, rel_l2, synth_w4a16
+from helpers import f16_normal, rel_l2, synth_w4a16, too_wide_gptq
 
 pytestmark = pytest.mark.gpu
 
@@ -309,6 +309,26 @@ def test_gptq_act_order(mcv, oracle, cuda):
         x = f16_normal(rng, (M, K), 1.0)
         out = _host_f32(mcv.matmul_w4a16(_to_dev(x), w))
         _check(out, oracle.w4a16_matmul(x, w8, scales), f"gptq act-order M={M}")
+
+
+def test_gptq_act_order_too_wide_dense(mcv, oracle, cuda):
+    # act-order blocks spanning more than 16 levels: the weight is kept as
+    # its exact dense fp16 values and matmul_w4a16 runs the vendor's fp16
+    # GEMM over it, within the GEMMs' tolerance of the oracle's product; the
+    # fused entry points refuse it
+    rng = np.random.default_rng(27)
+    K, N = 1024, 520
+    qweight, qzeros, g_idx = too_wide_gptq(rng, K, N)
+    scales = f16_normal(rng, (K // 128, N), 0.002)
+    w = mcv.W4A16QuantizedWeight.from_gptq(qweight, qzeros, g_idx, scales)
+    assert w.dense is not None and w.qweight is None
+    w8 = oracle.unpack_gptq(qweight, qzeros, g_idx, K // 128)
+    for M in (1, 64):
+        x = f16_normal(rng, (M, K), 1.0)
+        out = _host_f32(mcv.matmul_w4a16(_to_dev(x), w))
+        _check(out, oracle.w4a16_matmul(x, w8, scales), f"gptq act-order dense M={M}")
+    with pytest.raises(mcv.McvError, match="kept dense"):
+        mcv.matmul_w4a16_gemv(_to_dev(f16_normal(rng, (1, K), 1.0)), w)
 
 
 def _reference_tile_pack(w8, K, N):
