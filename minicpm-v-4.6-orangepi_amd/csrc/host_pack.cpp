@@ -300,10 +300,14 @@ uint16_t f2h_trunc_host(float f) {
 }
 
 // Clamp, then round half away from zero (quantized_weight.cpp:197-202).  The
-// volatile stores keep each fp32 operation separately rounded.
+// volatile stores keep each fp32 operation separately rounded.  A NaN product
+// (an inf weight times the zero inverse of an inf scale) passes both clamps
+// and becomes 0: the value the reference's float-to-int conversion gives it
+// on aarch64 and x86-64 alike (there the cast itself is undefined).
 int8_t quantize_i8_host(float v, float inv) {
     volatile float q = v * inv;
     float t = q;
+    if (t != t) return 0;
     if (t > 127.0f) t = 127.0f;
     if (t < -128.0f) t = -128.0f;
     volatile float r = t >= 0.0f ? t + 0.5f : t - 0.5f;
@@ -343,6 +347,9 @@ extern "C" int mcv_w8a8_quantize_weight_host(const uint16_t* w_kn, int64_t K, in
     if (K <= 0 || N <= 0) return fail(MCV_ERR_SHAPE, "mcv_w8a8_quantize_weight_host: K and N must be positive");
     if (out_layout != MCV_W8_KN && out_layout != MCV_W8_NK && out_layout != MCV_W8_TILED)
         return fail(MCV_ERR_INVALID_ARG, "mcv_w8a8_quantize_weight_host: bad layout %d", out_layout);
+    if (out_layout == MCV_W8_TILED && mcv_w8a8_tiled_bytes(K, N) == 0)
+        return fail(MCV_ERR_SHAPE, "mcv_w8a8_quantize_weight_host: K=%lld N=%lld too large for MCV_W8_TILED",
+                    (long long)K, (long long)N);
     const int64_t kblocks = ceil_div(K, 128) * 4;
     if (out_layout == MCV_W8_TILED) std::memset(q, 0, static_cast<size_t>(mcv_w8a8_tiled_bytes(K, N)));
     for (int64_t n = 0; n < N; ++n) {
@@ -423,6 +430,8 @@ extern "C" int mcv_w8a8_quantize_weight_nk_pad_host(const uint16_t* w_nk, int sr
         return fail(MCV_ERR_INVALID_ARG, "%s: bad source dtype %d", who, src_dtype);
     if (out_layout != MCV_W8_KN && out_layout != MCV_W8_NK && out_layout != MCV_W8_TILED)
         return fail(MCV_ERR_INVALID_ARG, "%s: bad layout %d", who, out_layout);
+    if (out_layout == MCV_W8_TILED && mcv_w8a8_tiled_bytes(K, N) == 0)
+        return fail(MCV_ERR_SHAPE, "%s: K=%lld N=%lld too large for MCV_W8_TILED", who, (long long)K, (long long)N);
     const int64_t kblocks = ceil_div(K, 128) * 4;
     if (out_layout == MCV_W8_TILED) std::memset(q, 0, static_cast<size_t>(mcv_w8a8_tiled_bytes(K, N)));
     const bool bf = src_dtype == MCV_SRC_BF16;
@@ -474,11 +483,13 @@ void quantize_group_int4(const float* v, uint16_t* s16_out, uint32_t* z_out, uin
     if (range < 1e-5f) range = 1e-5f;
     const uint16_t s16 = f2h_rne_host(range / 15.0f);
     const float sc = h2f_host(s16);
+    // clamp(x, 0, 15) with NaN -> 0 (a group holding an inf, e.g. a bf16
+    // value beyond the fp16 range, divides inf by inf)
     float zf = std::nearbyint(-lo / sc);
-    zf = zf < 0.0f ? 0.0f : (zf > 15.0f ? 15.0f : zf);
+    zf = zf > 0.0f ? (zf > 15.0f ? 15.0f : zf) : 0.0f;
     for (int kk = 0; kk < kGroup; ++kk) {
         float qf = std::nearbyint(v[kk] / sc) + zf;
-        qf = qf < 0.0f ? 0.0f : (qf > 15.0f ? 15.0f : qf);
+        qf = qf > 0.0f ? (qf > 15.0f ? 15.0f : qf) : 0.0f;
         q[kk] = static_cast<uint8_t>(qf);
     }
     *s16_out = s16;

@@ -216,7 +216,7 @@ int or_quantize_int4_awq(const uint16_t* w_kn, int64_t K, int64_t N,
             uint16_t s16 = or_f2h_rne(range / 15.0f);
             float s = or_h2f(s16);
             float zf = rintf(-lo / s);
-            if (zf < 0.0f) zf = 0.0f;
+            if (!(zf > 0.0f)) zf = 0.0f;   /* NaN (inf / inf) -> 0 */
             if (zf > 15.0f) zf = 15.0f;
             int zi = (int)zf;
             scales[g * N + n] = s16;
@@ -225,7 +225,7 @@ int or_quantize_int4_awq(const uint16_t* w_kn, int64_t K, int64_t N,
                 int64_t k = g * GROUP + kk;
                 float v = or_h2f(w_kn[k * N + n]);
                 float qf = rintf(v / s) + (float)zi;
-                if (qf < 0.0f) qf = 0.0f;
+                if (!(qf > 0.0f)) qf = 0.0f;
                 if (qf > 15.0f) qf = 15.0f;
                 q[k * N + n] = (uint8_t)qf;
             }
@@ -315,9 +315,12 @@ void or_w4a16_dequant_f16(const int8_t* w8, const uint16_t* scales, int64_t K, i
 /* ------------------------------------------------------------------------- */
 
 /* src/csrc/lib/quantized_weight.cpp:197-202: clamp first, then round half
- * away from zero by +-0.5 and truncation (each step one fp32 rounding). */
+ * away from zero by +-0.5 and truncation (each step one fp32 rounding).  A
+ * NaN product is 0, what the reference's (undefined) float-to-int8 cast gives
+ * on aarch64 (fcvtzs) and x86-64 (cvttss2si, low byte of 0x80000000). */
 int8_t or_quantize_i8(float value, float inv_scale) {
     float q = value * inv_scale;
+    if (q != q) return 0;
     if (q > 127.0f) q = 127.0f;
     if (q < -128.0f) q = -128.0f;
     return (int8_t)(q >= 0.0f ? q + 0.5f : q - 0.5f);

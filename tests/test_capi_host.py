@@ -190,6 +190,52 @@ def test_w8a8_host_quantizer_matches_oracle(mcv, oracle):
     assert np.array_equal(qtile, mcv.pack_w8a8_tiled(q_o))
 
 
+def test_quantisers_non_finite(mcv, oracle):
+    """Inf and NaN weights.  W8A8: max|w| skips NaN (the reference's std::max
+    keeps the running value), an inf makes the scale inf and its inverse 0,
+    so the channel quantises to 0, and a NaN product quantises to 0 (what the
+    reference's undefined float-to-int8 cast gives on aarch64 and x86-64).
+    Int4: a group holding an inf has scale inf and zero point 0 and every
+    nibble 0 (inf / inf = NaN -> 0).  Product and oracle agree bit for bit."""
+    rng = np.random.default_rng(31)
+    K, N = 256, 64
+    w = f16_normal(rng, (K, N), 0.02)
+    inf, ninf, nan = np.uint16(0x7C00), np.uint16(0xFC00), np.uint16(0x7E00)
+    w[5, 3], w[130, 9], w[7, 11], w[0, 12] = inf, ninf, nan, nan
+    q_o, s32_o, s16_o = oracle.w8a8_quantize_weight(w)
+    for layout in (mcv.W8_KN, mcv.W8_TILED):
+        q, s32, s16 = mcv.quantize_w8a8_weight_host(w, layout)
+        assert np.array_equal(q, q_o if layout == mcv.W8_KN else mcv.pack_w8a8_tiled(q_o))
+        assert np.array_equal(s32.view(np.uint32), s32_o.view(np.uint32)) and np.array_equal(s16, s16_o)
+    assert np.all(q_o[:, 3] == 0) and np.all(q_o[:, 9] == 0)
+    assert np.isinf(s32_o[3]) and s16_o[3] == 0x7C00
+    finite = w[:, 11].copy()
+    finite[7] = 0
+    want = oracle.w8a8_quantize_weight(np.ascontiguousarray(np.stack([finite] * 8, 1)))
+    assert q_o[7, 11] == 0 and np.array_equal(q_o[:, 11], want[0][:, 0]) and s32_o[11] == want[1][0]
+    # bf16 values beyond the fp16 range load as inf (weights.cpp:25-33)
+    bf = np.full((N, K), 0x3C00, np.uint16)                      # 2^-7
+    bf[2, 17] = 0x4780                                          # 65536.0 -> fp16 inf
+    qb, sb, _ = mcv.quantize_w8a8_weight_nk_host(bf, mcv.SRC_BF16, mcv.W8_KN)
+    assert np.all(qb[:, 2] == 0) and np.isinf(sb[2]) and np.all(qb[:, 3] == 127)
+    a = mcv.quantize_int4(w)
+    b = oracle.quantize_int4_awq(w)
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint8), y.view(np.uint8))
+    qweight, qzeros, scales = a
+    shifts = 4 * np.arange(8, dtype=np.uint32)
+    order = [0, 2, 4, 6, 1, 3, 5, 7]                            # AutoAWQ column order in a word
+    q_kn = np.zeros((K, N), np.uint32)
+    q_kn.reshape(K, N // 8, 8)[:, :, order] = (qweight.view(np.uint32)[:, :, None] >> shifts) & 15
+    z_gn = np.zeros((K // 128, N), np.uint32)
+    z_gn.reshape(K // 128, N // 8, 8)[:, :, order] = (qzeros.view(np.uint32)[:, :, None] >> shifts) & 15
+    for g, n in [(0, 3), (1, 9)]:                               # the groups holding +inf / -inf
+        assert scales[g, n] == 0x7C00 and z_gn[g, n] == 0
+        assert np.all(q_kn[g * 128:(g + 1) * 128, n] == 0)
+    assert q_kn[7, 11] == 0 and q_kn[0, 12] == 0                 # the NaN elements
+    assert np.all(np.isfinite(scales[:, 11].view(np.float16)))
+
+
 def _tiled_reference(q_kn):
     """MCV_W8_TILED restated from its definition in include/mcv_quant.h: pad
     to 64 columns / 128 k, then [slab][k-block of 32][half of 32 columns]
