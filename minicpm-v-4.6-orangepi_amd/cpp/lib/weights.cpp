@@ -99,19 +99,22 @@ public:
             return out;
         }
     }
-    // Skips any JSON value (used for __metadata__ and unknown keys).
-    void skip_value() {
+    // Skips any JSON value (used for __metadata__ and unknown keys); nesting
+    // deeper than kMaxDepth is refused rather than recursed into.
+    void skip_value(int depth = 0) {
         ws();
         if (i_ >= s_.size()) throw std::runtime_error("safetensors header: truncated");
         const char c = s_[i_];
         if (c == '"') { (void)str(); return; }
         if (c == '{' || c == '[') {
+            if (depth >= kMaxDepth)
+                throw std::runtime_error("safetensors header: values nested deeper than " + std::to_string(kMaxDepth));
             const char close = c == '{' ? '}' : ']';
             ++i_;
             if (peek(close)) { ++i_; return; }
             for (;;) {
                 if (c == '{') { (void)str(); expect(':'); }
-                skip_value();
+                skip_value(depth + 1);
                 if (peek(',')) { ++i_; continue; }
                 expect(close);
                 return;
@@ -125,6 +128,7 @@ public:
     }
 
 private:
+    static constexpr int kMaxDepth = 64;
     const std::string& s_;
     size_t i_{0};
 };
@@ -188,11 +192,16 @@ void WeightsIndex::parse() {
                     info.dtype = dtype_from_string(p.str());
                     have_dtype = true;
                 } else if (key == "shape") {
-                    for (uint64_t d : p.uint_array()) info.shape.push_back(static_cast<int64_t>(d));
+                    for (uint64_t d : p.uint_array()) {
+                        if (d > static_cast<uint64_t>(INT64_MAX)) throw std::runtime_error("bad shape for " + name);
+                        info.shape.push_back(static_cast<int64_t>(d));
+                    }
                     have_shape = true;
                 } else if (key == "data_offsets") {
                     const auto off = p.uint_array();
-                    if (off.size() != 2 || off[0] > off[1]) throw std::runtime_error("bad data_offsets for " + name);
+                    // offsets are relative to the data section and end inside the file
+                    if (off.size() != 2 || off[0] > off[1] || off[1] > map_size_ - data_base)
+                        throw std::runtime_error("bad data_offsets for " + name);
                     info.data_begin = data_base + off[0];
                     info.data_end = data_base + off[1];
                     have_offsets = true;
@@ -206,8 +215,12 @@ void WeightsIndex::parse() {
             if (!have_dtype || !have_shape || !have_offsets)
                 throw std::runtime_error("incomplete tensor entry for " + name);
             if (info.data_end > map_size_) throw std::runtime_error("tensor data beyond end of file for " + name);
-            size_t numel = 1;
-            for (int64_t d : info.shape) numel *= static_cast<size_t>(d);
+            uint64_t numel = 1;
+            for (int64_t d : info.shape) {
+                const uint64_t u = static_cast<uint64_t>(d);
+                if (u != 0 && numel > UINT64_MAX / u / 8) throw std::runtime_error("shape too large for " + name);
+                numel *= u;
+            }
             if (numel * dtype_size(info.dtype) != info.data_end - info.data_begin)
                 throw std::runtime_error("tensor byte size does not match its shape for " + name);
             tensors_.emplace(name, std::move(info));

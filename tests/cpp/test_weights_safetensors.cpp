@@ -66,7 +66,16 @@ int main(int argc, char** argv) {
     raw(dir + "/bad4.safetensors", "{\"x\":{\"dtype\":\"F16\",\"shape\":[2],\"data_offsets\":[0,40]}}", 4); // past EOF
     raw(dir + "/bad5.safetensors", "{\"x\":{\"dtype\":\"F16\",\"shape\":[2]}}", 4);                       // no offsets
     raw(dir + "/bad6.safetensors", "{}", 0, true);                                                           // header length lies
-    for (int i = 1; i <= 6; ++i)
+    // data_offsets whose sum with the data section's start wraps past 2^64
+    // (into the header, with a size that matches the shape)
+    raw(dir + "/bad8.safetensors", "{\"x\":{\"dtype\":\"F16\",\"shape\":[2],\"data_offsets\":[18446744073709551608,18446744073709551612]}}", 4);
+    // a shape whose element count wraps to 0 with empty data
+    raw(dir + "/bad9.safetensors", "{\"x\":{\"dtype\":\"F16\",\"shape\":[4294967296,4294967296],\"data_offsets\":[0,0]}}", 0);
+    // a shape dimension above INT64_MAX
+    raw(dir + "/bad10.safetensors", "{\"x\":{\"dtype\":\"U8\",\"shape\":[9223372036854775808,2],\"data_offsets\":[0,0]}}", 0);
+    // metadata nested a million levels deep (refused, not recursed into)
+    raw(dir + "/bad11.safetensors", "{\"__metadata__\":" + std::string(1000000, '[') + std::string(1000000, ']') + "}", 0);
+    for (int i : {1, 2, 3, 4, 5, 6, 8, 9, 10, 11})
         if (!throws(dir + "/bad" + std::to_string(i) + ".safetensors")) {
             std::printf("bad%d accepted\n", i);
             rc = 1;
