@@ -608,7 +608,7 @@ GemmLFn pick_epi(const ShapeL& s) {
 #define MCV_L(BM_, BN_, NS_, WR_) \
     if (s.bm == BM_ && s.bn == BN_ && s.ns == NS_ && s.wr == WR_) return w8a8_gemm_lds_kernel<BM_, BN_, NS_, EPI, WR_>;
     MCV_L(128, 128, 3, 0) MCV_L(128, 128, 4, 0) MCV_L(64, 128, 4, 0) MCV_L(128, 64, 4, 0) MCV_L(64, 64, 4, 0)
-    MCV_L(128, 128, 3, 1) MCV_L(128, 128, 4, 1) MCV_L(64, 128, 4, 1)
+    MCV_L(64, 64, 3, 0) MCV_L(128, 128, 3, 1) MCV_L(128, 128, 4, 1) MCV_L(64, 128, 4, 1)
 #undef MCV_L
     return nullptr;
 }
@@ -628,9 +628,11 @@ GemmLFn pick_l(const ShapeL& s, int epi) {
 // N=3584, 160 rotated weight sets, back to back, two passes of three timed
 // regions): M=1024 128x128 with 3 stages and the weights in registers 7.85-7.90
 // us (through LDS 7.91-7.95, 4 stages 8.26-8.37, 64x128 10.4-11.1, 64x64
-// 11.9-12.2); M=256 64x64 4.72-4.75 us (64x128 6.0-6.15, 128x128 7.4-7.8).
+// 11.9-12.2); M=256 64x64 4.72-4.75 us (64x128 6.0-6.15, 128x128 7.4-7.8),
+// and with 3 stages 4.66-4.68 us (2 stages 5.38-5.43; 32x128 with the
+// weights in registers 4.90-4.93 with 3 stages, 5.31-5.34 with 4).
 ShapeL choose_l(int64_t M, int64_t N) {
-    constexpr ShapeL kOrder[] = {{128, 128, 3, 1}, {64, 128, 4, 1}, {64, 64, 4, 0}};
+    constexpr ShapeL kOrder[] = {{128, 128, 3, 1}, {64, 128, 4, 1}, {64, 64, 3, 0}};
     ShapeL best = kOrder[0];
     int64_t best_t = -1;
     for (const ShapeL& s : kOrder) {

@@ -185,7 +185,7 @@ def test_w8a8_gemm_fused_ragged(mcv, oracle, cuda, M, K, N):
 # scales, on ragged shapes (a last tile past M and N, K padded with zero
 # weights, N % 4 != 0); then unbuilt configurations fail cleanly.
 W8_LDS_CONFIGS = [(128, 128, 3, 0), (128, 128, 4, 0), (64, 128, 4, 0), (128, 64, 4, 0), (64, 64, 4, 0),
-                  (128, 128, 3, 1), (128, 128, 4, 1), (64, 128, 4, 1)]
+                  (64, 64, 3, 0), (128, 128, 3, 1), (128, 128, 4, 1), (64, 128, 4, 1)]
 
 
 @pytest.mark.parametrize("M,K,N", [(257, 1040, 1000), (70, 384, 1003)], ids=lambda v: str(v))
