@@ -126,7 +126,18 @@ def time_queued(launch, n_sets, steps, warmup=3, regions=1):
                 break
             hold *= 2.0
         else:
-            raise RuntimeError(f"time_queued: the host could not enqueue {steps} launches within the hold")
+            # The host never got ahead of the GPU: a profiler that serialises
+            # dispatches blocks each launch until the one before has finished.
+            # Time the region without the hold; the figure then includes the
+            # host's enqueue time (an upper bound on the kernels' own).
+            sys.stderr.write(f"[time_queued] the host could not enqueue {steps} launches within a "
+                             f"{hold / 2:.1f} ms hold; timing without it (host-inclusive)\n")
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for i in range(steps):
+                launch(i % n_sets)
+            t1.record()
+            torch.cuda.synchronize()
         out.append(t0.elapsed_time(t1) / steps)
     return (out[0], enq_ms) if regions == 1 else (out, enq_ms)
 
