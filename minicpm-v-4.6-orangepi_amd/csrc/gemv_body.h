@@ -79,6 +79,42 @@ __device__ __forceinline__ float group_dot(const uint4 (&wv)[4], const uint32_t 
     return fmaf(group_sum(wv, xs, z, vmagic), scale, acc);
 }
 
+// group_sum in two steps, for a kernel that has the weights long before the
+// activations: the widened operands first (p[j] pairs with xs[j]), then the
+// same fdot2 chains in the same order, so the sum is group_sum's bit for bit.
+__device__ __forceinline__ void group_operands(const uint4 (&wv)[4], uint32_t z, uint32_t vmagic, half2_t (&p)[64]) {
+    const uint32_t zlo = (0x6400u + z) * 0x10001u;
+    const uint32_t zhi = (0x6400u + (z << 4)) * 0x10001u;
+    const uint32_t mlo = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+    const uint32_t mhi = __builtin_amdgcn_readfirstlane(0x00F000F0u);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t words[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int j = 16 * c + 4 * w;
+            const uint32_t q = words[w];
+            const uint32_t q8 = q >> 8;
+            p[j + 0] = as_h2(and_or(q, mlo, vmagic)) - as_h2(zlo);
+            p[j + 1] = as_h2(and_or(q, mhi, vmagic)) - as_h2(zhi);
+            p[j + 2] = as_h2(and_or(q8, mlo, vmagic)) - as_h2(zlo);
+            p[j + 3] = as_h2(and_or(q8, mhi, vmagic)) - as_h2(zhi);
+        }
+    }
+}
+
+__device__ __forceinline__ float group_sum_operands(const half2_t (&p)[64], const uint32_t (&xs)[64]) {
+    float alo = 0.f, ahi = 0.f;
+#pragma unroll
+    for (int j = 0; j < 64; j += 4) {
+        alo = __builtin_amdgcn_fdot2(p[j + 0], as_h2(xs[j + 0]), alo, false);
+        ahi = __builtin_amdgcn_fdot2(p[j + 1], as_h2(xs[j + 1]), ahi, false);
+        alo = __builtin_amdgcn_fdot2(p[j + 2], as_h2(xs[j + 2]), alo, false);
+        ahi = __builtin_amdgcn_fdot2(p[j + 3], as_h2(xs[j + 3]), ahi, false);
+    }
+    return alo + ahi * 0.0625f;
+}
+
 // One lane's column of a W4A16 weight in the slab-64 layout: its packed
 // words (slab base + lane), its scale and zero-word columns, and the zero
 // bias.  `zshift` selects the lane's nibble in the shared zero word.
@@ -96,6 +132,26 @@ __device__ __forceinline__ W4Column w4_column(const uint4* qw, const uint16_t* s
     const int n = slab * kSlab + lane;
     return W4Column{qw + static_cast<size_t>(slab) * (K / kChunkK) * kSlab + lane, scales + n, zeros + (n >> 3),
                     static_cast<uint32_t>(n & 7) * 4u, zero_bias, Npad};
+}
+
+// One weight's sum for one lane's column over the groups g0, g0 + step, ...
+// below G, in that order: one of the two chains of gate_up_partials below,
+// term for term.
+__device__ __forceinline__ float w4_partials(const uint32_t* __restrict__ xw, const W4Column& c, int g0, int step,
+                                             int G, uint32_t vmagic) {
+    float a = 0.f;
+    for (int g = g0; g < G; g += step) {
+        uint4 wv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[i] = load_weights(c.q + static_cast<size_t>(g * 4 + i) * kSlab);
+        const uint16_t sv = c.s[static_cast<size_t>(g) * c.npad];
+        const uint32_t zv = c.z[static_cast<size_t>(g) * (c.npad >> 3)];
+        uint32_t xs[64];
+        load_x_group(xw, g, xs);
+        issue_fence();
+        a = group_dot(wv, xs, ((zv >> c.zshift) & 15u) + c.zero_bias, h2f(sv), a, vmagic);
+    }
+    return a;
 }
 
 // Gate and up sums of one lane's column over the groups g0, g0 + step, ...

@@ -392,42 +392,43 @@ __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gemv_multi_kernel(const uin
 }
 
 // Decode MLP front half in one launch: act = silu(x . Wgate) * (x . Wup).
-// Each workgroup owns one 64-column slab of both weights; its waves split K
-// exactly like the GEMV (the same group_dot per weight), the two partial sums
-// meet in LDS, and wave 0 rounds gate and up to fp16 -- as the separate GEMV
-// launches store them -- before silu_mul_f16, so the result is bit-identical
-// to gate GEMV + up GEMV + silu_mul.  grid = (Nslab, M).
+// Each workgroup owns one 32-column half of a slab of both weights: lanes
+// 0-31 run the gate chains of its columns and lanes 32-63 the up chains of
+// the same columns (one chain per lane, half a slab's bytes per workgroup);
+// its waves split K exactly like the GEMV (the same group_dot per weight), the
+// partial sums meet in LDS, and wave 0 rounds gate and up to fp16 -- as the
+// separate GEMV launches store them -- before silu_mul_f16, so the result is
+// bit-identical to gate GEMV + up GEMV + silu_mul.  Measured on MI355X inside
+// the one-launch MLP block (H=1024, I=3584), half slabs against whole slabs
+// with both chains per lane: 6.98 against 7.62 us per block.
+// grid = (2 Nslab, M).
 template <int KSPLIT>
 __global__ __launch_bounds__(64 * KSPLIT) void w4a16_gate_up_silu_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qg, const uint16_t* __restrict__ sg,
     const uint32_t* __restrict__ zg, uint32_t zbg, const uint4* __restrict__ qu, const uint16_t* __restrict__ su,
     const uint32_t* __restrict__ zu, uint32_t zbu, uint16_t* __restrict__ act, int K, int N, int Npad) {
-    __shared__ float red[2][KSPLIT][kSlab];
+    __shared__ float red[2][KSPLIT][32];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int slab = blockIdx.x;
+    const int slab = blockIdx.x >> 1;
+    const int col = 32 * (blockIdx.x & 1) + (lane & 31), pj = lane >> 5;
     const int m = blockIdx.y;
-    const int n = slab * kSlab + lane;
     const int G = K / kGroup;
     const uint32_t* __restrict__ xw = reinterpret_cast<const uint32_t*>(x + static_cast<size_t>(m) * K);
     uint32_t vmagic;                                                     // 0x64006400 = half2(1024, 1024)
     asm("v_mov_b32 %0, 0x64006400" : "=v"(vmagic));
-    float ag = 0.f, au = 0.f;
-    gate_up_partials(xw, w4_column(qg, sg, zg, zbg, K, Npad, slab, lane), w4_column(qu, su, zu, zbu, K, Npad, slab, lane),
-                     wave, KSPLIT, G, ag, au, vmagic);
-    if constexpr (KSPLIT > 1) {
-        red[0][wave][lane] = ag;
-        red[1][wave][lane] = au;
-        __syncthreads();
-        if (wave != 0) return;
-        ag = red[0][0][lane];
-        au = red[1][0][lane];
+    red[pj][wave][lane & 31] = w4_partials(xw, pj ? w4_column(qu, su, zu, zbu, K, Npad, slab, col)
+                                                  : w4_column(qg, sg, zg, zbg, K, Npad, slab, col),
+                                           wave, KSPLIT, G, vmagic);
+    __syncthreads();
+    if (wave != 0 || lane >= 32) return;
+    float ag = red[0][0][lane], au = red[1][0][lane];
 #pragma unroll
-        for (int w = 1; w < KSPLIT; ++w) {
-            ag += red[0][w][lane];
-            au += red[1][w][lane];
-        }
+    for (int w = 1; w < KSPLIT; ++w) {
+        ag += red[0][w][lane];
+        au += red[1][w][lane];
     }
+    const int n = slab * kSlab + col;
     if (n < N) act[static_cast<size_t>(m) * N + n] = silu_mul_f16(f2h(ag), f2h(au));
 }
 
@@ -964,7 +965,7 @@ int mcv_w4a16_gate_up_silu(const void* x, int64_t M, int64_t K, int64_t N, const
           : ks == 8 ? w4a16_gate_up_silu_kernel<8>
           : ks == 4 ? w4a16_gate_up_silu_kernel<4>
           : ks == 2 ? w4a16_gate_up_silu_kernel<2> : w4a16_gate_up_silu_kernel<1>;
-    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(nslab), static_cast<unsigned>(M)), dim3(64 * ks), 0,
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(2 * nslab), static_cast<unsigned>(M)), dim3(64 * ks), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
                        static_cast<const uint4*>(qw_gate), static_cast<const uint16_t*>(scales_gate),
                        static_cast<const uint32_t*>(zeros_gate), static_cast<uint32_t>(zero_bias_gate),
