@@ -135,8 +135,8 @@ __device__ __forceinline__ W4Column w4_column(const uint4* qw, const uint16_t* s
 }
 
 // One weight's sum for one lane's column over the groups g0, g0 + step, ...
-// below G, in that order: one of the two chains of gate_up_partials below,
-// term for term.
+// below G, in that order (a GEMV wave's chain; the fused gate+up kernels run
+// the gate and the up chain of a column on two lanes).
 __device__ __forceinline__ float w4_partials(const uint32_t* __restrict__ xw, const W4Column& c, int g0, int step,
                                              int G, uint32_t vmagic) {
     float a = 0.f;
@@ -152,28 +152,6 @@ __device__ __forceinline__ float w4_partials(const uint32_t* __restrict__ xw, co
         a = group_dot(wv, xs, ((zv >> c.zshift) & 15u) + c.zero_bias, h2f(sv), a, vmagic);
     }
     return a;
-}
-
-// Gate and up sums of one lane's column over the groups g0, g0 + step, ...
-// below G, in that order (the fused gate+up kernels' per-wave loop).
-__device__ __forceinline__ void gate_up_partials(const uint32_t* __restrict__ xw, const W4Column& gc,
-                                                 const W4Column& uc, int g0, int step, int G, float& ag, float& au,
-                                                 uint32_t vmagic) {
-    for (int g = g0; g < G; g += step) {
-        uint4 wgv[4], wuv[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) wgv[c] = load_weights(gc.q + static_cast<size_t>(g * 4 + c) * kSlab);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) wuv[c] = load_weights(uc.q + static_cast<size_t>(g * 4 + c) * kSlab);
-        const uint16_t sgv = gc.s[static_cast<size_t>(g) * gc.npad], suv = uc.s[static_cast<size_t>(g) * uc.npad];
-        const uint32_t zgv = gc.z[static_cast<size_t>(g) * (gc.npad >> 3)];
-        const uint32_t zuv = uc.z[static_cast<size_t>(g) * (uc.npad >> 3)];
-        uint32_t xs[64];
-        load_x_group(xw, g, xs);
-        issue_fence();
-        ag = group_dot(wgv, xs, ((zgv >> gc.zshift) & 15u) + gc.zero_bias, h2f(sgv), ag, vmagic);
-        au = group_dot(wuv, xs, ((zuv >> uc.zshift) & 15u) + uc.zero_bias, h2f(suv), au, vmagic);
-    }
 }
 
 }  // namespace mcv
