@@ -198,8 +198,10 @@ const char* mcv_w4a16_gemm_kernel_name(int64_t M, int64_t K, int64_t N, int with
  * each wave's packed weights, zeros and scales straight into registers (the
  * stage buffers in LDS then hold x rows only), `tile_order` the order in
  * which the XCDs take the tiles (0 as the dispatch: down the tile columns when
- * x has fewer bytes than the packed weights, else along the rows; 1 along the
- * rows; 2 down the columns), K split `splits` ways across
+ * x has fewer bytes than the packed weights, else as 3; 1 along the rows; 2
+ * down the columns; 3 down the columns of groups of tile rows sized so that
+ * each XCD's run of tiles spans about as many x bytes as weight bytes), K
+ * split `splits` ways across
  * workgroups (groups_per_stage divides K / 128, splits at most
  * K / 128 / groups_per_stage; split p takes stages [p U / S, (p+1) U / S) of
  * the U = K / 128 / groups_per_stage), the partial tiles added inside the same launch by the

@@ -21,7 +21,8 @@ struct SkConfig {
     int kg = 1;
     int kw = 1;
     int wr = 0;             // 1: each wave loads its weights, zeros and scales into registers (LDS holds x only)
-    int order = 0;          // tile order: 0 by operand bytes, 1 along the rows, 2 down the columns
+    int order = 0;          // tile order: 0 by operand bytes (2 or 3), 1 along the rows, 2 down the
+                            // columns, 3 down the columns of groups of tile rows
 };
 
 // The workspace starts with the tile arrival counters, a fixed region for

@@ -75,6 +75,8 @@
 // The reference has no M > 1 quantised path: its prefill runs dense fp16
 // aclnnMm through matmul_b_transposed (src/csrc/lib/decoder_layer.cpp:459-462,
 // 656-659, 857-860; src/csrc/lib/ops.cpp:159-322).
+#include <cmath>
+
 #include "common.h"
 #include "w4a16_gemm_sk.h"
 
@@ -156,7 +158,7 @@ template <int TM, int NWV, int NS, int KG, int KW, int WR>
 __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
     const uint16_t* __restrict__ x, const uint4* __restrict__ qw, const uint16_t* __restrict__ scales,
     const uint32_t* __restrict__ zeros, uint32_t zero_bias, uint16_t* __restrict__ out, int M, int K, int N,
-    int nslab, int m_tiles, int n_tiles, int S, int col_major, uint8_t* __restrict__ ws, uint32_t ws_bytes) {
+    int nslab, int m_tiles, int n_tiles, int S, int order, uint8_t* __restrict__ ws, uint32_t ws_bytes) {
     using C = CfgS<TM, NWV, NS, KG, KW, WR>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
@@ -172,14 +174,27 @@ __global__ __launch_bounds__(64 * NWV * KW) void w4a16_gemm_sk_kernel(
     const int h = lane >> 5;
 
     // (tile, split): the split index is the slowest, then the tile order --
-    // down the tile columns (col_major, x rows shared within an XCD's run) or
-    // along the rows.
+    // along the rows (order 0), down the tile columns (1: x rows shared
+    // within an XCD's run), or down the columns of groups of `order` tile
+    // rows (>= 2: an XCD's run then covers a block of tile rows and columns).
     const int tiles = m_tiles * n_tiles;
     const int lin = xcd_run(static_cast<int>(blockIdx.x), tiles * S);
     const int p = lin / tiles;
     const int tile = lin - p * tiles;
-    const int tm = col_major ? tile % m_tiles : tile / n_tiles;
-    const int tn = col_major ? tile / m_tiles : tile - tm * n_tiles;
+    int tm, tn;
+    if (order >= 2) {
+        const int grp = tile / (order * n_tiles), first = grp * order;
+        const int rows = m_tiles - first < order ? m_tiles - first : order;
+        const int t = tile - grp * order * n_tiles;
+        tm = first + t % rows;
+        tn = t / rows;
+    } else if (order == 1) {
+        tm = tile % m_tiles;
+        tn = tile / m_tiles;
+    } else {
+        tm = tile / n_tiles;
+        tn = tile - tm * n_tiles;
+    }
     const int m0 = tm * TM;
     const int Npad = nslab * kSlab;
     const int CK = K / kChunkK;
@@ -665,15 +680,29 @@ int launch_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const v
     // along the rows, the reverse; so the order goes down the columns only
     // when x is the smaller operand (every XCD re-reads it from beyond its
     // L2 instead of the weights).  MI355X, M=2048 K=1024 N=3584 (x 4.2 MB,
-    // weights 2.3 MB): the column order fetched 36 MB per call.
+    // weights 2.3 MB): the column order fetched 36 MB per call.  Where x is
+    // the larger operand, groups of g tile rows taken down their columns
+    // give each XCD a block of rows and columns instead of whole rows
+    // (interleaved A/B, medians of 12 regions: M=2048 K=1024 19.23 against
+    // 19.35-19.53 us along the rows, M=2048 K=3584 20.66 against 20.80-21.17,
+    // M=512 K=3584 10.61 against 10.69-10.72; where x is the smaller operand
+    // the column order stays ahead: M=512 K=1024 8.67 against 8.72).
     const int64_t x_bytes = M * K * 2, w_bytes = K * N / 2 + (K / kGroup) * N * 5 / 2;
-    const int col_major = c.order == 2 || (c.order == 0 && x_bytes < w_bytes) ? 1 : 0;
+    int order = c.order == 2 || (c.order == 0 && x_bytes < w_bytes) ? 1 : 0;
+    if ((c.order == 3 || (c.order == 0 && x_bytes >= w_bytes)) && m_tiles >= 2) {
+        // groups of g tile rows, g balancing an XCD run's x rows (g of them)
+        // against its weight columns (run / g): g = sqrt(run * col / row)
+        const double run = double(m_tiles * n_tiles) / 8.0;
+        const double row = double(c.tm) * K * 2, col = double(c.nwv / 2) * (double(w_bytes) / nslab);
+        int g = static_cast<int>(std::lround(std::sqrt(run * col / row)));
+        order = g < 2 ? 2 : (g > m_tiles ? static_cast<int>(m_tiles) : g);
+    }
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(total)), dim3(64 * c.nwv * c.kw), 0, stream,
                        static_cast<const uint16_t*>(x), static_cast<const uint4*>(qw),
                        static_cast<const uint16_t*>(scales), static_cast<const uint32_t*>(zeros),
                        static_cast<uint32_t>(zero_bias), static_cast<uint16_t*>(out), static_cast<int>(M),
                        static_cast<int>(K), static_cast<int>(N), static_cast<int>(nslab), static_cast<int>(m_tiles),
-                       static_cast<int>(n_tiles), c.splits, col_major, static_cast<uint8_t*>(ws),
+                       static_cast<int>(n_tiles), c.splits, order, static_cast<uint8_t*>(ws),
                        static_cast<uint32_t>(c.splits > 1 ? need : 0));
     return check_launch("w4a16_gemm_sk_kernel");
 }
@@ -701,8 +730,8 @@ int mcv_w4a16_gemm_sk(const void* x, int64_t M, int64_t K, int64_t N, const void
     if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: x must be 16-byte aligned");
     int rc = require_device();
     if (rc != MCV_OK) return rc;
-    if (tile_order < 0 || tile_order > 2)
-        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: tile_order must be 0, 1 or 2 (%d)", tile_order);
+    if (tile_order < 0 || tile_order > 3)
+        return fail(MCV_ERR_INVALID_ARG, "mcv_w4a16_gemm_sk: tile_order must be 0, 1, 2 or 3 (%d)", tile_order);
     return launch_w4a16_gemm_sk(x, M, K, N, qw, scales, zeros, zero_bias, out,
                                 SkConfig{tm, waves, stages, splits, groups_per_stage, k_parts, weights_in_registers,
                                          tile_order},

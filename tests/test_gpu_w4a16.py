@@ -226,7 +226,7 @@ def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
             for _ in range(2 if S > 1 else 1):
                 out = torch.full((M, N), 7.0, dtype=torch.float16, device="cuda")
                 rc = L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, w.zero_bias, out.data_ptr(), tm, nwv,
-                                         ns, kg, kw, wr, 1 + (S + tm) % 2, S, ws.data_ptr(), ws.numel(), stream)
+                                         ns, kg, kw, wr, (S + tm + nwv) % 4, S, ws.data_ptr(), ws.numel(), stream)
                 assert rc == 0, L.mcv_last_error()
                 outs.append(out)
             torch.cuda.synchronize()
@@ -248,7 +248,7 @@ def test_gemm_every_configuration(mcv, oracle, cuda, M, K, N):
                                ws.data_ptr(), ws.numel(), stream) == 1
     assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 0, 2, None, 0,
                                stream) == 1
-    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 3, 1, None, 0,
+    assert L.mcv_w4a16_gemm_sk(xd.data_ptr(), M, w.K, w.N, q, sc, z, 0, xd.data_ptr(), 32, 4, 3, 1, 1, 0, 4, 1, None, 0,
                                stream) == 1
 
 
