@@ -847,9 +847,12 @@ def _lm_head_w8a8(pkg, args, part):
     434-480 with the argmax on the device): activation quantisation with the
     fp16 scale, then the W8A8 GEMV over V = 248094 columns with the fp16 weight
     scale and the argmax folded in (one key per slab, then their reduction);
-    4 rotated weight copies (1.0 GB).  part = "step", "unfused" (the same
-    GEMV without the fold, then the separate argmax over the logits), "gemv"
-    (the GEMV alone) or "argmax" (the separate argmax alone)."""
+    4 rotated weight copies (1.0 GB).  part = "step" (the whole step in one
+    launch, mcv_w8a8_lm_head_argmax), "parts" (the same in three launches:
+    the quantisation, the GEMV with the folded argmax, the key reduction),
+    "unfused" (the quantisation, the GEMV without the fold, then the separate
+    argmax over the logits), "gemv" (the GEMV alone) or "argmax" (the
+    separate argmax alone)."""
     import torch
     K, V = 1024, args.V or 248094
     rng = np.random.default_rng(1)
@@ -862,12 +865,16 @@ def _lm_head_w8a8(pkg, args, part):
     logits = torch.empty((1, V), dtype=torch.float16, device="cuda")
     keys = torch.empty(-(-V // 64), dtype=torch.int64, device="cuda")
     tok = torch.empty(1, dtype=torch.int64, device="cuda")
+    wsp = torch.zeros(pkg.lm_head_workspace_bytes(V), dtype=torch.uint8, device="cuda")
     pkg.w8a8_quantize(x, xq, pkg._NO_F32, xs)
 
     def step(i):
-        if part in ("step", "unfused"):
-            pkg.w8a8_quantize(x, xq, pkg._NO_F32, xs)
         if part == "step":
+            pkg.lm_head_argmax_w8a8_fused(x, ws[i], V, wsp, logits, tok)
+            return
+        if part in ("parts", "unfused"):
+            pkg.w8a8_quantize(x, xq, pkg._NO_F32, xs)
+        if part == "parts":
             pkg.lm_head_argmax_w8a8(xq, xs, ws[i], V, logits, keys, tok)
             return
         if part != "argmax":
@@ -875,7 +882,7 @@ def _lm_head_w8a8(pkg, args, part):
         if part != "gemv":
             pkg.argmax_last_dim(logits, tok)
     gemv_bytes = K * V + 2 * V + 2 * V + K                  # weights, fp16 scales, logits, int8 x
-    nbytes = {"gemv": gemv_bytes, "argmax": 2 * V, "step": gemv_bytes + 2 * K,
+    nbytes = {"gemv": gemv_bytes, "argmax": 2 * V, "step": gemv_bytes + 2 * K, "parts": gemv_bytes + 2 * K,
               "unfused": gemv_bytes + 2 * V + 2 * K}[part]
     return {"workload": f"w8a8_lm_head_{part}_V{V}", **gpu_result(
         f"lm_head_w8a8_{part}", f"w8a8 lm_head ({part})", nbytes, "GB/s", "hbm", step, len(ws), 200)}
@@ -918,6 +925,7 @@ EXTRA = {
     "vendor_int8": lambda p, a: _vendor(p, a, True),
     "copy": _copy,
     "lm_head_w8a8": lambda p, a: _lm_head_w8a8(p, a, "step"),
+    "lm_head_w8a8_parts": lambda p, a: _lm_head_w8a8(p, a, "parts"),
     "lm_head_w8a8_unfused": lambda p, a: _lm_head_w8a8(p, a, "unfused"),
     "lm_head_w8a8_gemv": lambda p, a: _lm_head_w8a8(p, a, "gemv"),
     "lm_head_w8a8_argmax": lambda p, a: _lm_head_w8a8(p, a, "argmax"),

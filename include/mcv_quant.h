@@ -501,6 +501,25 @@ int mcv_w8a8_gemv_argmax_partials(const int8_t* xq_dev, const void* x_scale_dev,
                                   int64_t N, int64_t V, const int8_t* w_dev, const void* w_scale_dev,
                                   int w_scale_dtype, void* logits_dev, void* keys_dev, mcv_stream_t stream);
 
+/* The whole W8A8 lm_head step in one launch (M = 1): the activation row x_dev
+ * (fp16 [K], K a multiple of 16 up to 2048) quantised as mcv_w8a8_quantize_act
+ * does it, the GEMV
+ * over the MCV_W8_TILED weight [K][N] with the fused epilogue for v < V
+ * (logits_dev, may be NULL) and the first-maximum argmax as an int64 token on
+ * the device -- bit-identical to mcv_w8a8_quantize_act +
+ * mcv_w8a8_gemv_argmax_partials + mcv_argmax_reduce_keys with the same scale
+ * dtypes.  x_scale_dtype MCV_F16: the epilogue multiplies by the fp16 x_scale
+ * the reference stores (language_model.cpp:439-441); w_scale in
+ * w_scale_dtype.  The workspace is mcv_w4a16_lm_head_argmax's
+ * (mcv_lm_head_workspace_bytes(V), 128-byte aligned, zero-filled once; the
+ * same generation word, key words and give-up word, so the two heads may
+ * share one, one call at a time).  MCV_ERR_SHAPE above K = 2048 (the three
+ * launches then serve).  Replaces the W8A8 branch of lm_head_greedy
+ * (src/csrc/lib/language_model.cpp:434-480). */
+int mcv_w8a8_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V, const int8_t* w_dev,
+                            const void* w_scale_dev, int w_scale_dtype, int x_scale_dtype, void* logits_dev,
+                            int64_t* token_dev, void* workspace_dev, uint32_t* status, mcv_stream_t stream);
+
 /* Bytes of a K x N weight in MCV_W8_TILED (0 on bad shape). */
 int64_t mcv_w8a8_tiled_bytes(int64_t K, int64_t N);
 

@@ -105,6 +105,8 @@ _SIGS = {
                                    _c_int, _c_int, _vp]),
     "mcv_w8a8_gemv_argmax_partials": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_int, _vp, _vp,
                                                _vp]),
+    "mcv_w8a8_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp,
+                                         _vp]),
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
     "mcv_w8a8_tiled_bytes": (_c_i64, [_c_i64, _c_i64]),
     "mcv_w8a8_gate_up_silu": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_int, _vp,
@@ -863,6 +865,37 @@ def lm_head_argmax_w8a8(x_int8, x_scale, w: W8A8QuantizedWeight, vocab: int, log
                                                _dev(logits) if logits is not None else None, _dev(keys),
                                                _stream(stream)), "mcv_w8a8_gemv_argmax_partials")
     _check(lib().mcv_argmax_reduce_keys(_dev(keys), nslab, _dev(token), _stream(stream)), "mcv_argmax_reduce_keys")
+    return token
+
+
+def lm_head_workspace_bytes(vocab: int) -> int:
+    """Bytes of the device-token lm_head workspace for `vocab` columns (0: unsupported)."""
+    return int(lib().mcv_lm_head_workspace_bytes(vocab))
+
+
+def lm_head_argmax_w8a8_fused(x, w: W8A8QuantizedWeight, vocab: int, workspace, logits=None, token=None,
+                              use_f32_scale=False, status=None, stream=None):
+    """The whole W8A8 lm_head step in one launch (mcv_w8a8_lm_head_argmax):
+    x fp16 [1, K] quantised on the device, the fused GEMV over the first
+    `vocab` columns (logits written when given) and the argmax as an int64
+    [1] token on the device -- bit-identical to w8a8_quantize +
+    lm_head_argmax_w8a8.  Scales: the fp16 x_scale and the weight's fp16
+    w_scale (the reference's), or fp32 both with use_f32_scale.  `workspace`
+    is a zero-filled uint8 tensor of lm_head_workspace_bytes(vocab) bytes
+    that later calls reuse (the W4A16 lm_head's workspace format)."""
+    torch = _torch()
+    if w.layout != W8_TILED:
+        raise McvError("lm_head_argmax_w8a8_fused needs an MCV_W8_TILED weight")
+    if x.dtype != torch.float16 or x.numel() != w.K or not x.is_contiguous():
+        raise McvError("lm_head_argmax_w8a8_fused x must be contiguous fp16 [1, K]")
+    if token is None:
+        token = torch.empty(1, dtype=torch.int64, device=x.device)
+    ws = w.w_scale_f32 if use_f32_scale else w.w_scale
+    _check(lib().mcv_w8a8_lm_head_argmax(_dev(x), w.K, w.N, vocab, _dev(w.w_int8), _dev(ws), _scale_dtype(ws),
+                                         MCV_F32 if use_f32_scale else MCV_F16,
+                                         _dev(logits) if logits is not None else None, _dev(token),
+                                         _dev(workspace), _dev(status) if status is not None else None,
+                                         _stream(stream)), "mcv_w8a8_lm_head_argmax")
     return token
 
 

@@ -61,10 +61,11 @@ struct LmHeadW8A8 {
     const W8A8QuantizedWeight* weight{nullptr};   // [hidden, >= vocab]
     int64_t vocab{0};
     Tensor normed;                 // Float16 [1, hidden]
-    Tensor xq;                     // Int8 [1, hidden]
+    Tensor xq;                     // Int8 [1, hidden] (weights not in MCV_W8_TILED)
     Tensor xs;                     // Float16 [1]
     Tensor logits;                 // Float16 [1, weight N]: the last call's logits (columns < vocab)
-    Tensor keys;                   // Int64 [ceil(vocab / 64)] (the fused argmax's per-slab keys)
+    Tensor keys;                   // Int64 [ceil(vocab / 64)]: per-slab keys (MCV_W8_TILED, hidden > 2048)
+    Tensor workspace;              // the one-launch step's (MCV_W8_TILED, hidden <= 2048), zero-filled once
     Tensor token;                  // Int64 [1]
 };
 LmHeadW8A8 make_lm_head_w8a8(const W8A8QuantizedWeight& weight, int64_t vocab);

@@ -119,6 +119,8 @@ LmHeadW8A8 make_lm_head_w8a8(const W8A8QuantizedWeight& weight, int64_t vocab) {
     head.keys = Tensor({(vocab + 63) / 64}, DType::Int64);
     head.token = Tensor({1}, DType::Int64);
     for (Tensor* t : {&head.normed, &head.xq, &head.xs, &head.logits, &head.keys, &head.token}) t->allocate();
+    head.workspace = Tensor({mcv_lm_head_workspace_bytes(vocab)}, DType::UInt8);
+    head.workspace.zero();
     return head;
 }
 
@@ -132,10 +134,19 @@ int64_t lm_head_greedy_w8a8(const Tensor& last_hidden_1xH, const Tensor* final_n
         rms_norm(last_hidden_1xH, *final_norm, head.normed, rms_epsilon, stream);
         x = &head.normed;
     }
-    w8a8_quantize(*x, head.xq, head.xs, stream);               // fp16 x_scale, as language_model.cpp:439-441
     int64_t* token = static_cast<int64_t*>(head.token.data());
-    if (w.layout == MCV_W8_TILED) {
-        // fp16 w_scale, as :465-466; the argmax folded into the GEMV
+    if (w.layout == MCV_W8_TILED && w.K <= 2048) {
+        // one launch: the activation quantisation with the fp16 x_scale (as
+        // language_model.cpp:439-441), the GEMV with the fp16 w_scale (:465-466)
+        // and the argmax on the device
+        check_mcv(mcv_w8a8_lm_head_argmax(x->data(), w.K, w.N, head.vocab, static_cast<const int8_t*>(w.w_int8.data()),
+                                          w.w_scale.data(), MCV_F16, MCV_F16, head.logits.data(), token,
+                                          head.workspace.data(), nullptr, stream),
+                  "lm_head W8A8");
+    } else if (w.layout == MCV_W8_TILED) {
+        // the same in three launches: quantisation, the GEMV with one argmax
+        // key per slab, the keys' reduction
+        w8a8_quantize(*x, head.xq, head.xs, stream);
         check_mcv(mcv_w8a8_gemv_argmax_partials(static_cast<const int8_t*>(head.xq.data()), head.xs.data(), MCV_F16,
                                                 w.K, w.N, head.vocab, static_cast<const int8_t*>(w.w_int8.data()),
                                                 w.w_scale.data(), MCV_F16, head.logits.data(), head.keys.data(),
@@ -143,12 +154,19 @@ int64_t lm_head_greedy_w8a8(const Tensor& last_hidden_1xH, const Tensor* final_n
                   "lm_head W8A8 GEMV");
         check_mcv(mcv_argmax_reduce_keys(head.keys.data(), head.keys.numel(), token, stream), "lm_head argmax");
     } else {
+        w8a8_quantize(*x, head.xq, head.xs, stream);
         matmul_w8a8(head.xq, head.xs, w, head.logits, stream);
         check_mcv(mcv_argmax_f16(head.logits.data(), 1, head.vocab, token, stream), "lm_head argmax");
     }
     int64_t t = 0;
     check_hip(hipMemcpyAsync(&t, head.token.data(), sizeof(t), hipMemcpyDeviceToHost, stream), "hipMemcpyAsync token");
     check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (t < 0) {
+        // the bounded wait for the workgroups' keys gave up: reset the
+        // workspace's give-up word and report it
+        head.workspace.zero();
+        throw std::runtime_error("lm_head_greedy_w8a8: the wait for the workgroups' argmax keys gave up (token -1)");
+    }
     return t;
 }
 

@@ -19,6 +19,8 @@ int launch_w8a8_tiled(const int8_t* xq, int64_t M, int64_t K, int64_t N, const i
                       const void* xs, int xs16, const void* ws, int ws16, hipStream_t stream);
 int launch_w8a8_gemv_argmax(const int8_t* xq, int64_t K, int64_t V, const int8_t* w, void* logits, const void* xs,
                             int xs16, const void* ws, int ws16, unsigned long long* keys, hipStream_t stream);
+int launch_w8a8_lm_head(const void* x, int64_t K, int64_t V, const int8_t* w, const void* wscale, int ws16, int xs16,
+                        void* logits, int64_t* token, void* ws, unsigned* status, hipStream_t stream);
 int launch_w8a8_gemm_lds_cfg(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
                              const void* xs, int xs16, const void* ws, int ws16, int bm, int bn, int ns, int wr,
                              hipStream_t stream);
@@ -446,6 +448,27 @@ int mcv_w8a8_gemv_argmax_partials(const int8_t* xq, const void* xs, int xs_dtype
     if ((rc = require_device()) != MCV_OK) return rc;
     return launch_w8a8_gemv_argmax(xq, K, V, w, logits, xs, xs_dtype == MCV_F16, ws, ws_dtype == MCV_F16,
                                    static_cast<unsigned long long*>(keys), static_cast<hipStream_t>(stream));
+}
+
+int mcv_w8a8_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, const int8_t* w, const void* w_scale,
+                            int w_scale_dtype, int x_scale_dtype, void* logits, int64_t* token, void* workspace,
+                            uint32_t* status, mcv_stream_t stream) {
+    const char* who = "mcv_w8a8_lm_head_argmax";
+    if (!x || !w || !w_scale || !token || !workspace) return fail(MCV_ERR_INVALID_ARG, "%s: null pointer", who);
+    if (!dtype_ok(w_scale_dtype) || !dtype_ok(x_scale_dtype))
+        return fail(MCV_ERR_INVALID_ARG, "%s: bad scale dtype", who);
+    if (K <= 0 || K > 2048 || K % 16 != 0 || N <= 0 || N > (int64_t(1) << 30))
+        return fail(MCV_ERR_SHAPE, "%s: need K a multiple of 16 up to 2048 (K=%lld N=%lld)", who, (long long)K,
+                    (long long)N);
+    if (V <= 0 || V > N || V >= (int64_t(1) << 24))
+        return fail(MCV_ERR_SHAPE, "%s: need 0 < V <= N and V < 2^24 (V=%lld N=%lld)", who, (long long)V, (long long)N);
+    if (reinterpret_cast<uintptr_t>(workspace) % 128 != 0)
+        return fail(MCV_ERR_INVALID_ARG, "%s: workspace must be 128-byte aligned", who);
+    if (reinterpret_cast<uintptr_t>(x) % 2 != 0) return fail(MCV_ERR_INVALID_ARG, "%s: x must be 2-byte aligned", who);
+    int rc = require_device();
+    if (rc != MCV_OK) return rc;
+    return launch_w8a8_lm_head(x, K, V, w, w_scale, w_scale_dtype == MCV_F16, x_scale_dtype == MCV_F16, logits, token,
+                               workspace, status, static_cast<hipStream_t>(stream));
 }
 
 int mcv_w8a8_dequant(const int32_t* acc, const void* xs, int xs_dtype, const void* ws, int ws_dtype, int64_t M, int64_t N,

@@ -20,6 +20,7 @@
 #include <cstring>
 #include <string>
 
+#include "argmax_exchange.h"
 #include "common.h"
 
 namespace mcv {
@@ -203,7 +204,174 @@ int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const in
     return check_launch(DUAL ? "w8a8_tiled_gemv_kernel<gate_up_silu>" : "w8a8_tiled_gemv_kernel");
 }
 
+// The whole W8A8 lm_head step in one launch (M = 1): the activation
+// quantisation, the GEMV over the slabs holding columns < V with the fused
+// epilogue, and the first-maximum argmax through the device-token exchange
+// (argmax_exchange.h).  The grid is the W4A16 lm_head's (lm_head_spw: SPW
+// consecutive slabs per workgroup, 243 workgroups at V = 248094), so the
+// quantisation and the exchange are paid per workgroup, not per slab (one
+// workgroup per slab, each quantising x itself: 47-48.6 us against 44.8 us
+// for the three launches).  16 waves; for each slab wave w takes k-blocks w,
+// w + 16, ... (both 32-column halves) with the next slab's weight lines in
+// flight; x is quantised once into LDS with the activation quantiser's
+// arithmetic (w8a8_quant_act_kernel: the row maximum is a maximum in any
+// order, every element the same act_quant) while the first slab's lines load;
+// the int32 partial sums (exact in any order) meet in LDS; wave w then
+// applies the GEMV's epilogue to slab w of the workgroup and forms its key.
+// So the logits and the token are bit-identical to mcv_w8a8_quantize_act +
+// mcv_w8a8_gemv_argmax_partials + mcv_argmax_reduce_keys.
+constexpr int kW8LmWaves = 16;
+
+template <int SPW, int U>
+__global__ __launch_bounds__(64 * kW8LmWaves) void w8a8_lm_head_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w, int K, int V, int KB, int nslab,
+    const void* __restrict__ wscale, int ws16, int xs16, uint16_t* __restrict__ logits,
+    unsigned long long* __restrict__ ws, int64_t* __restrict__ token, unsigned skew, unsigned* status) {
+    constexpr int NW = kW8LmWaves;
+    constexpr int XB = NW * U * 32;                      // bytes of the quantised row (zero past K)
+    constexpr int XPER = (XB + 64 * NW - 1) / (64 * NW);
+    static_assert(SPW <= NW, "one slab per wave in the epilogue");
+    __shared__ int part[SPW][NW][64];
+    __shared__ __attribute__((aligned(16))) int8_t xq[XB];
+    __shared__ float smax[NW];
+    __shared__ unsigned long long wbest[NW];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5;
+    const int s0 = static_cast<int>(blockIdx.x) * SPW;
+    const int ns = nslab - s0 < SPW ? nslab - s0 : SPW;  // workgroup-uniform
+    // the call's generation word (needed only at the end), x and the
+    // epilogue's scale go out first: a wave's loads return in issue order
+    unsigned gen = 0;
+    if (wave == 0)
+        gen = __hip_atomic_load(reinterpret_cast<unsigned*>(ws) + kLmGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint16_t xv[XPER];
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+        const int k = static_cast<int>(threadIdx.x) + i * 64 * NW;
+        xv[i] = k < K ? x[k] : uint16_t(0);
+    }
+    const int n = (s0 + wave) * kSlab + lane;           // wave w's epilogue column
+    uint32_t r_ws = 0;
+    if (wave < ns && n < V)
+        r_ws = ws16 ? static_cast<const uint16_t*>(wscale)[n] : static_cast<const uint32_t*>(wscale)[n];
+    // slab i's lines of this wave into ring slot i & 1; slabs past the
+    // workgroup's last re-read its last (never stored); k-blocks past the end
+    // get bit 31 in the offset and read zero (the weight is under 2 GiB).  No
+    // select in the offsets: a uniform select compiles to a branch, and the
+    // waitcnt pass then waits for every load in flight at the join.
+    const __amdgpu_buffer_rsrc_t wr = rsrc(w, static_cast<uint32_t>(nslab) * KB * 2 * kW8Block);
+    int4_t wv[2][U][2];
+    auto issue = [&](int slot, int i) {
+        const uint32_t sl = static_cast<uint32_t>(s0 + min(i, ns - 1));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kb = wave + u * NW;
+            const uint32_t dead = static_cast<uint32_t>(kb >= KB) << 31;
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const uint32_t off = (((sl * KB + kb) * 2 + jj) * kW8Block + lane * 16u) | dead;
+                wv[slot][u][jj] = __builtin_bit_cast(int4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2));
+            }
+        }
+    };
+    issue(0, 0);
+    // x -> int8 in LDS with the activation quantiser's arithmetic
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+        const float v = fabsf(h2f(xv[i]));                // padding contributes 0, never above the max
+        m = v > m ? v : m;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    if (lane == 0) smax[wave] = m;
+    __syncthreads();
+    m = smax[0];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) m = smax[v] > m ? smax[v] : m;
+    const float scale = act_scale(m);
+    const float inv = __fdiv_rn(1.0f, scale);
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+        const int k = static_cast<int>(threadIdx.x) + i * 64 * NW;
+        if (k < XB) xq[k] = k < K ? act_quant(xv[i], inv) : int8_t(0);
+    }
+    __syncthreads();
+    int4_t xb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) xb[u] = *reinterpret_cast<const int4_t*>(xq + (wave + u * NW) * 32 + h * 16);
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+        if (i + 1 < SPW) issue((i + 1) & 1, i + 1);
+        int a0 = 0, a1 = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a0 = __builtin_amdgcn_sdot4(wv[i & 1][u][0][q], xb[u][q], a0, false);
+                a1 = __builtin_amdgcn_sdot4(wv[i & 1][u][1][q], xb[u][q], a1, false);
+            }
+        // lanes l and l ^ 32 hold the two k-halves of the same column
+        a0 += __shfl_xor(a0, 32, 64);
+        a1 += __shfl_xor(a1, 32, 64);
+        part[i][wave][lane] = h ? a1 : a0;               // lane l: column l of the slab
+    }
+    __syncthreads();
+    unsigned long long best = 0ull;
+    if (wave < ns) {
+        int sum = 0;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) sum += part[wave][v][lane];
+        const float e_ws = ws16 ? h2f(static_cast<uint16_t>(r_ws)) : __uint_as_float(r_ws);
+        const float e_xs = xs16 ? h2f(f2h(scale)) : scale;
+        const uint16_t h16 = f2h(__fmul_rn(__fmul_rn(static_cast<float>(sum), e_ws), e_xs));
+        if (logits != nullptr && n < V) logits[n] = h16;
+        best = n < V ? argmax_key64(argmax_key16(h16), static_cast<uint32_t>(n)) : 0ull;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (wave != 0) return;
+    best = wave_max_u64(lane < NW ? wbest[lane] : 0ull);
+    argmax_publish(ws, best, gen, skew, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), lane, token,
+                   status);
+}
+
 }  // namespace
+
+unsigned lm_poll_skew();
+int lm_head_spw(int64_t nslab);
+
+// The one-launch W8A8 lm_head (M = 1, K <= 2048).  Shapes were validated by the caller.
+int launch_w8a8_lm_head(const void* x, int64_t K, int64_t V, const int8_t* w, const void* wscale, int ws16, int xs16,
+                        void* logits, int64_t* token, void* ws, unsigned* status, hipStream_t stream) {
+    const int64_t nslab = ceil_div(V, kSlab);
+    const int64_t KB = ceil_div(K, 128) * 4;
+    if (KB > 4 * kW8LmWaves) return fail(MCV_ERR_SHAPE, "w8a8 lm_head: K=%lld above 2048", (long long)K);
+    if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 31))
+        return fail(MCV_ERR_SHAPE, "w8a8 lm_head: weight exceeds 2 GiB");
+    const int spw = lm_head_spw(nslab);
+    const int u = KB <= kW8LmWaves ? 1 : (KB <= 2 * kW8LmWaves ? 2 : 4);
+    using Fn = void (*)(const uint16_t*, const int8_t*, int, int, int, int, const void*, int, int, uint16_t*,
+                        unsigned long long*, int64_t*, unsigned, unsigned*);
+    Fn fn = nullptr;
+#define MCV_LM8(SPW_)                                                                                        \
+    if (spw == SPW_)                                                                                         \
+        fn = u == 1 ? w8a8_lm_head_kernel<SPW_, 1> : (u == 2 ? w8a8_lm_head_kernel<SPW_, 2> : w8a8_lm_head_kernel<SPW_, 4>);
+    MCV_LM8(1) MCV_LM8(2) MCV_LM8(4) MCV_LM8(8) MCV_LM8(16)
+#undef MCV_LM8
+    if (fn == nullptr) return fail(MCV_ERR_INVALID_ARG, "w8a8 lm_head: no kernel for %d slabs per workgroup", spw);
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(ceil_div(nslab, spw))), dim3(64 * kW8LmWaves), 0, stream,
+                       static_cast<const uint16_t*>(x), w, static_cast<int>(K), static_cast<int>(V),
+                       static_cast<int>(KB), static_cast<int>(nslab), wscale, ws16, xs16,
+                       static_cast<uint16_t*>(logits), static_cast<unsigned long long*>(ws), token, lm_poll_skew(),
+                       status);
+    return check_launch("w8a8_lm_head_kernel");
+}
 
 // Columns pad to 64 (a slab), k to 128 (a GEMM stage); padding is zero.
 int64_t w8a8_tiled_bytes(int64_t K, int64_t N) {

@@ -414,6 +414,46 @@ def test_decode_mlp_block_falls_back(mcv, oracle, cuda):
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
 
 
+# The W8A8 lm_head step in one launch (mcv_w8a8_lm_head_argmax): the
+# activation quantisation, the GEMV and the argmax exchange inside one kernel,
+# bit-identical to w8a8_quantize + the argmax GEMV + the key reduction, call
+# after call through one workspace, with the fp16 (reference) and fp32 scales;
+# a forced give-up writes token -1 and the give-up words, and the next call
+# needs no reset.
+@pytest.mark.parametrize("K,N,V", [(1024, 20000, 19997), (256, 4096, 4096), (1040, 5000, 4999),
+                                   (1024, 248096, 248094)], ids=lambda v: str(v))
+def test_lm_head_w8a8_one_launch(mcv, oracle, cuda, K, N, V):
+    torch = _torch()
+    rng = np.random.default_rng(K * 3 + V)
+    x = f16_normal(rng, (1, K), 1.0)
+    wq = mcv.quantize_dense_weight_w8a8(f16_normal(rng, (K, N), 0.02))
+    xd = _f16_dev(x)
+    xq, xs, _ = mcv.w8a8_quantize(xd)
+    ws = torch.zeros(mcv.lm_head_workspace_bytes(V), dtype=torch.uint8, device="cuda")
+    for use32 in (False, True):
+        want_logits = torch.empty(V, dtype=torch.float16, device="cuda")
+        want = int(mcv.lm_head_argmax_w8a8(xq, xs if use32 else xs.half(), wq, V, want_logits,
+                                           use_f32_scale=use32).item())
+        for call in range(3):                    # the generation word advances call after call
+            logits = torch.full((V,), 7.0, dtype=torch.float16, device="cuda")
+            tok = int(mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws, logits, use_f32_scale=use32).item())
+            assert tok == want, (use32, call)
+            assert torch.equal(logits.view(torch.int16), want_logits.view(torch.int16)), (use32, call)
+        assert int(mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws, use_f32_scale=use32).item()) == want
+        if not use32:
+            assert want == oracle.argmax_f16(_u16(want_logits))
+    assert int(ws[:4].view(torch.int32).item()) == 0
+    if V == 4096:
+        status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        mcv.lib().mcv_testing_lm_head_skew_poll(1)
+        try:
+            tok = int(mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws, status=status).item())
+        finally:
+            mcv.lib().mcv_testing_lm_head_skew_poll(0)
+        assert tok == -1 and int(status.item()) == 1 and int(ws[:4].view(torch.int32).item()) != 0
+        assert int(mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws).item()) == want
+
+
 # The W8A8 lm_head with the argmax folded into the GEMV: logits bit-identical
 # to matmul_w8a8, the token the first maximum of them, with ragged V (keys for
 # 313 slabs), a tie at the maximum, and the model's vocabulary (3877 slabs).
