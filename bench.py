@@ -884,7 +884,7 @@ def _lm_head_w8a8(pkg, args, part):
     gemv_bytes = K * V + 2 * V + 2 * V + K                  # weights, fp16 scales, logits, int8 x
     nbytes = {"gemv": gemv_bytes, "argmax": 2 * V, "step": gemv_bytes + 2 * K, "parts": gemv_bytes + 2 * K,
               "unfused": gemv_bytes + 2 * V + 2 * K}[part]
-    spw, kb = pkg.lm_head_slabs_per_workgroup(V), -(-K // 128) * 4
+    spw, kb = pkg.w8a8_lm_head_slabs_per_workgroup(V), -(-K // 128) * 4
     kernel = {"step": f"w8a8_lm_head_kernel<{spw}, {1 if kb <= 16 else 2 if kb <= 32 else 4}> (one launch)",
               "parts": "w8a8_quant_act_kernel + w8a8_tiled_gemv_kernel<1, 16, 2, 2, true, false, true> + "
                        "argmax_reduce_kernel",

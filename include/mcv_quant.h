@@ -516,6 +516,11 @@ int mcv_w8a8_gemv_argmax_partials(const int8_t* xq_dev, const void* x_scale_dev,
  * share one, one call at a time).  MCV_ERR_SHAPE above K = 2048 (the three
  * launches then serve).  Replaces the W8A8 branch of lm_head_greedy
  * (src/csrc/lib/language_model.cpp:434-480). */
+/* The grid mcv_w8a8_lm_head_argmax launches for V: slabs of 64 columns per
+ * workgroup (4 from V = 130817 up, 2 from V = 65409, else 1); 0 for an
+ * unsupported V. */
+int64_t mcv_w8a8_lm_head_slabs_per_workgroup(int64_t V);
+
 int mcv_w8a8_lm_head_argmax(const void* x_dev, int64_t K, int64_t N, int64_t V, const int8_t* w_dev,
                             const void* w_scale_dev, int w_scale_dtype, int x_scale_dtype, void* logits_dev,
                             int64_t* token_dev, void* workspace_dev, uint32_t* status, mcv_stream_t stream);

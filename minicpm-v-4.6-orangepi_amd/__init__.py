@@ -105,6 +105,7 @@ _SIGS = {
                                    _c_int, _c_int, _vp]),
     "mcv_w8a8_gemv_argmax_partials": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_int, _vp, _vp,
                                                _vp]),
+    "mcv_w8a8_lm_head_slabs_per_workgroup": (_c_i64, [_c_i64]),
     "mcv_w8a8_lm_head_argmax": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp,
                                          _vp]),
     "mcv_w8a8_quantize_weight_host": (_c_int, [_vp, _c_i64, _c_i64, _vp, _c_int, _vp, _vp]),
@@ -1007,6 +1008,11 @@ def silu_mul(gate, up, out=None, stream=None):
 def lm_head_slabs_per_workgroup(vocab: int) -> int:
     """Slabs of 64 columns per workgroup the lm_head launches for `vocab` columns."""
     return int(lib().mcv_lm_head_slabs_per_workgroup(int(vocab)))
+
+
+def w8a8_lm_head_slabs_per_workgroup(vocab: int) -> int:
+    """Slabs of 64 columns per workgroup the one-launch W8A8 lm_head launches for `vocab` columns."""
+    return int(lib().mcv_w8a8_lm_head_slabs_per_workgroup(int(vocab)))
 
 
 def argmax_last_dim(x, out=None, stream=None):

@@ -21,6 +21,7 @@ int launch_w8a8_gemv_argmax(const int8_t* xq, int64_t K, int64_t V, const int8_t
                             int xs16, const void* ws, int ws16, unsigned long long* keys, hipStream_t stream);
 int launch_w8a8_lm_head(const void* x, int64_t K, int64_t V, const int8_t* w, const void* wscale, int ws16, int xs16,
                         void* logits, int64_t* token, void* ws, unsigned* status, hipStream_t stream);
+int w8a8_lm_head_spw(int64_t nslab);
 int launch_w8a8_gemm_lds_cfg(const int8_t* xq, int64_t M, int64_t K, int64_t N, const int8_t* w, void* out, bool f16,
                              const void* xs, int xs16, const void* ws, int ws16, int bm, int bn, int ns, int wr,
                              hipStream_t stream);
@@ -448,6 +449,11 @@ int mcv_w8a8_gemv_argmax_partials(const int8_t* xq, const void* xs, int xs_dtype
     if ((rc = require_device()) != MCV_OK) return rc;
     return launch_w8a8_gemv_argmax(xq, K, V, w, logits, xs, xs_dtype == MCV_F16, ws, ws_dtype == MCV_F16,
                                    static_cast<unsigned long long*>(keys), static_cast<hipStream_t>(stream));
+}
+
+int64_t mcv_w8a8_lm_head_slabs_per_workgroup(int64_t V) {
+    if (V <= 0 || V >= (int64_t(1) << 24)) return 0;
+    return w8a8_lm_head_spw(ceil_div(V, kSlab));
 }
 
 int mcv_w8a8_lm_head_argmax(const void* x, int64_t K, int64_t N, int64_t V, const int8_t* w, const void* w_scale,

@@ -207,11 +207,9 @@ int launch_w8a8_gemv(const int8_t* xq, int64_t M, int64_t K, int64_t N, const in
 // The whole W8A8 lm_head step in one launch (M = 1): the activation
 // quantisation, the GEMV over the slabs holding columns < V with the fused
 // epilogue, and the first-maximum argmax through the device-token exchange
-// (argmax_exchange.h).  The grid is the W4A16 lm_head's (lm_head_spw: SPW
-// consecutive slabs per workgroup, 243 workgroups at V = 248094), so the
-// quantisation and the exchange are paid per workgroup, not per slab (one
-// workgroup per slab, each quantising x itself: 47-48.6 us against 44.8 us
-// for the three launches).  16 waves; for each slab wave w takes k-blocks w,
+// (argmax_exchange.h).  A workgroup takes SPW consecutive slabs
+// (w8a8_lm_head_spw), so the quantisation is paid per workgroup, not per slab.
+// 16 waves; for each slab wave w takes k-blocks w,
 // w + 16, ... (both 32-column halves) with the next slab's weight lines in
 // flight; x is quantised once into LDS with the activation quantiser's
 // arithmetic (w8a8_quant_act_kernel: the row maximum is a maximum in any
@@ -344,7 +342,19 @@ __global__ __launch_bounds__(64 * kW8LmWaves) void w8a8_lm_head_kernel(
 }  // namespace
 
 unsigned lm_poll_skew();
-int lm_head_spw(int64_t nslab);
+
+// Slabs per workgroup of the W8A8 lm_head: 4 once that still gives >= 512
+// workgroups, fewer below.  Measured at V = 248094 (3877 slabs, 200 back-to-
+// back steps, MI355X): 4 slabs (970 workgroups) 41.8 us per step; 2 slabs
+// 42.1-42.3; 8 slabs 43.2; 16 slabs (one workgroup per CU, 243) 42.7; 1 slab
+// (every workgroup quantising x for one slab) 46-47.  The exchange's last
+// workgroup polls the others' keys: workgroups start in index order, so every
+// one it waits for has started and waits for nothing.
+int w8a8_lm_head_spw(int64_t nslab) {
+    int spw = 4;
+    while (spw > 1 && ceil_div(nslab, spw) < 512) spw /= 2;
+    return spw;
+}
 
 // The one-launch W8A8 lm_head (M = 1, K <= 2048).  Shapes were validated by the caller.
 int launch_w8a8_lm_head(const void* x, int64_t K, int64_t V, const int8_t* w, const void* wscale, int ws16, int xs16,
@@ -354,7 +364,7 @@ int launch_w8a8_lm_head(const void* x, int64_t K, int64_t V, const int8_t* w, co
     if (KB > 4 * kW8LmWaves) return fail(MCV_ERR_SHAPE, "w8a8 lm_head: K=%lld above 2048", (long long)K);
     if (nslab * KB * 2 * kW8Block >= (int64_t(1) << 31))
         return fail(MCV_ERR_SHAPE, "w8a8 lm_head: weight exceeds 2 GiB");
-    const int spw = lm_head_spw(nslab);
+    const int spw = w8a8_lm_head_spw(nslab);
     const int u = KB <= kW8LmWaves ? 1 : (KB <= 2 * kW8LmWaves ? 2 : 4);
     using Fn = void (*)(const uint16_t*, const int8_t*, int, int, int, int, const void*, int, int, uint16_t*,
                         unsigned long long*, int64_t*, unsigned, unsigned*);
@@ -362,7 +372,7 @@ int launch_w8a8_lm_head(const void* x, int64_t K, int64_t V, const int8_t* w, co
 #define MCV_LM8(SPW_)                                                                                        \
     if (spw == SPW_)                                                                                         \
         fn = u == 1 ? w8a8_lm_head_kernel<SPW_, 1> : (u == 2 ? w8a8_lm_head_kernel<SPW_, 2> : w8a8_lm_head_kernel<SPW_, 4>);
-    MCV_LM8(1) MCV_LM8(2) MCV_LM8(4) MCV_LM8(8) MCV_LM8(16)
+    MCV_LM8(1) MCV_LM8(2) MCV_LM8(4)
 #undef MCV_LM8
     if (fn == nullptr) return fail(MCV_ERR_INVALID_ARG, "w8a8 lm_head: no kernel for %d slabs per workgroup", spw);
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(ceil_div(nslab, spw))), dim3(64 * kW8LmWaves), 0, stream,

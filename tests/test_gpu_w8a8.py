@@ -420,9 +420,13 @@ def test_decode_mlp_block_falls_back(mcv, oracle, cuda):
 # after call through one workspace, with the fp16 (reference) and fp32 scales;
 # a forced give-up writes token -1 and the give-up words, and the next call
 # needs no reset.
+# The vocabularies take every grid the launcher picks (1, 2 and 4 slabs per
+# workgroup) and K every k-block count per wave (1, 2 and 4).
 @pytest.mark.parametrize("K,N,V", [(1024, 20000, 19997), (256, 4096, 4096), (1040, 5000, 4999),
+                                   (512, 40000, 39990), (2048, 100032, 100000), (1024, 150016, 150000),
                                    (1024, 248096, 248094)], ids=lambda v: str(v))
 def test_lm_head_w8a8_one_launch(mcv, oracle, cuda, K, N, V):
+    assert mcv.w8a8_lm_head_slabs_per_workgroup(V) == {39990: 1, 100000: 2, 150000: 4, 248094: 4}.get(V, 1)
     torch = _torch()
     rng = np.random.default_rng(K * 3 + V)
     x = f16_normal(rng, (1, K), 1.0)
