@@ -426,6 +426,22 @@ def test_lm_head_grid_choice(mcv):
     assert spw(0) == 0 and spw(1 << 24) == 0
 
 
+def test_w8a8_lm_head_grid_choice(mcv):
+    """The one-launch W8A8 lm_head: 4 slabs per workgroup while that still
+    gives >= 512 workgroups (970 on the full vocabulary), then 2, then 1; its
+    keys fit the same workspace (one key word per slab)."""
+    L = mcv.lib()
+    spw = L.mcv_w8a8_lm_head_slabs_per_workgroup
+    cases = {248094: 4, 150000: 4, 130817: 4, 130816: 2, 100000: 2, 65409: 2, 65408: 1, 31012: 1, 1: 1}
+    for V, want in cases.items():
+        assert spw(V) == want, V
+        assert mcv.w8a8_lm_head_slabs_per_workgroup(V) == want
+        nslab = -(-V // 64)
+        assert want == 1 or -(-nslab // want) >= 512
+        assert -(-nslab // want) <= nslab                    # one key word per workgroup fits
+    assert spw(0) == 0 and spw(1 << 24) == 0
+
+
 @pytest.mark.parametrize("K,N", [(1024, 3584), (200, 72), (2048, 1000)])
 def test_w8a8_checkpoint_quantiser(mcv, oracle, K, N):
     """[N, K] checkpoint bits -> int8 + scales in one host pass, bit-identical
