@@ -496,3 +496,45 @@ def test_lm_head_w8a8_fused_argmax(mcv, oracle, cuda, K, N, V):
     t32 = int(mcv.lm_head_argmax_w8a8(xq, xs, wq, V, l32, use_f32_scale=True).item())
     assert torch.equal(l32.view(torch.int16), mcv.matmul_w8a8(xq, xs, wq)[0, :V].view(torch.int16))
     assert t32 == oracle.argmax_f16(_u16(l32))
+
+
+@pytest.mark.gpu
+def test_lm_head_w8a8_one_launch_graph_replays(mcv, cuda):
+    """The one-launch W8A8 lm_head captured into a HIP graph: the kernel reads
+    the workspace's generation word afresh on every replay, so replays with
+    eager calls through the same workspace between them (the same head, and a
+    smaller vocabulary on another grid) all give the eager token and logits."""
+    torch = _torch()
+    K, N, V = 1024, 100032, 100000
+    rng = np.random.default_rng(4242)
+    x = f16_normal(rng, (1, K), 1.0)
+    wq = mcv.quantize_dense_weight_w8a8(f16_normal(rng, (K, N), 0.02))
+    xd = _f16_dev(x)
+    ws = torch.zeros(mcv.lm_head_workspace_bytes(V), dtype=torch.uint8, device="cuda")
+    want_logits = torch.empty(V, dtype=torch.float16, device="cuda")
+    want = int(mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws, want_logits).item())
+    Vs = V // 3                                          # another grid: 1 slab per workgroup instead of 2
+    assert mcv.w8a8_lm_head_slabs_per_workgroup(Vs) != mcv.w8a8_lm_head_slabs_per_workgroup(V)
+    want_s = int(np.argmax(want_logits[:Vs].float().cpu().numpy()))
+    logits = torch.empty_like(want_logits)
+    tok = torch.empty(1, dtype=torch.int64, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws, logits, tok)
+        with torch.cuda.graph(g, stream=s):
+            mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws, logits, tok)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(4):
+        logits.zero_()
+        tok.fill_(-2)
+        assert int(mcv.lm_head_argmax_w8a8_fused(xd, wq, V, ws).item()) == want, f"eager {i}"
+        assert int(mcv.lm_head_argmax_w8a8_fused(xd, wq, Vs, ws).item()) == want_s, f"eager small {i}"
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(tok.item()) == want, f"replay {i}"
+        assert torch.equal(logits.view(torch.int16), want_logits.view(torch.int16)), f"replay {i}"
+    assert int(ws[:4].view(torch.int32).item()) == 0         # no wait gave up
